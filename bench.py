@@ -1,0 +1,178 @@
+"""Batch-1 greedy decode throughput of the synthetic hybrid 4B-shape model on one MI355X.
+
+One step = one greedy decode token through all 32 layers and the LM head,
+entirely on the device (one HIP graph launch: embedding of the previous
+argmax, 24 DeltaNet + 8 gated-GQA layers, Q6_K LM head, argmax). The prompt
+(1024 uniform random ids) is prefilled first; W warm-up steps are not timed;
+exactly K steps are timed between device synchronisations.
+
+Also reported, on the same run:
+  roofline      the fused dequant-GEMV kernel (the decode's dominant kernel):
+                algorithmic bytes of the GEMV launches of one step divided by
+                their GPU time, measured with HIP events on the chain's stream
+                by replaying exactly those launches (weights 2.6 GB: cold).
+  cpu_baseline  the reference CPU path compiled from the reference sources
+                (oracle/_ref, OpenMP on this host's cores) on a bounded sample
+                of the same workload; the oracle's C restatement if that
+                library is absent.
+  gemv_*        stand-alone cold-cache GEMV legs (Q4_K / Q6_K LM-head shapes).
+  decode_0_8b   the same measurement on the 0.8B-shape model.
+
+usage: python bench.py [--gpus 1] [--steps 512] [--warmup 16] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "meta-work_amd"))
+
+import numpy as np  # noqa: E402
+
+import xjpipe as xp  # noqa: E402
+
+METRIC = "batch-1 decode tok/s (hybrid Q4_K 0.8B/4B shapes); GEMV HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def model_path(cfg, name):
+    d = os.environ.get("XJ_MODEL_DIR", "/tmp/xj_models")
+    os.makedirs(d, exist_ok=True)
+    p = os.path.join(d, f"{name}_{cfg.seed}.gguf")
+    if not os.path.exists(p):
+        t = time.time()
+        n = xp.write_model(p + ".tmp", cfg)
+        os.replace(p + ".tmp", p)
+        log(f"wrote {p} ({n / 1e9:.2f} GB) in {time.time() - t:.1f} s")
+    return p
+
+
+def decode_run(cfg, name, n_prompt, steps, warmup, seed):
+    m = xp.Model(model_path(cfg, name))
+    hp = m.hp
+    n_ctx = n_prompt + warmup + steps + 8
+    t = time.time()
+    st = xp.HipStage(m, 0, hp.n_layer, n_ctx, 8, True)
+    log(f"{name}: uploaded in {time.time() - t:.1f} s ({xp.tune_note()})")
+    ch = xp.Chain([st])
+    prompt = np.random.default_rng(seed).integers(0, hp.n_vocab, n_prompt).astype(np.int32)
+    t = time.time()
+    first = ch.eval(prompt)
+    log(f"{name}: prefill {n_prompt} tokens in {time.time() - t:.2f} s, first token {int(first[0])}")
+    if warmup:
+        ch.decode(warmup)
+    t0 = time.perf_counter()
+    toks = ch.decode(steps)          # synchronises before and after the replayed graphs
+    wall = time.perf_counter() - t0
+    gpu_ms = ch.last_decode_ms
+    return dict(m=m, st=st, ch=ch, prompt=prompt, first=int(first[0]), toks=toks, wall=wall, gpu_ms=gpu_ms)
+
+
+def cpu_baseline(cfg, name, n_prompt_cpu, n_steps_cpu, seed):
+    """Reference CPU path (oracle/_ref) or the oracle restatement on the host cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    kind = "reference" if orc.ref_available() else "port"
+    m = xp.Model(model_path(cfg, name))
+    hp = m.hp
+    stage = orc.CpuStage(m.ptr, 0, hp.n_layer, n_prompt_cpu + n_steps_cpu + 8, 8, True, ref=(kind == "reference"))
+    prompt = np.random.default_rng(seed).integers(0, hp.n_vocab, n_prompt_cpu).astype(np.int32)
+    x = np.stack([orc.embed(m.ptr, int(t)) for t in prompt])
+    stage.forward(x)
+    tok = int(np.argmax(stage.logits(x[-1:])[0]))
+    t0 = time.perf_counter()
+    for _ in range(n_steps_cpu):
+        x = orc.embed(m.ptr, tok)[None].copy()
+        stage.forward(x)
+        tok = int(np.argmax(stage.logits(x)[0]))
+    dt = time.perf_counter() - t0
+    stage.destroy()
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(n_steps_cpu / dt, 3), "unit": "tok/s", "cores": cores, "kind": kind,
+            "sample": f"{name} model, {n_prompt_cpu}-token random prompt, {n_steps_cpu} timed greedy decode steps "
+                      f"(fp32 KV, OpenMP over {cores} threads, {dt:.1f} s)"}
+
+
+def gemv_leg(t, rows, k, copies, iters):
+    """Cold-cache GEMV: `copies` distinct weights (> 512 MB in total) launched in rotation."""
+    xs = xp.fill_normal(k, 5, 1.0)[None]
+    blob = xp.quantize(t, xp.fill_normal(rows * k, 17, 0.02).reshape(rows, k))
+    ws = [xp.DevWeight(t, blob, rows, k) for _ in range(copies)]
+    ms = xp.gemv_time(ws, xs, iters)
+    by = rows * xp.row_bytes(t, k) + k * 4 + rows * 4
+    for w in ws:
+        w.free()
+    return {"shape": f"{xp.TYPE_NAMES[t]} {rows}x{k} T=1", "us": round(ms * 1e3, 2),
+            "GBps": round(by / (ms * 1e-3) / 1e9, 1), "frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=512)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the 0.8B run and the GEMV legs")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs the token loop on a single MI355X and has no "
+              f"multi-GPU path (--gpus {args.gpus} requested)", file=sys.stderr)
+        sys.exit(2)
+
+    log(f"device: {xp.device_name()}")
+    r = decode_run(xp.CONFIG_4B, "synth4b", 1024, args.steps, args.warmup, seed=20261107)
+    tok_s = args.steps / r["wall"]
+    ms_step = r["wall"] * 1e3 / args.steps
+    log(f"4B decode: {tok_s:.1f} tok/s wall, {r['gpu_ms']:.3f} ms/step GPU events")
+
+    g_ms, g_bytes, g_launch = r["ch"].time_gemv(8)
+    achieved = g_bytes / (g_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "gemv_kernel<1,1> (fused dequant-GEMV, T=1)",
+                "bytes_per_launch": round(g_bytes / g_launch), "launches_per_step": g_launch,
+                "us_per_launch": round(g_ms * 1e3 / g_launch, 3), "gemv_share_of_step": round(g_ms / r["gpu_ms"], 3)}
+    log(f"GEMV leg: {g_launch} launches/step, {g_bytes / 1e9:.3f} GB/step, {g_ms:.3f} ms -> {achieved:.0f} GB/s")
+    r["ch"].free()
+    r["st"].destroy()
+
+    extra = {}
+    if not args.no_extra:
+        r8 = decode_run(xp.CONFIG_0_8B, "synth08b", 512, 256, 8, seed=20261108)
+        extra["decode_0_8b"] = {"tok_s": round(256 / r8["wall"], 1), "gpu_ms_per_step": round(r8["gpu_ms"], 4),
+                                "prompt": 512, "steps": 256}
+        r8["ch"].free()
+        r8["st"].destroy()
+        extra["gemv_legs"] = [gemv_leg(xp.Q4_K, 151936, 1024, 8, 64), gemv_leg(xp.Q6_K, 151936, 2560, 3, 24),
+                              gemv_leg(xp.Q4_K, 4096, 1024, 256, 512)]
+        log(f"extra: {extra}")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(xp.CONFIG_4B, "synth4b", 16, 48, seed=20261107)
+        log(f"cpu baseline: {cpu}")
+
+    out = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (random-init weights, uniform random prompt ids)",
+        "config": {"workload": "greedy decode, synthetic hybrid 4B shape: hidden 2560, 32 layers (24 Gated-DeltaNet "
+                               "32x128 + 8 gated GQA 16q/4kv d256), FFN 9216, vocab 151936, Q4_K_M-style "
+                               "(Q4_K + Q6_K v/down/head), fp16 KV cache, 1024-token prompt, batch 1",
+                   "global_batch": 1, "prompt": 1024, "parallelism": "single GPU"},
+        "gpu_ms_per_step": round(r["gpu_ms"], 4),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    out.update(extra)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,202 @@
+/*
+ * xj_hip.h - the MI355X (gfx950) backend for the xiaoju-pipe token loop.
+ *
+ * Three layers, all C ABI (plain pointers and sizes):
+ *
+ *  1. The drop-in stage. xj_hip_stage_new returns a `struct xj_stage` whose
+ *     vtable behaves like the Metal stage it replaces, so the reference's
+ *     pipeline (xj_pipeline_eval/verify/rollback) and speculative driver run
+ *     on it unchanged.
+ *       xj_hip_stage_new    <- xj_metal_stage_new  src/xiaoju-pipe/core/xj_stage.h:46-47
+ *       xj_hip_device_name  <- xj_metal_device_name src/xiaoju-pipe/core/xj_stage.h:48
+ *       xj_hip_tune_note    <- xj_metal_tune_note  src/xiaoju-pipe/core/xj_stage.h:50
+ *
+ *  2. Host-side counterparts of the reference loader, needed because the
+ *     reference sources do not ship with this library:
+ *       xj_model_load / xj_model_free <- src/xiaoju-pipe/core/xj_model.h:125,130
+ *       xj_row_bytes / xj_type_block  <- src/xiaoju-pipe/core/gguf.h:81-83
+ *     plus a writer for synthetic qwen35 GGUF files and the Q4_K / Q6_K /
+ *     Q8_0 quantizers it uses (the reference has none for K-quants).
+ *
+ *  3. Device-resident extensions with no Metal counterpart: a chain of HIP
+ *     stages that keeps the hidden state in HBM between stages, embeds token
+ *     ids and takes the greedy argmax on the device, and replays one decode
+ *     step as a HIP graph; a speculative driver with a separate draft model;
+ *     and one C entry point per kernel (dequant, GEMV, norms, RoPE, attention,
+ *     DeltaNet, argmax) used by the parity tests and the benchmark.
+ *
+ * Errors: every function that can fail returns -1 (or NULL) and writes a
+ * message into err[errlen], as the reference does.
+ */
+#ifndef XJ_HIP_H
+#define XJ_HIP_H
+
+#include "xj_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- stage -- */
+
+/* Same contract as xj_metal_stage_new (xj_stage.h:46-47, semantics
+ * xj_metal.m:554-663): validates the layer range and weight mapping, copies
+ * the weights of [l0,l1) (and the head when has_head) into HBM, allocates the
+ * fp16 KV cache of every attention layer ([n_ctx][n_head_kv*head_dim]) and the
+ * fp32 conv/recurrent state of every DeltaNet layer. backend = "hip". */
+xj_stage   *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_ctx, int max_batch,
+                             bool has_head, char *err, size_t errlen);
+const char *xj_hip_device_name(void);
+const char *xj_hip_tune_note(void);
+
+/* Bytes of HBM a stage holds besides the repacked weights
+ * (counterpart of xj_stage_state_bytes, xj_stage.h:57). */
+uint64_t    xj_hip_stage_state_bytes(const xj_model *m, int l0, int l1, int n_ctx, int max_batch);
+
+/* Copy the whole recurrent state (conv + DeltaNet state of every layer) of a
+ * HIP stage into snapshot slot `slot` (0 <= slot < 8), and restore it while
+ * setting n_past. Lets a draft model roll back across separate T=1 calls,
+ * which the reference's keep/rollback (one forward call only) cannot. */
+int xj_hip_stage_snapshot(xj_stage *s, int slot, char *err, size_t errlen);
+int xj_hip_stage_restore(xj_stage *s, int slot, int n_past, char *err, size_t errlen);
+
+/* -------------------------------------------------------- host loader -- */
+
+int         xj_type_block(uint32_t type, int *block_bytes);
+uint64_t    xj_row_bytes(uint32_t type, int64_t n);
+const char *xj_type_name(uint32_t type);
+xj_model   *xj_model_load(const char *path, char *err, size_t errlen);
+void        xj_model_free(xj_model *m);
+
+/* --------------------------------------------------- synthetic models -- */
+
+/* Shape and quantization recipe of a random-weight qwen35 model. Matrices are
+ * N(0, w_std); norm weights 1 + 0.1 N; ssm_a = -exp(0.5 N); ssm_dt = 0.5 N;
+ * conv1d 0.5 N. Every value is a pure function of (seed, tensor name, row). */
+typedef struct {
+    int n_layer, n_embd, n_ff, n_vocab;
+    int n_head, n_head_kv, head_dim, n_rot;
+    float rope_base, eps;
+    int conv_k, s_k, h_k, h_v;          /* d_inner = h_v * s_k */
+    int full_attn_interval;
+    uint32_t type_default;              /* every matrix not named below */
+    uint32_t type_embd, type_out, type_v, type_down;
+    float w_std;
+    uint64_t seed;
+} xjs_config;
+
+/* Fill out[n] with N(0, std) from the build's generator: splitmix64 feeding
+ * Box-Muller in double, rounded to float. */
+void xjs_fill_normal(float *out, int64_t n, uint64_t seed, float std);
+/* Per-tensor seed = seed ^ FNV-1a(name). */
+uint64_t xjs_tensor_seed(uint64_t seed, const char *name);
+/* Quantize n_rows rows of k floats into `out` (row_bytes(type, k) each). */
+int  xjs_quantize(uint32_t type, const float *x, int64_t n_rows, int64_t k, void *out,
+                  char *err, size_t errlen);
+/* Write a qwen35 GGUF v3 file for cfg; returns total bytes or -1. */
+int64_t xjs_write_model(const char *path, const xjs_config *cfg, char *err, size_t errlen);
+
+/* ------------------------------------------ device chain (fast path) -- */
+
+typedef struct xjh_chain xjh_chain;
+
+/* A chain runs HIP stages in sequence on one stream with the hidden state
+ * kept in HBM; the last stage must have the head. Mirrors the no-remote branch
+ * of eval_once (xj_net.c:541-559) with embedding and argmax on the device. */
+xjh_chain *xjh_chain_new(xj_stage **stages, int n_stages, char *err, size_t errlen);
+void       xjh_chain_free(xjh_chain *c);
+/* Feed n tokens in chunks of max_batch. When nlog > 0 the logits of the last
+ * min(nlog, rows) rows of the final chunk are computed: copied to `logits`
+ * [nlog][n_vocab] when it is not NULL, and their greedy argmax (first maximum)
+ * written to `argmax`. keep != 0 turns this call into a verify (xj_net.c:668):
+ * all n tokens in one chunk, recurrent checkpoints kept for rollback. */
+int  xjh_chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int keep,
+                    float *logits, int32_t *argmax, char *err, size_t errlen);
+/* n_steps greedy steps entirely on the device. The first input token is the
+ * argmax left by the previous eval/decode; out[i] receives the token chosen
+ * after step i (so out[0] is the argmax of the first step's logits). One step
+ * is one HIP graph launch. */
+int  xjh_chain_decode(xjh_chain *c, int n_steps, int32_t *out, char *err, size_t errlen);
+/* Greedy token that the next decode step would feed (the last argmax). */
+int  xjh_chain_last_token(xjh_chain *c);
+int  xjh_chain_rollback(xjh_chain *c, int n_past, char *err, size_t errlen);
+void xjh_chain_reset(xjh_chain *c);
+int  xjh_chain_n_past(xjh_chain *c);
+/* Average GPU time of the last xjh_chain_decode, in ms per step, from HIP
+ * events recorded on the chain's stream around the replayed graphs. */
+double xjh_chain_last_decode_ms(xjh_chain *c);
+
+/* Run only the GEMV launches of one T=1 decode step (same shapes and weights,
+ * epilogues redirected to scratch so no state changes) `iters` times between
+ * HIP events on the chain's stream. Reports the mean GPU ms per step, the
+ * algorithmic HBM bytes of those launches per step, and the launch count. */
+int  xjh_chain_time_gemv(xjh_chain *c, int iters, double *ms_per_step, double *bytes_per_step,
+                         int *launches_per_step, char *err, size_t errlen);
+
+/* Speculative decoding with a separate draft model (no reference
+ * counterpart: the reference drafts with an MTP layer, xj_spec.c:131-209, and
+ * the accept/rollback rule below is that function's). Each step feeds the
+ * pending token t to the draft and lets it propose up to k tokens by greedy
+ * T=1 steps, verifies [t, d1..dk] on the target in one batch, accepts the
+ * longest prefix the target's argmax agrees with and rolls both models back.
+ * oracle (optional, n_oracle ids) replaces the drafts, with every
+ * (g*7+j) % oracle_miss == 0 draft made wrong, as xj_spec.c:173-177. */
+typedef struct {
+    long n_steps, n_drafted, n_accepted;
+    long acc_at[4];
+    double t_total_ms, t_draft_ms;
+} xjh_spec_stats;
+int xjh_spec_generate(xjh_chain *target, xjh_chain *draft, int k, int n_gen,
+                      const int32_t *oracle, int n_oracle, int oracle_miss,
+                      int32_t *out, xjh_spec_stats *stats, char *err, size_t errlen);
+
+/* ----------------------------------------------------- per-op kernels -- */
+
+/* Device memory and stream helpers for tests and benchmarks. All per-op
+ * entry points run on the library's own stream and return after the GPU
+ * finished unless stated otherwise. */
+void *xjh_malloc(size_t bytes);
+void  xjh_free(void *p);
+int   xjh_h2d(void *dst, const void *src, size_t bytes);
+int   xjh_d2h(void *dst, const void *src, size_t bytes);
+int   xjh_sync(void);
+const char *xjh_last_error(void);
+
+/* Repack a GGUF tensor (n_rows rows of k elements, GGUF block layout) into the
+ * device layout the kernels read; returns the device pointer, NULL on error.
+ * Q4_K and F32 keep the GGUF layout; Q6_K and Q8_0 are split into planes
+ * (quants, high bits, scales, d) so every load is 16-byte aligned. */
+void *xjh_upload_weight(uint32_t type, const void *host, int64_t n_rows, int64_t k,
+                        char *err, size_t errlen);
+/* Bit-exact dequantization of rows [r0, r0+n) of an uploaded weight into y. */
+int xjh_dequant(uint32_t type, const void *dw, int64_t n_rows, int64_t k, int64_t r0, int64_t n,
+                float *y, char *err, size_t errlen);
+/* y[t][r] = W[r] . x[t] (add != 0: y += ...), T in 1..max, fp32 accumulate. */
+int xjh_gemv(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T,
+             float *y, int add, char *err, size_t errlen);
+/* Time `iters` back-to-back launches of xjh_gemv over n_copies weights
+ * (rotating, to defeat the caches), with HIP events on the library stream.
+ * Returns the mean ms per launch, or -1. */
+double xjh_gemv_time(uint32_t type, void *const *dws, int n_copies, int64_t n_rows, int64_t k,
+                     const float *x, int T, float *y, int iters, char *err, size_t errlen);
+/* out[t] = rmsnorm(x[t]) * w  (mode 0) or x[t]/sqrt(sum x^2 + eps) (mode 1). */
+int xjh_norm(int mode, const float *x, const float *w, int n, int rows, float eps, float *out,
+             char *err, size_t errlen);
+/* First index of the maximum of each of T rows of n floats. */
+int xjh_argmax(const float *x, int n, int T, int32_t *out_host, char *err, size_t errlen);
+/* Gated delta rule (standalone, decay and beta given per token and head):
+ * state [H][S][S] ([head][value j][key i], as xj_cpu.c:203), q,k,v [T][H][S],
+ * decay,beta [T][H], out [T][H][S]. o = S^T q * qscale after the update. */
+int xjh_delta_recurrent(int H, int S, int T, const float *q, const float *k, const float *v,
+                        const float *decay, const float *beta, float qscale,
+                        float *state, float *out, char *err, size_t errlen);
+/* The same recurrence evaluated chunk-wise (chunk tokens per chunk) with the
+ * chunk-level products on MFMA; must agree with xjh_delta_recurrent. */
+int xjh_delta_chunked(int H, int S, int T, int chunk, const float *q, const float *k,
+                      const float *v, const float *decay, const float *beta, float qscale,
+                      float *state, float *out, char *err, size_t errlen);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* XJ_HIP_H */

@@ -1,0 +1,106 @@
+// Device-side helpers shared by the gfx950 kernels: fp16 conversion, 16-lane
+// DPP reductions, block reductions, and the error plumbing of the host side.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+
+#define XJ_CHECK(call, err, errlen, ...)                                                     \
+    do {                                                                                     \
+        hipError_t e_ = (call);                                                              \
+        if (e_ != hipSuccess) {                                                              \
+            snprintf(err, errlen, "%s: %s", #call, hipGetErrorString(e_));                   \
+            return __VA_ARGS__;                                                              \
+        }                                                                                    \
+    } while (0)
+
+namespace xjd {
+
+// fp16 bits -> fp32; the hardware conversion is exact, subnormals included.
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+    _Float16 h;
+    uint16_t b = (uint16_t)bits16;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;
+}
+
+// fp32 -> fp16 bits, round to nearest even (overflow -> inf).
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+    _Float16 h = (_Float16)f;
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+__device__ __forceinline__ float sigm(float v) { return 1.0f / (1.0f + expf(-v)); }
+__device__ __forceinline__ float softplus(float v) { return v > 20.0f ? v : log1pf(expf(v)); }
+
+// DPP row (16-lane) butterfly: after the four steps every lane of the row holds
+// the sum over the row. The order of additions is fixed, so results are
+// reproducible run to run.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);  // row_half_mirror
+    v += dpp<0x140>(v);  // row_mirror
+    return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    v = fmaxf(v, dpp<0x140>(v));
+    return v;
+}
+
+// Sum over the 64 lanes of a wavefront in double (fixed order).
+__device__ __forceinline__ double wave_sum_d(double v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// Block-wide sum (blockDim.x a multiple of 64, <= 1024) in double; every
+// thread gets the total. red must hold blockDim.x/64 doubles.
+__device__ __forceinline__ double block_sum_d(double v, double *red) {
+    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    v = wave_sum_d(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    double s = 0;
+    for (int i = 0; i < nw; i++) s += red[i];
+    return s;
+}
+__device__ __forceinline__ float block_max(float v, float *red) {
+    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float m = red[0];
+    for (int i = 1; i < nw; i++) m = fmaxf(m, red[i]);
+    return m;
+}
+
+// Greedy argmax key: larger key = larger value, ties -> lower index, NaN lowest.
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
+    uint32_t b = __float_as_uint(v);
+    uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    if (v != v) ord = 0;
+    return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
+}
+__device__ __forceinline__ uint32_t argmax_key_index(unsigned long long k) {
+    return 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull);
+}
+
+}  // namespace xjd

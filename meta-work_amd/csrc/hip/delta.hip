@@ -1,0 +1,141 @@
+// Gated DeltaNet recurrent update (gfx950).
+//
+// delta_kernel: the per-token body of attn_linear (src/xiaoju-pipe/core/xj_cpu.c:183-219)
+// after the conv (which the qkv GEMV epilogue already applied): L2-normalise
+// q and k of key head hk = hv % Hk (double sum, x / sqrt(sum + eps)), then for
+// every value row j of head hv
+//     S_j <- exp(softplus(alpha + dt) * A) * S_j
+//     delta_j = (v_j - S_j . k) * sigmoid(beta)
+//     S_j <- S_j + k * delta_j,   o_j = (S_j . q) / sqrt(S)
+// The gated RMSNorm of o happens in the ssm_out GEMV prologue.
+//
+// Mapping: work-group (hv, 16 value rows); a 16-lane team owns one row j and
+// each lane keeps S/16 consecutive entries of it in registers across all T
+// tokens, so the 64 KB (S=128) head state is read and written once per call.
+// Per element the updates are the reference's own: m*eg, fma(m, k, sk),
+// fma(k, delta, m), fma(m, q, acc); only the 16 lane partial sums are combined
+// in a fixed butterfly instead of one running sum. With keep, the state after
+// each token t < keep_n is written to checkpoint t (xj_cpu.c:218).
+//
+// delta_rec_kernel: the same rule with decay and beta given per token and head
+// (the standalone layer test), q and k used as given.
+#include "common.h"
+#include "kernels.h"
+
+namespace xjk {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int S>
+__device__ __forceinline__ void load_row(const float *p, float (&m)[S / 16]) {
+#pragma unroll
+    for (int i = 0; i < S / 16; i += 4) {
+        const f32x4 v = *(const f32x4 *)(p + i);
+        m[i] = v.x; m[i + 1] = v.y; m[i + 2] = v.z; m[i + 3] = v.w;
+    }
+}
+template <int S>
+__device__ __forceinline__ void store_row(float *p, const float (&m)[S / 16]) {
+#pragma unroll
+    for (int i = 0; i < S / 16; i += 4) {
+        f32x4 v = {m[i], m[i + 1], m[i + 2], m[i + 3]};
+        *(f32x4 *)(p + i) = v;
+    }
+}
+
+// one token of the rule for the row held in m; returns o_j (unscaled) in every lane
+template <int S>
+__device__ __forceinline__ float rule_step(float (&m)[S / 16], const float *ks, const float *qs, int i0,
+                                           float eg, float b, float vj) {
+    constexpr int IPL = S / 16;
+    float sk = 0.f;
+#pragma unroll
+    for (int i = 0; i < IPL; i++) {
+        m[i] = m[i] * eg;
+        sk = fmaf(m[i], ks[i0 + i], sk);
+    }
+    sk = xjd::row16_sum(sk);
+    const float delta = (vj - sk) * b;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < IPL; i++) {
+        m[i] = fmaf(ks[i0 + i], delta, m[i]);
+        acc = fmaf(m[i], qs[i0 + i], acc);
+    }
+    return xjd::row16_sum(acc);
+}
+
+template <int S>
+__global__ __launch_bounds__(256) void delta_kernel(const DeltaArgs a) {
+    constexpr int IPL = S / 16;
+    const int hv = blockIdx.x, tid = threadIdx.x;
+    const int j = blockIdx.y * 16 + (tid >> 4), l16 = tid & 15, i0 = l16 * IPL;
+    const int hk = hv % a.Hk;
+    __shared__ float qs[S], ks[S];
+    __shared__ double red[2][4];
+    float m[IPL];
+    float *Mp = a.state + ((int64_t)hv * S + j) * S + i0;
+    load_row<S>(Mp, m);
+    for (int t = 0; t < a.T; t++) {
+        const float *row = a.qkv + (int64_t)t * a.qkv_s;
+        const float qv = tid < S ? row[hk * S + tid] : 0.f, kv = tid < S ? row[a.k_off + hk * S + tid] : 0.f;
+        const double sq = xjd::block_sum_d((double)qv * qv, red[0]);
+        const double sk2 = xjd::block_sum_d((double)kv * kv, red[1]);
+        if (tid < S) {
+            qs[tid] = qv * (1.0f / sqrtf((float)sq + a.eps));
+            ks[tid] = kv * (1.0f / sqrtf((float)sk2 + a.eps));
+        }
+        __syncthreads();
+        const float b = xjd::sigm(a.beta[(int64_t)t * a.beta_s + hv]);
+        const float g = xjd::softplus(a.alpha[(int64_t)t * a.alpha_s + hv] + a.dt[hv]) * a.A[hv];
+        const float eg = expf(g);
+        const float vj = row[a.v_off + hv * S + j];
+        const float o = rule_step<S>(m, ks, qs, i0, eg, b, vj);
+        if (l16 == 0) a.out[(int64_t)t * a.out_s + hv * S + j] = o * a.qscale;
+        if (t < a.keep_n) store_row<S>(a.ck + (((int64_t)t * a.Hv + hv) * S + j) * S + i0, m);
+        __syncthreads();
+    }
+    store_row<S>(Mp, m);
+}
+
+template <int S>
+__global__ __launch_bounds__(256) void delta_rec_kernel(int H, int T, const float *q, const float *k, const float *v,
+                                                        const float *decay, const float *beta, float qscale,
+                                                        float *state, float *out) {
+    constexpr int IPL = S / 16;
+    const int hh = blockIdx.x, tid = threadIdx.x;
+    const int j = blockIdx.y * 16 + (tid >> 4), l16 = tid & 15, i0 = l16 * IPL;
+    __shared__ float qs[S], ks[S];
+    float m[IPL];
+    float *Mp = state + ((int64_t)hh * S + j) * S + i0;
+    load_row<S>(Mp, m);
+    for (int t = 0; t < T; t++) {
+        const int64_t base = ((int64_t)t * H + hh) * S;
+        if (tid < S) { qs[tid] = q[base + tid]; ks[tid] = k[base + tid]; }
+        __syncthreads();
+        const float o = rule_step<S>(m, ks, qs, i0, decay[(int64_t)t * H + hh], beta[(int64_t)t * H + hh], v[base + j]);
+        if (l16 == 0) out[base + j] = o * qscale;
+        __syncthreads();
+    }
+    store_row<S>(Mp, m);
+}
+
+int delta_launch(const DeltaArgs &a, hipStream_t st) {
+    if (a.S == 128) hipLaunchKernelGGL(delta_kernel<128>, dim3(a.Hv, 128 / 16), dim3(256), 0, st, a);
+    else if (a.S == 64) hipLaunchKernelGGL(delta_kernel<64>, dim3(a.Hv, 64 / 16), dim3(256), 0, st, a);
+    else return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int delta_recurrent_launch(int H, int S, int T, const float *q, const float *k, const float *v, const float *decay,
+                           const float *beta, float qscale, float *state, float *out, hipStream_t st) {
+    if (S == 128)
+        hipLaunchKernelGGL(delta_rec_kernel<128>, dim3(H, 128 / 16), dim3(256), 0, st, H, T, q, k, v, decay, beta, qscale, state, out);
+    else if (S == 64)
+        hipLaunchKernelGGL(delta_rec_kernel<64>, dim3(H, 64 / 16), dim3(256), 0, st, H, T, q, k, v, decay, beta, qscale, state, out);
+    else
+        return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace xjk

@@ -1,0 +1,131 @@
+// Host-side launch interface of the gfx950 kernels (internal to the library).
+//
+// Device weight layouts (produced by upload_repack, read by every kernel):
+//   F32   rows of K floats (GGUF layout)
+//   Q4_K  GGUF blocks of 144 B (16-byte aligned: 16 B header + 128 B nibbles)
+//   Q6_K  four planes over the tensor's blocks g = row*nb + b:
+//         ql[g][128] | qh[g][64] | sc[g][16] | d[g] (fp16)
+//   Q8_0  two planes: qs[g][32] | d[g] (fp16)
+// The repack only moves bytes; every decode reproduces the GGUF block exactly.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace xjk {
+
+constexpr int kMaxSeg = 4;
+constexpr int kTileT = 8;        // tokens per GEMV launch (larger T is tiled)
+
+enum Pro { PRO_NONE = 0, PRO_RMS = 1, PRO_SWIGLU = 2, PRO_GATED_RMS = 3 };
+enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_CONV = 2 };
+
+struct DevW {
+    const uint8_t *p = nullptr;
+    uint32_t type = 0;
+    int64_t n_rows = 0, k = 0;
+    size_t bytes = 0;
+};
+
+struct GSeg {
+    const uint8_t *w;
+    uint32_t type;
+    int32_t n_rows;
+    int32_t wg0, nwg;            // work-group range of this segment
+    int64_t nblk;                // blocks in the tensor (plane stride for Q6_K / Q8_0)
+    float *y;                    // y[t * ys + row]
+    int32_t ys;
+    int32_t epi;
+    // EPI_CONV: depthwise causal conv + SiLU on this segment's rows
+    float *conv_state;           // [rows][conv_k-1]
+    const float *conv_w;         // [rows][conv_k]
+    float *conv_ck;              // [keep][rows][conv_k-1]
+    int32_t conv_k;
+    // greedy argmax partials, one key per (token, work-group); may be null
+    unsigned long long *amax;
+};
+
+struct GArgs {
+    const float *x;  int32_t xs;   // input rows x[t * xs + k]
+    const float *x2; int32_t x2s;  // second input (SwiGLU up, gated-RMS z)
+    int32_t K, T;
+    int32_t pro;
+    const float *pro_w; float eps; int32_t group;
+    int32_t t0;                    // absolute index of token 0 of this tile (checkpoints)
+    int32_t keep_n;                // conv checkpoints for absolute tokens t < keep_n
+    int32_t *inc_ptr; int32_t inc_by;
+    int32_t nseg;
+    GSeg seg[kMaxSeg];
+};
+
+// One GEMV launch (T <= kTileT) over all segments. Segment i covers row
+// groups [wg0, wg0+nwg) with nwg = ceil(n_rows / gemv_rows_per_group(K)).
+int gemv_launch(const GArgs &a, hipStream_t st);
+int gemv_team_lanes(int K);        // lanes per row: 16, 32 or 64
+int gemv_rows_per_group(int K);    // rows per row group (256 / lanes)
+int gemv_init(char *err, size_t errlen);       // raise the dynamic-LDS limit once
+int gemv_max_tile(int K);                       // largest T tile whose activations fit in LDS
+
+// Repack a GGUF tensor into the device layout. dst must hold `bytes` =
+// n_rows * row_bytes(type, k); src is host memory in GGUF layout.
+int upload_repack(uint32_t type, const void *src, int64_t n_rows, int64_t k, uint8_t *dst,
+                  hipStream_t st, char *err, size_t errlen);
+
+int dequant_launch(const DevW &w, int64_t r0, int64_t n, float *y, hipStream_t st);
+
+struct AttnArgs {
+    const float *qg; int32_t qg_s;      // q|gate interleaved per head, token stride
+    const float *kn; int32_t kn_s;      // new keys [T][Hkv*D] (pre-norm)
+    const float *vn; int32_t vn_s;
+    uint16_t *kc, *vc;                   // fp16 caches [n_ctx][Hkv*D]
+    const float *qnorm_w, *knorm_w;
+    const float *inv_freq;               // [n_rot/2]
+    const int32_t *npast;
+    float *scores;                       // split partials [T][H][n_split][D+2]
+    float *out;                          // [T][H*D]
+    int32_t T, H, Hkv, D, n_rot, n_ctx, n_split;
+    float eps, scale;
+};
+int attn_launch(const AttnArgs &a, hipStream_t st);
+int attn_splits(int n_ctx);             // 64-position splits covering n_ctx
+
+struct DeltaArgs {
+    const float *qkv; int32_t qkv_s;    // conv+SiLU outputs [T][conv_dim]
+    int32_t k_off, v_off;
+    const float *beta; int32_t beta_s;  // raw projections [T][Hv]
+    const float *alpha; int32_t alpha_s;
+    const float *dt, *A;
+    float *state;                        // [Hv][S][S] ([value j][key i])
+    float *ck;                           // [keep][Hv][S][S]
+    float *out; int32_t out_s;           // [T][Hv*S]
+    int32_t T, Hk, Hv, S, keep_n;
+    float eps, qscale;
+};
+int delta_launch(const DeltaArgs &a, hipStream_t st);
+
+// Standalone gated delta rule (decay/beta given), recurrent and chunked.
+int delta_recurrent_launch(int H, int S, int T, const float *q, const float *k, const float *v,
+                           const float *decay, const float *beta, float qscale, float *state,
+                           float *out, hipStream_t st);
+int delta_chunked_launch(int H, int S, int T, int chunk, const float *q, const float *k,
+                         const float *v, const float *decay, const float *beta, float qscale,
+                         float *state, float *out, float *work, hipStream_t st);
+size_t delta_chunked_work_bytes(int H, int S, int T, int chunk);
+
+// Embedding rows for T tokens: x[t] = dequant(tok_embd row tokens[t]).
+struct EmbedArgs {
+    const int32_t *tokens;
+    DevW w;
+    float *x; int32_t T;
+};
+int embed_launch(const EmbedArgs &a, hipStream_t st);
+// out[t] (optional) = greedy argmax over amax[t][0..n_part); tok_out (optional)
+// receives the last row's id; hist/step (optional, T == 1 only) append it to a
+// device-side history and advance the step counter.
+int argmax_finalize_launch(const unsigned long long *amax, int n_part, int T, int32_t *out, int32_t *tok_out,
+                           int32_t *hist, int32_t *step, hipStream_t st);
+// Plain argmax of T rows of n floats (first maximum).
+int argmax_rows_launch(const float *x, int n, int T, int32_t *out, hipStream_t st);
+int norm_launch(int mode, const float *x, const float *w, int n, int rows, float eps, float *out, hipStream_t st);
+
+}  // namespace xjk

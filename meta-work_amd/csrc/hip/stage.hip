@@ -1,0 +1,1080 @@
+// The HIP stage: drop-in replacement for the Metal stage of the xiaoju-pipe
+// token loop, plus the device-resident chain and the speculative driver.
+//
+// Contract followed (behaviour, not code):
+//   constructor      xj_metal_stage_new  src/xiaoju-pipe/metal/xj_metal.m:554-663
+//   forward          metal_forward       xj_metal.m:422-475 (T and context checks,
+//                    keep only for T > 1, ck_start/ck_T, n_past += T, keep cleared)
+//   logits           metal_logits        xj_metal.m:477-497
+//   rollback         metal_rollback      xj_metal.m:500-534 (recurrent stages restore
+//                    checkpoint n_past-ck_start-1; attention-only stages truncate)
+//   reset            metal_reset         xj_metal.m:536-541 (state zeroed, KV kept)
+//   chain eval       eval_once, no-remote branch, src/xiaoju-pipe/core/xj_net.c:532-559
+//   spec accept      xj_spec_next        src/xiaoju-pipe/core/xj_spec.c:179-207
+//
+// Per layer the stage issues five kernels (plus one for attention's KV store):
+//   DeltaNet: GEMV[qkv(conv epilogue)|z|beta|alpha] -> delta -> GEMV ssm_out(+x)
+//   GQA:      GEMV[q|k|v] -> kv store -> attention -> GEMV wo(+x)
+//   both:     GEMV[gate|up] -> GEMV down(+x, SwiGLU prologue)
+// The hidden state, KV cache, recurrent state and checkpoints live in HBM.
+#include "common.h"
+#include "dequant.h"
+#include "kernels.h"
+#include "xj_hip.h"
+
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+using namespace xjk;
+
+namespace {
+
+constexpr int kSnapSlots = 8;
+
+struct HLayer {
+    bool rec = false;
+    const float *attn_norm = nullptr, *post_norm = nullptr;
+    DevW wq, wk, wv, wqkv, wo;
+    const float *q_norm = nullptr, *k_norm = nullptr;
+    DevW ssm_qkv, ssm_gate, ssm_beta, ssm_alpha, ssm_out;
+    const float *conv_w = nullptr, *dt = nullptr, *A = nullptr, *ssm_norm = nullptr;
+    DevW ffn_gate, ffn_up, ffn_down;
+    uint16_t *kc = nullptr, *vc = nullptr;
+    float *conv = nullptr, *ssm = nullptr;
+    float *ck_conv = nullptr, *ck_ssm = nullptr;
+    float *snap_conv[kSnapSlots] = {}, *snap_ssm[kSnapSlots] = {};
+};
+
+struct HStage {
+    xj_stage s;                      // first member: the vtable the callers see
+    hipStream_t st = nullptr;
+    std::vector<void *> allocs;
+    std::map<const void *, DevW> wcache;
+    std::vector<HLayer> L;
+    DevW output, tok_embd;
+    const float *out_norm = nullptr;
+    float *x = nullptr, *qkv = nullptr, *kb = nullptr, *vb = nullptr, *z = nullptr, *beta = nullptr,
+          *alpha = nullptr, *o = nullptr, *g = nullptr, *u = nullptr, *scores = nullptr, *logits = nullptr;
+    unsigned long long *amax = nullptr;
+    int head_nwg = 0;
+    int32_t *npast = nullptr;
+    float *inv_freq = nullptr;
+    float *h_x = nullptr;            // pinned staging [max_batch][n_embd]
+    int32_t *h_i = nullptr;          // pinned scalar
+    int n_ck = 0;
+    size_t conv_n = 0, ssm_n = 0;    // floats per layer
+    size_t weight_bytes = 0;
+};
+
+std::string g_name, g_note;
+thread_local char g_lasterr[512];
+
+int env_int(const char *k, int def) {
+    const char *v = getenv(k);
+    return v ? atoi(v) : def;
+}
+
+HStage *H(xj_stage *s) { return reinterpret_cast<HStage *>(s); }
+
+template <class T>
+T *dalloc(HStage *S, size_t n, char *err, size_t errlen) {
+    void *p = nullptr;
+    if (n == 0) n = 1;
+    if (hipMalloc(&p, n * sizeof(T)) != hipSuccess) {
+        snprintf(err, errlen, "HBM allocation of %zu bytes failed", n * sizeof(T));
+        return nullptr;
+    }
+    S->allocs.push_back(p);
+    return (T *)p;
+}
+
+bool gemv_type_ok(uint32_t t) { return t == XJ_F32 || t == XJ_Q4_K || t == XJ_Q6_K || t == XJ_Q8_0; }
+
+bool upload(HStage *S, const xj_w &w, DevW *out, char *err, size_t errlen) {
+    *out = DevW();
+    if (!w.nbytes) return true;
+    auto it = S->wcache.find(w.data);
+    if (it != S->wcache.end()) { *out = it->second; return true; }
+    if (!gemv_type_ok(w.type)) {
+        snprintf(err, errlen, "tensor type %s is not supported by the HIP backend", xj_type_name(w.type));
+        return false;
+    }
+    uint8_t *p = dalloc<uint8_t>(S, w.nbytes, err, errlen);
+    if (!p || upload_repack(w.type, w.data, w.ne1, w.ne0, p, S->st, err, errlen)) return false;
+    out->p = p; out->type = w.type; out->n_rows = w.ne1; out->k = w.ne0; out->bytes = w.nbytes;
+    S->wcache[w.data] = *out;
+    S->weight_bytes += w.nbytes;
+    return true;
+}
+
+bool upload_f32(HStage *S, const xj_w &w, const float **out, char *err, size_t errlen) {
+    *out = nullptr;
+    if (!w.nbytes) return true;
+    if (w.type != XJ_F32) { snprintf(err, errlen, "norm/conv tensors must be F32"); return false; }
+    DevW d;
+    if (!upload(S, w, &d, err, errlen)) return false;
+    *out = (const float *)d.p;
+    return true;
+}
+
+// ------------------------------------------------------------- GEMV helper --
+
+// Algorithmic HBM bytes of one GEMV launch over T tokens: every weight byte,
+// the activations read (x, and x2 for SwiGLU / gated RMSNorm), the outputs
+// written, and the outputs read back for a residual add.
+double gemv_algo_bytes(const GArgs &a, int T) {
+    double b = (double)T * a.K * 4 * (a.x2 ? 2 : 1);
+    for (int i = 0; i < a.nseg; i++) {
+        const GSeg &s = a.seg[i];
+        b += (double)s.n_rows * xj_row_bytes(s.type, a.K) + (double)T * s.n_rows * 4 * (s.epi == EPI_ADD ? 2 : 1);
+    }
+    return b;
+}
+
+// Profiling mode: the GEMV launches of a decode step only, with every
+// epilogue turned into a plain store into scratch so no model state changes.
+struct Profile {
+    float *sink = nullptr;
+    double bytes = 0;
+    int launches = 0;
+};
+
+struct Gemv {
+    GArgs a{};
+    Profile *prof = nullptr;
+    explicit Gemv(Profile *p = nullptr) : prof(p) {}
+    Gemv &seg(const DevW &w, float *y, int ys, int epi) {
+        GSeg &s = a.seg[a.nseg];
+        s = GSeg{};
+        s.w = w.p; s.type = w.type; s.n_rows = (int32_t)w.n_rows;
+        s.wg0 = a.nseg ? a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg : 0;
+        const int rows = gemv_rows_per_group((int)w.k);
+        s.nwg = (int32_t)((w.n_rows + rows - 1) / rows);
+        s.nblk = xjd::dev_nblk(w.type, w.n_rows, w.k);
+        s.y = y; s.ys = ys; s.epi = epi;
+        a.K = (int32_t)w.k;
+        a.nseg++;
+        return *this;
+    }
+    // Run over T tokens in tiles that fit LDS; row results do not depend on the tiling.
+    int run(int T, hipStream_t st) {
+        const int tile = gemv_max_tile(a.K);
+        if (tile < 1) return -1;
+        if (prof) {
+            prof->bytes += gemv_algo_bytes(a, T);
+            prof->launches += (T + tile - 1) / tile;
+            for (int i = 0; i < a.nseg; i++) {
+                a.seg[i].epi = EPI_STORE;
+                a.seg[i].y = prof->sink;
+                a.seg[i].amax = nullptr;
+            }
+            a.inc_ptr = nullptr;
+        }
+        for (int t0 = 0; t0 < T; t0 += tile) {
+            GArgs b = a;
+            b.T = T - t0 < tile ? T - t0 : tile;
+            b.t0 = a.t0 + t0;
+            b.x = a.x + (int64_t)t0 * a.xs;
+            if (a.x2) b.x2 = a.x2 + (int64_t)t0 * a.x2s;
+            for (int i = 0; i < a.nseg; i++) {
+                b.seg[i].y = a.seg[i].y + (int64_t)t0 * a.seg[i].ys;
+                if (a.seg[i].amax) b.seg[i].amax = a.seg[i].amax + (int64_t)t0 * a.seg[i].nwg;
+            }
+            if (t0 + b.T < T) b.inc_ptr = nullptr;
+            if (gemv_launch(b, st)) return -1;
+        }
+        return 0;
+    }
+};
+
+// --------------------------------------------------------------- layers --
+
+int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, hipStream_t st, Profile *pf = nullptr) {
+    const xj_hparams &hp = S->s.m->hp;
+    HLayer &L = S->L[il - S->s.l0];
+    const int E = hp.n_embd, FF = hp.n_ff;
+    if (L.rec) {
+        const int CD = hp.conv_dim, DI = hp.d_inner, Hv = hp.h_v;
+        Gemv p(pf);
+        p.a.x = x; p.a.xs = E; p.a.pro = PRO_RMS; p.a.pro_w = L.attn_norm; p.a.eps = hp.eps; p.a.keep_n = keep_n;
+        p.seg(L.ssm_qkv, S->qkv, CD, EPI_CONV).seg(L.ssm_gate, S->z, DI, EPI_STORE)
+         .seg(L.ssm_beta, S->beta, Hv, EPI_STORE).seg(L.ssm_alpha, S->alpha, Hv, EPI_STORE);
+        GSeg &cs = p.a.seg[0];
+        cs.conv_state = L.conv; cs.conv_w = L.conv_w; cs.conv_ck = L.ck_conv; cs.conv_k = hp.conv_k;
+        if (p.run(T, st)) return -1;
+        DeltaArgs d{};
+        d.qkv = S->qkv; d.qkv_s = CD; d.k_off = hp.key_dim; d.v_off = 2 * hp.key_dim;
+        d.beta = S->beta; d.beta_s = Hv; d.alpha = S->alpha; d.alpha_s = Hv; d.dt = L.dt; d.A = L.A;
+        d.state = L.ssm; d.ck = L.ck_ssm; d.out = S->o; d.out_s = DI;
+        d.T = T; d.Hk = hp.h_k; d.Hv = Hv; d.S = hp.s_k; d.keep_n = keep_n; d.eps = hp.eps;
+        d.qscale = 1.0f / sqrtf((float)hp.s_k);
+        if (!pf && delta_launch(d, st)) return -1;
+        Gemv q(pf);
+        q.a.x = S->o; q.a.xs = DI; q.a.x2 = S->z; q.a.x2s = DI; q.a.pro = PRO_GATED_RMS;
+        q.a.pro_w = L.ssm_norm; q.a.eps = hp.eps; q.a.group = hp.s_k;
+        q.seg(L.ssm_out, x, E, EPI_ADD);
+        if (q.run(T, st)) return -1;
+    } else {
+        const int D = hp.head_dim, Hq = hp.n_head, Hkv = hp.n_head_kv, nq = 2 * Hq * D, nk = Hkv * D;
+        Gemv p(pf);
+        p.a.x = x; p.a.xs = E; p.a.pro = PRO_RMS; p.a.pro_w = L.attn_norm; p.a.eps = hp.eps;
+        AttnArgs at{};
+        if (L.wqkv.p) {
+            p.seg(L.wqkv, S->qkv, nq + 2 * nk, EPI_STORE);
+            at.qg = S->qkv; at.qg_s = nq + 2 * nk;
+            at.kn = S->qkv + nq; at.kn_s = nq + 2 * nk;
+            at.vn = S->qkv + nq + nk; at.vn_s = nq + 2 * nk;
+        } else {
+            p.seg(L.wq, S->qkv, nq, EPI_STORE).seg(L.wk, S->kb, nk, EPI_STORE).seg(L.wv, S->vb, nk, EPI_STORE);
+            at.qg = S->qkv; at.qg_s = nq; at.kn = S->kb; at.kn_s = nk; at.vn = S->vb; at.vn_s = nk;
+        }
+        if (p.run(T, st)) return -1;
+        at.kc = L.kc; at.vc = L.vc; at.qnorm_w = L.q_norm; at.knorm_w = L.k_norm; at.inv_freq = S->inv_freq;
+        at.npast = S->npast; at.scores = S->scores; at.out = S->o;
+        at.T = T; at.H = Hq; at.Hkv = Hkv; at.D = D; at.n_rot = hp.n_rot; at.n_ctx = S->s.n_ctx;
+        at.n_split = attn_splits(S->s.n_ctx);
+        at.eps = hp.eps; at.scale = 1.0f / sqrtf((float)D);
+        if (!pf && attn_launch(at, st)) return -1;
+        Gemv q(pf);
+        q.a.x = S->o; q.a.xs = Hq * D; q.a.pro = PRO_NONE;
+        q.seg(L.wo, x, E, EPI_ADD);
+        if (q.run(T, st)) return -1;
+    }
+    Gemv f(pf);
+    f.a.x = x; f.a.xs = E; f.a.pro = PRO_RMS; f.a.pro_w = L.post_norm; f.a.eps = hp.eps;
+    f.seg(L.ffn_gate, S->g, FF, EPI_STORE).seg(L.ffn_up, S->u, FF, EPI_STORE);
+    if (f.run(T, st)) return -1;
+    Gemv dn(pf);
+    dn.a.x = S->g; dn.a.xs = FF; dn.a.x2 = S->u; dn.a.x2s = FF; dn.a.pro = PRO_SWIGLU;
+    dn.a.inc_ptr = inc; dn.a.inc_by = T;
+    dn.seg(L.ffn_down, x, E, EPI_ADD);
+    return dn.run(T, st);
+}
+
+int enqueue_layers(HStage *S, float *x, int T, int keep_n, bool inc, hipStream_t st) {
+    for (int il = S->s.l0; il < S->s.l1; il++)
+        if (enqueue_layer(S, il, x, T, keep_n, inc && il + 1 == S->s.l1 ? S->npast : nullptr, st)) return -1;
+    return 0;
+}
+
+// logits[t] = output . rmsnorm(x[t]) * output_norm; greedy partial keys into S->amax
+int enqueue_head(HStage *S, const float *x, int T, float *logits, hipStream_t st) {
+    const xj_hparams &hp = S->s.m->hp;
+    Gemv h;
+    h.a.x = x; h.a.xs = hp.n_embd; h.a.pro = PRO_RMS; h.a.pro_w = S->out_norm; h.a.eps = hp.eps;
+    h.seg(S->output, logits, (int)S->output.n_rows, EPI_STORE);
+    h.a.seg[0].amax = S->amax;
+    return h.run(T, st);
+}
+
+int sync_check(HStage *S, char *err, size_t errlen) {
+    hipError_t e = hipStreamSynchronize(S->st);
+    if (e == hipSuccess) e = hipGetLastError();
+    if (e != hipSuccess) { snprintf(err, errlen, "GPU error: %s", hipGetErrorString(e)); return -1; }
+    return 0;
+}
+
+int ensure_ck(HStage *S, int n, char *err, size_t errlen) {
+    if (n <= S->n_ck) return 0;
+    for (auto &L : S->L) {
+        if (!L.rec) continue;
+        if (L.ck_conv) { (void)hipFree(L.ck_conv); (void)hipFree(L.ck_ssm); }
+        L.ck_conv = L.ck_ssm = nullptr;
+        if (hipMalloc(&L.ck_conv, n * S->conv_n * 4) != hipSuccess || hipMalloc(&L.ck_ssm, n * S->ssm_n * 4) != hipSuccess) {
+            S->n_ck = 0;
+            snprintf(err, errlen, "out of HBM for speculative checkpoints");
+            return -1;
+        }
+    }
+    S->n_ck = n;
+    return 0;
+}
+
+int set_npast(HStage *S, hipStream_t st) {
+    *S->h_i = S->s.n_past;
+    return hipMemcpyAsync(S->npast, S->h_i, 4, hipMemcpyHostToDevice, st) == hipSuccess ? 0 : -1;
+}
+
+// forward-call bookkeeping shared by the vtable and the chain (xj_metal.m:426-431)
+int begin_forward(HStage *S, int T, int *keep_n, char *err, size_t errlen) {
+    xj_stage *s = &S->s;
+    if (T <= 0 || T > s->max_batch) { snprintf(err, errlen, "%d tokens exceed max_batch %d", T, s->max_batch); s->keep = 0; return -1; }
+    if (s->n_past + T > s->n_ctx) { snprintf(err, errlen, "context full (%d)", s->n_ctx); s->keep = 0; return -1; }
+    if (s->keep && T > 1 && ensure_ck(S, T - 1, err, errlen)) { s->keep = 0; return -1; }
+    if (T == 1) s->keep = 0;
+    s->ck_start = s->n_past;
+    s->ck_T = s->keep ? T : 0;
+    *keep_n = s->keep ? T - 1 : 0;
+    return 0;
+}
+
+int hip_forward(xj_stage *s, float *x, int T, char *err, size_t errlen) {
+    HStage *S = H(s);
+    const int E = s->m->hp.n_embd;
+    int keep_n = 0;
+    if (begin_forward(S, T, &keep_n, err, errlen)) return -1;
+    memcpy(S->h_x, x, sizeof(float) * T * E);
+    if (hipMemcpyAsync(S->x, S->h_x, sizeof(float) * T * E, hipMemcpyHostToDevice, S->st) != hipSuccess ||
+        set_npast(S, S->st) || enqueue_layers(S, S->x, T, keep_n, false, S->st) ||
+        hipMemcpyAsync(S->h_x, S->x, sizeof(float) * T * E, hipMemcpyDeviceToHost, S->st) != hipSuccess) {
+        snprintf(err, errlen, "kernel launch failed");
+        s->keep = 0;
+        return -1;
+    }
+    if (sync_check(S, err, errlen)) { s->keep = 0; return -1; }
+    memcpy(x, S->h_x, sizeof(float) * T * E);
+    s->n_past += T;
+    s->keep = 0;
+    return 0;
+}
+
+int hip_logits(xj_stage *s, const float *x, int T, float *logits, char *err, size_t errlen) {
+    HStage *S = H(s);
+    const int E = s->m->hp.n_embd;
+    if (!s->has_head) { snprintf(err, errlen, "this stage has no output head"); return -1; }
+    if (T < 1 || T > s->max_batch) { snprintf(err, errlen, "head called with %d tokens", T); return -1; }
+    memcpy(S->h_x, x, sizeof(float) * T * E);
+    if (hipMemcpyAsync(S->x, S->h_x, sizeof(float) * T * E, hipMemcpyHostToDevice, S->st) != hipSuccess ||
+        enqueue_head(S, S->x, T, S->logits, S->st)) {
+        snprintf(err, errlen, "kernel launch failed");
+        return -1;
+    }
+    if (sync_check(S, err, errlen)) return -1;
+    const size_t V = (size_t)S->output.n_rows;
+    if (hipMemcpy(logits, S->logits, sizeof(float) * V * T, hipMemcpyDeviceToHost) != hipSuccess) {
+        snprintf(err, errlen, "logits copy failed");
+        return -1;
+    }
+    return 0;
+}
+
+int hip_rollback(xj_stage *s, int n_past, char *err, size_t errlen) {
+    HStage *S = H(s);
+    if (n_past == s->n_past) { s->ck_T = 0; return 0; }
+    bool rec = false;
+    for (auto &L : S->L) rec |= L.rec;
+    if (!rec) {
+        if (n_past < 0 || n_past > s->n_past) { snprintf(err, errlen, "cannot roll back to %d", n_past); return -1; }
+        s->n_past = n_past;
+        return 0;
+    }
+    const int j = n_past - s->ck_start - 1;
+    if (!s->ck_T || s->n_past != s->ck_start + s->ck_T || j < 0 || j >= s->ck_T - 1) {
+        snprintf(err, errlen, "cannot roll back to %d (checkpoints %d+%d, now %d)", n_past, s->ck_start, s->ck_T, s->n_past);
+        return -1;
+    }
+    for (auto &L : S->L) {
+        if (!L.rec) continue;
+        if (hipMemcpyAsync(L.conv, L.ck_conv + j * S->conv_n, S->conv_n * 4, hipMemcpyDeviceToDevice, S->st) != hipSuccess ||
+            hipMemcpyAsync(L.ssm, L.ck_ssm + j * S->ssm_n, S->ssm_n * 4, hipMemcpyDeviceToDevice, S->st) != hipSuccess) {
+            snprintf(err, errlen, "checkpoint copy failed");
+            return -1;
+        }
+    }
+    if (sync_check(S, err, errlen)) return -1;
+    s->n_past = n_past;
+    s->ck_T = 0;
+    return 0;
+}
+
+void hip_reset(xj_stage *s) {
+    HStage *S = H(s);
+    for (auto &L : S->L) {
+        if (!L.rec) continue;
+        (void)hipMemsetAsync(L.conv, 0, S->conv_n * 4, S->st);
+        (void)hipMemsetAsync(L.ssm, 0, S->ssm_n * 4, S->st);
+    }
+    (void)hipStreamSynchronize(S->st);
+    s->n_past = 0;
+}
+
+void hip_destroy(xj_stage *s) {
+    if (!s) return;
+    HStage *S = H(s);
+    if (S->st) (void)hipStreamSynchronize(S->st);
+    for (auto &L : S->L) {
+        if (L.ck_conv) (void)hipFree(L.ck_conv);
+        if (L.ck_ssm) (void)hipFree(L.ck_ssm);
+        for (int i = 0; i < kSnapSlots; i++) {
+            if (L.snap_conv[i]) (void)hipFree(L.snap_conv[i]);
+            if (L.snap_ssm[i]) (void)hipFree(L.snap_ssm[i]);
+        }
+    }
+    for (void *p : S->allocs) (void)hipFree(p);
+    if (S->h_x) (void)hipHostFree(S->h_x);
+    if (S->h_i) (void)hipHostFree(S->h_i);
+    if (S->st) (void)hipStreamDestroy(S->st);
+    delete S;
+}
+
+void init_names() {
+    if (!g_name.empty()) return;
+    hipDeviceProp_t p;
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess)
+        g_name = std::string(p.name) + " (" + p.gcnArchName + ", " + std::to_string(p.multiProcessorCount) + " CUs)";
+    else
+        g_name = "hip";
+}
+
+}  // namespace
+
+// ================================================================= stage ==
+
+extern "C" const char *xj_hip_device_name(void) { init_names(); return g_name.c_str(); }
+extern "C" const char *xj_hip_tune_note(void) { return g_note.c_str(); }
+
+static size_t scratch_floats(const xj_hparams &hp) {
+    size_t n = (size_t)hp.n_ff;
+    const size_t qkv = 2 * (size_t)hp.n_head * hp.head_dim + 2 * (size_t)hp.n_head_kv * hp.head_dim;
+    if (qkv > n) n = qkv;
+    if ((size_t)hp.conv_dim > n) n = hp.conv_dim;
+    if ((size_t)hp.n_embd * 2 > n) n = 2 * (size_t)hp.n_embd;
+    return n;
+}
+
+extern "C" uint64_t xj_hip_stage_state_bytes(const xj_model *m, int l0, int l1, int n_ctx, int max_batch) {
+    const xj_hparams &hp = m->hp;
+    uint64_t b = 0;
+    for (int il = l0; il < l1; il++) {
+        if (m->layers[il].recurrent)
+            b += 4ull * ((uint64_t)hp.conv_dim * (hp.conv_k - 1) + (uint64_t)hp.h_v * hp.s_v * hp.s_k);
+        else
+            b += 2ull * 2 * n_ctx * hp.n_head_kv * hp.head_dim;
+    }
+    b += 10ull * 4 * max_batch * scratch_floats(hp) +
+         4ull * max_batch * hp.n_head * ((n_ctx + 63) / 64) * (hp.head_dim + 2);
+    return b;
+}
+
+extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_ctx, int max_batch, bool has_head,
+                                      char *err, size_t errlen) {
+    const xj_hparams &hp = m->hp;
+    if (m->has_mtp && l0 == hp.n_layer && l1 == hp.n_layer + 1) {
+        snprintf(err, errlen, "the HIP backend has no MTP stage");
+        return nullptr;
+    }
+    if (l0 < 0 || l1 > hp.n_layer || l0 > l1) { snprintf(err, errlen, "bad layer range [%d,%d)", l0, l1); return nullptr; }
+    for (int il = l0; il < l1; il++)
+        if (!m->layers[il].ffn_down.data) { snprintf(err, errlen, "layer %d weights are not mapped", il); return nullptr; }
+    if (has_head && !m->output.data) { snprintf(err, errlen, "output head is not mapped"); return nullptr; }
+    if (max_batch < 1 || n_ctx < 1) { snprintf(err, errlen, "bad n_ctx/max_batch"); return nullptr; }
+    bool any_attn = false, any_rec = false;
+    for (int il = l0; il < l1; il++) (m->layers[il].recurrent ? any_rec : any_attn) = true;
+    if (any_attn && hp.head_dim != 64 && hp.head_dim != 128 && hp.head_dim != 256) {
+        snprintf(err, errlen, "head_dim %d not supported (64/128/256)", hp.head_dim); return nullptr;
+    }
+    if (any_rec && hp.s_k != 64 && hp.s_k != 128) { snprintf(err, errlen, "ssm state_size %d not supported (64/128)", hp.s_k); return nullptr; }
+    if (any_rec && (hp.conv_k < 2 || hp.conv_k > 8)) { snprintf(err, errlen, "conv kernel %d not supported", hp.conv_k); return nullptr; }
+    if (hp.n_embd % 256 || hp.n_ff % 32) { snprintf(err, errlen, "n_embd must be a multiple of 256"); return nullptr; }
+    if (hp.n_head_kv < 1 || hp.n_head % hp.n_head_kv) { snprintf(err, errlen, "n_head must be a multiple of n_head_kv"); return nullptr; }
+    {   // every tensor a kernel reads must have the shape the kernel assumes
+        const int64_t E = hp.n_embd, FF = hp.n_ff, D = hp.head_dim, nq = 2 * (int64_t)hp.n_head * D, nk = (int64_t)hp.n_head_kv * D;
+        auto bad = [&](const xj_w &w, int64_t ne0, int64_t ne1, const char *what, int il) {
+            if (w.ne0 == ne0 && w.ne1 == ne1) return false;
+            snprintf(err, errlen, "layer %d: %s has shape %lldx%lld, expected %lldx%lld", il, what, (long long)w.ne0,
+                     (long long)w.ne1, (long long)ne0, (long long)ne1);
+            return true;
+        };
+        for (int il = l0; il < l1; il++) {
+            const xj_layer &w = m->layers[il];
+            if (bad(w.attn_norm, E, 1, "attn_norm", il) || bad(w.post_norm, E, 1, "post_norm", il) ||
+                bad(w.ffn_gate, E, FF, "ffn_gate", il) || bad(w.ffn_up, E, FF, "ffn_up", il) || bad(w.ffn_down, FF, E, "ffn_down", il))
+                return nullptr;
+            if (w.recurrent) {
+                if (bad(w.ssm_qkv, E, hp.conv_dim, "attn_qkv", il) || bad(w.ssm_gate, E, hp.d_inner, "attn_gate", il) ||
+                    bad(w.ssm_beta, E, hp.h_v, "ssm_beta", il) || bad(w.ssm_alpha, E, hp.h_v, "ssm_alpha", il) ||
+                    bad(w.ssm_out, hp.d_inner, E, "ssm_out", il) || bad(w.ssm_conv1d, hp.conv_k, hp.conv_dim, "ssm_conv1d", il) ||
+                    bad(w.ssm_dt, hp.h_v, 1, "ssm_dt", il) || bad(w.ssm_a, hp.h_v, 1, "ssm_a", il) || bad(w.ssm_norm, hp.s_k, 1, "ssm_norm", il))
+                    return nullptr;
+            } else {
+                if (w.wqkv.nbytes ? bad(w.wqkv, E, nq + 2 * nk, "attn_qkv", il)
+                                  : (bad(w.wq, E, nq, "attn_q", il) || bad(w.wk, E, nk, "attn_k", il) || bad(w.wv, E, nk, "attn_v", il)))
+                    return nullptr;
+                if (bad(w.wo, (int64_t)hp.n_head * D, E, "attn_output", il) || bad(w.q_norm, D, 1, "q_norm", il) ||
+                    bad(w.k_norm, D, 1, "k_norm", il))
+                    return nullptr;
+            }
+        }
+        if (has_head && (bad(m->output, E, m->output.ne1, "output", -1) || bad(m->output_norm, E, 1, "output_norm", -1))) return nullptr;
+        if (bad(m->tok_embd, E, m->tok_embd.ne1, "token_embd", -1)) return nullptr;
+    }
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) { snprintf(err, errlen, "no HIP device"); return nullptr; }
+    if (gemv_init(err, errlen)) return nullptr;
+    init_names();
+
+    HStage *S = new HStage();
+    xj_stage *s = &S->s;
+    memset(s, 0, sizeof(*s));
+    s->m = m; s->l0 = l0; s->l1 = l1; s->n_ctx = n_ctx; s->max_batch = max_batch; s->has_head = has_head;
+    s->mtp = false; s->backend = "hip";
+    s->forward = hip_forward; s->logits = hip_logits; s->rollback = hip_rollback; s->reset = hip_reset;
+    s->destroy = hip_destroy; s->impl = S;
+    auto fail = [&]() -> xj_stage * { hip_destroy(s); return nullptr; };
+    if (hipStreamCreateWithFlags(&S->st, hipStreamNonBlocking) != hipSuccess) { snprintf(err, errlen, "stream creation failed"); return fail(); }
+
+    S->conv_n = (size_t)hp.conv_dim * (hp.conv_k - 1);
+    S->ssm_n = (size_t)hp.h_v * hp.s_v * hp.s_k;
+    S->L.resize(l1 - l0);
+    for (int il = l0; il < l1; il++) {
+        const xj_layer &w = m->layers[il];
+        HLayer &L = S->L[il - l0];
+        L.rec = w.recurrent;
+        bool ok = upload_f32(S, w.attn_norm, &L.attn_norm, err, errlen) && upload_f32(S, w.post_norm, &L.post_norm, err, errlen) &&
+                  upload(S, w.ffn_gate, &L.ffn_gate, err, errlen) && upload(S, w.ffn_up, &L.ffn_up, err, errlen) &&
+                  upload(S, w.ffn_down, &L.ffn_down, err, errlen);
+        if (ok && L.rec) {
+            ok = upload(S, w.ssm_qkv, &L.ssm_qkv, err, errlen) && upload(S, w.ssm_gate, &L.ssm_gate, err, errlen) &&
+                 upload(S, w.ssm_beta, &L.ssm_beta, err, errlen) && upload(S, w.ssm_alpha, &L.ssm_alpha, err, errlen) &&
+                 upload(S, w.ssm_out, &L.ssm_out, err, errlen) && upload_f32(S, w.ssm_conv1d, &L.conv_w, err, errlen) &&
+                 upload_f32(S, w.ssm_dt, &L.dt, err, errlen) && upload_f32(S, w.ssm_a, &L.A, err, errlen) &&
+                 upload_f32(S, w.ssm_norm, &L.ssm_norm, err, errlen);
+            if (ok) {
+                L.conv = dalloc<float>(S, S->conv_n, err, errlen);
+                L.ssm = dalloc<float>(S, S->ssm_n, err, errlen);
+                ok = L.conv && L.ssm;
+            }
+        } else if (ok) {
+            ok = upload(S, w.wqkv, &L.wqkv, err, errlen) && upload(S, w.wq, &L.wq, err, errlen) &&
+                 upload(S, w.wk, &L.wk, err, errlen) && upload(S, w.wv, &L.wv, err, errlen) &&
+                 upload(S, w.wo, &L.wo, err, errlen) && upload_f32(S, w.q_norm, &L.q_norm, err, errlen) &&
+                 upload_f32(S, w.k_norm, &L.k_norm, err, errlen);
+            if (ok) {
+                const size_t kvn = (size_t)n_ctx * hp.n_head_kv * hp.head_dim;
+                L.kc = dalloc<uint16_t>(S, kvn, err, errlen);
+                L.vc = dalloc<uint16_t>(S, kvn, err, errlen);
+                ok = L.kc && L.vc;
+            }
+        }
+        if (!ok) return fail();
+    }
+    if (has_head) {
+        if (!upload(S, m->output, &S->output, err, errlen) || !upload_f32(S, m->output_norm, &S->out_norm, err, errlen))
+            return fail();
+        if (S->output.k != hp.n_embd) { snprintf(err, errlen, "output head shape mismatch"); return fail(); }
+    }
+    const size_t mb = max_batch, E = hp.n_embd;
+    const size_t sf = scratch_floats(hp);
+    S->x = dalloc<float>(S, mb * E, err, errlen);
+    S->qkv = dalloc<float>(S, mb * sf, err, errlen);
+    S->kb = dalloc<float>(S, mb * sf, err, errlen);
+    S->vb = dalloc<float>(S, mb * sf, err, errlen);
+    S->z = dalloc<float>(S, mb * sf, err, errlen);
+    S->beta = dalloc<float>(S, mb * (hp.h_v + 1), err, errlen);
+    S->alpha = dalloc<float>(S, mb * (hp.h_v + 1), err, errlen);
+    S->o = dalloc<float>(S, mb * sf, err, errlen);
+    S->g = dalloc<float>(S, mb * sf, err, errlen);
+    S->u = dalloc<float>(S, mb * sf, err, errlen);
+    S->scores = dalloc<float>(S, mb * hp.n_head * (size_t)attn_splits(n_ctx) * (hp.head_dim + 2), err, errlen);
+    S->npast = dalloc<int32_t>(S, 1, err, errlen);
+    const int half = hp.n_rot / 2 > 0 ? hp.n_rot / 2 : 1;
+    S->inv_freq = dalloc<float>(S, half, err, errlen);
+    if (!S->x || !S->qkv || !S->kb || !S->vb || !S->z || !S->beta || !S->alpha || !S->o || !S->g || !S->u ||
+        !S->scores || !S->npast || !S->inv_freq)
+        return fail();
+    if (has_head) {
+        S->logits = dalloc<float>(S, mb * (size_t)S->output.n_rows, err, errlen);
+        const int rows = gemv_rows_per_group((int)S->output.k);
+        S->head_nwg = (int)((S->output.n_rows + rows - 1) / rows);
+        S->amax = dalloc<unsigned long long>(S, mb * (size_t)S->head_nwg, err, errlen);
+        if (!S->logits || !S->amax) return fail();
+    }
+    {   // theta_i = pos * base^(-2i/n_rot), the exponent evaluated as the reference does (xj_cpu.c:71)
+        std::vector<float> f(half, 0.f);
+        for (int i = 0; i < hp.n_rot / 2; i++) f[i] = powf(hp.rope_base, -2.0f * i / hp.n_rot);
+        XJ_CHECK(hipMemcpy(S->inv_freq, f.data(), half * 4, hipMemcpyHostToDevice), err, errlen, fail());
+    }
+    XJ_CHECK(hipHostMalloc((void **)&S->h_x, sizeof(float) * mb * E, hipHostMallocDefault), err, errlen, fail());
+    XJ_CHECK(hipHostMalloc((void **)&S->h_i, 64, hipHostMallocDefault), err, errlen, fail());
+    hip_reset(s);
+    char note[160];
+    snprintf(note, sizeof note, "gemv lanes/row %d (K=n_embd), %.0f MB weights in HBM", gemv_team_lanes(hp.n_embd),
+             S->weight_bytes / 1048576.0);
+    g_note = note;
+    return s;
+}
+
+extern "C" int xj_hip_stage_snapshot(xj_stage *s, int slot, char *err, size_t errlen) {
+    HStage *S = H(s);
+    if (slot < 0 || slot >= kSnapSlots) { snprintf(err, errlen, "snapshot slot %d out of range", slot); return -1; }
+    for (auto &L : S->L) {
+        if (!L.rec) continue;
+        if (!L.snap_conv[slot]) {
+            if (hipMalloc(&L.snap_conv[slot], S->conv_n * 4) != hipSuccess || hipMalloc(&L.snap_ssm[slot], S->ssm_n * 4) != hipSuccess) {
+                snprintf(err, errlen, "out of HBM for snapshots");
+                return -1;
+            }
+        }
+        if (hipMemcpyAsync(L.snap_conv[slot], L.conv, S->conv_n * 4, hipMemcpyDeviceToDevice, S->st) != hipSuccess ||
+            hipMemcpyAsync(L.snap_ssm[slot], L.ssm, S->ssm_n * 4, hipMemcpyDeviceToDevice, S->st) != hipSuccess) {
+            snprintf(err, errlen, "snapshot copy failed");
+            return -1;
+        }
+    }
+    return 0;
+}
+
+extern "C" int xj_hip_stage_restore(xj_stage *s, int slot, int n_past, char *err, size_t errlen) {
+    HStage *S = H(s);
+    if (slot < 0 || slot >= kSnapSlots) { snprintf(err, errlen, "snapshot slot %d out of range", slot); return -1; }
+    if (n_past < 0 || n_past > s->n_ctx) { snprintf(err, errlen, "bad n_past %d", n_past); return -1; }
+    for (auto &L : S->L) {
+        if (!L.rec) continue;
+        if (!L.snap_conv[slot]) { snprintf(err, errlen, "snapshot slot %d is empty", slot); return -1; }
+        if (hipMemcpyAsync(L.conv, L.snap_conv[slot], S->conv_n * 4, hipMemcpyDeviceToDevice, S->st) != hipSuccess ||
+            hipMemcpyAsync(L.ssm, L.snap_ssm[slot], S->ssm_n * 4, hipMemcpyDeviceToDevice, S->st) != hipSuccess) {
+            snprintf(err, errlen, "restore copy failed");
+            return -1;
+        }
+    }
+    s->n_past = n_past;
+    s->ck_T = 0;
+    return sync_check(S, err, errlen);
+}
+
+// ================================================================= chain ==
+
+struct xjh_chain {
+    std::vector<HStage *> st;
+    hipStream_t stream = nullptr;
+    float *x = nullptr;
+    int mb = 0, hist_cap = 0;
+    int32_t *d_tokens = nullptr, *d_argmax = nullptr, *d_tok = nullptr, *d_hist = nullptr, *d_step = nullptr;
+    int32_t *h_buf = nullptr;   // pinned
+    hipGraphExec_t exec = nullptr;
+    hipGraph_t graph = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    double last_ms = 0;
+    int last_tok = -1;
+};
+
+extern "C" void xjh_chain_free(xjh_chain *c) {
+    if (!c) return;
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    if (c->exec) (void)hipGraphExecDestroy(c->exec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    if (c->ev0) (void)hipEventDestroy(c->ev0);
+    if (c->ev1) (void)hipEventDestroy(c->ev1);
+    for (int32_t *p : {c->d_tokens, c->d_argmax, c->d_tok, c->d_hist, c->d_step}) if (p) (void)hipFree(p);
+    if (c->h_buf) (void)hipHostFree(c->h_buf);
+    delete c;
+}
+
+extern "C" xjh_chain *xjh_chain_new(xj_stage **stages, int n, char *err, size_t errlen) {
+    if (n < 1) { snprintf(err, errlen, "empty chain"); return nullptr; }
+    auto *c = new xjh_chain();
+    for (int i = 0; i < n; i++) {
+        if (!stages[i] || strcmp(stages[i]->backend, "hip") != 0) { snprintf(err, errlen, "chain stage %d is not a HIP stage", i); xjh_chain_free(c); return nullptr; }
+        if (stages[i]->m != stages[0]->m) { snprintf(err, errlen, "chain stages use different models"); xjh_chain_free(c); return nullptr; }
+        if (i > 0 && stages[i]->l0 != stages[i - 1]->l1) { snprintf(err, errlen, "chain stages are not contiguous"); xjh_chain_free(c); return nullptr; }
+        c->st.push_back(H(stages[i]));
+    }
+    if (c->st[0]->s.l0 != 0 || !c->st.back()->s.has_head || c->st.back()->s.l1 != c->st[0]->s.m->hp.n_layer) {
+        snprintf(err, errlen, "a chain must cover all layers and end with the head");
+        xjh_chain_free(c);
+        return nullptr;
+    }
+    HStage *S0 = c->st[0];
+    const xj_model *m = S0->s.m;
+    if (!S0->tok_embd.p && !upload(S0, m->tok_embd, &S0->tok_embd, err, errlen)) { xjh_chain_free(c); return nullptr; }
+    c->stream = S0->st;
+    c->x = S0->x;
+    c->mb = S0->s.max_batch;
+    for (auto *S : c->st) if (S->s.max_batch < c->mb) c->mb = S->s.max_batch;
+    c->hist_cap = 1 << 16;
+    if (hipMalloc(&c->d_tokens, 4 * c->mb) != hipSuccess || hipMalloc(&c->d_argmax, 4 * c->mb) != hipSuccess ||
+        hipMalloc(&c->d_tok, 4) != hipSuccess || hipMalloc(&c->d_hist, 4 * c->hist_cap) != hipSuccess ||
+        hipMalloc(&c->d_step, 4) != hipSuccess || hipHostMalloc((void **)&c->h_buf, 4 * (c->mb + 16), hipHostMallocDefault) != hipSuccess ||
+        hipEventCreate(&c->ev0) != hipSuccess || hipEventCreate(&c->ev1) != hipSuccess) {
+        snprintf(err, errlen, "chain allocation failed");
+        xjh_chain_free(c);
+        return nullptr;
+    }
+    return c;
+}
+
+static int chain_sync(xjh_chain *c, char *err, size_t errlen) {
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e == hipSuccess) e = hipGetLastError();
+    if (e != hipSuccess) { snprintf(err, errlen, "GPU error: %s", hipGetErrorString(e)); return -1; }
+    return 0;
+}
+
+extern "C" int xjh_chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int keep, float *logits,
+                              int32_t *argmax, char *err, size_t errlen) {
+    const int B = c->mb, E = c->st[0]->s.m->hp.n_embd;
+    if (n <= 0) { snprintf(err, errlen, "no tokens"); return -1; }
+    if (keep && n > B) { snprintf(err, errlen, "verify batch %d exceeds max_batch %d", n, B); return -1; }
+    HStage *head = c->st.back();
+    for (int i = 0; i < n; i += B) {
+        const int T = n - i < B ? n - i : B;
+        memcpy(c->h_buf, tokens + i, 4 * T);
+        if (hipMemcpyAsync(c->d_tokens, c->h_buf, 4 * T, hipMemcpyHostToDevice, c->stream) != hipSuccess) {
+            snprintf(err, errlen, "token upload failed"); return -1;
+        }
+        EmbedArgs ea{c->d_tokens, c->st[0]->tok_embd, c->x, T};
+        if (embed_launch(ea, c->stream)) { snprintf(err, errlen, "embed launch failed"); return -1; }
+        for (auto *S : c->st) {
+            if (keep) S->s.keep = T;
+            int keep_n = 0;
+            if (begin_forward(S, T, &keep_n, err, errlen)) return -1;
+            *S->h_i = S->s.n_past;
+            if (hipMemcpyAsync(S->npast, S->h_i, 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+                enqueue_layers(S, c->x, T, keep_n, false, c->stream)) {
+                snprintf(err, errlen, "layer launch failed"); S->s.keep = 0; return -1;
+            }
+        }
+        const bool last = i + T == n;
+        if (last && nlog > 0) {
+            const int nl = nlog < T ? nlog : T;
+            if (enqueue_head(head, c->x + (int64_t)(T - nl) * E, nl, head->logits, c->stream) ||
+                argmax_finalize_launch(head->amax, head->head_nwg, nl, c->d_argmax, c->d_tok, nullptr, nullptr, c->stream)) {
+                snprintf(err, errlen, "head launch failed"); return -1;
+            }
+            if (chain_sync(c, err, errlen)) return -1;
+            if (logits && hipMemcpy(logits, head->logits, sizeof(float) * nl * head->output.n_rows, hipMemcpyDeviceToHost) != hipSuccess) {
+                snprintf(err, errlen, "logits copy failed"); return -1;
+            }
+            if (hipMemcpy(c->h_buf, c->d_argmax, 4 * nl, hipMemcpyDeviceToHost) != hipSuccess) { snprintf(err, errlen, "argmax copy failed"); return -1; }
+            if (argmax) memcpy(argmax, c->h_buf, 4 * nl);
+            c->last_tok = c->h_buf[nl - 1];
+        } else if (chain_sync(c, err, errlen)) {
+            return -1;
+        }
+        for (auto *S : c->st) { S->s.n_past += T; S->s.keep = 0; }
+    }
+    return 0;
+}
+
+static int build_decode_graph(xjh_chain *c, char *err, size_t errlen) {
+    HStage *head = c->st.back();
+    if (hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        snprintf(err, errlen, "graph capture failed to start"); return -1;
+    }
+    EmbedArgs ea{c->d_tok, c->st[0]->tok_embd, c->x, 1};
+    int rc = embed_launch(ea, c->stream);
+    for (auto *S : c->st) rc = rc ? rc : enqueue_layers(S, c->x, 1, 0, true, c->stream);
+    if (!rc) rc = enqueue_head(head, c->x, 1, head->logits, c->stream);
+    if (!rc) rc = argmax_finalize_launch(head->amax, head->head_nwg, 1, nullptr, c->d_tok, c->d_hist, c->d_step, c->stream);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(c->stream, &g);
+    if (rc || e != hipSuccess) { snprintf(err, errlen, "graph capture failed"); if (g) (void)hipGraphDestroy(g); return -1; }
+    if (hipGraphInstantiate(&c->exec, g, nullptr, nullptr, 0) != hipSuccess) {
+        snprintf(err, errlen, "graph instantiation failed"); (void)hipGraphDestroy(g); return -1;
+    }
+    c->graph = g;
+    return 0;
+}
+
+extern "C" int xjh_chain_decode(xjh_chain *c, int n_steps, int32_t *out, char *err, size_t errlen) {
+    if (n_steps <= 0) return 0;
+    if (c->last_tok < 0) { snprintf(err, errlen, "decode needs a previous eval with logits"); return -1; }
+    for (auto *S : c->st)
+        if (S->s.n_past + n_steps > S->s.n_ctx) { snprintf(err, errlen, "context full (%d)", S->s.n_ctx); return -1; }
+    if (!c->exec && build_decode_graph(c, err, errlen)) return -1;
+    double total_ms = 0;
+    for (int done = 0; done < n_steps;) {
+        const int n = n_steps - done < c->hist_cap ? n_steps - done : c->hist_cap;
+        c->h_buf[0] = 0;
+        c->h_buf[1] = c->last_tok;
+        if (hipMemcpyAsync(c->d_step, &c->h_buf[0], 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+            hipMemcpyAsync(c->d_tok, &c->h_buf[1], 4, hipMemcpyHostToDevice, c->stream) != hipSuccess) {
+            snprintf(err, errlen, "decode setup failed"); return -1;
+        }
+        for (auto *S : c->st) if (set_npast(S, c->stream)) { snprintf(err, errlen, "decode setup failed"); return -1; }
+        if (chain_sync(c, err, errlen)) return -1;
+        (void)hipEventRecord(c->ev0, c->stream);
+        for (int i = 0; i < n; i++)
+            if (hipGraphLaunch(c->exec, c->stream) != hipSuccess) { snprintf(err, errlen, "graph launch failed"); return -1; }
+        (void)hipEventRecord(c->ev1, c->stream);
+        if (chain_sync(c, err, errlen)) return -1;
+        float ms = 0;
+        (void)hipEventElapsedTime(&ms, c->ev0, c->ev1);
+        total_ms += ms;
+        if (hipMemcpy(out + done, c->d_hist, 4 * n, hipMemcpyDeviceToHost) != hipSuccess) { snprintf(err, errlen, "history copy failed"); return -1; }
+        for (auto *S : c->st) S->s.n_past += n;
+        c->last_tok = out[done + n - 1];
+        done += n;
+    }
+    c->last_ms = total_ms / n_steps;
+    return 0;
+}
+
+extern "C" int xjh_chain_last_token(xjh_chain *c) { return c->last_tok; }
+extern "C" double xjh_chain_last_decode_ms(xjh_chain *c) { return c->last_ms; }
+extern "C" int xjh_chain_n_past(xjh_chain *c) { return c->st[0]->s.n_past; }
+
+extern "C" int xjh_chain_rollback(xjh_chain *c, int n_past, char *err, size_t errlen) {
+    for (auto *S : c->st)
+        if (S->s.rollback(&S->s, n_past, err, errlen)) return -1;
+    return 0;
+}
+
+extern "C" void xjh_chain_reset(xjh_chain *c) {
+    for (auto *S : c->st) S->s.reset(&S->s);
+    c->last_tok = -1;
+}
+
+// one greedy step of the draft fed with token t; returns its argmax
+static int draft_step(xjh_chain *d, int t, int *next, char *err, size_t errlen) {
+    d->last_tok = t;
+    int32_t o;
+    if (xjh_chain_decode(d, 1, &o, err, errlen)) return -1;
+    *next = o;
+    return 0;
+}
+
+static int snapshot_all(xjh_chain *c, int slot, char *err, size_t errlen) {
+    for (auto *S : c->st)
+        if (xj_hip_stage_snapshot(&S->s, slot, err, errlen)) return -1;
+    return 0;
+}
+
+extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_gen, const int32_t *oracle, int n_oracle,
+                                 int oracle_miss, int32_t *out, xjh_spec_stats *stats, char *err, size_t errlen) {
+    xjh_spec_stats st{};
+    const int V = (int)tgt->st.back()->output.n_rows;
+    if (k < 1) k = 1;
+    if (k > 4) k = 4;
+    if (k + 1 > tgt->mb) k = tgt->mb - 1;
+    if (tgt->last_tok < 0 || dft->st[0]->s.n_past != tgt->st[0]->s.n_past) {
+        snprintf(err, errlen, "target and draft must have been fed the same prompt"); return -1;
+    }
+    (void)hipEventRecord(tgt->ev0, tgt->stream);
+    auto now_ms = []() { timespec t; clock_gettime(CLOCK_MONOTONIC, &t); return t.tv_sec * 1e3 + t.tv_nsec * 1e-6; };
+    const double t_start = now_ms();
+    int produced = 0;
+    long n_gen_tok = 0;
+    int pending = tgt->last_tok;
+    while (produced < n_gen) {
+        const int P = tgt->st[0]->s.n_past;
+        int kk = k;
+        if (kk > n_gen - produced - 1) kk = n_gen - produced - 1;
+        for (auto *S : tgt->st) if (kk > S->s.n_ctx - P - 1) kk = S->s.n_ctx - P - 1;
+        if (kk <= 0) {   // no room to speculate: plain step on both models
+            out[produced++] = pending;
+            int32_t nt, dn;
+            if (xjh_chain_eval(tgt, &pending, 1, 1, 0, nullptr, &nt, err, errlen) ||
+                xjh_chain_eval(dft, &pending, 1, 1, 0, nullptr, &dn, err, errlen)) return -1;
+            pending = nt;
+            n_gen_tok++;
+            continue;
+        }
+        // 1) draft proposes kk tokens by greedy T=1 steps, snapshot after each
+        const double t0 = now_ms();
+        int32_t toks[5];
+        toks[0] = pending;
+        int cur = pending;
+        for (int j = 0; j < kk; j++) {
+            int nx;
+            if (draft_step(dft, cur, &nx, err, errlen) || snapshot_all(dft, j, err, errlen)) return -1;
+            toks[j + 1] = nx;
+            cur = nx;
+        }
+        st.t_draft_ms += now_ms() - t0;
+        for (int j = 1; j <= kk && oracle; j++) {
+            const long gi = n_gen_tok + j;   // index of the generated token this draft stands for
+            if (gi < n_oracle) toks[j] = oracle[gi];
+            if (oracle_miss && (gi * 7 + j) % oracle_miss == 0) toks[j] = (toks[j] + 1) % V;
+        }
+        // 2) verify [t, d1..dk] on the target in one batch with checkpoints
+        int32_t am[5];
+        if (xjh_chain_eval(tgt, toks, kk + 1, kk + 1, 1, nullptr, am, err, errlen)) return -1;
+        // 3) accept the longest agreeing prefix (xj_spec.c:184-191)
+        int a = 0;
+        while (a < kk && am[a] == toks[a + 1]) { st.acc_at[a]++; a++; }
+        const int fed = a + 1;
+        for (int i = 0; i < fed && produced < n_gen; i++) out[produced++] = toks[i];
+        n_gen_tok += fed;
+        st.n_steps++; st.n_drafted += kk; st.n_accepted += a;
+        if (fed < kk + 1 && xjh_chain_rollback(tgt, P + fed, err, errlen)) return -1;
+        // 4) bring the draft to the same prefix [.., t, d1..da]
+        if (a < kk) {
+            for (auto *S : dft->st)
+                if (xj_hip_stage_restore(&S->s, a, P + fed, err, errlen)) return -1;
+        } else {
+            int nx;
+            if (draft_step(dft, toks[kk], &nx, err, errlen)) return -1;
+        }
+        pending = am[a];
+        tgt->last_tok = pending;
+    }
+    (void)hipEventRecord(tgt->ev1, tgt->stream);
+    st.t_total_ms = now_ms() - t_start;
+    if (stats) *stats = st;
+    tgt->last_tok = pending;
+    return 0;
+}
+
+extern "C" int xjh_chain_time_gemv(xjh_chain *c, int iters, double *ms_per_step, double *bytes_per_step,
+                                   int *launches_per_step, char *err, size_t errlen) {
+    if (iters < 1) iters = 1;
+    Profile pf;
+    HStage *head = c->st.back();
+    pf.sink = head->logits;   // [max_batch][n_vocab] floats: larger than any GEMV output
+    auto enqueue_step = [&](Profile *p) -> int {
+        for (auto *S : c->st)
+            for (int il = S->s.l0; il < S->s.l1; il++)
+                if (enqueue_layer(S, il, c->x, 1, 0, nullptr, c->stream, p)) return -1;
+        Gemv h(p);
+        const xj_hparams &hp = head->s.m->hp;
+        h.a.x = c->x; h.a.xs = hp.n_embd; h.a.pro = PRO_RMS; h.a.pro_w = head->out_norm; h.a.eps = hp.eps;
+        h.seg(head->output, head->logits, (int)head->output.n_rows, EPI_STORE);
+        return h.run(1, c->stream);
+    };
+    if (enqueue_step(&pf)) { snprintf(err, errlen, "profile launch failed"); return -1; }   // warm-up, counts bytes
+    if (chain_sync(c, err, errlen)) return -1;
+    const double bytes = pf.bytes;
+    const int launches = pf.launches;
+    (void)hipEventRecord(c->ev0, c->stream);
+    for (int i = 0; i < iters; i++) {
+        Profile q;
+        q.sink = pf.sink;
+        if (enqueue_step(&q)) { snprintf(err, errlen, "profile launch failed"); return -1; }
+    }
+    (void)hipEventRecord(c->ev1, c->stream);
+    if (chain_sync(c, err, errlen)) return -1;
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, c->ev0, c->ev1);
+    *ms_per_step = ms / iters;
+    *bytes_per_step = bytes;
+    *launches_per_step = launches;
+    return 0;
+}
+
+// ======================================================= per-op entries ==
+
+namespace {
+hipStream_t g_stream = nullptr;
+
+hipStream_t ops_stream() {
+    if (!g_stream) {
+        if (hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking) != hipSuccess) return nullptr;
+        char err[128];
+        gemv_init(err, sizeof err);
+    }
+    return g_stream;
+}
+
+int ops_done(char *err, size_t errlen) {
+    hipError_t e = hipStreamSynchronize(g_stream);
+    if (e == hipSuccess) e = hipGetLastError();
+    if (e != hipSuccess) { snprintf(err, errlen, "GPU error: %s", hipGetErrorString(e)); return -1; }
+    return 0;
+}
+}  // namespace
+
+extern "C" void *xjh_malloc(size_t bytes) {
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) { snprintf(g_lasterr, sizeof g_lasterr, "hipMalloc(%zu) failed", bytes); return nullptr; }
+    return p;
+}
+extern "C" void xjh_free(void *p) { if (p) (void)hipFree(p); }
+extern "C" int xjh_h2d(void *dst, const void *src, size_t n) { return hipMemcpy(dst, src, n, hipMemcpyHostToDevice) == hipSuccess ? 0 : -1; }
+extern "C" int xjh_d2h(void *dst, const void *src, size_t n) { return hipMemcpy(dst, src, n, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1; }
+extern "C" int xjh_sync(void) { return hipDeviceSynchronize() == hipSuccess ? 0 : -1; }
+extern "C" const char *xjh_last_error(void) { return g_lasterr; }
+
+extern "C" void *xjh_upload_weight(uint32_t type, const void *host, int64_t n_rows, int64_t k, char *err, size_t errlen) {
+    if (!ops_stream()) { snprintf(err, errlen, "no HIP stream"); return nullptr; }
+    if (!gemv_type_ok(type)) { snprintf(err, errlen, "type %s has no device layout", xj_type_name(type)); return nullptr; }
+    const uint64_t bytes = xj_row_bytes(type, k) * (uint64_t)n_rows;
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) { snprintf(err, errlen, "hipMalloc failed"); return nullptr; }
+    if (upload_repack(type, host, n_rows, k, (uint8_t *)p, g_stream, err, errlen)) { (void)hipFree(p); return nullptr; }
+    return p;
+}
+
+extern "C" int xjh_dequant(uint32_t type, const void *dw, int64_t n_rows, int64_t k, int64_t r0, int64_t n, float *y,
+                           char *err, size_t errlen) {
+    if (!ops_stream()) return -1;
+    if (r0 < 0 || n < 0 || r0 + n > n_rows || k % 32) { snprintf(err, errlen, "bad dequant range"); return -1; }
+    DevW w;
+    w.p = (const uint8_t *)dw; w.type = type; w.n_rows = n_rows; w.k = k;
+    if (dequant_launch(w, r0, n, y, g_stream)) { snprintf(err, errlen, "dequant launch failed"); return -1; }
+    return ops_done(err, errlen);
+}
+
+static int gemv_enqueue(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T, float *y, int add,
+                        hipStream_t st) {
+    DevW w;
+    w.p = (const uint8_t *)dw; w.type = type; w.n_rows = n_rows; w.k = k;
+    Gemv g;
+    g.a.x = x; g.a.xs = (int32_t)k; g.a.pro = PRO_NONE;
+    g.seg(w, y, (int32_t)n_rows, add ? EPI_ADD : EPI_STORE);
+    return g.run(T, st);
+}
+
+extern "C" int xjh_gemv(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T, float *y, int add,
+                        char *err, size_t errlen) {
+    if (!ops_stream()) return -1;
+    if (!gemv_type_ok(type) || T < 1 || n_rows < 1 || k % 32 || ((type == XJ_Q4_K || type == XJ_Q6_K) && k % 256)) {
+        snprintf(err, errlen, "unsupported GEMV shape/type"); return -1;
+    }
+    if (gemv_enqueue(type, dw, n_rows, k, x, T, y, add, g_stream)) { snprintf(err, errlen, "GEMV launch failed"); return -1; }
+    return ops_done(err, errlen);
+}
+
+extern "C" double xjh_gemv_time(uint32_t type, void *const *dws, int n_copies, int64_t n_rows, int64_t k, const float *x,
+                                int T, float *y, int iters, char *err, size_t errlen) {
+    if (!ops_stream()) return -1;
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) { snprintf(err, errlen, "event creation failed"); return -1; }
+    for (int i = 0; i < n_copies; i++)   // warm-up pass over every copy
+        if (gemv_enqueue(type, dws[i], n_rows, k, x, T, y, 0, g_stream)) { snprintf(err, errlen, "GEMV launch failed"); return -1; }
+    (void)hipEventRecord(e0, g_stream);
+    for (int i = 0; i < iters; i++)
+        if (gemv_enqueue(type, dws[i % n_copies], n_rows, k, x, T, y, 0, g_stream)) { snprintf(err, errlen, "GEMV launch failed"); return -1; }
+    (void)hipEventRecord(e1, g_stream);
+    if (ops_done(err, errlen)) return -1;
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return (double)ms / iters;
+}
+
+extern "C" int xjh_norm(int mode, const float *x, const float *w, int n, int rows, float eps, float *out, char *err, size_t errlen) {
+    if (!ops_stream()) return -1;
+    if (norm_launch(mode, x, w, n, rows, eps, out, g_stream)) { snprintf(err, errlen, "norm launch failed"); return -1; }
+    return ops_done(err, errlen);
+}
+
+extern "C" int xjh_argmax(const float *x, int n, int T, int32_t *out_host, char *err, size_t errlen) {
+    if (!ops_stream()) return -1;
+    int32_t *d = nullptr;
+    if (hipMalloc(&d, 4 * T) != hipSuccess) { snprintf(err, errlen, "hipMalloc failed"); return -1; }
+    int rc = argmax_rows_launch(x, n, T, d, g_stream) ? -1 : ops_done(err, errlen);
+    if (!rc && hipMemcpy(out_host, d, 4 * T, hipMemcpyDeviceToHost) != hipSuccess) rc = -1;
+    (void)hipFree(d);
+    return rc;
+}
+
+extern "C" int xjh_delta_recurrent(int H, int S, int T, const float *q, const float *k, const float *v, const float *decay,
+                                   const float *beta, float qscale, float *state, float *out, char *err, size_t errlen) {
+    if (!ops_stream()) return -1;
+    if (delta_recurrent_launch(H, S, T, q, k, v, decay, beta, qscale, state, out, g_stream)) {
+        snprintf(err, errlen, "delta launch failed (S must be 64 or 128)"); return -1;
+    }
+    return ops_done(err, errlen);
+}
+
+extern "C" int xjh_delta_chunked(int H, int S, int T, int chunk, const float *q, const float *k, const float *v,
+                                 const float *decay, const float *beta, float qscale, float *state, float *out,
+                                 char *err, size_t errlen) {
+    if (!ops_stream()) return -1;
+    const size_t wb = delta_chunked_work_bytes(H, S, T, chunk);
+    if (!wb) { snprintf(err, errlen, "chunked delta: unsupported shape (S=%d, chunk=%d)", S, chunk); return -1; }
+    void *work = nullptr;
+    if (hipMalloc(&work, wb) != hipSuccess) { snprintf(err, errlen, "hipMalloc failed"); return -1; }
+    int rc = delta_chunked_launch(H, S, T, chunk, q, k, v, decay, beta, qscale, state, out, (float *)work, g_stream);
+    if (rc) snprintf(err, errlen, "chunked delta launch failed");
+    else rc = ops_done(err, errlen);
+    (void)hipFree(work);
+    return rc;
+}

@@ -1,0 +1,534 @@
+"""Python bindings of libxjhip.so, the MI355X backend of the xiaoju-pipe token loop.
+
+Everything here is a thin ctypes layer over the C ABI declared in
+include/xj_hip.h; the compute runs in the hand-written gfx950 kernels of the
+library. Importing this module never falls back to anything else: if the
+library is missing it raises.
+
+    import xjpipe as xp
+    m = xp.Model(path)                       # xj_model_load
+    a = xp.HipStage(m, 0, m.hp.n_layer, n_ctx=1024, max_batch=8, has_head=True)
+    x = m.embed_host(token)  ...             # or a device chain:
+    c = xp.Chain([a]); c.eval(prompt); toks = c.decode(256)
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+from .configs import CONFIG_0_8B, CONFIG_4B, TINY, TINY_DRAFT, SynthConfig  # noqa: F401
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.normpath(os.path.join(HERE, "..", "_build", "libxjhip.so"))
+
+# ggml type ids (include/xj_abi.h)
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 8, 12, 13, 14, 30
+TYPE_NAMES = {F32: "F32", F16: "F16", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", BF16: "BF16"}
+BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
+
+
+def row_bytes(t, k):
+    n, b = BLOCK[t]
+    return (k // n) * b
+
+
+# ------------------------------------------------------------------ ABI --
+
+class XjW(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("file_off", C.c_uint64), ("nbytes", C.c_uint64),
+                ("type", C.c_uint32), ("ne0", C.c_int64), ("ne1", C.c_int64)]
+
+
+_LAYER_W = ["attn_norm", "post_norm", "wqkv", "wq", "wk", "wv", "wo", "q_norm", "k_norm",
+            "ssm_qkv", "ssm_gate", "ssm_conv1d", "ssm_dt", "ssm_a", "ssm_beta", "ssm_alpha", "ssm_norm", "ssm_out",
+            "ffn_gate", "ffn_up", "ffn_down"]
+
+
+class XjLayer(C.Structure):
+    _fields_ = [("recurrent", C.c_bool)] + [(n, XjW) for n in _LAYER_W]
+
+
+class XjHparams(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_layer", "n_embd", "n_ff", "n_vocab", "n_head", "n_head_kv", "head_dim",
+                                       "n_rot")] + \
+               [("rope_base", C.c_float), ("eps", C.c_float)] + \
+               [(n, C.c_int) for n in ("conv_k", "d_inner", "s_k", "h_k", "h_v", "s_v", "key_dim", "conv_dim",
+                                       "full_attn_interval")] + \
+               [("eos", C.c_uint32), ("eot", C.c_uint32)]
+
+
+class XjModel(C.Structure):
+    _fields_ = [("gguf", C.c_void_p), ("hp", XjHparams), ("tok_embd", XjW), ("output_norm", XjW), ("output", XjW),
+                ("layers", XjLayer * 128), ("fingerprint", C.c_uint64), ("has_mtp", C.c_bool),
+                ("mtp_eh", XjW), ("mtp_enorm", XjW), ("mtp_hnorm", XjW), ("mtp_head_norm", XjW), ("mtp_gguf", C.c_void_p)]
+
+
+class XjStage(C.Structure):
+    pass
+
+
+_FWD = C.CFUNCTYPE(C.c_int, C.POINTER(XjStage), C.POINTER(C.c_float), C.c_int, C.c_char_p, C.c_size_t)
+_LOG = C.CFUNCTYPE(C.c_int, C.POINTER(XjStage), C.POINTER(C.c_float), C.c_int, C.POINTER(C.c_float), C.c_char_p,
+                   C.c_size_t)
+_RB = C.CFUNCTYPE(C.c_int, C.POINTER(XjStage), C.c_int, C.c_char_p, C.c_size_t)
+_VOID = C.CFUNCTYPE(None, C.POINTER(XjStage))
+XjStage._fields_ = [("m", C.POINTER(XjModel)), ("l0", C.c_int), ("l1", C.c_int), ("n_ctx", C.c_int),
+                    ("max_batch", C.c_int), ("n_past", C.c_int), ("has_head", C.c_bool), ("mtp", C.c_bool),
+                    ("backend", C.c_char_p), ("keep", C.c_int), ("ck_start", C.c_int), ("ck_T", C.c_int),
+                    ("forward", _FWD), ("logits", _LOG), ("rollback", _RB), ("reset", _VOID), ("destroy", _VOID),
+                    ("impl", C.c_void_p)]
+
+
+class XjhSpecStats(C.Structure):
+    _fields_ = [("n_steps", C.c_long), ("n_drafted", C.c_long), ("n_accepted", C.c_long), ("acc_at", C.c_long * 4),
+                ("t_total_ms", C.c_double), ("t_draft_ms", C.c_double)]
+
+
+class XjsConfig(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_layer", "n_embd", "n_ff", "n_vocab", "n_head", "n_head_kv", "head_dim",
+                                       "n_rot")] + \
+               [("rope_base", C.c_float), ("eps", C.c_float)] + \
+               [(n, C.c_int) for n in ("conv_k", "s_k", "h_k", "h_v", "full_attn_interval")] + \
+               [(n, C.c_uint32) for n in ("type_default", "type_embd", "type_out", "type_v", "type_down")] + \
+               [("w_std", C.c_float), ("seed", C.c_uint64)]
+
+
+# -------------------------------------------------------------- library --
+
+_lib = None
+ERR = 512
+
+
+class XjError(RuntimeError):
+    pass
+
+
+def _sig(lib, name, res, *args):
+    f = getattr(lib, name)
+    f.restype = res
+    f.argtypes = list(args)
+
+
+def lib():
+    """Load libxjhip.so (built by __graft_entry__.build()); raise if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise XjError(f"{LIB_PATH} is not built; run __graft_entry__.build() first")
+    L = C.CDLL(LIB_PATH)
+    P, I, I64, U32, U64, F, D, S = C.c_void_p, C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_float, C.c_double, C.c_size_t
+    CP = C.c_char_p
+    PS = C.POINTER(XjStage)
+    _sig(L, "xj_hip_stage_new", PS, C.POINTER(XjModel), I, I, I, I, C.c_bool, CP, S)
+    _sig(L, "xj_hip_device_name", CP)
+    _sig(L, "xj_hip_tune_note", CP)
+    _sig(L, "xj_hip_stage_state_bytes", U64, C.POINTER(XjModel), I, I, I, I)
+    _sig(L, "xj_hip_stage_snapshot", I, PS, I, CP, S)
+    _sig(L, "xj_hip_stage_restore", I, PS, I, I, CP, S)
+    _sig(L, "xj_type_block", I, U32, C.POINTER(I))
+    _sig(L, "xj_row_bytes", U64, U32, I64)
+    _sig(L, "xj_type_name", CP, U32)
+    _sig(L, "xj_model_load", C.POINTER(XjModel), CP, CP, S)
+    _sig(L, "xj_model_free", None, C.POINTER(XjModel))
+    _sig(L, "xjs_fill_normal", None, P, I64, U64, F)
+    _sig(L, "xjs_tensor_seed", U64, U64, CP)
+    _sig(L, "xjs_quantize", I, U32, P, I64, I64, P, CP, S)
+    _sig(L, "xjs_write_model", I64, CP, C.POINTER(XjsConfig), CP, S)
+    _sig(L, "xjh_chain_new", P, C.POINTER(PS), I, CP, S)
+    _sig(L, "xjh_chain_free", None, P)
+    _sig(L, "xjh_chain_eval", I, P, P, I, I, I, P, P, CP, S)
+    _sig(L, "xjh_chain_decode", I, P, I, P, CP, S)
+    _sig(L, "xjh_chain_last_token", I, P)
+    _sig(L, "xjh_chain_rollback", I, P, I, CP, S)
+    _sig(L, "xjh_chain_reset", None, P)
+    _sig(L, "xjh_chain_n_past", I, P)
+    _sig(L, "xjh_chain_last_decode_ms", D, P)
+    _sig(L, "xjh_chain_time_gemv", I, P, I, C.POINTER(D), C.POINTER(D), C.POINTER(I), CP, S)
+    _sig(L, "xjh_spec_generate", I, P, P, I, I, P, I, I, P, C.POINTER(XjhSpecStats), CP, S)
+    _sig(L, "xjh_malloc", P, S)
+    _sig(L, "xjh_free", None, P)
+    _sig(L, "xjh_h2d", I, P, P, S)
+    _sig(L, "xjh_d2h", I, P, P, S)
+    _sig(L, "xjh_sync", I)
+    _sig(L, "xjh_last_error", CP)
+    _sig(L, "xjh_upload_weight", P, U32, P, I64, I64, CP, S)
+    _sig(L, "xjh_dequant", I, U32, P, I64, I64, I64, I64, P, CP, S)
+    _sig(L, "xjh_gemv", I, U32, P, I64, I64, P, I, P, I, CP, S)
+    _sig(L, "xjh_gemv_time", D, U32, C.POINTER(P), I, I64, I64, P, I, P, I, CP, S)
+    _sig(L, "xjh_norm", I, I, P, P, I, I, F, P, CP, S)
+    _sig(L, "xjh_argmax", I, P, I, I, P, CP, S)
+    _sig(L, "xjh_delta_recurrent", I, I, I, I, P, P, P, P, P, F, P, P, CP, S)
+    _sig(L, "xjh_delta_chunked", I, I, I, I, I, P, P, P, P, P, F, P, P, CP, S)
+    _lib = L
+    return L
+
+
+def _err():
+    return C.create_string_buffer(ERR)
+
+
+def _check(rc, err, what):
+    if rc != 0:
+        raise XjError(f"{what}: {err.value.decode(errors='replace')}")
+
+
+def _ptr(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# ----------------------------------------------------- synthetic models --
+
+def config_struct(cfg):
+    c = XjsConfig()
+    for name, _ in XjsConfig._fields_:
+        setattr(c, name, getattr(cfg, name))
+    return c
+
+
+def write_model(path, cfg):
+    """Write the synthetic qwen35 GGUF of `cfg` to `path`; returns its size in bytes."""
+    err = _err()
+    c = config_struct(cfg)
+    n = lib().xjs_write_model(path.encode(), C.byref(c), err, ERR)
+    if n < 0:
+        raise XjError(err.value.decode())
+    return n
+
+
+def fill_normal(n, seed, std=1.0):
+    out = np.empty(n, np.float32)
+    lib().xjs_fill_normal(_ptr(out), n, seed, std)
+    return out
+
+
+def tensor_seed(seed, name):
+    return lib().xjs_tensor_seed(seed, name.encode())
+
+
+def quantize(t, x):
+    """Quantize a [rows][k] float32 array with the library's quantizers; returns uint8 bytes."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, k = x.shape
+    out = np.empty(rows * row_bytes(t, k), np.uint8)
+    err = _err()
+    _check(lib().xjs_quantize(t, _ptr(x), rows, k, _ptr(out), err, ERR), err, "quantize")
+    return out
+
+
+class Model:
+    """xj_model_load: the GGUF is mmapped; weights stay on the host until a stage uploads them."""
+
+    def __init__(self, path):
+        err = _err()
+        self.ptr = lib().xj_model_load(path.encode(), err, ERR)
+        if not self.ptr:
+            raise XjError(err.value.decode())
+        self.path = path
+
+    @property
+    def m(self):
+        return self.ptr.contents
+
+    @property
+    def hp(self):
+        return self.ptr.contents.hp
+
+    def close(self):
+        if self.ptr:
+            lib().xj_model_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensor_bytes(self, w):
+        """Raw GGUF bytes of an XjW as a numpy uint8 view (no copy)."""
+        buf = (C.c_uint8 * w.nbytes).from_address(w.data)
+        return np.frombuffer(buf, np.uint8)
+
+    def tensor_f32(self, w):
+        assert w.type == F32
+        return self.tensor_bytes(w).view(np.float32).reshape(w.ne1, w.ne0)
+
+
+# ---------------------------------------------------------------- stage --
+
+class HipStage:
+    """xj_hip_stage_new: layers [l0, l1) (+ head) in HBM behind the xj_stage vtable."""
+
+    def __init__(self, model, l0, l1, n_ctx, max_batch, has_head):
+        err = _err()
+        self.model = model
+        self.ptr = lib().xj_hip_stage_new(model.ptr, l0, l1, n_ctx, max_batch, has_head, err, ERR)
+        if not self.ptr:
+            raise XjError(err.value.decode())
+
+    @property
+    def s(self):
+        return self.ptr.contents
+
+    @property
+    def n_past(self):
+        return self.ptr.contents.n_past
+
+    def forward(self, x):
+        """x: float32 [T][n_embd], updated in place (vtable forward)."""
+        assert x.dtype == np.float32 and x.flags.c_contiguous
+        err = _err()
+        rc = self.s.forward(self.ptr, x.ctypes.data_as(C.POINTER(C.c_float)), x.shape[0], err, ERR)
+        _check(rc, err, "forward")
+        return x
+
+    def logits(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        T = x.shape[0]
+        out = np.empty((T, self.model.hp.n_vocab), np.float32)
+        err = _err()
+        rc = self.s.logits(self.ptr, x.ctypes.data_as(C.POINTER(C.c_float)), T,
+                           out.ctypes.data_as(C.POINTER(C.c_float)), err, ERR)
+        _check(rc, err, "logits")
+        return out
+
+    def rollback(self, n_past):
+        err = _err()
+        _check(self.s.rollback(self.ptr, n_past, err, ERR), err, "rollback")
+
+    def set_keep(self, k):
+        self.ptr.contents.keep = k
+
+    def reset(self):
+        self.s.reset(self.ptr)
+
+    def snapshot(self, slot):
+        err = _err()
+        _check(lib().xj_hip_stage_snapshot(self.ptr, slot, err, ERR), err, "snapshot")
+
+    def restore(self, slot, n_past):
+        err = _err()
+        _check(lib().xj_hip_stage_restore(self.ptr, slot, n_past, err, ERR), err, "restore")
+
+    def destroy(self):
+        if self.ptr:
+            self.s.destroy(self.ptr)
+            self.ptr = None
+
+
+class Chain:
+    """Device-resident pipeline over HIP stages (embedding, layers, head, argmax on the GPU)."""
+
+    def __init__(self, stages):
+        self.stages = stages
+        arr = (C.POINTER(XjStage) * len(stages))(*[s.ptr for s in stages])
+        err = _err()
+        self.ptr = lib().xjh_chain_new(arr, len(stages), err, ERR)
+        if not self.ptr:
+            raise XjError(err.value.decode())
+        self.V = stages[-1].model.hp.n_vocab
+
+    def eval(self, tokens, nlog=1, keep=False, want_logits=False):
+        toks = np.ascontiguousarray(tokens, np.int32)
+        nl = min(nlog, len(toks)) if nlog else 0
+        am = np.empty(max(nl, 1), np.int32)
+        lg = np.empty((max(nl, 1), self.V), np.float32) if want_logits else None
+        err = _err()
+        rc = lib().xjh_chain_eval(self.ptr, _ptr(toks), len(toks), nlog, int(keep),
+                                  _ptr(lg) if lg is not None else None, _ptr(am), err, ERR)
+        _check(rc, err, "chain eval")
+        return (am[:nl], lg[:nl]) if want_logits else am[:nl]
+
+    def decode(self, n):
+        out = np.empty(n, np.int32)
+        err = _err()
+        _check(lib().xjh_chain_decode(self.ptr, n, _ptr(out), err, ERR), err, "chain decode")
+        return out
+
+    @property
+    def last_token(self):
+        return lib().xjh_chain_last_token(self.ptr)
+
+    @property
+    def n_past(self):
+        return lib().xjh_chain_n_past(self.ptr)
+
+    @property
+    def last_decode_ms(self):
+        return lib().xjh_chain_last_decode_ms(self.ptr)
+
+    def rollback(self, n_past):
+        err = _err()
+        _check(lib().xjh_chain_rollback(self.ptr, n_past, err, ERR), err, "chain rollback")
+
+    def time_gemv(self, iters):
+        """(ms per step, algorithmic bytes per step, launches per step) of the GEMV launches of one decode step."""
+        ms, by, n = C.c_double(), C.c_double(), C.c_int()
+        err = _err()
+        _check(lib().xjh_chain_time_gemv(self.ptr, iters, C.byref(ms), C.byref(by), C.byref(n), err, ERR), err,
+               "time_gemv")
+        return ms.value, by.value, n.value
+
+    def reset(self):
+        lib().xjh_chain_reset(self.ptr)
+
+    def free(self):
+        if self.ptr:
+            lib().xjh_chain_free(self.ptr)
+            self.ptr = None
+
+
+def spec_generate(target, draft, k, n_gen, oracle=None, oracle_miss=0):
+    out = np.empty(n_gen, np.int32)
+    st = XjhSpecStats()
+    err = _err()
+    orc = np.ascontiguousarray(oracle, np.int32) if oracle is not None else None
+    rc = lib().xjh_spec_generate(target.ptr, draft.ptr, k, n_gen, _ptr(orc) if orc is not None else None,
+                                 len(orc) if orc is not None else 0, oracle_miss, _ptr(out), C.byref(st), err, ERR)
+    _check(rc, err, "spec generate")
+    return out, st
+
+
+# --------------------------------------------------------- device memory --
+
+class Dev:
+    """A device buffer holding a numpy array's bytes."""
+
+    def __init__(self, arr=None, nbytes=None):
+        if arr is not None:
+            arr = np.ascontiguousarray(arr)
+            nbytes = arr.nbytes
+        self.nbytes = nbytes
+        self.ptr = lib().xjh_malloc(nbytes)
+        if not self.ptr:
+            raise XjError(lib().xjh_last_error().decode())
+        if arr is not None:
+            self.put(arr)
+
+    def put(self, arr):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        if lib().xjh_h2d(self.ptr, _ptr(arr), arr.nbytes):
+            raise XjError("h2d copy failed")
+
+    def get(self, dtype, shape):
+        out = np.empty(shape, dtype)
+        if lib().xjh_d2h(_ptr(out), self.ptr, out.nbytes):
+            raise XjError("d2h copy failed")
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().xjh_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class DevWeight:
+    """A GGUF tensor repacked into the kernels' device layout."""
+
+    def __init__(self, t, blob, rows, k):
+        err = _err()
+        blob = np.ascontiguousarray(blob, np.uint8)
+        assert blob.nbytes == rows * row_bytes(t, k)
+        self.t, self.rows, self.k = t, rows, k
+        self.ptr = lib().xjh_upload_weight(t, _ptr(blob), rows, k, err, ERR)
+        if not self.ptr:
+            raise XjError(err.value.decode())
+
+    def free(self):
+        if self.ptr:
+            lib().xjh_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def dequant(w, r0=0, n=None):
+    n = w.rows - r0 if n is None else n
+    y = Dev(nbytes=max(1, n * w.k * 4))
+    err = _err()
+    _check(lib().xjh_dequant(w.t, w.ptr, w.rows, w.k, r0, n, y.ptr, err, ERR), err, "dequant")
+    return y.get(np.float32, (n, w.k))
+
+
+def gemv(w, x, add_to=None):
+    """y[t] = W x[t] on the GPU; x float32 [T][k]."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, w.k)
+    T = x.shape[0]
+    dx = Dev(x)
+    dy = Dev(add_to.astype(np.float32)) if add_to is not None else Dev(nbytes=T * w.rows * 4)
+    err = _err()
+    _check(lib().xjh_gemv(w.t, w.ptr, w.rows, w.k, dx.ptr, T, dy.ptr, int(add_to is not None), err, ERR), err, "gemv")
+    return dy.get(np.float32, (T, w.rows))
+
+
+def gemv_time(weights, x, iters):
+    """Mean ms per GEMV launch over rotating copies (HIP events on the library stream)."""
+    w0 = weights[0]
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, w0.k)
+    T = x.shape[0]
+    dx, dy = Dev(x), Dev(nbytes=T * w0.rows * 4)
+    arr = (C.c_void_p * len(weights))(*[w.ptr for w in weights])
+    err = _err()
+    ms = lib().xjh_gemv_time(w0.t, arr, len(weights), w0.rows, w0.k, dx.ptr, T, dy.ptr, iters, err, ERR)
+    if ms < 0:
+        raise XjError(err.value.decode())
+    return ms
+
+
+def norm(x, w, mode, eps):
+    x = np.ascontiguousarray(x, np.float32)
+    rows, n = x.shape
+    dx, dout = Dev(x), Dev(nbytes=x.nbytes)
+    dw = Dev(np.ascontiguousarray(w, np.float32)) if w is not None else None
+    err = _err()
+    _check(lib().xjh_norm(mode, dx.ptr, dw.ptr if dw else None, n, rows, eps, dout.ptr, err, ERR), err, "norm")
+    return dout.get(np.float32, x.shape)
+
+
+def argmax(x):
+    x = np.ascontiguousarray(x, np.float32)
+    if x.ndim == 1:
+        x = x[None]
+    dx = Dev(x)
+    out = np.empty(x.shape[0], np.int32)
+    err = _err()
+    _check(lib().xjh_argmax(dx.ptr, x.shape[1], x.shape[0], _ptr(out), err, ERR), err, "argmax")
+    return out
+
+
+def delta(q, k, v, decay, beta, state, qscale, chunk=0):
+    """Gated delta rule on the GPU; q,k,v [T][H][S], decay,beta [T][H], state [H][S][S].
+    chunk=0 runs the recurrent kernel, chunk=64 the chunk-wise one. Returns (out, new_state)."""
+    T, H, S = q.shape
+    dq, dk, dv = Dev(q.astype(np.float32)), Dev(k.astype(np.float32)), Dev(v.astype(np.float32))
+    dd, db = Dev(decay.astype(np.float32)), Dev(beta.astype(np.float32))
+    ds, do = Dev(state.astype(np.float32)), Dev(nbytes=T * H * S * 4)
+    err = _err()
+    if chunk:
+        rc = lib().xjh_delta_chunked(H, S, T, chunk, dq.ptr, dk.ptr, dv.ptr, dd.ptr, db.ptr, qscale, ds.ptr, do.ptr,
+                                     err, ERR)
+    else:
+        rc = lib().xjh_delta_recurrent(H, S, T, dq.ptr, dk.ptr, dv.ptr, dd.ptr, db.ptr, qscale, ds.ptr, do.ptr,
+                                       err, ERR)
+    _check(rc, err, "delta")
+    return do.get(np.float32, (T, H, S)), ds.get(np.float32, (H, S, S))
+
+
+def device_name():
+    return lib().xj_hip_device_name().decode()
+
+
+def tune_note():
+    return lib().xj_hip_tune_note().decode()

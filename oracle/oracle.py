@@ -1,0 +1,245 @@
+"""ctypes bindings of the oracle (oracle/_build/libxjoracle.so) and, when it was
+built in this container, of the reference compiled from source
+(oracle/_ref/libxjref.so).
+
+Test infrastructure only: imported by tests/, __graft_entry__.smoke() and the
+CPU-baseline leg of bench.py, always as the checker or the timed baseline,
+never as part of the product.
+"""
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.normpath(os.path.join(HERE, "..", "meta-work_amd")))
+import xjpipe as xp  # noqa: E402  (ABI struct definitions only)
+
+ORACLE_LIB = os.path.join(HERE, "_build", "libxjoracle.so")
+REF_LIB = os.path.join(HERE, "_ref", "libxjref.so")
+REF_NATIVE_LIB = os.path.join(HERE, "_ref", "libxjref_native.so")
+ERR = 512
+
+_o = None
+_r = {}
+
+
+def _sig(lib, name, res, *args):
+    f = getattr(lib, name)
+    f.restype = res
+    f.argtypes = list(args)
+
+
+def _ptr(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def olib():
+    global _o
+    if _o is None:
+        if not os.path.exists(ORACLE_LIB):
+            raise RuntimeError(f"{ORACLE_LIB} not built; run __graft_entry__.build()")
+        L = C.CDLL(ORACLE_LIB)
+        P, I, I64, U32, F, S, CP = C.c_void_p, C.c_int, C.c_int64, C.c_uint32, C.c_float, C.c_size_t, C.c_char_p
+        PS = C.POINTER(xp.XjStage)
+        _sig(L, "xjo_f16", F, C.c_uint16)
+        _sig(L, "xjo_to_f16", C.c_uint16, F)
+        _sig(L, "xjo_row_bytes", C.c_uint64, U32, I64)
+        _sig(L, "xjo_dequant_row", None, U32, P, P, I64)
+        _sig(L, "xjo_matmul", None, U32, P, I64, I64, P, P, I)
+        _sig(L, "xjo_rmsnorm", None, P, P, P, I, F)
+        _sig(L, "xjo_l2norm", None, P, I, F)
+        _sig(L, "xjo_rope", None, P, I, I, F)
+        _sig(L, "xjo_embed", None, C.POINTER(xp.XjModel), C.c_int32, P)
+        _sig(L, "xjo_stage_new", PS, C.POINTER(xp.XjModel), I, I, I, I, C.c_bool, I, CP, S)
+        _sig(L, "xjo_greedy", I, C.POINTER(PS), I, P, I, I, P, P, CP, S)
+        _sig(L, "xjo_argmax", I, P, I)
+        _sig(L, "xjo_delta_recurrent", None, I, I, I, P, P, P, P, P, F, P, P)
+        _sig(L, "xjo_abi_offsets", I, C.POINTER(C.c_long), I)
+        _o = L
+    return _o
+
+
+def ref_available(native=False):
+    return os.path.exists(REF_NATIVE_LIB if native else REF_LIB)
+
+
+def rlib(native=False):
+    key = "native" if native else "v3"
+    if key not in _r:
+        path = REF_NATIVE_LIB if native else REF_LIB
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} not built (needs the reference sources; see oracle/Makefile)")
+        L = C.CDLL(path)
+        P, I, I64, U32, F, S, CP = C.c_void_p, C.c_int, C.c_int64, C.c_uint32, C.c_float, C.c_size_t, C.c_char_p
+        PS = C.POINTER(xp.XjStage)
+        PM = C.POINTER(xp.XjModel)
+        _sig(L, "ref_dequant_row", None, U32, P, P, I64)
+        _sig(L, "ref_to_f16", C.c_uint16, F)
+        _sig(L, "ref_f16", F, C.c_uint16)
+        _sig(L, "ref_row_bytes", C.c_uint64, U32, I64)
+        _sig(L, "ref_matmul", None, U32, P, I64, I64, P, P, I)
+        _sig(L, "ref_rmsnorm", None, P, P, P, I, F)
+        _sig(L, "ref_rope", None, P, I, I, F)
+        _sig(L, "ref_model_load", PM, CP, CP, S)
+        _sig(L, "ref_model_free", None, PM)
+        _sig(L, "ref_stage_new", PS, PM, I, I, I, I, C.c_bool, CP, S)
+        _sig(L, "ref_embed", None, PM, C.c_int32, P)
+        _sig(L, "ref_greedy", I, PM, I, I, I, P, I, I, P, P, CP, S)
+        _sig(L, "ref_abi_offsets", I, C.POINTER(C.c_long), I)
+        _r[key] = L
+    return _r[key]
+
+
+# ---------------------------------------------------------------- oracle --
+
+def f16_to_f32(h):
+    return olib().xjo_f16(int(h))
+
+
+def f32_to_f16(f):
+    return olib().xjo_to_f16(float(f))
+
+
+def dequant_rows(t, blob, rows, k, lib=None):
+    L = lib or olib()
+    fn = L.xjo_dequant_row if lib is None else L.ref_dequant_row
+    rb = xp.row_bytes(t, k)
+    blob = np.ascontiguousarray(blob, np.uint8)
+    out = np.empty((rows, k), np.float32)
+    for r in range(rows):
+        fn(t, blob[r * rb:].ctypes.data_as(C.c_void_p), out[r].ctypes.data_as(C.c_void_p), k)
+    return out
+
+
+def matmul(t, blob, K, N, x, ref=False):
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, K)
+    y = np.empty((x.shape[0], N), np.float32)
+    blob = np.ascontiguousarray(blob, np.uint8)
+    f = rlib().ref_matmul if ref else olib().xjo_matmul
+    f(t, _ptr(blob), K, N, _ptr(x), _ptr(y), x.shape[0])
+    return y
+
+
+def rmsnorm(x, w, eps, ref=False):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    f = rlib().ref_rmsnorm if ref else olib().xjo_rmsnorm
+    f(_ptr(out), _ptr(x), _ptr(np.ascontiguousarray(w, np.float32)) if w is not None else None, x.size, eps)
+    return out
+
+
+def rope(v, n_rot, pos, base, ref=False):
+    v = np.array(v, np.float32)
+    f = rlib().ref_rope if ref else olib().xjo_rope
+    f(_ptr(v), n_rot, pos, base)
+    return v
+
+
+def delta_recurrent(q, k, v, decay, beta, state, qscale):
+    T, H, S = q.shape
+    st = np.ascontiguousarray(state, np.float32).copy()
+    out = np.empty((T, H, S), np.float32)
+    args = [np.ascontiguousarray(a, np.float32) for a in (q, k, v, decay, beta)]
+    olib().xjo_delta_recurrent(H, S, T, *[_ptr(a) for a in args], qscale, _ptr(st), _ptr(out))
+    return out, st
+
+
+def abi_offsets(ref=False):
+    buf = (C.c_long * 256)()
+    n = (rlib().ref_abi_offsets if ref else olib().xjo_abi_offsets)(buf, 256)
+    return list(buf[:n])
+
+
+class CpuStage:
+    """A CPU stage behind the xj_stage vtable: the oracle restatement (kv_f16 selects
+    the fp16 KV cache) or, with ref=True, the reference's own xj_cpu_stage_new."""
+
+    def __init__(self, model_ptr, l0, l1, n_ctx, max_batch, has_head, kv_f16=False, ref=False):
+        err = C.create_string_buffer(ERR)
+        if ref:
+            self.ptr = rlib().ref_stage_new(model_ptr, l0, l1, n_ctx, max_batch, has_head, err, ERR)
+        else:
+            self.ptr = olib().xjo_stage_new(model_ptr, l0, l1, n_ctx, max_batch, has_head, int(kv_f16), err, ERR)
+        if not self.ptr:
+            raise RuntimeError(err.value.decode())
+        self.E = model_ptr.contents.hp.n_embd
+        self.V = model_ptr.contents.hp.n_vocab
+
+    @property
+    def s(self):
+        return self.ptr.contents
+
+    @property
+    def n_past(self):
+        return self.ptr.contents.n_past
+
+    def forward(self, x):
+        err = C.create_string_buffer(ERR)
+        rc = self.s.forward(self.ptr, x.ctypes.data_as(C.POINTER(C.c_float)), x.shape[0], err, ERR)
+        if rc:
+            raise RuntimeError(err.value.decode())
+        return x
+
+    def logits(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty((x.shape[0], self.V), np.float32)
+        err = C.create_string_buffer(ERR)
+        rc = self.s.logits(self.ptr, x.ctypes.data_as(C.POINTER(C.c_float)), x.shape[0],
+                           out.ctypes.data_as(C.POINTER(C.c_float)), err, ERR)
+        if rc:
+            raise RuntimeError(err.value.decode())
+        return out
+
+    def rollback(self, n_past):
+        err = C.create_string_buffer(ERR)
+        if self.s.rollback(self.ptr, n_past, err, ERR):
+            raise RuntimeError(err.value.decode())
+
+    def set_keep(self, k):
+        self.ptr.contents.keep = k
+
+    def reset(self):
+        self.s.reset(self.ptr)
+
+    def destroy(self):
+        if self.ptr:
+            self.s.destroy(self.ptr)
+            self.ptr = None
+
+
+def embed(model_ptr, token):
+    out = np.empty(model_ptr.contents.hp.n_embd, np.float32)
+    olib().xjo_embed(model_ptr, token, _ptr(out))
+    return out
+
+
+def greedy(stages, prompt, n_gen):
+    """xjo_greedy over oracle CpuStages; returns (tokens, top1-top2 margins)."""
+    arr = (C.POINTER(xp.XjStage) * len(stages))(*[s.ptr for s in stages])
+    p = np.ascontiguousarray(prompt, np.int32)
+    out = np.empty(n_gen, np.int32)
+    mg = np.empty(n_gen, np.float32)
+    err = C.create_string_buffer(ERR)
+    rc = olib().xjo_greedy(arr, len(stages), _ptr(p), len(p), n_gen, _ptr(out), _ptr(mg), err, ERR)
+    if rc:
+        raise RuntimeError(err.value.decode())
+    return out, mg
+
+
+def ref_greedy(path, prompt, n_gen, split=0, n_ctx=1024, max_batch=8):
+    """The reference's own pipeline + greedy driver on its own loader (fp32 KV)."""
+    L = rlib()
+    err = C.create_string_buffer(ERR)
+    m = L.ref_model_load(path.encode(), err, ERR)
+    if not m:
+        raise RuntimeError(err.value.decode())
+    p = np.ascontiguousarray(prompt, np.int32)
+    out = np.empty(n_gen, np.int32)
+    mg = np.empty(n_gen, np.float32)
+    rc = L.ref_greedy(m, split, n_ctx, max_batch, _ptr(p), len(p), n_gen, _ptr(out), _ptr(mg), err, ERR)
+    L.ref_model_free(m)
+    if rc:
+        raise RuntimeError(err.value.decode())
+    return out, mg

@@ -1,0 +1,62 @@
+/*
+ * xjo.h - the oracle: a CPU restatement of the reference's token loop, used
+ * ONLY as the checker by tests/, __graft_entry__.smoke() and the CPU-baseline
+ * leg of bench.py. Nothing in the product links or calls it.
+ *
+ *   xjo_f16 / xjo_to_f16 / xjo_dequant_row  <- src/xiaoju-pipe/core/xj_quant.h:9-122
+ *   xjo_matmul, xjo_rmsnorm, xjo_rope,       <- src/xiaoju-pipe/core/xj_cpu.c:36-77
+ *   xjo_stage_new (forward/logits/rollback/  <- src/xiaoju-pipe/core/xj_cpu.c:83-418
+ *     reset/destroy, embed)
+ *   xjo_greedy                               <- src/xiaoju-pipe/core/xj_net.c:532-559 (no-remote
+ *                                               eval) + src/xiaoju-pipe/tools/xjpipe-host.c:17-18,131-144
+ *   xjo_delta_recurrent                      <- the delta rule of src/xiaoju-pipe/core/xj_cpu.c:196-213
+ *                                               with decay and beta passed in directly
+ *
+ * kv_f16 != 0 rounds every K/V value through fp16 (round to nearest even) when
+ * it is stored, as the Metal backend's cache does (xj_kernels.metal:440-452);
+ * kv_f16 == 0 is the reference CPU path's own fp32 cache (xj_cpu.c:411-412).
+ *
+ * How each part is pinned: see the module header of each .c file and the
+ * tests that compare it with the reference compiled from source (oracle/_ref)
+ * and with the committed golden vectors in tests/golden/.
+ */
+#ifndef XJO_H
+#define XJO_H
+
+#include "../include/xj_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+float    xjo_f16(uint16_t h);
+uint16_t xjo_to_f16(float f);
+uint64_t xjo_row_bytes(uint32_t type, int64_t n);
+void     xjo_dequant_row(uint32_t type, const void *src, float *y, int64_t n);
+/* y[t][r] = dot(dequant(W[r]), x[t]); OpenMP over rows. */
+void     xjo_matmul(uint32_t type, const void *w, int64_t K, int64_t N, const float *x, float *y, int T);
+void     xjo_rmsnorm(float *out, const float *x, const float *w, int n, float eps);
+void     xjo_l2norm(float *x, int n, float eps);
+void     xjo_rope(float *v, int n_rot, int pos, float base);
+void     xjo_embed(const xj_model *m, int32_t token, float *out);
+
+xj_stage *xjo_stage_new(const xj_model *m, int l0, int l1, int n_ctx, int max_batch, bool has_head,
+                        int kv_f16, char *err, size_t errlen);
+
+/* Greedy decoding through stages[0..n_stages) (the last has the head):
+ * prefill `prompt` in chunks of the smallest max_batch, then produce n_gen
+ * tokens: out[0] = argmax of the prompt's last logits, out[i] = argmax after
+ * feeding out[i-1]. margins[i] (optional) = top-1 minus top-2 logit. */
+int xjo_greedy(xj_stage **stages, int n_stages, const int32_t *prompt, int n_prompt, int n_gen,
+               int32_t *out, float *margins, char *err, size_t errlen);
+
+/* First index of the maximum (strict >), xj_spec.c:12-16. */
+int xjo_argmax(const float *x, int n);
+
+void xjo_delta_recurrent(int H, int S, int T, const float *q, const float *k, const float *v,
+                         const float *decay, const float *beta, float qscale, float *state, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

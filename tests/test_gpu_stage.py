@@ -1,0 +1,210 @@
+"""The HIP stage behind the xj_stage vtable and the device chain, against the
+oracle's CPU stage with an fp16 KV cache, on identical seeded inputs.
+
+Mirrors the reference's own GPU-vs-CPU check (src/xiaoju-pipe/tools/xjpipe-check.c:61-109):
+prefill 12 tokens then 3 single tokens, head top-1, keep/rollback equal to
+never having computed the rolled-back tokens; plus greedy token identity.
+"""
+import numpy as np
+import pytest
+
+import oracle as orc
+import xjpipe as xp
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def tiny(tiny_path):
+    return xp.Model(tiny_path)
+
+
+def embed(m, toks):
+    return np.stack([orc.embed(m.ptr, int(t)) for t in toks]).astype(np.float32)
+
+
+def prompt_ids(m, n, seed):
+    return np.random.default_rng(seed).integers(0, m.hp.n_vocab, n).astype(np.int32)
+
+
+def test_forward_and_head_match_oracle(tiny):
+    m, L = tiny, tiny.hp.n_layer
+    toks = prompt_ids(m, 15, 1)
+    g = xp.HipStage(m, 0, L, 128, 16, True)
+    c = orc.CpuStage(m.ptr, 0, L, 128, 16, True, kv_f16=True)
+    pos = 0
+    for T in (12, 1, 1, 1):
+        x = embed(m, toks[pos:pos + T])
+        xg, xc = g.forward(x.copy()), c.forward(x.copy())
+        assert rel_l2(xg, xc) < 1e-3, T
+        pos += T
+    assert g.n_past == c.n_past == 15
+    lg, lc = g.logits(xg[-1:]), c.logits(xc[-1:])
+    assert rel_l2(lg, lc) < 1e-3
+    assert int(np.argmax(lg)) == int(np.argmax(lc))
+    g.destroy()
+    c.destroy()
+
+
+def test_two_stages_equal_one(tiny):
+    m, L = tiny, tiny.hp.n_layer
+    toks = prompt_ids(m, 10, 2)
+    one = xp.HipStage(m, 0, L, 64, 8, True)
+    a, b = xp.HipStage(m, 0, 4, 64, 8, False), xp.HipStage(m, 4, L, 64, 8, True)
+    for T in (8, 2):
+        x = embed(m, toks[:T]) if T == 8 else embed(m, toks[8:10])
+        x1 = one.forward(x.copy())
+        x2 = b.forward(a.forward(x.copy()))
+        assert np.array_equal(x1, x2)
+    for s in (one, a, b):
+        s.destroy()
+
+
+def test_keep_rollback_equals_never_computed(tiny):
+    """forward 6, verify 4 with keep, roll back to 8, forward 2 others == forward the 10 kept tokens."""
+    m, L = tiny, tiny.hp.n_layer
+    toks = prompt_ids(m, 14, 3)
+    g = xp.HipStage(m, 0, L, 64, 8, True)
+    g.forward(embed(m, toks[:6]))
+    g.set_keep(4)
+    g.forward(embed(m, toks[6:10]))
+    assert g.s.ck_start == 6 and g.s.ck_T == 4
+    g.rollback(8)
+    assert g.n_past == 8
+    x_after = g.forward(embed(m, toks[12:14]))
+    ref = xp.HipStage(m, 0, L, 64, 16, True)
+    seq = np.concatenate([toks[:8], toks[12:14]])
+    xr = ref.forward(embed(m, seq))
+    assert rel_l2(x_after, xr[8:]) < 1e-6
+    c = orc.CpuStage(m.ptr, 0, L, 64, 16, True, kv_f16=True)
+    xc = c.forward(embed(m, seq))
+    assert rel_l2(x_after, xc[8:]) < 1e-3
+    for s in (g, ref, c):
+        s.destroy()
+
+
+def test_rollback_rules(tiny):
+    m, L = tiny, tiny.hp.n_layer
+    toks = prompt_ids(m, 8, 4)
+    g = xp.HipStage(m, 0, L, 64, 8, True)
+    g.forward(embed(m, toks[:4]))
+    with pytest.raises(xp.XjError):       # no checkpoint window
+        g.rollback(2)
+    g.rollback(4)                          # unchanged position is a no-op
+    g.set_keep(3)
+    g.forward(embed(m, toks[4:7]))
+    with pytest.raises(xp.XjError):       # outside [ck_start+1, ck_start+ck_T-1]
+        g.rollback(4)
+    g.rollback(6)
+    # attention-only stage (layer 3 is full attention) truncates freely
+    att = xp.HipStage(m, 3, 4, 64, 8, False)
+    att.forward(embed(m, toks[:5]))
+    att.rollback(2)
+    assert att.n_past == 2
+    with pytest.raises(xp.XjError):
+        att.rollback(3)
+    with pytest.raises(xp.XjError):       # T > max_batch
+        g.forward(embed(m, np.zeros(9, np.int32)))
+    g.destroy()
+    att.destroy()
+
+
+def test_reset_and_context_limit(tiny):
+    m, L = tiny, tiny.hp.n_layer
+    toks = prompt_ids(m, 8, 5)
+    g = xp.HipStage(m, 0, L, 8, 8, True)
+    x1 = g.forward(embed(m, toks))
+    with pytest.raises(xp.XjError):
+        g.forward(embed(m, toks[:1]))      # context full
+    g.reset()
+    assert g.n_past == 0
+    x2 = g.forward(embed(m, toks))
+    assert np.array_equal(x1, x2)
+    g.destroy()
+
+
+def test_chain_greedy_matches_oracle(tiny):
+    m, L = tiny, tiny.hp.n_layer
+    prompt = prompt_ids(m, 21, 6)
+    g = xp.HipStage(m, 0, L, 256, 8, True)
+    ch = xp.Chain([g])
+    toks = np.concatenate([ch.eval(prompt), ch.decode(63)])
+    c = orc.CpuStage(m.ptr, 0, L, 256, 8, True, kv_f16=True)
+    want, margins = orc.greedy([c], prompt, 64)
+    assert np.array_equal(toks, want), (toks, want, margins)
+    ch.free()
+    g.destroy()
+    c.destroy()
+
+
+def test_chain_split_and_vtable_agree(tiny):
+    """Two chained stages on the device give the same tokens as the host-driven vtable loop."""
+    m, L = tiny, tiny.hp.n_layer
+    prompt = prompt_ids(m, 9, 7)
+    a, b = xp.HipStage(m, 0, 4, 128, 8, False), xp.HipStage(m, 4, L, 128, 8, True)
+    ch = xp.Chain([a, b])
+    toks = np.concatenate([ch.eval(prompt), ch.decode(31)])
+    ch.free()
+    a.destroy()
+    b.destroy()
+    g = xp.HipStage(m, 0, L, 128, 8, True)
+    x = g.forward(embed(m, prompt[:8]))
+    x = g.forward(embed(m, prompt[8:]))
+    host = []
+    for _ in range(32):
+        t = int(np.argmax(g.logits(x[-1:])[0]))
+        host.append(t)
+        x = g.forward(embed(m, [t]))
+    assert toks.tolist() == host
+    g.destroy()
+
+
+def test_chain_verify_and_rollback(tiny):
+    m, L = tiny, tiny.hp.n_layer
+    prompt = prompt_ids(m, 16, 8)
+    g = xp.HipStage(m, 0, L, 128, 8, True)
+    ch = xp.Chain([g])
+    ch.eval(prompt)
+    greedy = ch.decode(5)                       # reference continuation
+    g2 = xp.HipStage(m, 0, L, 128, 8, True)
+    c2 = xp.Chain([g2])
+    first = c2.eval(prompt)
+    cand = np.concatenate([first, greedy[:4]])  # [t, d1..d4] all correct
+    am = c2.eval(cand, nlog=5, keep=True)
+    assert am.tolist() == greedy.tolist()
+    c2.rollback(16 + 2)                          # keep t, d1
+    nxt = c2.eval(greedy[1:2])
+    assert int(nxt[0]) == int(greedy[2])
+    for o in (ch, c2):
+        o.free()
+    g.destroy()
+    g2.destroy()
+
+
+@pytest.mark.parametrize("mode", ["draft", "oracle_all", "oracle_miss"])
+def test_spec_decode_equals_greedy(tiny, tiny_draft_path, mode):
+    m, L = tiny, tiny.hp.n_layer
+    dm = xp.Model(tiny_draft_path)
+    prompt = prompt_ids(m, 13, 9)
+    n_gen = 40
+    g = xp.HipStage(m, 0, L, 256, 8, True)
+    ch = xp.Chain([g])
+    plain = np.concatenate([ch.eval(prompt), ch.decode(n_gen - 1)])
+    ch.free()
+    g.destroy()
+    t = xp.HipStage(m, 0, L, 256, 8, True)
+    d = xp.HipStage(dm, 0, dm.hp.n_layer, 256, 8, True)
+    tc, dc = xp.Chain([t]), xp.Chain([d])
+    tc.eval(prompt)
+    dc.eval(prompt)
+    oracle = None if mode == "draft" else plain
+    miss = 3 if mode == "oracle_miss" else 0
+    out, st = xp.spec_generate(tc, dc, 4, n_gen, oracle=oracle, oracle_miss=miss)
+    assert out.tolist() == plain.tolist()
+    if mode == "oracle_all":
+        assert st.n_accepted == st.n_drafted
+    for o in (tc, dc):
+        o.free()
+    t.destroy()
+    d.destroy()
