@@ -42,15 +42,7 @@ def log(*a):
 
 
 def model_path(cfg, name):
-    d = os.environ.get("XJ_MODEL_DIR", "/tmp/xj_models")
-    os.makedirs(d, exist_ok=True)
-    p = os.path.join(d, f"{name}_{cfg.seed}.gguf")
-    if not os.path.exists(p):
-        t = time.time()
-        n = xp.write_model(p + ".tmp", cfg)
-        os.replace(p + ".tmp", p)
-        log(f"wrote {p} ({n / 1e9:.2f} GB) in {time.time() - t:.1f} s")
-    return p
+    return xp.cached_model(cfg, name)
 
 
 def decode_run(cfg, name, n_prompt, steps, warmup, seed):
@@ -81,7 +73,8 @@ def cpu_baseline(cfg, name, n_prompt_cpu, n_steps_cpu, seed):
     kind = "reference" if orc.ref_available() else "port"
     m = xp.Model(model_path(cfg, name))
     hp = m.hp
-    stage = orc.CpuStage(m.ptr, 0, hp.n_layer, n_prompt_cpu + n_steps_cpu + 8, 8, True, ref=(kind == "reference"))
+    stage = orc.CpuStage(m.ptr, 0, hp.n_layer, n_prompt_cpu + n_steps_cpu + 8, n_prompt_cpu, True,
+                         ref=(kind == "reference"))
     prompt = np.random.default_rng(seed).integers(0, hp.n_vocab, n_prompt_cpu).astype(np.int32)
     x = np.stack([orc.embed(m.ptr, int(t)) for t in prompt])
     stage.forward(x)

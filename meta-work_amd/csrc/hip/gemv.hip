@@ -2,29 +2,33 @@
 //
 // Computes the reference's matmul (src/xiaoju-pipe/core/xj_cpu.c:36-54,
 // y[t][r] = dot(dequant(W[r]), x[t])) with the neighbouring element-wise work
-// folded in:
-//   prologue (activations into LDS): RMSNorm (xj_cpu.c:56-61, double sum),
-//     SwiGLU silu(g)*u (xj_cpu.c:273), per-head gated RMSNorm
-//     norm(o)*w*silu(z) (xj_cpu.c:215-217)
-//   epilogue: store, residual add (xj_cpu.c:268,275), depthwise causal conv +
-//     SiLU with state carry and checkpoints (xj_cpu.c:172-182,220), and greedy
-//     argmax partials for the LM head (xj_spec.c:12-16 tie rule).
-// One launch serves up to four weight segments that share K (e.g. qkv, gate,
-// beta and alpha of a DeltaNet layer) so a layer needs few launches.
+// folded in, in two launches:
+//   prep  the prologue, once per launch: RMSNorm (xj_cpu.c:56-61, double
+//         sum), SwiGLU silu(g)*u (xj_cpu.c:273) or per-head gated RMSNorm
+//         norm(o)*w*silu(z) (xj_cpu.c:215-217); the result v is written as
+//         21-bit integers X = rint(v * 2^(20-E)) per 32-element group (E the
+//         group's binary exponent), split into three int8 digit planes.
+//   gemv  weights x activations with v_dot4_i32_i8: for every quantization
+//         sub-block, sum_l q_l X_l is formed exactly in 32-bit integers, then
+//         scaled once in fp32 (d*sc, the group's 2^(E-20)) and the block
+//         minimum term dmin*m*sum(X) subtracted. Epilogues: store, residual
+//         add (xj_cpu.c:268,275), depthwise causal conv + SiLU with state
+//         carry and checkpoints (xj_cpu.c:172-182,220), greedy argmax
+//         partials for the LM head (xj_spec.c:12-16 tie rule).
+// The activation digits add at most 2^-21 of the group maximum per element,
+// about 2e-6 relative on a dot product, below the 1e-3 parity bar by three
+// orders of magnitude (fp32 accumulation itself is ~1e-6).
 //
-// Work mapping. A team of TS lanes (16, 32 or 64, chosen from K so that each
-// lane owns about four 32-element chunks) owns one row; a 256-thread
-// work-group holds 256/TS teams. One chunk is 16 B of Q4_K nibbles (+ the
-// block header), 3 x 8 B of Q6_K planes, 32 B of Q8_0 quants or 128 B of F32.
-// A lane loads all of its chunks (up to NPF) before using any, and the first
-// round is issued before the activations are staged in LDS, so the weight
-// latency overlaps the prologue. Quantized products are factored per
-// sub-block, sum_l (d*sc*q_l - dmin*m) x_l = d*sc*sum q_l x_l - dmin*m*sum x_l,
-// with the sums of x precomputed per 8 elements in the prologue. Lane partials
-// are combined in a fixed butterfly (DPP within 16 lanes, then cross-row
-// shuffles), so a row's result does not depend on T, on the grid, or on which
-// work-group computed it. Work-groups loop over row groups when there are
-// more than eight per CU, so the LDS fill is amortised on the LM head.
+// Work mapping. A team of `lanes` lanes owns `rpt` rows; a 256-thread
+// work-group holds 256/lanes teams. A lane takes 64-element units (one Q4_K
+// scale pair, one Q6_K half-block column of 16, two Q8_0 blocks) of its rows
+// with stride `lanes`, so consecutive lanes read consecutive weight bytes.
+// Each unit's activation digits are read from LDS once per token and used for
+// all of the team's rows. Lane partials are combined in a fixed butterfly
+// (DPP within 16 lanes, then cross-row shuffles), so a row's result does not
+// depend on T, on the grid, or on which work-group computed it. One launch
+// serves up to four weight segments that share K (e.g. qkv, gate, beta and
+// alpha of a DeltaNet layer).
 #include "common.h"
 #include "dequant.h"
 #include "kernels.h"
@@ -40,323 +44,396 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 static int g_lds_max = 64 * 1024;
+static int g_cus = 256;
 static int g_grid_cap = 256 * 8;
-
-// x is stored in LDS with 4 floats of padding per 64 so that the chunk
-// pattern of a team spreads over the banks.
-__device__ __forceinline__ int xpad(int e) { return e + 4 * (e >> 6); }
-__host__ __device__ inline int kpad(int K) { return K + 4 * ((K + 63) / 64); }
-
-// byte i of w as float (selected into one v_cvt_f32_ubyte{0..3})
-__device__ __forceinline__ float ub(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xFFu); }
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
 
-// s = sum_i bytes(w)[i] * x[i] over 4 elements, in order
-__device__ __forceinline__ float dot4(uint32_t w, f32x4 x, float s) {
-    s = fmaf(ub(w, 0), x.x, s);
-    s = fmaf(ub(w, 1), x.y, s);
-    s = fmaf(ub(w, 2), x.z, s);
-    s = fmaf(ub(w, 3), x.w, s);
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+__device__ __forceinline__ int row16_sum_i(int v) {
+    v += dpp_i<0xB1>(v);
+    v += dpp_i<0x4E>(v);
+    v += dpp_i<0x141>(v);
+    v += dpp_i<0x140>(v);
+    return v;
+}
+
+__device__ __forceinline__ u32x4 ld16(const uint8_t *p) { return *(const u32x4 *)p; }
+__device__ __forceinline__ u32x4 lds16(const uint8_t *p) { return *(const u32x4 *)p; }
+
+// ---------------------------------------------------------------- prep --
+// One thread per input element k of token blockIdx.y; 32 consecutive lanes
+// form one digit group.
+__global__ __launch_bounds__(256) void prep_kernel(const GArgs a) {
+    const int K = a.K, t = blockIdx.y, tid = threadIdx.x, k = blockIdx.x * 256 + tid;
+    const XqOff o = xq_off(K);
+    const bool in = k < K;
+    __shared__ double red[4];
+    const float *x = a.x + (int64_t)t * a.xs;
+    float v = 0.f;
+    if (a.pro == PRO_RMS) {
+        double ss = 0;
+        for (int i = tid; i < K; i += 256) ss += (double)x[i] * x[i];
+        ss = xjd::block_sum_d(ss, red);
+        const float sc = 1.0f / sqrtf((float)(ss / K) + a.eps);
+        if (in) v = x[k] * sc * a.pro_w[k];
+    } else if (a.pro == PRO_SWIGLU) {
+        if (in) v = xjd::silu(x[k]) * a.x2[(int64_t)t * a.x2s + k];
+    } else if (a.pro == PRO_GATED_RMS) {
+        const int G = a.group;
+        float gsc;
+        if (G % 64 == 0 && 256 % G == 0) {
+            // each wavefront lies inside one head: combine the wavefront sums of the head
+            const float o1 = in ? x[k] : 0.f;
+            const double ws = xjd::wave_sum_d((double)o1 * o1);
+            if ((tid & 63) == 0) red[tid >> 6] = ws;
+            __syncthreads();
+            const int w0 = (tid / G) * (G / 64);
+            double ss = 0;
+            for (int w = w0; w < w0 + G / 64; w++) ss += red[w];
+            gsc = 1.0f / sqrtf((float)(ss / G) + a.eps);
+        } else {
+            const int h0 = in ? (k / G) * G : 0;
+            double ss = 0;
+            for (int i = h0; in && i < h0 + G; i++) ss += (double)x[i] * x[i];
+            gsc = 1.0f / sqrtf((float)(ss / G) + a.eps);
+        }
+        if (in) v = x[k] * gsc * a.pro_w[k % G] * xjd::silu(a.x2[(int64_t)t * a.x2s + k]);
+    } else {
+        if (in) v = x[k];
+    }
+    // group exponent: max|v| over the 32 lanes of the group < 2^E
+    float m = fabsf(v);
+    m = xjd::row16_max(m);
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    int E = 0;
+    (void)frexpf(m, &E);
+    if (E < -100) E = -100;
+    const int X = (int)rintf(v * ldexpf(1.0f, 20 - E));
+    const int c = ((X + 64) & 127) - 64;
+    const int X1 = (X - c) / 128;
+    const int b = ((X1 + 64) & 127) - 64;
+    const int a8 = (X1 - b) / 128;
+    const int sx = row16_sum_i(X);
+    if (!in) return;
+    uint8_t *dst = a.xq + (int64_t)t * o.stride;
+    const int g = k >> 5, l = k & 31;
+    dst[g * 96 + l] = (uint8_t)(int8_t)a8;
+    dst[g * 96 + 32 + l] = (uint8_t)(int8_t)b;
+    dst[g * 96 + 64 + l] = (uint8_t)(int8_t)c;
+    if (l == 0) ((float *)(dst + o.f_off))[g] = ldexpf(1.0f, E - 20);
+    if ((k & 15) == 0) ((int *)(dst + o.sx_off))[k >> 4] = sx;
+    ((float *)(dst + o.v_off))[k] = v;
+}
+
+// -------------------------------------------------------- unit kernels --
+// Exact integer sum over 4N elements of q (packed signed bytes) times X,
+// whose digit planes start at p, p + 32 and p + 64:
+//   ((sum q*a) * 128 + sum q*b) * 128 + sum q*c.
+// Q4_K (q <= 15, 32 elements) and Q6_K (q <= 63, 16 elements) stay below
+// 2^31 at every step.
+template <int N>
+__device__ __forceinline__ int qdot(const uint32_t (&q)[N], const u32x4 (&pa)[N / 4], const u32x4 (&pb)[N / 4],
+                                    const u32x4 (&pc)[N / 4]) {
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < N; j++) s = sdot4(q[j], pa[j >> 2][j & 3], s);
+    s *= 128;
+#pragma unroll
+    for (int j = 0; j < N; j++) s = sdot4(q[j], pb[j >> 2][j & 3], s);
+    s *= 128;
+#pragma unroll
+    for (int j = 0; j < N; j++) s = sdot4(q[j], pc[j >> 2][j & 3], s);
     return s;
 }
 
-// Raw bytes of one 32-element chunk, fetched ahead of use (9 dwords):
-//   Q4_K  r0..3 block header (d|dmin, 12 scale bytes), r4..7 the chunk's 16 nibble bytes
-//   Q6_K  r0..1 ql (low-half group), r2..3 ql (+32), r4..5 qh, r6..7 the half's 8 scales, r8 d
-//   Q8_0  r0..7 the 32 quants, r8 d
-struct Raw {
-    uint32_t r[9];
-};
-
-__device__ __forceinline__ void put4(uint32_t *d, u32x4 v) { d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w; }
-__device__ __forceinline__ void put2(uint32_t *d, u32x2 v) { d[0] = v.x; d[1] = v.y; }
-
-// chunk c of a row whose first block index is rowblk (row * blocks_per_row)
-__device__ __forceinline__ void load_chunk(uint32_t type, const uint8_t *__restrict__ W, int64_t nblk, int64_t rowblk,
-                                           int c, Raw &raw) {
-    if (type == XJ_Q4_K) {
-        const uint8_t *blk = W + (rowblk + (c >> 3)) * 144;
-        put4(raw.r, __builtin_nontemporal_load((const u32x4 *)blk));
-        put4(raw.r + 4, __builtin_nontemporal_load((const u32x4 *)(blk + 16 + 16 * (c & 7))));
-    } else if (type == XJ_Q6_K) {
-        const int q = c & 7, h = q >> 2, l0 = (q & 3) * 8;
-        const int64_t g = rowblk + (c >> 3);
-        const uint8_t *ql = W + g * 128 + 64 * h + l0;
-        put2(raw.r, __builtin_nontemporal_load((const u32x2 *)ql));
-        put2(raw.r + 2, __builtin_nontemporal_load((const u32x2 *)(ql + 32)));
-        put2(raw.r + 4, __builtin_nontemporal_load((const u32x2 *)(W + nblk * 128 + g * 64 + 32 * h + l0)));
-        put2(raw.r + 6, __builtin_nontemporal_load((const u32x2 *)(W + nblk * 192 + g * 16 + 8 * h)));
-        raw.r[8] = *(const uint16_t *)(W + nblk * 208 + g * 2);
-    } else {  // Q8_0
-        const int64_t g = rowblk + c;
-        put4(raw.r, __builtin_nontemporal_load((const u32x4 *)(W + g * 32)));
-        put4(raw.r + 4, __builtin_nontemporal_load((const u32x4 *)(W + g * 32 + 16)));
-        raw.r[8] = *(const uint16_t *)(W + nblk * 32 + g * 2);
+template <int N>
+__device__ __forceinline__ void planes(const uint8_t *p, u32x4 (&pa)[N / 4], u32x4 (&pb)[N / 4], u32x4 (&pc)[N / 4]) {
+#pragma unroll
+    for (int j = 0; j < N / 4; j++) {
+        pa[j] = lds16(p + 16 * j);
+        pb[j] = lds16(p + 32 + 16 * j);
+        pc[j] = lds16(p + 64 + 16 * j);
     }
 }
 
-// acc[t] += sum over the chunk's 32 elements of dequant(w) * x[t]
-template <int T>
-__device__ __forceinline__ void dot_q4k(const Raw &raw, int c, const float *xl, const float *xs8, int KP, int K8, float (&acc)[T]) {
-    const int q = c & 7, p = q >> 1, jm = (2 * p) & 3;
+// Q4_K unit u = (block u/4, scale pair p = u%4): elements 64p..64p+63 of the
+// block, i.e. sub-blocks 2p (low nibbles of qs[32p..32p+31]) and 2p+1 (high
+// nibbles); scale/min decoding as get_scale_min_k4 (xj_quant.c).
+template <int T, int RPT>
+__device__ __forceinline__ void unit_q4k(const u32x4 (&h)[RPT], const u32x4 (&q0)[RPT], const u32x4 (&q1)[RPT], int u,
+                                         const uint8_t *xl, int ldsT, const XqOff &o, float (&acc)[RPT][T]) {
+    const int p = u & 3, g0 = 8 * (u >> 2) + 2 * p, jm = (2 * p) & 3;
     const bool hi4 = p >= 2;
-    const int e0 = (c >> 3) * 256 + 64 * p + (q & 1) * 16;
-    const float d = xjd::f16_to_f32(raw.r[0] & 0xFFFFu), dmin = xjd::f16_to_f32(raw.r[0] >> 16);
-    float ds[2], dm[2];
+    float ds[RPT][2], dm[RPT][2];
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        const float d = xjd::f16_to_f32(h[i].x & 0xFFFFu), dmin = xjd::f16_to_f32(h[i].x >> 16);
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const uint32_t A = byte_of(h[i].y, jm + s), B = byte_of(h[i].z, jm + s), C = byte_of(h[i].w, jm + s);
+            const uint32_t sc = hi4 ? ((C & 0xF) | ((A >> 6) << 4)) : (A & 63);
+            const uint32_t mn = hi4 ? ((C >> 4) | ((B >> 6) << 4)) : (B & 63);
+            ds[i][s] = d * (float)sc;
+            dm[i][s] = dmin * (float)mn;
+        }
+    }
 #pragma unroll
     for (int s = 0; s < 2; s++) {
-        const uint32_t A = byte_of(raw.r[1], jm + s), B = byte_of(raw.r[2], jm + s), C = byte_of(raw.r[3], jm + s);
-        const uint32_t sc = hi4 ? ((C & 0xF) | ((A >> 6) << 4)) : (A & 63);
-        const uint32_t mn = hi4 ? ((C >> 4) | ((B >> 6) << 4)) : (B & 63);
-        ds[s] = d * (float)sc;
-        dm[s] = dmin * (float)mn;
-    }
-    float s0[T], s1[T];
+        uint32_t nib[RPT][8];
 #pragma unroll
-    for (int t = 0; t < T; t++) { s0[t] = 0.f; s1[t] = 0.f; }
+        for (int i = 0; i < RPT; i++)
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const uint32_t w = raw.r[4 + u];
-        const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+            for (int j = 0; j < 8; j++) {
+                const uint32_t w = j < 4 ? q0[i][j] : q1[i][j - 4];
+                nib[i][j] = s ? (w >> 4) & 0x0F0F0F0Fu : w & 0x0F0F0F0Fu;
+            }
+        const int g = g0 + s;
 #pragma unroll
         for (int t = 0; t < T; t++) {
-            const f32x4 xa = *(const f32x4 *)(xl + t * KP + xpad(e0 + 4 * u));
-            const f32x4 xb = *(const f32x4 *)(xl + t * KP + xpad(e0 + 32 + 4 * u));
-            s0[t] = dot4(lo, xa, s0[t]);
-            s1[t] = dot4(hi, xb, s1[t]);
-        }
-    }
+            const uint8_t *xt = xl + t * ldsT;
+            u32x4 pa[2], pb[2], pc[2];
+            planes<8>(xt + g * 96, pa, pb, pc);
+            const float f = ((const float *)(xt + o.f_off))[g];
+            const int2 sxp = ((const int2 *)(xt + o.sx_off))[g];
+            const float SX = (float)(sxp.x + sxp.y);
 #pragma unroll
-    for (int t = 0; t < T; t++) {
-        const float xsa = xs8[t * K8 + (e0 >> 3)] + xs8[t * K8 + (e0 >> 3) + 1];
-        const float xsb = xs8[t * K8 + ((e0 + 32) >> 3)] + xs8[t * K8 + ((e0 + 32) >> 3) + 1];
-        acc[t] += ds[0] * s0[t] - dm[0] * xsa + (ds[1] * s1[t] - dm[1] * xsb);
+            for (int i = 0; i < RPT; i++) {
+                const int S = qdot<8>(nib[i], pa, pb, pc);
+                const float part = (float)S * ds[i][s] - SX * dm[i][s];
+                acc[i][t] = fmaf(part, f, acc[i][t]);
+            }
+        }
     }
 }
 
-template <int T>
-__device__ __forceinline__ void dot_q6k(const Raw &raw, int c, const float *xl, const float *xs8, int KP, int K8, float (&acc)[T]) {
-    const int q = c & 7, h = q >> 2, l0 = (q & 3) * 8, is = l0 >> 4;
-    const int e0 = (c >> 3) * 256 + 128 * h + l0;
-    const float d = xjd::f16_to_f32(raw.r[8]);
-    float dsc[4];
+// Q6_K unit u = (block u/4, half h = (u/2)%2, column half hl = u%2): for each
+// of the four 32-element groups G of the half, the 16 elements
+// 128h + 32G + 16hl .. +15 (one scale sub-block each). Bit layout as
+// dequantize_row_q6_K: q = (ql & 15 | ql >> 4) | qh bit pair << 4, value q - 32.
+template <int T, int RPT>
+__device__ __forceinline__ void unit_q6k(const u32x4 (&l0)[RPT], const u32x4 (&l1)[RPT], const u32x4 (&qh)[RPT],
+                                         const u32x2 (&sc)[RPT], const uint32_t (&dd)[RPT], int u, const uint8_t *xl,
+                                         int ldsT, const XqOff &o, float (&acc)[RPT][T]) {
+    const int h = (u >> 1) & 1, hl = u & 1, gb = 8 * (u >> 2) + 4 * h;
 #pragma unroll
     for (int G = 0; G < 4; G++) {
-        const int bi = is + 2 * G;
-        dsc[G] = d * (float)(int8_t)byte_of(bi < 4 ? raw.r[6] : raw.r[7], bi & 3);
-    }
-    float sq[T][4];
+        uint32_t q6[RPT][4];
+        float dsc[RPT];
 #pragma unroll
-    for (int t = 0; t < T; t++)
+        for (int i = 0; i < RPT; i++) {
 #pragma unroll
-        for (int G = 0; G < 4; G++) sq[t][G] = 0.f;
-#pragma unroll
-    for (int v = 0; v < 2; v++) {
-        const uint32_t la = raw.r[v], lb = raw.r[2 + v], hb = raw.r[4 + v];
-#pragma unroll
-        for (int G = 0; G < 4; G++) {
-            const uint32_t nib = (G == 0) ? (la & 0x0F0F0F0Fu) : (G == 1) ? (lb & 0x0F0F0F0Fu)
-                               : (G == 2) ? ((la >> 4) & 0x0F0F0F0Fu) : ((lb >> 4) & 0x0F0F0F0Fu);
-            const uint32_t q6 = nib | (((hb >> (2 * G)) & 0x03030303u) << 4);
-#pragma unroll
-            for (int t = 0; t < T; t++)
-                sq[t][G] = dot4(q6, *(const f32x4 *)(xl + t * KP + xpad(e0 + 32 * G + 4 * v)), sq[t][G]);
+            for (int j = 0; j < 4; j++) {
+                const uint32_t a0 = l0[i][j], a1 = l1[i][j], hb = qh[i][j];
+                q6[i][j] = G == 0 ? (a0 & 0x0F0F0F0Fu) | ((hb << 4) & 0x30303030u)
+                         : G == 1 ? (a1 & 0x0F0F0F0Fu) | ((hb << 2) & 0x30303030u)
+                         : G == 2 ? ((a0 >> 4) & 0x0F0F0F0Fu) | (hb & 0x30303030u)
+                                  : ((a1 >> 4) & 0x0F0F0F0Fu) | ((hb >> 2) & 0x30303030u);
+            }
+            const uint32_t sw = G < 2 ? sc[i].x : sc[i].y;
+            dsc[i] = xjd::f16_to_f32(dd[i]) * (float)(int8_t)byte_of(sw, 2 * (G & 1) + hl);
         }
-    }
-#pragma unroll
-    for (int t = 0; t < T; t++)
-#pragma unroll
-        for (int G = 0; G < 4; G++) acc[t] += dsc[G] * (sq[t][G] - 32.0f * xs8[t * K8 + ((e0 + 32 * G) >> 3)]);
-}
-
-template <int T>
-__device__ __forceinline__ void dot_q80(const Raw &raw, int c, const float *xl, int KP, float (&acc)[T]) {
-    const int e0 = c * 32;
-    const float d = xjd::f16_to_f32(raw.r[8]);
-    float s[T];
-#pragma unroll
-    for (int t = 0; t < T; t++) s[t] = 0.f;
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-        const uint32_t w = raw.r[u];
+        const int g = gb + G;
 #pragma unroll
         for (int t = 0; t < T; t++) {
-            const f32x4 xv = *(const f32x4 *)(xl + t * KP + xpad(e0 + 4 * u));
-            float a = s[t];
-            a = fmaf((float)(int8_t)(w & 0xFF), xv.x, a);
-            a = fmaf((float)(int8_t)((w >> 8) & 0xFF), xv.y, a);
-            a = fmaf((float)(int8_t)((w >> 16) & 0xFF), xv.z, a);
-            a = fmaf((float)(int8_t)(w >> 24), xv.w, a);
-            s[t] = a;
-        }
-    }
+            const uint8_t *xt = xl + t * ldsT;
+            u32x4 pa[1], pb[1], pc[1];
+            planes<4>(xt + g * 96 + 16 * hl, pa, pb, pc);
+            const float f = ((const float *)(xt + o.f_off))[g];
+            const int sxh = ((const int *)(xt + o.sx_off))[2 * g + hl];
 #pragma unroll
-    for (int t = 0; t < T; t++) acc[t] += d * s[t];
-}
-
-template <int T>
-__device__ __forceinline__ void dot_f32(const uint8_t *__restrict__ W, int K, int64_t row, int c, const float *xl, int KP,
-                                        float (&acc)[T]) {
-    const int e0 = c * 32;
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-        const f32x4 w = __builtin_nontemporal_load((const f32x4 *)(W + (row * K + e0 + 4 * u) * 4));
-#pragma unroll
-        for (int t = 0; t < T; t++) {
-            const f32x4 xv = *(const f32x4 *)(xl + t * KP + xpad(e0 + 4 * u));
-            float a = acc[t];
-            a = fmaf(w.x, xv.x, a);
-            a = fmaf(w.y, xv.y, a);
-            a = fmaf(w.z, xv.z, a);
-            a = fmaf(w.w, xv.w, a);
-            acc[t] = a;
+            for (int i = 0; i < RPT; i++) {
+                const int S = qdot<4>(q6[i], pa, pb, pc) - 32 * sxh;
+                acc[i][t] = fmaf((float)S * dsc[i], f, acc[i][t]);
+            }
         }
     }
 }
 
-// ------------------------------------------------------------ prologue --
-template <int T>
-__device__ void prologue(const GArgs &a, float *xl, float *xs8, float *gsc, int KP, int K8) {
-    const int K = a.K, tid = threadIdx.x;
-    __shared__ double red[4];
-    if (a.pro == PRO_RMS) {
-        for (int t = 0; t < T; t++) {
-            const float *x = a.x + (int64_t)t * a.xs;
-            double ss = 0;
-            for (int k = tid; k < K; k += 256) ss += (double)x[k] * x[k];
-            ss = xjd::block_sum_d(ss, red);
-            const float sc = 1.0f / sqrtf((float)(ss / K) + a.eps);
-            for (int k = tid; k < K; k += 256) xl[t * KP + xpad(k)] = x[k] * sc * a.pro_w[k];
-        }
-    } else if (a.pro == PRO_SWIGLU) {
-        for (int t = 0; t < T; t++) {
-            const float *g = a.x + (int64_t)t * a.xs, *u = a.x2 + (int64_t)t * a.x2s;
-            for (int k = tid; k < K; k += 256) xl[t * KP + xpad(k)] = xjd::silu(g[k]) * u[k];
-        }
-    } else if (a.pro == PRO_GATED_RMS) {
-        // one wavefront per (token, group); group = head size S
-        const int G = a.group, ng = K / G, w = tid >> 6, ln = tid & 63;
-        for (int tg = w; tg < T * ng; tg += 4) {
-            const int t = tg / ng, g = tg % ng;
-            const float *o = a.x + (int64_t)t * a.xs + g * G;
-            double ss = 0;
-            for (int k = ln; k < G; k += 64) ss += (double)o[k] * o[k];
-            ss = xjd::wave_sum_d(ss);
-            if (ln == 0) gsc[tg] = 1.0f / sqrtf((float)(ss / G) + a.eps);
-        }
-        __syncthreads();
-        for (int t = 0; t < T; t++) {
-            const float *o = a.x + (int64_t)t * a.xs, *z = a.x2 + (int64_t)t * a.x2s;
-            for (int k = tid; k < K; k += 256)
-                xl[t * KP + xpad(k)] = o[k] * gsc[t * ng + k / G] * a.pro_w[k % G] * xjd::silu(z[k]);
-        }
-    } else {
-        for (int t = 0; t < T; t++) {
-            const float *x = a.x + (int64_t)t * a.xs;
-            for (int k = tid; k < K; k += 256) xl[t * KP + xpad(k)] = x[k];
+// Q8_0 unit u = block u (32 elements). |q| <= 128 can reach 2^32 over 32
+// elements, so the c plane is added in fp32: ((sum q*a) * 128 + sum q*b) * 128 + sum q*c.
+template <int T, int RPT>
+__device__ __forceinline__ void unit_q80(const u32x4 (&qa)[RPT], const u32x4 (&qb)[RPT], const uint32_t (&dd)[RPT], int u,
+                                         const uint8_t *xl, int ldsT, const XqOff &o, float (&acc)[RPT][T]) {
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        const uint8_t *xt = xl + t * ldsT;
+        u32x4 pa[2], pb[2], pc[2];
+        planes<8>(xt + u * 96, pa, pb, pc);
+        const float f = ((const float *)(xt + o.f_off))[u];
+#pragma unroll
+        for (int i = 0; i < RPT; i++) {
+            const uint32_t q[8] = {qa[i].x, qa[i].y, qa[i].z, qa[i].w, qb[i].x, qb[i].y, qb[i].z, qb[i].w};
+            int sa = 0, sb = 0, sc = 0;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                sa = sdot4(q[j], pa[j >> 2][j & 3], sa);
+                sb = sdot4(q[j], pb[j >> 2][j & 3], sb);
+                sc = sdot4(q[j], pc[j >> 2][j & 3], sc);
+            }
+            const float S = (float)(sa * 128 + sb) * 128.0f + (float)sc;
+            acc[i][t] = fmaf(S * xjd::f16_to_f32(dd[i]), f, acc[i][t]);
         }
     }
-    __syncthreads();
-    for (int i = tid; i < T * K8; i += 256) {
-        const int t = i / K8, g = i % K8;
-        const float *p = xl + t * KP + xpad(8 * g);   // 8 consecutive elements never straddle a pad
-        xs8[i] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-    }
-    __syncthreads();
 }
 
-// Team reduction over TS lanes (16, 32 or 64) in a fixed order.
+// ---------------------------------------------------------- row loops --
+template <int T, int TS, int RPT>
+__device__ __forceinline__ void rows_q4k(const uint8_t *__restrict__ W, const int64_t (&rb)[RPT], int nu, int lane,
+                                         const uint8_t *xl, int ldsT, const XqOff &o, float (&acc)[RPT][T]) {
+    for (int u = lane; u < nu; u += TS) {
+        u32x4 h[RPT], q0[RPT], q1[RPT];
+#pragma unroll
+        for (int i = 0; i < RPT; i++) {
+            const uint8_t *blk = W + (rb[i] + (u >> 2)) * 144;
+            h[i] = ld16(blk);
+            q0[i] = ld16(blk + 16 + 32 * (u & 3));
+            q1[i] = ld16(blk + 32 + 32 * (u & 3));
+        }
+        unit_q4k<T, RPT>(h, q0, q1, u, xl, ldsT, o, acc);
+    }
+}
+
+template <int T, int TS, int RPT>
+__device__ __forceinline__ void rows_q6k(const uint8_t *__restrict__ W, int64_t nblk, const int64_t (&rb)[RPT], int nu,
+                                         int lane, const uint8_t *xl, int ldsT, const XqOff &o, float (&acc)[RPT][T]) {
+    for (int u = lane; u < nu; u += TS) {
+        u32x4 l0[RPT], l1[RPT], qh[RPT];
+        u32x2 sc[RPT];
+        uint32_t dd[RPT];
+        const int h = (u >> 1) & 1, hl = u & 1;
+#pragma unroll
+        for (int i = 0; i < RPT; i++) {
+            const int64_t g = rb[i] + (u >> 2);
+            const uint8_t *ql = W + g * 128 + 64 * h + 16 * hl;
+            l0[i] = ld16(ql);
+            l1[i] = ld16(ql + 32);
+            qh[i] = ld16(W + nblk * 128 + g * 64 + 32 * h + 16 * hl);
+            sc[i] = *(const u32x2 *)(W + nblk * 192 + g * 16 + 8 * h);
+            dd[i] = *(const uint16_t *)(W + nblk * 208 + g * 2);
+        }
+        unit_q6k<T, RPT>(l0, l1, qh, sc, dd, u, xl, ldsT, o, acc);
+    }
+}
+
+template <int T, int TS, int RPT>
+__device__ __forceinline__ void rows_q80(const uint8_t *__restrict__ W, int64_t nblk, const int64_t (&rb)[RPT], int nu,
+                                         int lane, const uint8_t *xl, int ldsT, const XqOff &o, float (&acc)[RPT][T]) {
+    for (int u = lane; u < nu; u += TS) {
+        u32x4 qa[RPT], qb[RPT];
+        uint32_t dd[RPT];
+#pragma unroll
+        for (int i = 0; i < RPT; i++) {
+            const int64_t g = rb[i] + u;
+            qa[i] = ld16(W + g * 32);
+            qb[i] = ld16(W + g * 32 + 16);
+            dd[i] = *(const uint16_t *)(W + nblk * 32 + g * 2);
+        }
+        unit_q80<T, RPT>(qa, qb, dd, u, xl, ldsT, o, acc);
+    }
+}
+
+// F32 rows (small tensors and tests): fp32 products with the prepared v, read from global memory.
+template <int T, int TS, int RPT>
+__device__ __forceinline__ void rows_f32(const uint8_t *__restrict__ W, const int64_t (&row)[RPT], int K, int lane,
+                                         const uint8_t *xq, const XqOff &o, float (&acc)[RPT][T]) {
+    for (int c = lane; c < K / 32; c += TS) {
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const float *v = (const float *)(xq + (int64_t)t * o.stride + o.v_off) + c * 32;
+#pragma unroll
+            for (int i = 0; i < RPT; i++) {
+                const float *w = (const float *)W + row[i] * K + c * 32;
+                float s = acc[i][t];
+#pragma unroll
+                for (int e = 0; e < 32; e += 4) {
+                    const f32x4 wv = *(const f32x4 *)(w + e), xv = *(const f32x4 *)(v + e);
+                    s = fmaf(wv.x, xv.x, s);
+                    s = fmaf(wv.y, xv.y, s);
+                    s = fmaf(wv.z, xv.z, s);
+                    s = fmaf(wv.w, xv.w, s);
+                }
+                acc[i][t] = s;
+            }
+        }
+    }
+}
+
+// Team reduction over TS lanes (8, 16, 32 or 64) in a fixed order.
 template <int TS>
 __device__ __forceinline__ float team_sum(float v) {
-    v = xjd::row16_sum(v);
+    v += xjd::dpp<0xB1>(v);
+    v += xjd::dpp<0x4E>(v);
+    v += xjd::dpp<0x141>(v);
+    if (TS >= 16) v += xjd::dpp<0x140>(v);
     if (TS >= 32) v += __shfl_xor(v, 16, 64);
     if (TS >= 64) v += __shfl_xor(v, 32, 64);
     return v;
 }
 
 // -------------------------------------------------------------- kernel --
-// A row group is 256/TS rows, one per TS-lane team. Lanes take chunks
-// c = lane, lane+TS, ...; NPF of them are loaded before any is used, and the
-// first round of the first row group is issued before the LDS prologue so
-// both latencies overlap.
-constexpr int NPF = 5;
-
-template <int T, int TS>
+// A row group is (256/TS) teams x RPT rows; team j owns rows j*RPT ..
+// j*RPT+RPT-1 of the group. The work-group stages the T tokens' prepared
+// activations (digits, scales, sums) in LDS once and then loops over row
+// groups with stride gridDim.x.
+template <int T, int TS, int RPT>
 __global__ __launch_bounds__(256) void gemv_kernel(const GArgs a) {
-    extern __shared__ float lds[];
-    constexpr int NT = 256 / TS;
+    extern __shared__ u32x4 lds_v[];
+    constexpr int NT = 256 / TS, ROWS = NT * RPT;
     __shared__ unsigned long long amax_sh[NT][T];
-    const int K = a.K, KP = kpad(K), K8 = K / 8, nch = K / 32;
+    const int K = a.K;
+    const XqOff o = xq_off(K);
     const int tid = threadIdx.x, team = tid / TS, lane = tid % TS;
-    float *xl = lds, *xs8 = lds + T * KP, *gsc = xs8 + T * K8;
     const int n_rg = a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg;
-
-    auto seg_of = [&](int rg) {
-        int si = 0;
-        while (si + 1 < a.nseg && rg >= a.seg[si + 1].wg0) si++;
-        return si;
-    };
-    auto row_of = [&](const GSeg &sg, int rg) {
-        const int64_t r = (int64_t)(rg - sg.wg0) * NT + team;
-        return r < sg.n_rows ? r : (int64_t)sg.n_rows - 1;
-    };
-
-    Raw raw[NPF];
-    int rg = blockIdx.x;
-    if (rg < n_rg) {   // first round of the first row group, before the prologue
-        const GSeg &sg = a.seg[seg_of(rg)];
-        if (sg.type != XJ_F32) {
-            const int64_t rowblk = row_of(sg, rg) * (sg.type == XJ_Q8_0 ? K / 32 : K / 256);
-#pragma unroll
-            for (int i = 0; i < NPF; i++) {
-                const int c = lane + i * TS;
-                if (c < nch) load_chunk(sg.type, sg.w, sg.nblk, rowblk, c, raw[i]);
-            }
+    {
+        const int n16 = o.v_off >> 4;
+        for (int i = tid; i < T * n16; i += 256) {
+            const int t = i / n16, j = i - t * n16;
+            lds_v[i] = ld16(a.xq + (int64_t)t * o.stride + 16 * j);
         }
     }
-    prologue<T>(a, xl, xs8, gsc, KP, K8);
+    __syncthreads();
+    const uint8_t *xl = (const uint8_t *)lds_v;
 
-    bool first = true;
-    for (; rg < n_rg; rg += gridDim.x) {
-        const GSeg &sg = a.seg[seg_of(rg)];
-        const int64_t row = row_of(sg, rg);
-        const int64_t rowblk = row * (sg.type == XJ_Q8_0 ? K / 32 : K / 256);
-        float acc[T];
+    for (int rg = blockIdx.x; rg < n_rg; rg += gridDim.x) {
+        int si = 0;
+        while (si + 1 < a.nseg && rg >= a.seg[si + 1].wg0) si++;
+        const GSeg &sg = a.seg[si];
+        const int64_t bpr = (sg.type == XJ_Q4_K || sg.type == XJ_Q6_K) ? K / 256 : K / 32;
+        int64_t row[RPT], rb[RPT];
 #pragma unroll
-        for (int t = 0; t < T; t++) acc[t] = 0.f;
-        if (sg.type == XJ_F32) {
-            for (int c = lane; c < nch; c += TS) dot_f32<T>(sg.w, K, row, c, xl, KP, acc);
-        } else {
-            for (int base = 0; base < nch; base += NPF * TS) {
-                if (!first) {
-#pragma unroll
-                    for (int i = 0; i < NPF; i++) {
-                        const int c = base + lane + i * TS;
-                        if (c < nch) load_chunk(sg.type, sg.w, sg.nblk, rowblk, c, raw[i]);
-                    }
-                }
-                first = false;
-#pragma unroll
-                for (int i = 0; i < NPF; i++) {
-                    const int c = base + lane + i * TS;
-                    if (c >= nch) break;
-                    if (sg.type == XJ_Q4_K) dot_q4k<T>(raw[i], c, xl, xs8, KP, K8, acc);
-                    else if (sg.type == XJ_Q6_K) dot_q6k<T>(raw[i], c, xl, xs8, KP, K8, acc);
-                    else dot_q80<T>(raw[i], c, xl, KP, acc);
-                }
-            }
+        for (int i = 0; i < RPT; i++) {
+            const int64_t r = (int64_t)(rg - sg.wg0) * ROWS + team * RPT + i;
+            row[i] = r < sg.n_rows ? r : (int64_t)sg.n_rows - 1;
+            rb[i] = row[i] * bpr;
         }
-        first = false;
+        float acc[RPT][T];
 #pragma unroll
-        for (int t = 0; t < T; t++) acc[t] = team_sum<TS>(acc[t]);
+        for (int i = 0; i < RPT; i++)
+#pragma unroll
+            for (int t = 0; t < T; t++) acc[i][t] = 0.f;
+        if (sg.type == XJ_Q4_K) rows_q4k<T, TS, RPT>(sg.w, rb, K / 64, lane, xl, o.v_off, o, acc);
+        else if (sg.type == XJ_Q6_K) rows_q6k<T, TS, RPT>(sg.w, sg.nblk, rb, K / 64, lane, xl, o.v_off, o, acc);
+        else if (sg.type == XJ_Q8_0) rows_q80<T, TS, RPT>(sg.w, sg.nblk, rb, K / 32, lane, xl, o.v_off, o, acc);
+        else rows_f32<T, TS, RPT>(sg.w, row, K, lane, a.xq, o, acc);
+#pragma unroll
+        for (int i = 0; i < RPT; i++)
+#pragma unroll
+            for (int t = 0; t < T; t++) acc[i][t] = team_sum<TS>(acc[i][t]);
 
-        // epilogue: lane 0 of the team owns the row
-        const int64_t r = (int64_t)(rg - sg.wg0) * NT + team;
+        // epilogue: lane i of the team owns row i of the team's RPT rows
         unsigned long long best[T];
 #pragma unroll
         for (int t = 0; t < T; t++) best[t] = 0ull;
-        if (lane == 0 && r < sg.n_rows) {
+#pragma unroll
+        for (int i = 0; i < RPT; i++) {
+            const int64_t r = (int64_t)(rg - sg.wg0) * ROWS + team * RPT + i;
+            if (lane != i || r >= sg.n_rows) continue;
             if (sg.epi == EPI_CONV) {
                 const int KC = sg.conv_k;
                 float st[8], wc[8];
@@ -364,7 +441,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GArgs a) {
                 for (int k = 0; k < KC; k++) wc[k] = sg.conv_w[r * KC + k];
 #pragma unroll
                 for (int t = 0; t < T; t++) {
-                    const float xv = acc[t];
+                    const float xv = acc[i][t];
                     float s = 0.f;
                     for (int k = 0; k + 1 < KC; k++) s = fmaf(st[k], wc[k], s);
                     s = fmaf(xv, wc[KC - 1], s);
@@ -380,12 +457,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GArgs a) {
 #pragma unroll
                 for (int t = 0; t < T; t++) {
                     float *yp = sg.y + (int64_t)t * sg.ys + r;
-                    *yp = sg.epi == EPI_ADD ? *yp + acc[t] : acc[t];
-                    if (sg.amax) best[t] = xjd::argmax_key(acc[t], (uint32_t)r);
+                    *yp = sg.epi == EPI_ADD ? *yp + acc[i][t] : acc[i][t];
+                    if (sg.amax) best[t] = xjd::argmax_key(acc[i][t], (uint32_t)r);
                 }
             }
         }
         if (sg.amax) {  // uniform per work-group
+            // lanes 0..RPT-1 of each team hold one row's key each: reduce them first
+#pragma unroll
+            for (int t = 0; t < T; t++)
+#pragma unroll
+                for (int off = 1; off < RPT; off <<= 1) {
+                    const unsigned long long q = __shfl_xor(best[t], off, 64);
+                    best[t] = q > best[t] ? q : best[t];
+                }
             if (lane == 0)
 #pragma unroll
                 for (int t = 0; t < T; t++) amax_sh[team][t] = best[t];
@@ -402,75 +487,112 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GArgs a) {
 }
 
 // -------------------------------------------------------------- host side --
-int gemv_team_lanes(int K) {
-    const int nch = K / 32;
-    return nch <= 16 * NPF ? 16 : nch <= 32 * NPF ? 32 : 64;
+static int env_or(const char *k, int d) {
+    const char *v = getenv(k);
+    return v ? atoi(v) : d;
 }
 
-int gemv_rows_per_group(int K) { return 256 / gemv_team_lanes(K); }
-
-static size_t lds_bytes(const GArgs &a, int T) {
-    size_t n = (size_t)T * kpad(a.K) + (size_t)T * (a.K / 8);
-    if (a.pro == PRO_GATED_RMS) n += (size_t)T * (a.K / a.group);
-    return n * 4;
+// Lanes per row: among 8..64, the team that wastes the fewest lane slots with
+// at most five 64-element units per lane (ties: the smaller team). Rows per
+// team: 2 when that still leaves two work-groups per CU, else 1, widening the
+// team while the grid is short of two work-groups per CU.
+GemvPlan gemv_plan(int K, int64_t rows) {
+    const int nu = K / 64 > 0 ? K / 64 : 1;
+    int ts = 64;
+    double best = -1;
+    for (int c = 8; c <= 64; c *= 2) {
+        const int upl = (nu + c - 1) / c;
+        if (upl > 5 && c < 64) continue;
+        const double eff = (double)nu / ((double)c * upl);
+        if (eff > best + 1e-9) { best = eff; ts = c; }
+    }
+    const int64_t want = 2LL * g_cus;
+    int rpt = (rows + 2 * (256 / ts) - 1) / (2 * (256 / ts)) >= want ? 2 : 1;
+    while (rpt == 1 && ts < 64 && (rows + (256 / ts) - 1) / (256 / ts) < want) ts *= 2;
+    const int fts = env_or("XJ_GEMV_TS", 0), frpt = env_or("XJ_GEMV_RPT", 0);
+    if (fts == 8 || fts == 16 || fts == 32 || fts == 64) ts = fts;
+    if (frpt == 1 || frpt == 2) rpt = frpt;
+    return GemvPlan{ts, rpt, 256 / ts * rpt};
 }
 
 int gemv_max_tile(int K) {
-    const size_t per_t = (size_t)(kpad(K) + K / 8 + K / 64) * 4;
+    const int per_t = xq_off(K).v_off;
     int t = (int)(g_lds_max / per_t);
     return t < 1 ? 0 : t > kTileT ? kTileT : t;
 }
 
-template <int T, int TS>
-static hipError_t launch_t(const GArgs &a, hipStream_t st) {
-    const int n_rg = a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg;
-    const int grid = n_rg < g_grid_cap ? n_rg : g_grid_cap;
-    hipLaunchKernelGGL((gemv_kernel<T, TS>), dim3(grid), dim3(256), lds_bytes(a, T), st, a);
+size_t gemv_xq_bytes(int K) { return (size_t)(gemv_max_tile(K) > 0 ? gemv_max_tile(K) : 1) * xq_off(K).stride; }
+
+int prep_launch(const GArgs &a, hipStream_t st) {
+    if (a.T < 1 || a.K < 32 || a.K % 32 || !a.xq) return -1;
+    if (a.pro == PRO_GATED_RMS && (a.group < 1 || a.K % a.group)) return -1;
+    hipLaunchKernelGGL(prep_kernel, dim3((a.K + 255) / 256, a.T), dim3(256), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+template <int T, int TS, int RPT>
+static hipError_t launch_v(const GArgs &a, int grid, hipStream_t st) {
+    hipLaunchKernelGGL((gemv_kernel<T, TS, RPT>), dim3(grid), dim3(256), (size_t)T * xq_off(a.K).v_off, st, a);
     return hipGetLastError();
 }
 
-template <int TS>
-static hipError_t launch_ts(const GArgs &a, hipStream_t st) {
+template <int TS, int RPT>
+static hipError_t launch_t(const GArgs &a, int grid, hipStream_t st) {
     switch (a.T) {
-    case 1: return launch_t<1, TS>(a, st);
-    case 2: return launch_t<2, TS>(a, st);
-    case 3: return launch_t<3, TS>(a, st);
-    case 4: return launch_t<4, TS>(a, st);
-    case 5: return launch_t<5, TS>(a, st);
-    case 6: return launch_t<6, TS>(a, st);
-    case 7: return launch_t<7, TS>(a, st);
-    case 8: return launch_t<8, TS>(a, st);
+    case 1: return launch_v<1, TS, RPT>(a, grid, st);
+    case 2: return launch_v<2, TS, RPT>(a, grid, st);
+    case 3: return launch_v<3, TS, RPT>(a, grid, st);
+    case 4: return launch_v<4, TS, RPT>(a, grid, st);
+    case 5: return launch_v<5, TS, RPT>(a, grid, st);
+    case 6: return launch_v<6, TS, RPT>(a, grid, st);
+    case 7: return launch_v<7, TS, RPT>(a, grid, st);
+    case 8: return launch_v<8, TS, RPT>(a, grid, st);
     default: return hipErrorInvalidValue;
     }
 }
 
+template <int TS>
+static hipError_t launch_ts(const GArgs &a, int grid, int rpt, hipStream_t st) {
+    return rpt == 2 ? launch_t<TS, 2>(a, grid, st) : launch_t<TS, 1>(a, grid, st);
+}
+
 int gemv_launch(const GArgs &a, hipStream_t st) {
-    if (a.T < 1 || a.T > kTileT || a.nseg < 1 || a.nseg > kMaxSeg || a.K % 32) return -1;
-    if (lds_bytes(a, a.T) > (size_t)g_lds_max) return -1;
-    const int rows = gemv_rows_per_group(a.K);
+    if (a.T < 1 || a.T > kTileT || a.nseg < 1 || a.nseg > kMaxSeg || a.K < 32 || a.K % 32 || !a.xq) return -1;
+    if ((size_t)a.T * xq_off(a.K).v_off > (size_t)g_lds_max) return -1;
+    int64_t total = 0;
+    for (int i = 0; i < a.nseg; i++) total += a.seg[i].n_rows;
+    const GemvPlan p = gemv_plan(a.K, total);
     for (int i = 0; i < a.nseg; i++) {
         const GSeg &s = a.seg[i];
         if ((s.type == XJ_Q4_K || s.type == XJ_Q6_K) && a.K % 256) return -1;
         if (s.type != XJ_Q4_K && s.type != XJ_Q6_K && s.type != XJ_Q8_0 && s.type != XJ_F32) return -1;
-        if (s.n_rows < 1 || s.nwg != (s.n_rows + rows - 1) / rows) return -1;
-        if (i > 0 && s.wg0 != a.seg[i - 1].wg0 + a.seg[i - 1].nwg) return -1;
+        if (s.n_rows < 1 || s.nwg != (s.n_rows + p.rows_per_group - 1) / p.rows_per_group) return -1;
+        if (s.wg0 != (i ? a.seg[i - 1].wg0 + a.seg[i - 1].nwg : 0)) return -1;
+        if (s.epi == EPI_CONV && (s.conv_k < 2 || s.conv_k > 8)) return -1;
     }
-    if (a.seg[0].wg0 != 0) return -1;
-    const int ts = gemv_team_lanes(a.K);
-    hipError_t e = ts == 16 ? launch_ts<16>(a, st) : ts == 32 ? launch_ts<32>(a, st) : launch_ts<64>(a, st);
+    const int n_rg = a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg;
+    const int grid = n_rg < g_grid_cap ? n_rg : g_grid_cap;
+    hipError_t e;
+    switch (p.lanes) {
+    case 8: e = launch_ts<8>(a, grid, p.rpt, st); break;
+    case 16: e = launch_ts<16>(a, grid, p.rpt, st); break;
+    case 32: e = launch_ts<32>(a, grid, p.rpt, st); break;
+    default: e = launch_ts<64>(a, grid, p.rpt, st); break;
+    }
     return e == hipSuccess ? 0 : -1;
 }
 
-template <int T, int TS>
-static void raise_lds(int bytes) {
-    (void)hipFuncSetAttribute((const void *)gemv_kernel<T, TS>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+template <int TS, int RPT>
+static void raise_t(int bytes) {
+    const void *f[] = {(const void *)gemv_kernel<1, TS, RPT>, (const void *)gemv_kernel<2, TS, RPT>,
+                       (const void *)gemv_kernel<3, TS, RPT>, (const void *)gemv_kernel<4, TS, RPT>,
+                       (const void *)gemv_kernel<5, TS, RPT>, (const void *)gemv_kernel<6, TS, RPT>,
+                       (const void *)gemv_kernel<7, TS, RPT>, (const void *)gemv_kernel<8, TS, RPT>};
+    for (const void *k : f) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 
 template <int TS>
-static void raise_all(int bytes) {
-    raise_lds<1, TS>(bytes); raise_lds<2, TS>(bytes); raise_lds<3, TS>(bytes); raise_lds<4, TS>(bytes);
-    raise_lds<5, TS>(bytes); raise_lds<6, TS>(bytes); raise_lds<7, TS>(bytes); raise_lds<8, TS>(bytes);
-}
+static void raise_ts(int bytes) { raise_t<TS, 1>(bytes); raise_t<TS, 2>(bytes); }
 
 int gemv_init(char *err, size_t errlen) {
     static bool done = false;
@@ -479,10 +601,13 @@ int gemv_init(char *err, size_t errlen) {
     XJ_CHECK(hipGetDevice(&dev), err, errlen, -1);
     XJ_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), err, errlen, -1);
     if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) lds = 65536;
-    if (cus > 0) g_grid_cap = cus * 8;
+    if (cus > 0) {
+        g_cus = cus;
+        g_grid_cap = cus * env_or("XJ_GEMV_WG_PER_CU", 8);
+    }
     // keep 4 KB for the static reduction buffers
     int want = lds > 65536 ? lds - 4096 : 65536 - 4096;
-    raise_all<16>(want); raise_all<32>(want); raise_all<64>(want);
+    raise_ts<8>(want); raise_ts<16>(want); raise_ts<32>(want); raise_ts<64>(want);
     (void)hipGetLastError();
     g_lds_max = want;
     done = true;

@@ -45,12 +45,38 @@ struct GSeg {
     unsigned long long *amax;
 };
 
+// Prepared activations, written once per GEMV launch by the prep kernel and
+// staged in LDS by every GEMV work-group. Per token, for each 32-element group
+// g of the K inputs (v = the activation after the prologue):
+//   dig [G][3][32] int8   balanced base-128 digits a, b, c of
+//                         X = rint(v * 2^(20 - E_g)) = a*2^14 + b*2^7 + c,
+//                         |X| <= 2^20, |a| <= 64, b, c in [-64, 63]
+//   f   [G] float         2^(E_g - 20), where max|v| over the group < 2^E_g
+//   sx  [2G] int32        sum of X over each 16-element half of the group
+//   v   [K] float         v itself (read by F32 rows only)
+// Integer dot products of quantized weights with X are exact in 32 bits for
+// every block type, so sub-block sums do not depend on the summation order.
+struct XqOff {
+    int G, f_off, sx_off, v_off, stride;   // bytes; v_off = the LDS bytes per token
+};
+__host__ __device__ inline XqOff xq_off(int K) {
+    XqOff o;
+    o.G = K / 32;
+    o.f_off = o.G * 96;
+    o.sx_off = o.f_off + ((o.G * 4 + 15) & ~15);
+    o.v_off = o.sx_off + ((o.G * 8 + 15) & ~15);
+    o.stride = (o.v_off + K * 4 + 255) & ~255;
+    return o;
+}
+
 struct GArgs {
+    // prologue inputs (read by the prep kernel)
     const float *x;  int32_t xs;   // input rows x[t * xs + k]
     const float *x2; int32_t x2s;  // second input (SwiGLU up, gated-RMS z)
-    int32_t K, T;
     int32_t pro;
     const float *pro_w; float eps; int32_t group;
+    uint8_t *xq;                   // prepared activations [T][xq_off(K).stride]
+    int32_t K, T;
     int32_t t0;                    // absolute index of token 0 of this tile (checkpoints)
     int32_t keep_n;                // conv checkpoints for absolute tokens t < keep_n
     int32_t *inc_ptr; int32_t inc_by;
@@ -58,13 +84,23 @@ struct GArgs {
     GSeg seg[kMaxSeg];
 };
 
-// One GEMV launch (T <= kTileT) over all segments. Segment i covers row
-// groups [wg0, wg0+nwg) with nwg = ceil(n_rows / gemv_rows_per_group(K)).
+// Launch plan of one GEMV over `rows` output rows of inner size K: a team of
+// `lanes` lanes per row, `rpt` rows per team, `rows_per_group` rows per
+// 256-thread work-group. The plan depends on (K, rows) only, never on T.
+struct GemvPlan {
+    int lanes, rpt, rows_per_group;
+};
+GemvPlan gemv_plan(int K, int64_t rows);
+
+// prep kernel: xq for the T tokens of a tile (grid ceil(K/256) x T)
+int prep_launch(const GArgs &a, hipStream_t st);
+// One GEMV launch (T <= kTileT) over all segments, reading a.xq. Segment i
+// covers row groups [wg0, wg0+nwg) with nwg = ceil(n_rows / rows_per_group)
+// of gemv_plan(K, total rows of all segments).
 int gemv_launch(const GArgs &a, hipStream_t st);
-int gemv_team_lanes(int K);        // lanes per row: 16, 32 or 64
-int gemv_rows_per_group(int K);    // rows per row group (256 / lanes)
 int gemv_init(char *err, size_t errlen);       // raise the dynamic-LDS limit once
 int gemv_max_tile(int K);                       // largest T tile whose activations fit in LDS
+size_t gemv_xq_bytes(int K);                    // xq bytes for the largest tile of this K
 
 // Repack a GGUF tensor into the device layout. dst must hold `bytes` =
 // n_rows * row_bytes(type, k); src is host memory in GGUF layout.

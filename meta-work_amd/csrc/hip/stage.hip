@@ -62,6 +62,7 @@ struct HStage {
     unsigned long long *amax = nullptr;
     int head_nwg = 0;
     int32_t *npast = nullptr;
+    uint8_t *xq = nullptr;           // prepared GEMV activations (largest tile of any K)
     float *inv_freq = nullptr;
     float *h_x = nullptr;            // pinned staging [max_batch][n_embd]
     int32_t *h_i = nullptr;          // pinned scalar
@@ -127,7 +128,7 @@ bool upload_f32(HStage *S, const xj_w &w, const float **out, char *err, size_t e
 // the activations read (x, and x2 for SwiGLU / gated RMSNorm), the outputs
 // written, and the outputs read back for a residual add.
 double gemv_algo_bytes(const GArgs &a, int T) {
-    double b = (double)T * a.K * 4 * (a.x2 ? 2 : 1);
+    double b = (double)T * xq_off(a.K).v_off;
     for (int i = 0; i < a.nseg; i++) {
         const GSeg &s = a.seg[i];
         b += (double)s.n_rows * xj_row_bytes(s.type, a.K) + (double)T * s.n_rows * 4 * (s.epi == EPI_ADD ? 2 : 1);
@@ -135,35 +136,47 @@ double gemv_algo_bytes(const GArgs &a, int T) {
     return b;
 }
 
-// Profiling mode: the GEMV launches of a decode step only, with every
-// epilogue turned into a plain store into scratch so no model state changes.
+// Profiling mode: the GEMV launches of a decode step only (the prep launches
+// are left out; the prepared activations of the last real step stay in xq),
+// with every epilogue turned into a plain store into scratch so no model
+// state changes.
 struct Profile {
     float *sink = nullptr;
     double bytes = 0;
     int launches = 0;
 };
 
+// One fused GEMV: segments sharing the input, a prologue (prep kernel) and
+// the GEMV itself, tiled over T.
 struct Gemv {
     GArgs a{};
     Profile *prof = nullptr;
-    explicit Gemv(Profile *p = nullptr) : prof(p) {}
+    explicit Gemv(uint8_t *xq, Profile *p = nullptr) : prof(p) { a.xq = xq; }
     Gemv &seg(const DevW &w, float *y, int ys, int epi) {
         GSeg &s = a.seg[a.nseg];
         s = GSeg{};
         s.w = w.p; s.type = w.type; s.n_rows = (int32_t)w.n_rows;
-        s.wg0 = a.nseg ? a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg : 0;
-        const int rows = gemv_rows_per_group((int)w.k);
-        s.nwg = (int32_t)((w.n_rows + rows - 1) / rows);
         s.nblk = xjd::dev_nblk(w.type, w.n_rows, w.k);
         s.y = y; s.ys = ys; s.epi = epi;
         a.K = (int32_t)w.k;
         a.nseg++;
         return *this;
     }
+    // work-group ranges of the segments under the launch plan for (K, all rows)
+    void place() {
+        int64_t total = 0;
+        for (int i = 0; i < a.nseg; i++) total += a.seg[i].n_rows;
+        const int rows = gemv_plan(a.K, total).rows_per_group;
+        for (int i = 0; i < a.nseg; i++) {
+            a.seg[i].wg0 = i ? a.seg[i - 1].wg0 + a.seg[i - 1].nwg : 0;
+            a.seg[i].nwg = (int32_t)((a.seg[i].n_rows + rows - 1) / rows);
+        }
+    }
     // Run over T tokens in tiles that fit LDS; row results do not depend on the tiling.
     int run(int T, hipStream_t st) {
         const int tile = gemv_max_tile(a.K);
-        if (tile < 1) return -1;
+        if (tile < 1 || !a.xq) return -1;
+        place();
         if (prof) {
             prof->bytes += gemv_algo_bytes(a, T);
             prof->launches += (T + tile - 1) / tile;
@@ -185,6 +198,7 @@ struct Gemv {
                 if (a.seg[i].amax) b.seg[i].amax = a.seg[i].amax + (int64_t)t0 * a.seg[i].nwg;
             }
             if (t0 + b.T < T) b.inc_ptr = nullptr;
+            if (!prof && prep_launch(b, st)) return -1;
             if (gemv_launch(b, st)) return -1;
         }
         return 0;
@@ -199,7 +213,7 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
     const int E = hp.n_embd, FF = hp.n_ff;
     if (L.rec) {
         const int CD = hp.conv_dim, DI = hp.d_inner, Hv = hp.h_v;
-        Gemv p(pf);
+        Gemv p(S->xq, pf);
         p.a.x = x; p.a.xs = E; p.a.pro = PRO_RMS; p.a.pro_w = L.attn_norm; p.a.eps = hp.eps; p.a.keep_n = keep_n;
         p.seg(L.ssm_qkv, S->qkv, CD, EPI_CONV).seg(L.ssm_gate, S->z, DI, EPI_STORE)
          .seg(L.ssm_beta, S->beta, Hv, EPI_STORE).seg(L.ssm_alpha, S->alpha, Hv, EPI_STORE);
@@ -213,14 +227,14 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
         d.T = T; d.Hk = hp.h_k; d.Hv = Hv; d.S = hp.s_k; d.keep_n = keep_n; d.eps = hp.eps;
         d.qscale = 1.0f / sqrtf((float)hp.s_k);
         if (!pf && delta_launch(d, st)) return -1;
-        Gemv q(pf);
+        Gemv q(S->xq, pf);
         q.a.x = S->o; q.a.xs = DI; q.a.x2 = S->z; q.a.x2s = DI; q.a.pro = PRO_GATED_RMS;
         q.a.pro_w = L.ssm_norm; q.a.eps = hp.eps; q.a.group = hp.s_k;
         q.seg(L.ssm_out, x, E, EPI_ADD);
         if (q.run(T, st)) return -1;
     } else {
         const int D = hp.head_dim, Hq = hp.n_head, Hkv = hp.n_head_kv, nq = 2 * Hq * D, nk = Hkv * D;
-        Gemv p(pf);
+        Gemv p(S->xq, pf);
         p.a.x = x; p.a.xs = E; p.a.pro = PRO_RMS; p.a.pro_w = L.attn_norm; p.a.eps = hp.eps;
         AttnArgs at{};
         if (L.wqkv.p) {
@@ -239,16 +253,16 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
         at.n_split = attn_splits(S->s.n_ctx);
         at.eps = hp.eps; at.scale = 1.0f / sqrtf((float)D);
         if (!pf && attn_launch(at, st)) return -1;
-        Gemv q(pf);
+        Gemv q(S->xq, pf);
         q.a.x = S->o; q.a.xs = Hq * D; q.a.pro = PRO_NONE;
         q.seg(L.wo, x, E, EPI_ADD);
         if (q.run(T, st)) return -1;
     }
-    Gemv f(pf);
+    Gemv f(S->xq, pf);
     f.a.x = x; f.a.xs = E; f.a.pro = PRO_RMS; f.a.pro_w = L.post_norm; f.a.eps = hp.eps;
     f.seg(L.ffn_gate, S->g, FF, EPI_STORE).seg(L.ffn_up, S->u, FF, EPI_STORE);
     if (f.run(T, st)) return -1;
-    Gemv dn(pf);
+    Gemv dn(S->xq, pf);
     dn.a.x = S->g; dn.a.xs = FF; dn.a.x2 = S->u; dn.a.x2s = FF; dn.a.pro = PRO_SWIGLU;
     dn.a.inc_ptr = inc; dn.a.inc_by = T;
     dn.seg(L.ffn_down, x, E, EPI_ADD);
@@ -264,7 +278,7 @@ int enqueue_layers(HStage *S, float *x, int T, int keep_n, bool inc, hipStream_t
 // logits[t] = output . rmsnorm(x[t]) * output_norm; greedy partial keys into S->amax
 int enqueue_head(HStage *S, const float *x, int T, float *logits, hipStream_t st) {
     const xj_hparams &hp = S->s.m->hp;
-    Gemv h;
+    Gemv h(S->xq);
     h.a.x = x; h.a.xs = hp.n_embd; h.a.pro = PRO_RMS; h.a.pro_w = S->out_norm; h.a.eps = hp.eps;
     h.seg(S->output, logits, (int)S->output.n_rows, EPI_STORE);
     h.a.seg[0].amax = S->amax;
@@ -572,6 +586,13 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
     S->u = dalloc<float>(S, mb * sf, err, errlen);
     S->scores = dalloc<float>(S, mb * hp.n_head * (size_t)attn_splits(n_ctx) * (hp.head_dim + 2), err, errlen);
     S->npast = dalloc<int32_t>(S, 1, err, errlen);
+    {
+        size_t xb = gemv_xq_bytes(hp.n_embd);
+        for (int K : {hp.d_inner, hp.n_head * hp.head_dim, hp.n_ff})
+            if (K >= 32 && gemv_xq_bytes(K) > xb) xb = gemv_xq_bytes(K);
+        S->xq = dalloc<uint8_t>(S, xb, err, errlen);
+        if (!S->xq) return fail();
+    }
     const int half = hp.n_rot / 2 > 0 ? hp.n_rot / 2 : 1;
     S->inv_freq = dalloc<float>(S, half, err, errlen);
     if (!S->x || !S->qkv || !S->kb || !S->vb || !S->z || !S->beta || !S->alpha || !S->o || !S->g || !S->u ||
@@ -579,7 +600,7 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
         return fail();
     if (has_head) {
         S->logits = dalloc<float>(S, mb * (size_t)S->output.n_rows, err, errlen);
-        const int rows = gemv_rows_per_group((int)S->output.k);
+        const int rows = gemv_plan((int)S->output.k, S->output.n_rows).rows_per_group;
         S->head_nwg = (int)((S->output.n_rows + rows - 1) / rows);
         S->amax = dalloc<unsigned long long>(S, mb * (size_t)S->head_nwg, err, errlen);
         if (!S->logits || !S->amax) return fail();
@@ -593,7 +614,8 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
     XJ_CHECK(hipHostMalloc((void **)&S->h_i, 64, hipHostMallocDefault), err, errlen, fail());
     hip_reset(s);
     char note[160];
-    snprintf(note, sizeof note, "gemv lanes/row %d (K=n_embd), %.0f MB weights in HBM", gemv_team_lanes(hp.n_embd),
+    const GemvPlan pe = gemv_plan(hp.n_embd, hp.n_ff);
+    snprintf(note, sizeof note, "gemv K=n_embd: %d lanes x %d rows per team, %.0f MB weights in HBM", pe.lanes, pe.rpt,
              S->weight_bytes / 1048576.0);
     g_note = note;
     return s;
@@ -921,7 +943,7 @@ extern "C" int xjh_chain_time_gemv(xjh_chain *c, int iters, double *ms_per_step,
         for (auto *S : c->st)
             for (int il = S->s.l0; il < S->s.l1; il++)
                 if (enqueue_layer(S, il, c->x, 1, 0, nullptr, c->stream, p)) return -1;
-        Gemv h(p);
+        Gemv h(head->xq, p);
         const xj_hparams &hp = head->s.m->hp;
         h.a.x = c->x; h.a.xs = hp.n_embd; h.a.pro = PRO_RMS; h.a.pro_w = head->out_norm; h.a.eps = hp.eps;
         h.seg(head->output, head->logits, (int)head->output.n_rows, EPI_STORE);
@@ -1004,7 +1026,17 @@ static int gemv_enqueue(uint32_t type, const void *dw, int64_t n_rows, int64_t k
                         hipStream_t st) {
     DevW w;
     w.p = (const uint8_t *)dw; w.type = type; w.n_rows = n_rows; w.k = k;
-    Gemv g;
+    static uint8_t *xq = nullptr;   // grown on demand; the per-op entries are synchronous on one stream
+    static size_t xq_cap = 0;
+    const size_t need = gemv_xq_bytes((int)k);
+    if (need > xq_cap) {
+        if (xq) (void)hipFree(xq);
+        xq = nullptr;
+        xq_cap = 0;
+        if (hipMalloc(&xq, need) != hipSuccess) return -1;
+        xq_cap = need;
+    }
+    Gemv g(xq);
     g.a.x = x; g.a.xs = (int32_t)k; g.a.pro = PRO_NONE;
     g.seg(w, y, (int32_t)n_rows, add ? EPI_ADD : EPI_STORE);
     return g.run(T, st);

@@ -196,6 +196,23 @@ def write_model(path, cfg):
     return n
 
 
+def cached_model(cfg, name):
+    """Path of the synthetic model for cfg, written once per machine under
+    $XJ_MODEL_DIR (default /tmp/xj_models) and reused afterwards."""
+    import time
+    d = os.environ.get("XJ_MODEL_DIR", "/tmp/xj_models")
+    os.makedirs(d, exist_ok=True)
+    path = os.path.join(d, f"{name}_{cfg.seed}.gguf")
+    if not os.path.exists(path):
+        t = time.time()
+        tmp = f"{path}.{os.getpid()}.tmp"
+        n = write_model(tmp, cfg)
+        os.replace(tmp, path)
+        import sys
+        print(f"wrote {path} ({n / 1e9:.2f} GB) in {time.time() - t:.1f} s", file=sys.stderr, flush=True)
+    return path
+
+
 def fill_normal(n, seed, std=1.0):
     out = np.empty(n, np.float32)
     lib().xjs_fill_normal(_ptr(out), n, seed, std)

@@ -13,6 +13,8 @@ Outputs (data only, no reference code):
                        (one stage and split 3:8), tokens and top-2 margins
   greedy_0_8b.json     0.8B-shape model, 512-token prompt, 256 greedy steps:
                        reference (fp32 KV) and oracle (fp32 and fp16 KV)
+  greedy_4b.json       4B-shape model, 1024-token prompt, 512 greedy steps:
+                       oracle (fp16 KV) and the reference split 0-15 | 16-31
 The synthetic models are regenerated from (config, seed) by the library's
 writer; each record stores the GGUF size and a checksum to detect drift.
 """
@@ -114,11 +116,40 @@ def gen_m08b():
         json.dump(rec, f)
 
 
+def gen_m4b():
+    """4B-shape model, 1024-token prompt, 512 greedy tokens: oracle with the fp16
+    KV cache (the GPU's parity target) and the reference itself (fp32 KV)."""
+    path = "/tmp/xj_golden_4b.gguf"
+    t = time.time()
+    xp.write_model(path, xp.CONFIG_4B)
+    print(f"4B model written in {time.time() - t:.1f} s", flush=True)
+    cfg = xp.CONFIG_4B
+    prompt = np.random.default_rng(20261107).integers(0, cfg.n_vocab, 1024).astype(np.int32)
+    rec = model_record(path, cfg, "CONFIG_4B")
+    rec["prompt_seed"] = 20261107
+    rec["n_prompt"], rec["n_gen"], rec["n_ctx"], rec["max_batch"] = 1024, 512, 2048, 8
+    m = xp.Model(path)
+    t = time.time()
+    st = orc.CpuStage(m.ptr, 0, cfg.n_layer, 2048, 8, True, kv_f16=True)
+    toks, mg = orc.greedy([st], prompt, 512)
+    st.destroy()
+    rec["oracle_kvf16"] = {"tokens": toks.tolist(), "margins": [float(v) for v in mg]}
+    print(f"oracle kv_f16: {time.time() - t:.1f} s", flush=True)
+    with open(os.path.join(HERE, "greedy_4b.json"), "w") as f:
+        json.dump(rec, f)
+    t = time.time()
+    toks, mg = orc.ref_greedy(path, prompt, 512, split=16, n_ctx=2048, max_batch=8)
+    rec["ref_kvf32_split16"] = {"tokens": toks.tolist(), "margins": [float(v) for v in mg]}
+    print(f"reference (layers 0-15 | 16-31): {time.time() - t:.1f} s", flush=True)
+    with open(os.path.join(HERE, "greedy_4b.json"), "w") as f:
+        json.dump(rec, f)
+
+
 if __name__ == "__main__":
     if not orc.ref_available():
         sys.exit("oracle/_ref/libxjref.so is not built: run `make -C oracle ref` where the reference sources exist")
     what = sys.argv[1:] or ["dequant", "matmul", "tiny", "m08b"]
     for w in what:
         t = time.time()
-        {"dequant": gen_dequant, "matmul": gen_matmul, "tiny": gen_tiny, "m08b": gen_m08b}[w]()
+        {"dequant": gen_dequant, "matmul": gen_matmul, "tiny": gen_tiny, "m08b": gen_m08b, "m4b": gen_m4b}[w]()
         print(f"{w}: {time.time() - t:.1f} s", flush=True)

@@ -1,0 +1,102 @@
+"""Greedy token identity at the real model shapes, against the committed
+oracle runs (tests/golden/greedy_*.json, fp16 KV like the GPU; the fixtures
+also hold the reference's own fp32-KV run, whose agreement is reported).
+
+  * 0.8B shape: 512-token prompt, 256 greedy steps, one stage
+  * 4B shape:   1024-token prompt, 512 greedy steps, layers 0-15 and 16-31 as two
+                stages run in sequence on one GPU (the reference's two-device split)
+  * 4B with the 0.8B model drafting 4 tokens per step: the speculative output
+    equals plain greedy decoding
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import xjpipe as xp
+from conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+
+def fixture(name):
+    path = os.path.join(GOLDEN, name)
+    if not os.path.exists(path):
+        pytest.skip(f"{name} not generated")
+    return json.load(open(path))
+
+
+def check_model(path, rec):
+    assert os.path.getsize(path) == rec["bytes"], "synthetic model drifted from the fixture"
+
+
+def first_divergence(a, b):
+    return next((i for i, (x, y) in enumerate(zip(a, b)) if x != y), None)
+
+
+def test_0_8b_greedy_256_steps():
+    rec = fixture("greedy_0_8b.json")
+    path = xp.cached_model(xp.CONFIG_0_8B, "synth08b")
+    check_model(path, rec)
+    m = xp.Model(path)
+    prompt = np.random.default_rng(rec["prompt_seed"]).integers(0, m.hp.n_vocab, rec["n_prompt"]).astype(np.int32)
+    st = xp.HipStage(m, 0, m.hp.n_layer, rec["n_ctx"], rec["max_batch"], True)
+    ch = xp.Chain([st])
+    toks = np.concatenate([ch.eval(prompt), ch.decode(rec["n_gen"] - 1)]).tolist()
+    want = rec["oracle_kvf16"]["tokens"]
+    div = first_divergence(toks, want)
+    print(f"0.8B: first divergence from the fp16-KV oracle: {div}; "
+          f"from the reference (fp32 KV): {first_divergence(toks, rec['ref_kvf32']['tokens'])}")
+    assert toks == want, f"diverges at step {div} (oracle top-2 margin there {rec['oracle_kvf16']['margins'][div]})"
+    ch.free()
+    st.destroy()
+
+
+def test_4b_two_stage_greedy_512_steps():
+    rec = fixture("greedy_4b.json")
+    path = xp.cached_model(xp.CONFIG_4B, "synth4b")
+    check_model(path, rec)
+    m = xp.Model(path)
+    prompt = np.random.default_rng(rec["prompt_seed"]).integers(0, m.hp.n_vocab, rec["n_prompt"]).astype(np.int32)
+    a = xp.HipStage(m, 0, 16, rec["n_ctx"], rec["max_batch"], False)
+    b = xp.HipStage(m, 16, 32, rec["n_ctx"], rec["max_batch"], True)
+    ch = xp.Chain([a, b])
+    toks = np.concatenate([ch.eval(prompt), ch.decode(rec["n_gen"] - 1)]).tolist()
+    want = rec["oracle_kvf16"]["tokens"]
+    div = first_divergence(toks, want)
+    if "ref_kvf32_split16" in rec:
+        print(f"4B: first divergence from the reference (fp32 KV): {first_divergence(toks, rec['ref_kvf32_split16']['tokens'])}")
+    assert toks == want, f"diverges at step {div} (oracle top-2 margin there {rec['oracle_kvf16']['margins'][div]})"
+    ch.free()
+    a.destroy()
+    b.destroy()
+
+
+@pytest.mark.parametrize("mode", ["draft_0_8b", "oracle_drafts"])
+def test_4b_speculative_with_0_8b_draft(mode):
+    path = xp.cached_model(xp.CONFIG_4B, "synth4b")
+    dpath = xp.cached_model(xp.CONFIG_0_8B, "synth08b")
+    m, dm = xp.Model(path), xp.Model(dpath)
+    prompt = np.random.default_rng(11).integers(0, m.hp.n_vocab, 256).astype(np.int32)
+    n_gen = 96
+    st = xp.HipStage(m, 0, 32, 512, 8, True)
+    ch = xp.Chain([st])
+    plain = np.concatenate([ch.eval(prompt), ch.decode(n_gen - 1)])
+    ch.free()
+    st.destroy()
+    a, b = xp.HipStage(m, 0, 16, 512, 8, False), xp.HipStage(m, 16, 32, 512, 8, True)
+    d = xp.HipStage(dm, 0, dm.hp.n_layer, 512, 8, True)
+    tc, dc = xp.Chain([a, b]), xp.Chain([d])
+    tc.eval(prompt)
+    dc.eval(prompt)
+    out, stats = xp.spec_generate(tc, dc, 4, n_gen, oracle=plain if mode == "oracle_drafts" else None)
+    print(f"{mode}: steps {stats.n_steps}, drafted {stats.n_drafted}, accepted {stats.n_accepted}, "
+          f"{n_gen / (stats.t_total_ms / 1e3):.1f} tok/s")
+    assert out.tolist() == plain.tolist()
+    if mode == "oracle_drafts":
+        assert stats.n_accepted == stats.n_drafted
+    for o in (tc, dc):
+        o.free()
+    for s in (a, b, d):
+        s.destroy()
