@@ -15,10 +15,12 @@
 //                    and unnormalised sum_j e_j v_j (positions in order)
 //   attn_combine     merges the splits with the usual max rescaling, divides
 //                    by the total, applies sigmoid(gate) (xj_cpu.c:128-147:
-//                    the same softmax(qK^T/sqrt(D)) V, reassociated by split).
+//                    the same softmax(qK^T/sqrt(D)) V, reassociated by split)
+//                    and, when asked, writes the wo GEMV's prepared activations.
 // Query rows are [q(D) | gate(D)] per head (xj_cpu.c:118); kv head = h / (H/Hkv).
 #include "common.h"
 #include "kernels.h"
+#include "xq.h"
 
 namespace xjk {
 
@@ -143,7 +145,10 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
     }
     __syncthreads();
     const float *qr = a.qg + (int64_t)t * a.qg_s + (int64_t)h * 2 * D;
-    for (int d = tid; d < D; d += 256) {
+    const int d = tid;   // D <= 256
+    const bool in = d < D;
+    float r = 0.f;
+    if (in) {
         float o = 0.f, M2 = -INFINITY;
         if (ns > 64)   // more splits than cached weights: recompute the maximum
             for (int s = 0; s < ns; s++) M2 = fmaxf(M2, part[(int64_t)s * (D + 2)]);
@@ -151,8 +156,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
             const float ws = ns > 64 ? expf(part[(int64_t)s * (D + 2)] - M2) : w[s];
             o = fmaf(ws, part[(int64_t)s * (D + 2) + 2 + d], o);
         }
-        a.out[(int64_t)t * a.H * D + (int64_t)h * D + d] = o * inv_l * xjd::sigm(qr[D + d]);
+        r = o * inv_l * xjd::sigm(qr[D + d]);
+        a.out[(int64_t)t * a.H * D + (int64_t)h * D + d] = r;
     }
+    // the wo GEMV's prepared activations (no prologue): groups of 32 lie inside the head
+    if (a.xq) xjd::emit_xq(r, h * D + d, in, a.xq + (int64_t)t * xq_off(a.H * D).stride, xq_off(a.H * D));
 }
 
 template <int D>

@@ -7,7 +7,9 @@
 //     S_j <- exp(softplus(alpha + dt) * A) * S_j
 //     delta_j = (v_j - S_j . k) * sigmoid(beta)
 //     S_j <- S_j + k * delta_j,   o_j = (S_j . q) / sqrt(S)
-// The gated RMSNorm of o happens in the ssm_out GEMV prologue.
+// With a.xq set, the last work-group of each head also applies the gated
+// RMSNorm of o (xj_cpu.c:215-217) and writes the ssm_out GEMV's prepared
+// activations, so that GEMV needs no prep launch.
 //
 // Mapping: work-group (hv, 16 value rows); a 16-lane team owns one row j and
 // each lane keeps S/16 consecutive entries of it in registers across all T
@@ -21,6 +23,7 @@
 // (the standalone layer test), q and k used as given.
 #include "common.h"
 #include "kernels.h"
+#include "xq.h"
 
 namespace xjk {
 
@@ -91,11 +94,30 @@ __global__ __launch_bounds__(256) void delta_kernel(const DeltaArgs a) {
         const float eg = expf(g);
         const float vj = row[a.v_off + hv * S + j];
         const float o = rule_step<S>(m, ks, qs, i0, eg, b, vj);
-        if (l16 == 0) a.out[(int64_t)t * a.out_s + hv * S + j] = o * a.qscale;
+        if (l16 == 0) {
+            float *op = a.out + (int64_t)t * a.out_s + hv * S + j;
+            if (a.xq) xjd::store_sys(op, o * a.qscale);   // read by the head's last work-group
+            else *op = o * a.qscale;
+        }
         if (t < a.keep_n) store_row<S>(a.ck + (((int64_t)t * a.Hv + hv) * S + j) * S + i0, m);
         __syncthreads();
     }
     store_row<S>(Mp, m);
+    if (!a.xq) return;
+    // gated RMSNorm tail: the last of the head's S/16 work-groups emits the
+    // ssm_out GEMV's activations norm(o) * norm_w * silu(z) for every token
+    __shared__ int flag_sh;
+    if (!xjd::arrive_last(a.cnt + hv, S / 16, &flag_sh)) return;
+    const XqOff o = xq_off(a.Hv * S);
+    const bool in = tid < S;
+    for (int t = 0; t < a.T; t++) {
+        const float ov = in ? xjd::load_sys(a.out + (int64_t)t * a.out_s + hv * S + tid) : 0.f;
+        const double ss = xjd::block_sum_d((double)ov * ov, red[0]);
+        const float gsc = 1.0f / sqrtf((float)(ss / S) + a.eps);
+        const float v = in ? ov * gsc * a.norm_w[tid] * xjd::silu(a.z[(int64_t)t * a.z_s + hv * S + tid]) : 0.f;
+        xjd::emit_xq(v, hv * S + tid, in, a.xq + (int64_t)t * o.stride, o);
+        __syncthreads();
+    }
 }
 
 template <int S>
@@ -121,6 +143,7 @@ __global__ __launch_bounds__(256) void delta_rec_kernel(int H, int T, const floa
 }
 
 int delta_launch(const DeltaArgs &a, hipStream_t st) {
+    if (a.xq && (!a.cnt || !a.z || !a.norm_w)) return -1;
     if (a.S == 128) hipLaunchKernelGGL(delta_kernel<128>, dim3(a.Hv, 128 / 16), dim3(256), 0, st, a);
     else if (a.S == 64) hipLaunchKernelGGL(delta_kernel<64>, dim3(a.Hv, 64 / 16), dim3(256), 0, st, a);
     else return -1;

@@ -53,16 +53,6 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
-__device__ __forceinline__ int row16_sum_i(int v) {
-    v += dpp_i<0xB1>(v);
-    v += dpp_i<0x4E>(v);
-    v += dpp_i<0x141>(v);
-    v += dpp_i<0x140>(v);
-    return v;
-}
-
 __device__ __forceinline__ u32x4 ld16(const uint8_t *p) { return *(const u32x4 *)p; }
 __device__ __forceinline__ u32x4 lds16(const uint8_t *p) { return *(const u32x4 *)p; }
 
@@ -107,28 +97,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const GArgs a) {
     } else {
         if (in) v = x[k];
     }
-    // group exponent: max|v| over the 32 lanes of the group < 2^E
-    float m = fabsf(v);
-    m = xjd::row16_max(m);
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    int E = 0;
-    (void)frexpf(m, &E);
-    if (E < -100) E = -100;
-    const int X = (int)rintf(v * ldexpf(1.0f, 20 - E));
-    const int c = ((X + 64) & 127) - 64;
-    const int X1 = (X - c) / 128;
-    const int b = ((X1 + 64) & 127) - 64;
-    const int a8 = (X1 - b) / 128;
-    const int sx = row16_sum_i(X);
-    if (!in) return;
-    uint8_t *dst = a.xq + (int64_t)t * o.stride;
-    const int g = k >> 5, l = k & 31;
-    dst[g * 96 + l] = (uint8_t)(int8_t)a8;
-    dst[g * 96 + 32 + l] = (uint8_t)(int8_t)b;
-    dst[g * 96 + 64 + l] = (uint8_t)(int8_t)c;
-    if (l == 0) ((float *)(dst + o.f_off))[g] = ldexpf(1.0f, E - 20);
-    if ((k & 15) == 0) ((int *)(dst + o.sx_off))[k >> 4] = sx;
-    ((float *)(dst + o.v_off))[k] = v;
+    xjd::emit_xq(v, k, in, a.xq + (int64_t)t * o.stride, o);
 }
 
 // -------------------------------------------------------- unit kernels --
@@ -283,41 +252,58 @@ __device__ __forceinline__ void unit_q80(const u32x4 (&qa)[RPT], const u32x4 (&q
 }
 
 // ---------------------------------------------------------- row loops --
-template <int T, int TS, int RPT>
-__device__ __forceinline__ void rows_q4k(const uint8_t *__restrict__ W, const int64_t (&rb)[RPT], int nu, int lane,
-                                         const uint8_t *xl, int ldsT, const XqOff &o, float (&acc)[RPT][T]) {
-    for (int u = lane; u < nu; u += TS) {
-        u32x4 h[RPT], q0[RPT], q1[RPT];
-#pragma unroll
-        for (int i = 0; i < RPT; i++) {
-            const uint8_t *blk = W + (rb[i] + (u >> 2)) * 144;
-            h[i] = ld16(blk);
-            q0[i] = ld16(blk + 16 + 32 * (u & 3));
-            q1[i] = ld16(blk + 32 + 32 * (u & 3));
-        }
-        unit_q4k<T, RPT>(h, q0, q1, u, xl, ldsT, o, acc);
-    }
+// Raw bytes of one 64-element unit of a Q4_K or Q6_K row:
+//   Q4_K  a = block header (d|dmin, 12 scale bytes), b, c = the pair's 32 nibble bytes
+//   Q6_K  a, b = ql columns (+0, +32), c = qh column, e = the half's 8 scales, f = d
+struct RawU {
+    u32x4 a, b, c;
+    u32x2 e;
+    uint32_t f;
+};
+
+// The same five loads for every type, addresses chosen without branches: a
+// load whose result reaches a register through a control-flow merge has to
+// complete before the merge, which would serialise the prefetch. Q4_K
+// re-reads header bytes for e and f, other types read the row's first bytes;
+// the extra values are ignored.
+__device__ __forceinline__ RawU load_unit(uint32_t type, const uint8_t *__restrict__ W, int64_t nblk, int64_t rb, int u) {
+    const bool q4 = type == XJ_Q4_K, q6 = type == XJ_Q6_K;
+    const int h = (u >> 1) & 1, hl = u & 1;
+    const int64_t b = rb + (u >> 2);
+    const uint8_t *blk = W + b * 144, *ql = W + b * 128 + 64 * h + 16 * hl, *w0 = W + rb * 32;
+    const uint8_t *pa = q4 ? blk : q6 ? ql : w0;
+    const uint8_t *pb = q4 ? blk + 16 + 32 * (u & 3) : q6 ? ql + 32 : w0;
+    const uint8_t *pc = q4 ? blk + 32 + 32 * (u & 3) : q6 ? W + nblk * 128 + b * 64 + 32 * h + 16 * hl : w0;
+    const uint8_t *pe = q6 ? W + nblk * 192 + b * 16 + 8 * h : pa;
+    const uint8_t *pf = q6 ? W + nblk * 208 + b * 2 : pa;
+    RawU r;
+    r.a = ld16(pa);
+    r.b = ld16(pb);
+    r.c = ld16(pc);
+    r.e = *(const u32x2 *)pe;
+    r.f = *(const uint16_t *)pf;
+    return r;
 }
 
-template <int T, int TS, int RPT>
-__device__ __forceinline__ void rows_q6k(const uint8_t *__restrict__ W, int64_t nblk, const int64_t (&rb)[RPT], int nu,
-                                         int lane, const uint8_t *xl, int ldsT, const XqOff &o, float (&acc)[RPT][T]) {
+// Q4_K / Q6_K rows: the lane's units u = lane, lane + TS, ... with the next
+// unit's loads in flight while the current one is computed; `cur` holds unit
+// `lane` on entry (loaded early by the caller).
+template <int T, int TS>
+__device__ __forceinline__ void rows_kq(uint32_t type, const uint8_t *__restrict__ W, int64_t nblk, int64_t rb, int nu,
+                                        int lane, RawU cur, const uint8_t *xl, int ldsT, const XqOff &o,
+                                        float (&acc)[1][T]) {
     for (int u = lane; u < nu; u += TS) {
-        u32x4 l0[RPT], l1[RPT], qh[RPT];
-        u32x2 sc[RPT];
-        uint32_t dd[RPT];
-        const int h = (u >> 1) & 1, hl = u & 1;
-#pragma unroll
-        for (int i = 0; i < RPT; i++) {
-            const int64_t g = rb[i] + (u >> 2);
-            const uint8_t *ql = W + g * 128 + 64 * h + 16 * hl;
-            l0[i] = ld16(ql);
-            l1[i] = ld16(ql + 32);
-            qh[i] = ld16(W + nblk * 128 + g * 64 + 32 * h + 16 * hl);
-            sc[i] = *(const u32x2 *)(W + nblk * 192 + g * 16 + 8 * h);
-            dd[i] = *(const uint16_t *)(W + nblk * 208 + g * 2);
+        const RawU nxt = load_unit(type, W, nblk, rb, u + TS < nu ? u + TS : u);
+        if (type == XJ_Q4_K) {
+            const u32x4 h[1] = {cur.a}, q0[1] = {cur.b}, q1[1] = {cur.c};
+            unit_q4k<T, 1>(h, q0, q1, u, xl, ldsT, o, acc);
+        } else {
+            const u32x4 l0[1] = {cur.a}, l1[1] = {cur.b}, qh[1] = {cur.c};
+            const u32x2 sc[1] = {cur.e};
+            const uint32_t dd[1] = {cur.f};
+            unit_q6k<T, 1>(l0, l1, qh, sc, dd, u, xl, ldsT, o, acc);
         }
-        unit_q6k<T, RPT>(l0, l1, qh, sc, dd, u, xl, ldsT, o, acc);
+        cur = nxt;
     }
 }
 
@@ -376,112 +362,199 @@ __device__ __forceinline__ float team_sum(float v) {
     return v;
 }
 
-// -------------------------------------------------------------- kernel --
-// A row group is (256/TS) teams x RPT rows; team j owns rows j*RPT ..
-// j*RPT+RPT-1 of the group. The work-group stages the T tokens' prepared
-// activations (digits, scales, sums) in LDS once and then loops over row
-// groups with stride gridDim.x.
+__device__ __forceinline__ int seg_of(const GArgs &a, int rg) {
+    int si = 0;
+    while (si + 1 < a.nseg && rg >= a.seg[si + 1].wg0) si++;
+    return si;
+}
+
+// Team-reduced results acc[i][t] of rows (rg - wg0) * ROWS + team * RPT + i:
+// lane i of the team stores row i (plain, residual add or conv + SiLU), and
+// the work-group's greedy argmax partial is written when the segment has one.
 template <int T, int TS, int RPT>
-__global__ __launch_bounds__(256) void gemv_kernel(const GArgs a) {
-    extern __shared__ u32x4 lds_v[];
+__device__ __forceinline__ void epilogue(const GArgs &a, const GSeg &sg, int rg, int team, int lane, int tid,
+                                         const float (&acc)[RPT][T], unsigned long long (*amax_sh)[T]) {
     constexpr int NT = 256 / TS, ROWS = NT * RPT;
-    __shared__ unsigned long long amax_sh[NT][T];
-    const int K = a.K;
-    const XqOff o = xq_off(K);
-    const int tid = threadIdx.x, team = tid / TS, lane = tid % TS;
-    const int n_rg = a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg;
-    {
-        const int n16 = o.v_off >> 4;
-        for (int i = tid; i < T * n16; i += 256) {
-            const int t = i / n16, j = i - t * n16;
-            lds_v[i] = ld16(a.xq + (int64_t)t * o.stride + 16 * j);
+    unsigned long long best[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) best[t] = 0ull;
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        const int64_t r = (int64_t)(rg - sg.wg0) * ROWS + team * RPT + i;
+        if (lane != i || r >= sg.n_rows) continue;
+        if (sg.epi == EPI_CONV) {
+            const int KC = sg.conv_k;
+            float st[8], wc[8];
+            for (int k = 0; k + 1 < KC; k++) st[k] = sg.conv_state[r * (KC - 1) + k];
+            for (int k = 0; k < KC; k++) wc[k] = sg.conv_w[r * KC + k];
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+                const float xv = acc[i][t];
+                float s = 0.f;
+                for (int k = 0; k + 1 < KC; k++) s = fmaf(st[k], wc[k], s);
+                s = fmaf(xv, wc[KC - 1], s);
+                for (int k = 0; k + 2 < KC; k++) st[k] = st[k + 1];
+                st[KC - 2] = xv;
+                sg.y[(int64_t)t * sg.ys + r] = xjd::silu(s);
+                const int ta = a.t0 + t;
+                if (ta < a.keep_n)
+                    for (int k = 0; k + 1 < KC; k++) sg.conv_ck[((int64_t)ta * sg.n_rows + r) * (KC - 1) + k] = st[k];
+            }
+            for (int k = 0; k + 1 < KC; k++) sg.conv_state[r * (KC - 1) + k] = st[k];
+        } else {
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+                float *yp = sg.y + (int64_t)t * sg.ys + r;
+                const float yv = sg.epi == EPI_ADD ? *yp + acc[i][t] : acc[i][t];
+                if (a.post.mode != POST_NONE) xjd::store_sys(yp, yv);   // read by this launch's tail
+                else *yp = yv;
+                if (sg.amax) best[t] = xjd::argmax_key(acc[i][t], (uint32_t)r);
+            }
         }
     }
+    if (sg.amax) {  // uniform per work-group
+        // lanes 0..RPT-1 of each team hold one row's key each: reduce them first
+#pragma unroll
+        for (int t = 0; t < T; t++)
+#pragma unroll
+            for (int off = 1; off < RPT; off <<= 1) {
+                const unsigned long long q = __shfl_xor(best[t], off, 64);
+                best[t] = q > best[t] ? q : best[t];
+            }
+        if (lane == 0)
+#pragma unroll
+            for (int t = 0; t < T; t++) amax_sh[team][t] = best[t];
+        __syncthreads();
+        if (tid < T) {
+            unsigned long long m = 0ull;
+            for (int j = 0; j < NT; j++) m = amax_sh[j][tid] > m ? amax_sh[j][tid] : m;
+            sg.amax[(int64_t)tid * sg.nwg + (rg - sg.wg0)] = m;
+        }
+        __syncthreads();
+    }
+}
+
+// POST_SWIGLU tail of row group rg: the last of the 2 * 32/ROWS work-groups
+// that wrote gate (segment 0) and up (segment 1) rows of its 32-index group
+// emits silu(gate) * up for the group's T tokens (xj_cpu.c:273).
+template <int T, int ROWS>
+__device__ __forceinline__ void tail_swiglu(const GArgs &a, int rg, int *flag_sh) {
+    const GSeg &g = a.seg[0], &u = a.seg[1];
+    const int j = rg < u.wg0 ? rg - g.wg0 : rg - u.wg0;
+    const int grp = j * ROWS / 32;
+    if (!xjd::arrive_last(a.post.cnt + grp, 2 * (32 / ROWS), flag_sh)) return;
+    const int tid = threadIdx.x, t = tid >> 5, k = grp * 32 + (tid & 31);
+    const bool in = t < T;
+    float v = 0.f;
+    if (in) v = xjd::silu(xjd::load_sys(g.y + (int64_t)t * g.ys + k)) * xjd::load_sys(u.y + (int64_t)t * u.ys + k);
+    const XqOff o = xq_off(g.n_rows);
+    xjd::emit_xq(v, k, in, a.post.xq + (int64_t)(in ? t : 0) * o.stride, o);
+}
+
+// Copy the T tokens' prepared activations (digits, scales, sums) into LDS.
+template <int T>
+__device__ __forceinline__ void stage_xq(const GArgs &a, const XqOff &o, u32x4 *lds_v) {
+    const int n16 = o.v_off >> 4;
+    for (int i = threadIdx.x; i < T * n16; i += 256) {
+        const int t = i / n16, j = i - t * n16;
+        lds_v[i] = ld16(a.xq + (int64_t)t * o.stride + 16 * j);
+    }
+}
+
+// In-work-group prologue for inputs on the residual stream: the prepared
+// activations of RMSNorm(x[t]) * w (xj_cpu.c:56-61: double sum of squares,
+// x * sc * w) for the T tokens, built straight into LDS. Each thread holds
+// its K/256 inputs in registers between the sum and the conversion.
+template <int T>
+__device__ __forceinline__ void prologue_rms(const GArgs &a, const XqOff &o, uint8_t *xl, double *red) {
+    constexpr int NJ = 16;   // K <= 4096 from registers; larger K re-reads x
+    const int K = a.K, tid = threadIdx.x;
+    for (int t = 0; t < T; t++) {
+        const float *x = a.x + (int64_t)t * a.xs;
+        uint8_t *dst = xl + t * o.v_off;
+        if (K <= 256 * NJ) {
+            float xv[NJ], wv[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const int k = tid + 256 * j;
+                xv[j] = k < K ? x[k] : 0.f;
+                wv[j] = k < K ? a.pro_w[k] : 0.f;
+            }
+            double ss = 0;
+#pragma unroll
+            for (int j = 0; j < NJ; j++) ss += (double)xv[j] * xv[j];
+            ss = xjd::block_sum_d(ss, red);
+            const float sc = 1.0f / sqrtf((float)(ss / K) + a.eps);
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const int k = tid + 256 * j;
+                if (256 * j < K) xjd::emit_xq(xv[j] * sc * wv[j], k, k < K, dst, o, false);
+            }
+        } else {
+            double ss = 0;
+            for (int k = tid; k < K; k += 256) ss += (double)x[k] * x[k];
+            ss = xjd::block_sum_d(ss, red);
+            const float sc = 1.0f / sqrtf((float)(ss / K) + a.eps);
+            for (int k0 = 0; k0 < K; k0 += 256) {
+                const int k = k0 + tid;
+                xjd::emit_xq(k < K ? x[k] * sc * a.pro_w[k] : 0.f, k, k < K, dst, o, false);
+            }
+        }
+        __syncthreads();   // red is reused by the next token
+    }
+}
+
+// -------------------------------------------------------------- kernels --
+// A row group is 256/TS rows, one per team of TS lanes. The work-group
+// issues the first unit of its first row group, stages the T tokens'
+// prepared activations in LDS meanwhile, then loops over row groups with
+// stride gridDim.x (prefetching each next group's first unit after the
+// previous group's epilogue).
+template <int T, int TS>
+__global__ __launch_bounds__(256) void gemv_kernel(const GArgs a) {
+    extern __shared__ u32x4 lds_v[];
+    constexpr int NT = 256 / TS;
+    __shared__ unsigned long long amax_sh[NT][T];
+    __shared__ int flag_sh;
+    __shared__ double red_sh[4];
+    const int K = a.K, nu = K / 64;
+    const XqOff o = xq_off(K);
+    const int tid = threadIdx.x, team = tid / TS, lane = tid % TS;
+    const int n_rg = a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg;   // gridDim.x <= n_rg
+    auto row_of = [&](const GSeg &sg, int rg) {
+        const int64_t r = (int64_t)(rg - sg.wg0) * NT + team;
+        return r < sg.n_rows ? r : (int64_t)sg.n_rows - 1;
+    };
+    auto blocks_per_row = [&](uint32_t type) { return (type == XJ_Q4_K || type == XJ_Q6_K) ? K / 256 : K / 32; };
+    auto first_unit = [&](int rg) {
+        const GSeg &sg = a.seg[seg_of(a, rg)];
+        return load_unit(sg.type, sg.w, sg.nblk, row_of(sg, rg) * blocks_per_row(sg.type), lane < nu ? lane : nu - 1);
+    };
+    int rg = blockIdx.x;
+    RawU pre = first_unit(rg);
+    if (a.pro == PRO_RMS) prologue_rms<T>(a, o, (uint8_t *)lds_v, red_sh);
+    else stage_xq<T>(a, o, lds_v);
     __syncthreads();
     const uint8_t *xl = (const uint8_t *)lds_v;
 
-    for (int rg = blockIdx.x; rg < n_rg; rg += gridDim.x) {
-        int si = 0;
-        while (si + 1 < a.nseg && rg >= a.seg[si + 1].wg0) si++;
-        const GSeg &sg = a.seg[si];
-        const int64_t bpr = (sg.type == XJ_Q4_K || sg.type == XJ_Q6_K) ? K / 256 : K / 32;
-        int64_t row[RPT], rb[RPT];
+    for (; rg < n_rg; rg += gridDim.x) {
+        const GSeg &sg = a.seg[seg_of(a, rg)];
+        const int64_t row = row_of(sg, rg), rb = row * blocks_per_row(sg.type);
+        float acc[1][T];
 #pragma unroll
-        for (int i = 0; i < RPT; i++) {
-            const int64_t r = (int64_t)(rg - sg.wg0) * ROWS + team * RPT + i;
-            row[i] = r < sg.n_rows ? r : (int64_t)sg.n_rows - 1;
-            rb[i] = row[i] * bpr;
+        for (int t = 0; t < T; t++) acc[0][t] = 0.f;
+        if (sg.type == XJ_Q4_K || sg.type == XJ_Q6_K) {
+            rows_kq<T, TS>(sg.type, sg.w, sg.nblk, rb, nu, lane, pre, xl, o.v_off, o, acc);
+        } else {
+            const int64_t rr[1] = {row}, rbb[1] = {rb};
+            if (sg.type == XJ_Q8_0) rows_q80<T, TS, 1>(sg.w, sg.nblk, rbb, K / 32, lane, xl, o.v_off, o, acc);
+            else rows_f32<T, TS, 1>(sg.w, rr, K, lane, a.xq, o, acc);
         }
-        float acc[RPT][T];
 #pragma unroll
-        for (int i = 0; i < RPT; i++)
-#pragma unroll
-            for (int t = 0; t < T; t++) acc[i][t] = 0.f;
-        if (sg.type == XJ_Q4_K) rows_q4k<T, TS, RPT>(sg.w, rb, K / 64, lane, xl, o.v_off, o, acc);
-        else if (sg.type == XJ_Q6_K) rows_q6k<T, TS, RPT>(sg.w, sg.nblk, rb, K / 64, lane, xl, o.v_off, o, acc);
-        else if (sg.type == XJ_Q8_0) rows_q80<T, TS, RPT>(sg.w, sg.nblk, rb, K / 32, lane, xl, o.v_off, o, acc);
-        else rows_f32<T, TS, RPT>(sg.w, row, K, lane, a.xq, o, acc);
-#pragma unroll
-        for (int i = 0; i < RPT; i++)
-#pragma unroll
-            for (int t = 0; t < T; t++) acc[i][t] = team_sum<TS>(acc[i][t]);
-
-        // epilogue: lane i of the team owns row i of the team's RPT rows
-        unsigned long long best[T];
-#pragma unroll
-        for (int t = 0; t < T; t++) best[t] = 0ull;
-#pragma unroll
-        for (int i = 0; i < RPT; i++) {
-            const int64_t r = (int64_t)(rg - sg.wg0) * ROWS + team * RPT + i;
-            if (lane != i || r >= sg.n_rows) continue;
-            if (sg.epi == EPI_CONV) {
-                const int KC = sg.conv_k;
-                float st[8], wc[8];
-                for (int k = 0; k + 1 < KC; k++) st[k] = sg.conv_state[r * (KC - 1) + k];
-                for (int k = 0; k < KC; k++) wc[k] = sg.conv_w[r * KC + k];
-#pragma unroll
-                for (int t = 0; t < T; t++) {
-                    const float xv = acc[i][t];
-                    float s = 0.f;
-                    for (int k = 0; k + 1 < KC; k++) s = fmaf(st[k], wc[k], s);
-                    s = fmaf(xv, wc[KC - 1], s);
-                    for (int k = 0; k + 2 < KC; k++) st[k] = st[k + 1];
-                    st[KC - 2] = xv;
-                    sg.y[(int64_t)t * sg.ys + r] = xjd::silu(s);
-                    const int ta = a.t0 + t;
-                    if (ta < a.keep_n)
-                        for (int k = 0; k + 1 < KC; k++) sg.conv_ck[((int64_t)ta * sg.n_rows + r) * (KC - 1) + k] = st[k];
-                }
-                for (int k = 0; k + 1 < KC; k++) sg.conv_state[r * (KC - 1) + k] = st[k];
-            } else {
-#pragma unroll
-                for (int t = 0; t < T; t++) {
-                    float *yp = sg.y + (int64_t)t * sg.ys + r;
-                    *yp = sg.epi == EPI_ADD ? *yp + acc[i][t] : acc[i][t];
-                    if (sg.amax) best[t] = xjd::argmax_key(acc[i][t], (uint32_t)r);
-                }
-            }
-        }
-        if (sg.amax) {  // uniform per work-group
-            // lanes 0..RPT-1 of each team hold one row's key each: reduce them first
-#pragma unroll
-            for (int t = 0; t < T; t++)
-#pragma unroll
-                for (int off = 1; off < RPT; off <<= 1) {
-                    const unsigned long long q = __shfl_xor(best[t], off, 64);
-                    best[t] = q > best[t] ? q : best[t];
-                }
-            if (lane == 0)
-#pragma unroll
-                for (int t = 0; t < T; t++) amax_sh[team][t] = best[t];
-            __syncthreads();
-            if (tid < T) {
-                unsigned long long m = 0ull;
-                for (int j = 0; j < NT; j++) m = amax_sh[j][tid] > m ? amax_sh[j][tid] : m;
-                sg.amax[(int64_t)tid * sg.nwg + (rg - sg.wg0)] = m;
-            }
-            __syncthreads();
-        }
+        for (int t = 0; t < T; t++) acc[0][t] = team_sum<TS>(acc[0][t]);
+        epilogue<T, TS, 1>(a, sg, rg, team, lane, tid, acc, amax_sh);
+        if (a.post.mode == POST_SWIGLU) tail_swiglu<T, NT>(a, rg, &flag_sh);
+        pre = first_unit(rg + (int)gridDim.x < n_rg ? rg + (int)gridDim.x : rg);
     }
     if (a.inc_ptr && blockIdx.x == 0 && tid == 0) *a.inc_ptr += a.inc_by;
 }
@@ -493,9 +566,8 @@ static int env_or(const char *k, int d) {
 }
 
 // Lanes per row: among 8..64, the team that wastes the fewest lane slots with
-// at most five 64-element units per lane (ties: the smaller team). Rows per
-// team: 2 when that still leaves two work-groups per CU, else 1, widening the
-// team while the grid is short of two work-groups per CU.
+// at most five 64-element units per lane (ties: the smaller team), widened
+// while the grid is short of two work-groups per CU. One row per team.
 GemvPlan gemv_plan(int K, int64_t rows) {
     const int nu = K / 64 > 0 ? K / 64 : 1;
     int ts = 64;
@@ -507,12 +579,10 @@ GemvPlan gemv_plan(int K, int64_t rows) {
         if (eff > best + 1e-9) { best = eff; ts = c; }
     }
     const int64_t want = 2LL * g_cus;
-    int rpt = (rows + 2 * (256 / ts) - 1) / (2 * (256 / ts)) >= want ? 2 : 1;
-    while (rpt == 1 && ts < 64 && (rows + (256 / ts) - 1) / (256 / ts) < want) ts *= 2;
-    const int fts = env_or("XJ_GEMV_TS", 0), frpt = env_or("XJ_GEMV_RPT", 0);
+    while (ts < 64 && (rows + (256 / ts) - 1) / (256 / ts) < want) ts *= 2;
+    const int fts = env_or("XJ_GEMV_TS", 0);
     if (fts == 8 || fts == 16 || fts == 32 || fts == 64) ts = fts;
-    if (frpt == 1 || frpt == 2) rpt = frpt;
-    return GemvPlan{ts, rpt, 256 / ts * rpt};
+    return GemvPlan{ts, 1, 256 / ts};
 }
 
 int gemv_max_tile(int K) {
@@ -530,30 +600,25 @@ int prep_launch(const GArgs &a, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-template <int T, int TS, int RPT>
+template <int T, int TS>
 static hipError_t launch_v(const GArgs &a, int grid, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_kernel<T, TS, RPT>), dim3(grid), dim3(256), (size_t)T * xq_off(a.K).v_off, st, a);
+    hipLaunchKernelGGL((gemv_kernel<T, TS>), dim3(grid), dim3(256), (size_t)T * xq_off(a.K).v_off, st, a);
     return hipGetLastError();
 }
 
-template <int TS, int RPT>
-static hipError_t launch_t(const GArgs &a, int grid, hipStream_t st) {
+template <int TS>
+static hipError_t launch_ts(const GArgs &a, int grid, hipStream_t st) {
     switch (a.T) {
-    case 1: return launch_v<1, TS, RPT>(a, grid, st);
-    case 2: return launch_v<2, TS, RPT>(a, grid, st);
-    case 3: return launch_v<3, TS, RPT>(a, grid, st);
-    case 4: return launch_v<4, TS, RPT>(a, grid, st);
-    case 5: return launch_v<5, TS, RPT>(a, grid, st);
-    case 6: return launch_v<6, TS, RPT>(a, grid, st);
-    case 7: return launch_v<7, TS, RPT>(a, grid, st);
-    case 8: return launch_v<8, TS, RPT>(a, grid, st);
+    case 1: return launch_v<1, TS>(a, grid, st);
+    case 2: return launch_v<2, TS>(a, grid, st);
+    case 3: return launch_v<3, TS>(a, grid, st);
+    case 4: return launch_v<4, TS>(a, grid, st);
+    case 5: return launch_v<5, TS>(a, grid, st);
+    case 6: return launch_v<6, TS>(a, grid, st);
+    case 7: return launch_v<7, TS>(a, grid, st);
+    case 8: return launch_v<8, TS>(a, grid, st);
     default: return hipErrorInvalidValue;
     }
-}
-
-template <int TS>
-static hipError_t launch_ts(const GArgs &a, int grid, int rpt, hipStream_t st) {
-    return rpt == 2 ? launch_t<TS, 2>(a, grid, st) : launch_t<TS, 1>(a, grid, st);
 }
 
 int gemv_launch(const GArgs &a, hipStream_t st) {
@@ -566,33 +631,36 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
         const GSeg &s = a.seg[i];
         if ((s.type == XJ_Q4_K || s.type == XJ_Q6_K) && a.K % 256) return -1;
         if (s.type != XJ_Q4_K && s.type != XJ_Q6_K && s.type != XJ_Q8_0 && s.type != XJ_F32) return -1;
+        if (s.type == XJ_F32 && a.pro == PRO_RMS) return -1;   // F32 rows read v from a prep launch's xq
         if (s.n_rows < 1 || s.nwg != (s.n_rows + p.rows_per_group - 1) / p.rows_per_group) return -1;
         if (s.wg0 != (i ? a.seg[i - 1].wg0 + a.seg[i - 1].nwg : 0)) return -1;
         if (s.epi == EPI_CONV && (s.conv_k < 2 || s.conv_k > 8)) return -1;
     }
+    if (a.post.mode != POST_NONE && a.post.mode != POST_SWIGLU) return -1;
+    if (a.pro != PRO_NONE && a.pro != PRO_RMS) return -1;   // other prologues come prepared
+    if (a.pro == PRO_RMS && (!a.x || !a.pro_w)) return -1;
+    if (a.post.mode == POST_SWIGLU &&
+        (!a.post.xq || !a.post.cnt || a.nseg != 2 || a.seg[0].n_rows != a.seg[1].n_rows || a.seg[0].n_rows % 32 ||
+         32 % p.rows_per_group)) return -1;
     const int n_rg = a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg;
     const int grid = n_rg < g_grid_cap ? n_rg : g_grid_cap;
     hipError_t e;
     switch (p.lanes) {
-    case 8: e = launch_ts<8>(a, grid, p.rpt, st); break;
-    case 16: e = launch_ts<16>(a, grid, p.rpt, st); break;
-    case 32: e = launch_ts<32>(a, grid, p.rpt, st); break;
-    default: e = launch_ts<64>(a, grid, p.rpt, st); break;
+    case 8: e = launch_ts<8>(a, grid, st); break;
+    case 16: e = launch_ts<16>(a, grid, st); break;
+    case 32: e = launch_ts<32>(a, grid, st); break;
+    default: e = launch_ts<64>(a, grid, st); break;
     }
     return e == hipSuccess ? 0 : -1;
 }
 
-template <int TS, int RPT>
-static void raise_t(int bytes) {
-    const void *f[] = {(const void *)gemv_kernel<1, TS, RPT>, (const void *)gemv_kernel<2, TS, RPT>,
-                       (const void *)gemv_kernel<3, TS, RPT>, (const void *)gemv_kernel<4, TS, RPT>,
-                       (const void *)gemv_kernel<5, TS, RPT>, (const void *)gemv_kernel<6, TS, RPT>,
-                       (const void *)gemv_kernel<7, TS, RPT>, (const void *)gemv_kernel<8, TS, RPT>};
+template <int TS>
+static void raise_ts(int bytes) {
+    const void *f[] = {(const void *)gemv_kernel<1, TS>, (const void *)gemv_kernel<2, TS>, (const void *)gemv_kernel<3, TS>,
+                       (const void *)gemv_kernel<4, TS>, (const void *)gemv_kernel<5, TS>, (const void *)gemv_kernel<6, TS>,
+                       (const void *)gemv_kernel<7, TS>, (const void *)gemv_kernel<8, TS>};
     for (const void *k : f) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
-
-template <int TS>
-static void raise_ts(int bytes) { raise_t<TS, 1>(bytes); raise_t<TS, 2>(bytes); }
 
 int gemv_init(char *err, size_t errlen) {
     static bool done = false;

@@ -12,6 +12,8 @@
 
 #include <cstdint>
 
+#include "xq.h"
+
 namespace xjk {
 
 constexpr int kMaxSeg = 4;
@@ -45,32 +47,22 @@ struct GSeg {
     unsigned long long *amax;
 };
 
-// Prepared activations, written once per GEMV launch by the prep kernel and
-// staged in LDS by every GEMV work-group. Per token, for each 32-element group
-// g of the K inputs (v = the activation after the prologue):
-//   dig [G][3][32] int8   balanced base-128 digits a, b, c of
-//                         X = rint(v * 2^(20 - E_g)) = a*2^14 + b*2^7 + c,
-//                         |X| <= 2^20, |a| <= 64, b, c in [-64, 63]
-//   f   [G] float         2^(E_g - 20), where max|v| over the group < 2^E_g
-//   sx  [2G] int32        sum of X over each 16-element half of the group
-//   v   [K] float         v itself (read by F32 rows only)
-// Integer dot products of quantized weights with X are exact in 32 bits for
-// every block type, so sub-block sums do not depend on the summation order.
-struct XqOff {
-    int G, f_off, sx_off, v_off, stride;   // bytes; v_off = the LDS bytes per token
+// Tail that leaves the next GEMV's prepared activations (xq.h) behind, so the
+// next GEMV needs no prep launch:
+//   POST_SWIGLU  per 32-index group, the last of the work-groups that wrote
+//                its gate rows (segment 0) and up rows (segment 1) emits
+//                silu(gate) * up
+enum Post { POST_NONE = 0, POST_SWIGLU = 2 };
+struct PostPrep {
+    int32_t mode;
+    uint8_t *xq;                   // token 0 of this tile
+    const float *w; float eps;
+    int32_t *cnt;                  // zero between launches; POST_SWIGLU: one per group
 };
-__host__ __device__ inline XqOff xq_off(int K) {
-    XqOff o;
-    o.G = K / 32;
-    o.f_off = o.G * 96;
-    o.sx_off = o.f_off + ((o.G * 4 + 15) & ~15);
-    o.v_off = o.sx_off + ((o.G * 8 + 15) & ~15);
-    o.stride = (o.v_off + K * 4 + 255) & ~255;
-    return o;
-}
 
 struct GArgs {
-    // prologue inputs (read by the prep kernel)
+    // prologue inputs: read by the prep kernel, or, with pro == PRO_RMS, by
+    // the GEMV itself (each work-group builds the activations in LDS)
     const float *x;  int32_t xs;   // input rows x[t * xs + k]
     const float *x2; int32_t x2s;  // second input (SwiGLU up, gated-RMS z)
     int32_t pro;
@@ -80,6 +72,7 @@ struct GArgs {
     int32_t t0;                    // absolute index of token 0 of this tile (checkpoints)
     int32_t keep_n;                // conv checkpoints for absolute tokens t < keep_n
     int32_t *inc_ptr; int32_t inc_by;
+    PostPrep post;
     int32_t nseg;
     GSeg seg[kMaxSeg];
 };
@@ -121,6 +114,7 @@ struct AttnArgs {
     float *out;                          // [T][H*D]
     int32_t T, H, Hkv, D, n_rot, n_ctx, n_split;
     float eps, scale;
+    uint8_t *xq;                         // optional: prepared activations of out (no prologue)
 };
 int attn_launch(const AttnArgs &a, hipStream_t st);
 int attn_splits(int n_ctx);             // 64-position splits covering n_ctx
@@ -136,6 +130,13 @@ struct DeltaArgs {
     float *out; int32_t out_s;           // [T][Hv*S]
     int32_t T, Hk, Hv, S, keep_n;
     float eps, qscale;
+    // optional tail: per head, the last of its work-groups writes the
+    // prepared activations of norm(out) * norm_w * silu(z) (gated RMSNorm,
+    // xj_cpu.c:215-217) into xq (token stride xq_off(Hv*S).stride)
+    uint8_t *xq;
+    const float *z; int32_t z_s;
+    const float *norm_w;
+    int32_t *cnt;                        // [Hv], zero between launches
 };
 int delta_launch(const DeltaArgs &a, hipStream_t st);
 

@@ -62,7 +62,12 @@ struct HStage {
     unsigned long long *amax = nullptr;
     int head_nwg = 0;
     int32_t *npast = nullptr;
-    uint8_t *xq = nullptr;           // prepared GEMV activations (largest tile of any K)
+    // prepared GEMV activations, max_batch tokens each: inputs of K = n_embd
+    // (attention/DeltaNet in-projections, gate|up, head), d_inner (ssm_out),
+    // n_head*head_dim (wo) and n_ff (down)
+    uint8_t *xq_e = nullptr, *xq_di = nullptr, *xq_att = nullptr, *xq_ff = nullptr;
+    // arrival counters of the producer tails (zero between launches)
+    int32_t *cnt_grp = nullptr, *cnt_head = nullptr;
     float *inv_freq = nullptr;
     float *h_x = nullptr;            // pinned staging [max_batch][n_embd]
     int32_t *h_i = nullptr;          // pinned scalar
@@ -136,21 +141,26 @@ double gemv_algo_bytes(const GArgs &a, int T) {
     return b;
 }
 
-// Profiling mode: the GEMV launches of a decode step only (the prep launches
-// are left out; the prepared activations of the last real step stay in xq),
-// with every epilogue turned into a plain store into scratch so no model
-// state changes.
+// Profiling mode: the GEMV launches of a decode step only (prep, attention
+// and DeltaNet launches are left out), with every epilogue turned into a
+// plain store into scratch so no model state changes; the GEMVs' own
+// activation tails still run (into the xq buffers, which the next real step
+// rewrites before reading).
 struct Profile {
     float *sink = nullptr;
     double bytes = 0;
     int launches = 0;
 };
 
-// One fused GEMV: segments sharing the input, a prologue (prep kernel) and
-// the GEMV itself, tiled over T.
+// One fused GEMV: segments sharing the input, its prepared activations
+// (built by the GEMV's own work-groups for an RMSNorm prologue, else by a
+// prep launch unless `prepared`), an optional tail that leaves the next
+// GEMV's activations behind, tiled over T. Token t of the tile that starts at
+// t0 uses xq + (t0 + t) * stride, so every buffer holds max_batch tokens.
 struct Gemv {
     GArgs a{};
     Profile *prof = nullptr;
+    bool prepared = false;
     explicit Gemv(uint8_t *xq, Profile *p = nullptr) : prof(p) { a.xq = xq; }
     Gemv &seg(const DevW &w, float *y, int ys, int epi) {
         GSeg &s = a.seg[a.nseg];
@@ -160,6 +170,10 @@ struct Gemv {
         s.y = y; s.ys = ys; s.epi = epi;
         a.K = (int32_t)w.k;
         a.nseg++;
+        return *this;
+    }
+    Gemv &post(int mode, uint8_t *xq, int32_t *cnt, const float *w = nullptr, float eps = 0.f) {
+        a.post = PostPrep{mode, xq, w, eps, cnt};
         return *this;
     }
     // work-group ranges of the segments under the launch plan for (K, all rows)
@@ -187,18 +201,28 @@ struct Gemv {
             }
             a.inc_ptr = nullptr;
         }
+        // RMSNorm prologues run inside the GEMV's work-groups (F32 rows need a prep launch's xq)
+        bool inwg = a.pro == PRO_RMS && !prepared;
+        for (int i = 0; i < a.nseg; i++) inwg = inwg && a.seg[i].type != XJ_F32;
+        const int64_t xs_in = xq_off(a.K).stride;
+        const int64_t xs_out = a.post.mode != POST_NONE ? xq_off(a.seg[0].n_rows).stride : 0;
         for (int t0 = 0; t0 < T; t0 += tile) {
             GArgs b = a;
             b.T = T - t0 < tile ? T - t0 : tile;
             b.t0 = a.t0 + t0;
-            b.x = a.x + (int64_t)t0 * a.xs;
+            b.x = a.x ? a.x + (int64_t)t0 * a.xs : nullptr;
             if (a.x2) b.x2 = a.x2 + (int64_t)t0 * a.x2s;
+            b.xq = a.xq + t0 * xs_in;
+            if (a.post.mode != POST_NONE) b.post.xq = a.post.xq + t0 * xs_out;
             for (int i = 0; i < a.nseg; i++) {
                 b.seg[i].y = a.seg[i].y + (int64_t)t0 * a.seg[i].ys;
                 if (a.seg[i].amax) b.seg[i].amax = a.seg[i].amax + (int64_t)t0 * a.seg[i].nwg;
             }
             if (t0 + b.T < T) b.inc_ptr = nullptr;
-            if (!prof && prep_launch(b, st)) return -1;
+            if (!inwg) {
+                if (!prof && !prepared && prep_launch(b, st)) return -1;
+                b.pro = PRO_NONE;   // the GEMV reads xq
+            }
             if (gemv_launch(b, st)) return -1;
         }
         return 0;
@@ -207,14 +231,22 @@ struct Gemv {
 
 // --------------------------------------------------------------- layers --
 
+// Layer il on T tokens of x. The GEMVs that read the residual stream apply
+// their RMSNorm inside their own work-groups; every other prologue is
+// produced by the kernel before its GEMV: the down input by gate|up, the
+// ssm_out input by the DeltaNet kernel, the wo input by attention.
 int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, hipStream_t st, Profile *pf = nullptr) {
     const xj_hparams &hp = S->s.m->hp;
     HLayer &L = S->L[il - S->s.l0];
     const int E = hp.n_embd, FF = hp.n_ff;
+    auto rms_in = [&](Gemv &g, const float *w) {
+        g.a.x = x; g.a.xs = E; g.a.pro = PRO_RMS; g.a.pro_w = w; g.a.eps = hp.eps;
+    };
     if (L.rec) {
         const int CD = hp.conv_dim, DI = hp.d_inner, Hv = hp.h_v;
-        Gemv p(S->xq, pf);
-        p.a.x = x; p.a.xs = E; p.a.pro = PRO_RMS; p.a.pro_w = L.attn_norm; p.a.eps = hp.eps; p.a.keep_n = keep_n;
+        Gemv p(S->xq_e, pf);
+        rms_in(p, L.attn_norm);
+        p.a.keep_n = keep_n;
         p.seg(L.ssm_qkv, S->qkv, CD, EPI_CONV).seg(L.ssm_gate, S->z, DI, EPI_STORE)
          .seg(L.ssm_beta, S->beta, Hv, EPI_STORE).seg(L.ssm_alpha, S->alpha, Hv, EPI_STORE);
         GSeg &cs = p.a.seg[0];
@@ -226,16 +258,16 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
         d.state = L.ssm; d.ck = L.ck_ssm; d.out = S->o; d.out_s = DI;
         d.T = T; d.Hk = hp.h_k; d.Hv = Hv; d.S = hp.s_k; d.keep_n = keep_n; d.eps = hp.eps;
         d.qscale = 1.0f / sqrtf((float)hp.s_k);
+        d.xq = S->xq_di; d.z = S->z; d.z_s = DI; d.norm_w = L.ssm_norm; d.cnt = S->cnt_head;
         if (!pf && delta_launch(d, st)) return -1;
-        Gemv q(S->xq, pf);
-        q.a.x = S->o; q.a.xs = DI; q.a.x2 = S->z; q.a.x2s = DI; q.a.pro = PRO_GATED_RMS;
-        q.a.pro_w = L.ssm_norm; q.a.eps = hp.eps; q.a.group = hp.s_k;
+        Gemv q(S->xq_di, pf);
+        q.prepared = true;
         q.seg(L.ssm_out, x, E, EPI_ADD);
         if (q.run(T, st)) return -1;
     } else {
         const int D = hp.head_dim, Hq = hp.n_head, Hkv = hp.n_head_kv, nq = 2 * Hq * D, nk = Hkv * D;
-        Gemv p(S->xq, pf);
-        p.a.x = x; p.a.xs = E; p.a.pro = PRO_RMS; p.a.pro_w = L.attn_norm; p.a.eps = hp.eps;
+        Gemv p(S->xq_e, pf);
+        rms_in(p, L.attn_norm);
         AttnArgs at{};
         if (L.wqkv.p) {
             p.seg(L.wqkv, S->qkv, nq + 2 * nk, EPI_STORE);
@@ -252,33 +284,34 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
         at.T = T; at.H = Hq; at.Hkv = Hkv; at.D = D; at.n_rot = hp.n_rot; at.n_ctx = S->s.n_ctx;
         at.n_split = attn_splits(S->s.n_ctx);
         at.eps = hp.eps; at.scale = 1.0f / sqrtf((float)D);
+        at.xq = S->xq_att;
         if (!pf && attn_launch(at, st)) return -1;
-        Gemv q(S->xq, pf);
-        q.a.x = S->o; q.a.xs = Hq * D; q.a.pro = PRO_NONE;
+        Gemv q(S->xq_att, pf);
+        q.prepared = true;
         q.seg(L.wo, x, E, EPI_ADD);
         if (q.run(T, st)) return -1;
     }
-    Gemv f(S->xq, pf);
-    f.a.x = x; f.a.xs = E; f.a.pro = PRO_RMS; f.a.pro_w = L.post_norm; f.a.eps = hp.eps;
-    f.seg(L.ffn_gate, S->g, FF, EPI_STORE).seg(L.ffn_up, S->u, FF, EPI_STORE);
+    Gemv f(S->xq_e, pf);
+    rms_in(f, L.post_norm);
+    f.seg(L.ffn_gate, S->g, FF, EPI_STORE).seg(L.ffn_up, S->u, FF, EPI_STORE).post(POST_SWIGLU, S->xq_ff, S->cnt_grp);
     if (f.run(T, st)) return -1;
-    Gemv dn(S->xq, pf);
-    dn.a.x = S->g; dn.a.xs = FF; dn.a.x2 = S->u; dn.a.x2s = FF; dn.a.pro = PRO_SWIGLU;
+    Gemv dn(S->xq_ff, pf);
+    dn.prepared = true;
     dn.a.inc_ptr = inc; dn.a.inc_by = T;
     dn.seg(L.ffn_down, x, E, EPI_ADD);
     return dn.run(T, st);
 }
 
-int enqueue_layers(HStage *S, float *x, int T, int keep_n, bool inc, hipStream_t st) {
+int enqueue_layers(HStage *S, float *x, int T, int keep_n, bool inc, hipStream_t st, Profile *pf = nullptr) {
     for (int il = S->s.l0; il < S->s.l1; il++)
-        if (enqueue_layer(S, il, x, T, keep_n, inc && il + 1 == S->s.l1 ? S->npast : nullptr, st)) return -1;
+        if (enqueue_layer(S, il, x, T, keep_n, inc && il + 1 == S->s.l1 ? S->npast : nullptr, st, pf)) return -1;
     return 0;
 }
 
 // logits[t] = output . rmsnorm(x[t]) * output_norm; greedy partial keys into S->amax
-int enqueue_head(HStage *S, const float *x, int T, float *logits, hipStream_t st) {
+int enqueue_head(HStage *S, const float *x, int T, float *logits, hipStream_t st, Profile *pf = nullptr) {
     const xj_hparams &hp = S->s.m->hp;
-    Gemv h(S->xq);
+    Gemv h(S->xq_e, pf);
     h.a.x = x; h.a.xs = hp.n_embd; h.a.pro = PRO_RMS; h.a.pro_w = S->out_norm; h.a.eps = hp.eps;
     h.seg(S->output, logits, (int)S->output.n_rows, EPI_STORE);
     h.a.seg[0].amax = S->amax;
@@ -587,11 +620,17 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
     S->scores = dalloc<float>(S, mb * hp.n_head * (size_t)attn_splits(n_ctx) * (hp.head_dim + 2), err, errlen);
     S->npast = dalloc<int32_t>(S, 1, err, errlen);
     {
-        size_t xb = gemv_xq_bytes(hp.n_embd);
-        for (int K : {hp.d_inner, hp.n_head * hp.head_dim, hp.n_ff})
-            if (K >= 32 && gemv_xq_bytes(K) > xb) xb = gemv_xq_bytes(K);
-        S->xq = dalloc<uint8_t>(S, xb, err, errlen);
-        if (!S->xq) return fail();
+        auto xqb = [&](int K) { return K >= 32 ? mb * (size_t)xq_off(K).stride : 256; };
+        S->xq_e = dalloc<uint8_t>(S, xqb(hp.n_embd), err, errlen);
+        S->xq_di = dalloc<uint8_t>(S, xqb(hp.d_inner), err, errlen);
+        S->xq_att = dalloc<uint8_t>(S, xqb(hp.n_head * hp.head_dim), err, errlen);
+        S->xq_ff = dalloc<uint8_t>(S, xqb(hp.n_ff), err, errlen);
+        const size_t nc = (size_t)(hp.n_ff / 32) + (size_t)(hp.h_v > 0 ? hp.h_v : 1);
+        int32_t *cnt = dalloc<int32_t>(S, nc, err, errlen);
+        if (!S->xq_e || !S->xq_di || !S->xq_att || !S->xq_ff || !cnt) return fail();
+        XJ_CHECK(hipMemset(cnt, 0, nc * 4), err, errlen, fail());
+        S->cnt_grp = cnt;
+        S->cnt_head = cnt + hp.n_ff / 32;
     }
     const int half = hp.n_rot / 2 > 0 ? hp.n_rot / 2 : 1;
     S->inv_freq = dalloc<float>(S, half, err, errlen);
@@ -741,6 +780,7 @@ extern "C" int xjh_chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nl
         }
         EmbedArgs ea{c->d_tokens, c->st[0]->tok_embd, c->x, T};
         if (embed_launch(ea, c->stream)) { snprintf(err, errlen, "embed launch failed"); return -1; }
+        const bool last = i + T == n;
         for (auto *S : c->st) {
             if (keep) S->s.keep = T;
             int keep_n = 0;
@@ -751,7 +791,6 @@ extern "C" int xjh_chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nl
                 snprintf(err, errlen, "layer launch failed"); S->s.keep = 0; return -1;
             }
         }
-        const bool last = i + T == n;
         if (last && nlog > 0) {
             const int nl = nlog < T ? nlog : T;
             if (enqueue_head(head, c->x + (int64_t)(T - nl) * E, nl, head->logits, c->stream) ||
@@ -773,16 +812,24 @@ extern "C" int xjh_chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nl
     return 0;
 }
 
-static int build_decode_graph(xjh_chain *c, char *err, size_t errlen) {
+// One greedy decode step, entirely on the device: embedding of d_tok, every
+// stage (the last GEMV of each advances its n_past), the head, and the argmax
+// that writes d_tok and appends it to the history.
+static int enqueue_decode_step(xjh_chain *c) {
     HStage *head = c->st.back();
-    if (hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
-        snprintf(err, errlen, "graph capture failed to start"); return -1;
-    }
     EmbedArgs ea{c->d_tok, c->st[0]->tok_embd, c->x, 1};
     int rc = embed_launch(ea, c->stream);
     for (auto *S : c->st) rc = rc ? rc : enqueue_layers(S, c->x, 1, 0, true, c->stream);
     if (!rc) rc = enqueue_head(head, c->x, 1, head->logits, c->stream);
     if (!rc) rc = argmax_finalize_launch(head->amax, head->head_nwg, 1, nullptr, c->d_tok, c->d_hist, c->d_step, c->stream);
+    return rc;
+}
+
+static int build_decode_graph(xjh_chain *c, char *err, size_t errlen) {
+    if (hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        snprintf(err, errlen, "graph capture failed to start"); return -1;
+    }
+    const int rc = enqueue_decode_step(c);
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(c->stream, &g);
     if (rc || e != hipSuccess) { snprintf(err, errlen, "graph capture failed"); if (g) (void)hipGraphDestroy(g); return -1; }
@@ -798,7 +845,10 @@ extern "C" int xjh_chain_decode(xjh_chain *c, int n_steps, int32_t *out, char *e
     if (c->last_tok < 0) { snprintf(err, errlen, "decode needs a previous eval with logits"); return -1; }
     for (auto *S : c->st)
         if (S->s.n_past + n_steps > S->s.n_ctx) { snprintf(err, errlen, "context full (%d)", S->s.n_ctx); return -1; }
-    if (!c->exec && build_decode_graph(c, err, errlen)) return -1;
+    // XJ_DECODE_GRAPH=0 enqueues the same kernels step by step instead of
+    // replaying the captured graph (for tracing tools that do not follow graphs)
+    const bool direct = env_int("XJ_DECODE_GRAPH", 1) == 0;
+    if (!direct && !c->exec && build_decode_graph(c, err, errlen)) return -1;
     double total_ms = 0;
     for (int done = 0; done < n_steps;) {
         const int n = n_steps - done < c->hist_cap ? n_steps - done : c->hist_cap;
@@ -812,7 +862,9 @@ extern "C" int xjh_chain_decode(xjh_chain *c, int n_steps, int32_t *out, char *e
         if (chain_sync(c, err, errlen)) return -1;
         (void)hipEventRecord(c->ev0, c->stream);
         for (int i = 0; i < n; i++)
-            if (hipGraphLaunch(c->exec, c->stream) != hipSuccess) { snprintf(err, errlen, "graph launch failed"); return -1; }
+            if (direct ? enqueue_decode_step(c) != 0 : hipGraphLaunch(c->exec, c->stream) != hipSuccess) {
+                snprintf(err, errlen, "decode step launch failed"); return -1;
+            }
         (void)hipEventRecord(c->ev1, c->stream);
         if (chain_sync(c, err, errlen)) return -1;
         float ms = 0;
@@ -941,13 +993,8 @@ extern "C" int xjh_chain_time_gemv(xjh_chain *c, int iters, double *ms_per_step,
     pf.sink = head->logits;   // [max_batch][n_vocab] floats: larger than any GEMV output
     auto enqueue_step = [&](Profile *p) -> int {
         for (auto *S : c->st)
-            for (int il = S->s.l0; il < S->s.l1; il++)
-                if (enqueue_layer(S, il, c->x, 1, 0, nullptr, c->stream, p)) return -1;
-        Gemv h(head->xq, p);
-        const xj_hparams &hp = head->s.m->hp;
-        h.a.x = c->x; h.a.xs = hp.n_embd; h.a.pro = PRO_RMS; h.a.pro_w = head->out_norm; h.a.eps = hp.eps;
-        h.seg(head->output, head->logits, (int)head->output.n_rows, EPI_STORE);
-        return h.run(1, c->stream);
+            if (enqueue_layers(S, c->x, 1, 0, false, c->stream, p)) return -1;
+        return enqueue_head(head, c->x, 1, head->logits, c->stream, p);
     };
     if (enqueue_step(&pf)) { snprintf(err, errlen, "profile launch failed"); return -1; }   // warm-up, counts bytes
     if (chain_sync(c, err, errlen)) return -1;
@@ -1028,7 +1075,7 @@ static int gemv_enqueue(uint32_t type, const void *dw, int64_t n_rows, int64_t k
     w.p = (const uint8_t *)dw; w.type = type; w.n_rows = n_rows; w.k = k;
     static uint8_t *xq = nullptr;   // grown on demand; the per-op entries are synchronous on one stream
     static size_t xq_cap = 0;
-    const size_t need = gemv_xq_bytes((int)k);
+    const size_t need = (size_t)T * xq_off((int)k).stride;
     if (need > xq_cap) {
         if (xq) (void)hipFree(xq);
         xq = nullptr;

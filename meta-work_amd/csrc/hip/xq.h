@@ -1,0 +1,112 @@
+// Prepared GEMV activations ("xq"), shared by the prep kernel, the producers
+// that emit them directly (GEMV tails, the DeltaNet and attention kernels)
+// and the GEMV that stages them in LDS.
+//
+// Per token, for each 32-element group g of the K inputs (v = the activation
+// after its prologue: RMSNorm, SwiGLU, gated RMSNorm or none):
+//   dig [G][3][32] int8   balanced base-128 digits a, b, c of
+//                         X = rint(v * 2^(20 - E_g)) = a*2^14 + b*2^7 + c,
+//                         |X| <= 2^20, |a| <= 64, b, c in [-64, 63]
+//   f   [G] float         2^(E_g - 20), where max|v| over the group < 2^E_g
+//   sx  [2G] int32        sum of X over each 16-element half of the group
+//   v   [K] float         v itself (read by F32 rows only)
+// Integer dot products of quantized weights with X are exact in 32 bits for
+// every block type, so sub-block sums do not depend on the summation order.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace xjk {
+
+struct XqOff {
+    int G, f_off, sx_off, v_off, stride;   // bytes; v_off = the LDS bytes per token
+};
+__host__ __device__ inline XqOff xq_off(int K) {
+    XqOff o;
+    o.G = K / 32;
+    o.f_off = o.G * 96;
+    o.sx_off = o.f_off + ((o.G * 4 + 15) & ~15);
+    o.v_off = o.sx_off + ((o.G * 8 + 15) & ~15);
+    o.stride = (o.v_off + K * 4 + 255) & ~255;
+    return o;
+}
+
+}  // namespace xjk
+
+#ifdef __HIPCC__
+#include "common.h"
+
+namespace xjd {
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+__device__ __forceinline__ int row16_sum_i(int v) {
+    v += dpp_i<0xB1>(v);
+    v += dpp_i<0x4E>(v);
+    v += dpp_i<0x141>(v);
+    v += dpp_i<0x140>(v);
+    return v;
+}
+
+// Writes element k (value v) of one token's xq at dst. Called by all 64
+// lanes of a wavefront with k = k0 + lane, k0 a multiple of 64, so that each
+// half-wavefront holds one 32-element group; lanes with in == false (k >= K,
+// always whole groups since K % 32 == 0) pass v = 0 and store nothing.
+// dst may be global memory or LDS (with_v = false: the LDS copy has no v).
+__device__ __forceinline__ void emit_xq(float v, int k, bool in, uint8_t *dst, const xjk::XqOff &o, bool with_v = true) {
+    float m = fabsf(v);
+    m = row16_max(m);
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    int E = 0;
+    (void)frexpf(m, &E);
+    if (E < -100) E = -100;
+    const int X = (int)rintf(v * ldexpf(1.0f, 20 - E));
+    const int c = ((X + 64) & 127) - 64;
+    const int X1 = (X - c) / 128;
+    const int b = ((X1 + 64) & 127) - 64;
+    const int a = (X1 - b) / 128;
+    const int sx = row16_sum_i(X);
+    if (!in) return;
+    const int g = k >> 5, l = k & 31;
+    dst[g * 96 + l] = (uint8_t)(int8_t)a;
+    dst[g * 96 + 32 + l] = (uint8_t)(int8_t)b;
+    dst[g * 96 + 64 + l] = (uint8_t)(int8_t)c;
+    if (l == 0) ((float *)(dst + o.f_off))[g] = ldexpf(1.0f, E - 20);
+    if ((k & 15) == 0) ((int *)(dst + o.sx_off))[k >> 4] = sx;
+    if (with_v) ((float *)(dst + o.v_off))[k] = v;
+}
+
+// Cross-work-group hand-off inside one launch. The producers store the
+// values a tail will read with system-scope stores (written through every
+// cache level) and the tail reads them with system-scope loads (which bypass
+// the caches), so no cache write-back or invalidation is needed: a store is
+// complete, and visible to such loads, once the storing thread's vmcnt has
+// drained. The arrival counter itself is a device-scope atomic.
+__device__ __forceinline__ void store_sys(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ float load_sys(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// "The last work-group finishes the job": every thread's earlier stores are
+// drained, then one thread counts the arrival; returns true (to every
+// thread) in the work-group that arrives as number `target`, which also
+// resets the counter for the next launch. Every work-group reaches this point
+// once and none waits for another.
+__device__ __forceinline__ bool arrive_last(int *cnt, int target, int *flag_sh) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int n = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = n == target - 1;
+        if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag_sh = last;
+    }
+    __syncthreads();
+    return *flag_sh != 0;
+}
+
+}  // namespace xjd
+#endif

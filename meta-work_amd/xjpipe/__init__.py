@@ -19,7 +19,8 @@ import numpy as np
 from .configs import CONFIG_0_8B, CONFIG_4B, TINY, TINY_DRAFT, SynthConfig  # noqa: F401
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.normpath(os.path.join(HERE, "..", "_build", "libxjhip.so"))
+# XJ_HIP_LIB selects another build of the same library (e.g. a tuning variant)
+LIB_PATH = os.environ.get("XJ_HIP_LIB") or os.path.normpath(os.path.join(HERE, "..", "_build", "libxjhip.so"))
 
 # ggml type ids (include/xj_abi.h)
 F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 8, 12, 13, 14, 30
