@@ -11,6 +11,8 @@ Also reported, on the same run:
                 algorithmic bytes of the GEMV launches of one step divided by
                 their GPU time, measured with HIP events on the chain's stream
                 by replaying exactly those launches (weights 2.6 GB: cold).
+                traffic = measured HBM bytes per GEMV launch from the committed
+                counter summary profiles/traffic_gemv_4b_decode.json, if present.
   cpu_baseline  the reference CPU path compiled from the reference sources
                 (oracle/_ref, OpenMP on this host's cores) on a bounded sample
                 of the same workload; the oracle's C restatement if that
@@ -18,7 +20,10 @@ Also reported, on the same run:
   gemv_*        stand-alone cold-cache GEMV legs (Q4_K / Q6_K LM-head shapes).
   decode_0_8b   the same measurement on the 0.8B-shape model.
 
-usage: python bench.py [--gpus 1] [--steps 512] [--warmup 16] [--no-cpu]
+usage: python bench.py [--gpus 1] [--steps 512] [--warmup 16] [--no-cpu] [--no-extra]
+                       [--copy-calibration MB]
+--copy-calibration MB first copies MB megabytes device-to-device (one runtime
+copy kernel of known size, to calibrate the HBM byte counters of a profiler run).
 """
 import argparse
 import json
@@ -112,6 +117,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the 0.8B run and the GEMV legs")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the token loop on a single MI355X and has no "
@@ -119,6 +125,14 @@ def main():
         sys.exit(2)
 
     log(f"device: {xp.device_name()}")
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src, dst = xp.Dev(nbytes=n), xp.Dev(nbytes=n)
+        if xp.lib().xjh_d2d(dst.ptr, src.ptr, n):
+            raise SystemExit("calibration copy failed")
+        log(f"calibration: copied {n} bytes device-to-device")
+        src.free()
+        dst.free()
     r = decode_run(xp.CONFIG_4B, "synth4b", 1024, args.steps, args.warmup, seed=20261107)
     tok_s = args.steps / r["wall"]
     ms_step = r["wall"] * 1e3 / args.steps
@@ -126,9 +140,14 @@ def main():
 
     g_ms, g_bytes, g_launch = r["ch"].time_gemv(8)
     achieved = g_bytes / (g_ms * 1e-3) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_gemv_4b_decode.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("bytes_per_launch")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "gemv_kernel<1,1> (fused dequant-GEMV, T=1)",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": "gemv_kernel<1,lanes> (fused dequant-GEMV, T=1, with its prologue/tails)",
                 "bytes_per_launch": round(g_bytes / g_launch), "launches_per_step": g_launch,
                 "us_per_launch": round(g_ms * 1e3 / g_launch, 3), "gemv_share_of_step": round(g_ms / r["gpu_ms"], 3)}
     log(f"GEMV leg: {g_launch} launches/step, {g_bytes / 1e9:.3f} GB/step, {g_ms:.3f} ms -> {achieved:.0f} GB/s")

@@ -159,6 +159,9 @@ void *xjh_malloc(size_t bytes);
 void  xjh_free(void *p);
 int   xjh_h2d(void *dst, const void *src, size_t bytes);
 int   xjh_d2h(void *dst, const void *src, size_t bytes);
+/* Device-to-device copy (the runtime's copy kernel): the known-size transfer
+ * that calibrates the HBM byte counters of a profiler run. */
+int   xjh_d2d(void *dst, const void *src, size_t bytes);
 int   xjh_sync(void);
 const char *xjh_last_error(void);
 

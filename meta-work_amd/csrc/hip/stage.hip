@@ -1046,6 +1046,7 @@ extern "C" void *xjh_malloc(size_t bytes) {
 extern "C" void xjh_free(void *p) { if (p) (void)hipFree(p); }
 extern "C" int xjh_h2d(void *dst, const void *src, size_t n) { return hipMemcpy(dst, src, n, hipMemcpyHostToDevice) == hipSuccess ? 0 : -1; }
 extern "C" int xjh_d2h(void *dst, const void *src, size_t n) { return hipMemcpy(dst, src, n, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1; }
+extern "C" int xjh_d2d(void *dst, const void *src, size_t n) { return hipMemcpy(dst, src, n, hipMemcpyDeviceToDevice) == hipSuccess ? 0 : -1; }
 extern "C" int xjh_sync(void) { return hipDeviceSynchronize() == hipSuccess ? 0 : -1; }
 extern "C" const char *xjh_last_error(void) { return g_lasterr; }
 

@@ -151,6 +151,7 @@ def lib():
     _sig(L, "xjh_free", None, P)
     _sig(L, "xjh_h2d", I, P, P, S)
     _sig(L, "xjh_d2h", I, P, P, S)
+    _sig(L, "xjh_d2d", I, P, P, S)
     _sig(L, "xjh_sync", I)
     _sig(L, "xjh_last_error", CP)
     _sig(L, "xjh_upload_weight", P, U32, P, I64, I64, CP, S)

@@ -1,0 +1,103 @@
+"""Summaries of rocprofv3 CSV output for the decode benchmark.
+
+    python -m xjpipe.rocprof_summary trace <dir with *_kernel_stats.csv and *_kernel_trace.csv>
+    python -m xjpipe.rocprof_summary traffic <FETCH_SIZE dir> <WRITE_SIZE dir> <copy bytes> [out.json]
+
+trace    per-kernel statistics, and the decode step broken down by kernel
+         (steps delimited by the single-token embedding launch)
+traffic  HBM bytes per single-token GEMV launch from FETCH_SIZE / WRITE_SIZE
+         (KiB per dispatch), each scaled by the factor that makes the same
+         counter read the known size of the calibration copy (the largest
+         runtime copy-kernel dispatch of the run)
+"""
+import collections
+import csv
+import glob
+import json
+import os
+import statistics
+import sys
+
+
+def _one(d, suffix):
+    f = glob.glob(os.path.join(d, "*" + suffix))
+    if not f:
+        raise SystemExit(f"no *{suffix} in {d}")
+    return f[0]
+
+
+def _short(name):
+    return name.split("(")[0].replace("void ", "")
+
+
+def trace(d):
+    out = ["| kernel | calls | avg us | total ms | % |", "|---|---:|---:|---:|---:|"]
+    for r in list(csv.DictReader(open(_one(d, "_kernel_stats.csv"))))[:16]:
+        out.append(f"| `{_short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                   f"{float(r['TotalDurationNs']) / 1e6:.2f} | {float(r['Percentage']):.1f} |")
+    rows = list(csv.DictReader(open(_one(d, "_kernel_trace.csv"))))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    starts = [i for i, r in enumerate(rows) if r["Kernel_Name"].startswith("xjk::embed_kernel")
+              and int(r["Grid_Size_X"]) == 256]
+    steps = [rows[a:b] for a, b in zip(starts, starts[1:])
+             if any(r["Kernel_Name"].startswith("xjk::finalize") for r in rows[a:b])][2:]
+    per = collections.defaultdict(list)
+    busy, wall = [], []
+    for seg in steps:
+        acc = collections.defaultdict(lambda: [0.0, 0])
+        for r in seg:
+            k = f"{_short(r['Kernel_Name'])} grid {int(r['Grid_Size_X']) // int(r['Workgroup_Size_X'])}x{r['Grid_Size_Y']}"
+            acc[k][0] += int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            acc[k][1] += 1
+        for k, v in acc.items():
+            per[k].append(v)
+        busy.append(sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in seg))
+        wall.append(int(seg[-1]["End_Timestamp"]) - int(seg[0]["Start_Timestamp"]))
+    out += ["", f"Decode steps analysed: {len(steps)}; kernels per step: {len(steps[-1]) if steps else 0}; "
+            f"sum of kernel durations per step (median) {statistics.median(busy) / 1e3:.1f} us; "
+            f"first start to last end {statistics.median(wall) / 1e3:.1f} us.", "",
+            "| kernel (grid in work-groups) | launches/step | us/step | us/launch |", "|---|---:|---:|---:|"]
+    for k, v in sorted(per.items(), key=lambda kv: -statistics.median(x[0] for x in kv[1])):
+        t = statistics.median(x[0] for x in v) / 1e3
+        n = v[0][1]
+        out.append(f"| `{k}` | {n} | {t:.1f} | {t / n:.2f} |")
+    g1 = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for seg in steps for r in seg
+          if r["Kernel_Name"].startswith("void xjk::gemv_kernel<1,")]
+    if g1:
+        out += ["", f"Single-token GEMV launches in the decode steps: {len(g1)}, average duration "
+                f"{sum(g1) / len(g1) / 1e3:.3f} us."]
+    return "\n".join(out)
+
+
+def _counter(d, name):
+    rows = list(csv.DictReader(open(_one(d, "_counter_collection.csv"))))
+    return [(r["Kernel_Name"], float(r["Counter_Value"])) for r in rows if r["Counter_Name"] == name]
+
+
+def traffic(dfetch, dwrite, copy_bytes, out_json=None):
+    res = {}
+    for name, d in (("FETCH_SIZE", dfetch), ("WRITE_SIZE", dwrite)):
+        vals = _counter(d, name)
+        copies = [v for k, v in vals if k.startswith("__amd_rocclr_copyBuffer")]
+        factor = copy_bytes / (max(copies) * 1024.0)
+        g1 = [v for k, v in vals if k.startswith("void xjk::gemv_kernel<1,")]
+        res[name] = {"factor": factor, "launches": len(g1), "kib_per_launch_raw": sum(g1) / len(g1),
+                     "bytes_per_launch": sum(g1) / len(g1) * 1024.0 * factor}
+    total = res["FETCH_SIZE"]["bytes_per_launch"] + res["WRITE_SIZE"]["bytes_per_launch"]
+    doc = {"kernel": "gemv_kernel<1,lanes> (single-token GEMV launches of the decode step)",
+           "bytes_per_launch": round(total), "fetch": res["FETCH_SIZE"], "write": res["WRITE_SIZE"],
+           "calibration_copy_bytes": copy_bytes}
+    if out_json:
+        with open(out_json, "w") as f:
+            json.dump(doc, f, indent=1)
+    return doc
+
+
+if __name__ == "__main__":
+    if len(sys.argv) >= 3 and sys.argv[1] == "trace":
+        print(trace(sys.argv[2]))
+    elif len(sys.argv) >= 5 and sys.argv[1] == "traffic":
+        print(json.dumps(traffic(sys.argv[2], sys.argv[3], int(sys.argv[4]),
+                                 sys.argv[5] if len(sys.argv) > 5 else None), indent=1))
+    else:
+        raise SystemExit(__doc__)
