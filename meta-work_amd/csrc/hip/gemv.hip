@@ -131,37 +131,40 @@ __device__ __forceinline__ void planes(const uint8_t *p, u32x4 (&pa)[N / 4], u32
     }
 }
 
-// Q4_K unit u = (block u/4, scale pair p = u%4): elements 64p..64p+63 of the
-// block, i.e. sub-blocks 2p (low nibbles of qs[32p..32p+31]) and 2p+1 (high
-// nibbles); scale/min decoding as get_scale_min_k4 (xj_quant.c).
-template <int T, int RPT>
-__device__ __forceinline__ void unit_q4k(const u32x4 (&h)[RPT], const u32x4 (&q0)[RPT], const u32x4 (&q1)[RPT], int u,
-                                         const uint8_t *xl, int ldsT, const XqOff &o, float (&acc)[RPT][T]) {
-    const int p = u & 3, g0 = 8 * (u >> 2) + 2 * p, jm = (2 * p) & 3;
+// Raw bytes of one 64-element unit of a Q4_K or Q6_K row:
+//   Q4_K  a = block header (d|dmin, 12 scale bytes), b, c = the pair's 32 nibble bytes
+//   Q6_K  a, b = ql columns (+0, +32), c = qh column, e = the half's 8 scales, f = d
+struct RawU {
+    u32x4 a, b, c;
+    u32x2 e;
+    uint32_t f;
+};
+
+// Q4_K unit = scale pair p of a block: elements 64p..64p+63, i.e. sub-blocks
+// 2p (low nibbles of qs[32p..32p+31]) and 2p+1 (high nibbles), whose
+// activations are x-groups g0 and g0+1. Scale/min decoding as
+// get_scale_min_k4 (xj_quant.h:49-52).
+template <int T>
+__device__ __forceinline__ void q4k_unit(const RawU &w, int p, int g0, const uint8_t *xl, int ldsT, const XqOff &o,
+                                         float (&acc)[T]) {
+    const int jm = (2 * p) & 3;
     const bool hi4 = p >= 2;
-    float ds[RPT][2], dm[RPT][2];
-#pragma unroll
-    for (int i = 0; i < RPT; i++) {
-        const float d = xjd::f16_to_f32(h[i].x & 0xFFFFu), dmin = xjd::f16_to_f32(h[i].x >> 16);
-#pragma unroll
-        for (int s = 0; s < 2; s++) {
-            const uint32_t A = byte_of(h[i].y, jm + s), B = byte_of(h[i].z, jm + s), C = byte_of(h[i].w, jm + s);
-            const uint32_t sc = hi4 ? ((C & 0xF) | ((A >> 6) << 4)) : (A & 63);
-            const uint32_t mn = hi4 ? ((C >> 4) | ((B >> 6) << 4)) : (B & 63);
-            ds[i][s] = d * (float)sc;
-            dm[i][s] = dmin * (float)mn;
-        }
-    }
+    const float d = xjd::f16_to_f32(w.a.x & 0xFFFFu), dmin = xjd::f16_to_f32(w.a.x >> 16);
+    float ds[2], dm[2];
 #pragma unroll
     for (int s = 0; s < 2; s++) {
-        uint32_t nib[RPT][8];
+        const uint32_t A = byte_of(w.a.y, jm + s), B = byte_of(w.a.z, jm + s), C = byte_of(w.a.w, jm + s);
+        const uint32_t sc = hi4 ? ((C & 0xF) | ((A >> 6) << 4)) : (A & 63);
+        const uint32_t mn = hi4 ? ((C >> 4) | ((B >> 6) << 4)) : (B & 63);
+        ds[s] = d * (float)sc;
+        dm[s] = dmin * (float)mn;
+    }
+    const uint32_t q[8] = {w.b.x, w.b.y, w.b.z, w.b.w, w.c.x, w.c.y, w.c.z, w.c.w};
 #pragma unroll
-        for (int i = 0; i < RPT; i++)
+    for (int s = 0; s < 2; s++) {
+        uint32_t nib[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const uint32_t w = j < 4 ? q0[i][j] : q1[i][j - 4];
-                nib[i][j] = s ? (w >> 4) & 0x0F0F0F0Fu : w & 0x0F0F0F0Fu;
-            }
+        for (int j = 0; j < 8; j++) nib[j] = s ? (q[j] >> 4) & 0x0F0F0F0Fu : q[j] & 0x0F0F0F0Fu;
         const int g = g0 + s;
 #pragma unroll
         for (int t = 0; t < T; t++) {
@@ -171,42 +174,34 @@ __device__ __forceinline__ void unit_q4k(const u32x4 (&h)[RPT], const u32x4 (&q0
             const float f = ((const float *)(xt + o.f_off))[g];
             const int2 sxp = ((const int2 *)(xt + o.sx_off))[g];
             const float SX = (float)(sxp.x + sxp.y);
-#pragma unroll
-            for (int i = 0; i < RPT; i++) {
-                const int S = qdot<8>(nib[i], pa, pb, pc);
-                const float part = (float)S * ds[i][s] - SX * dm[i][s];
-                acc[i][t] = fmaf(part, f, acc[i][t]);
-            }
+            const int S = qdot<8>(nib, pa, pb, pc);
+            const float part = (float)S * ds[s] - SX * dm[s];
+            acc[t] = fmaf(part, f, acc[t]);
         }
     }
 }
 
-// Q6_K unit u = (block u/4, half h = (u/2)%2, column half hl = u%2): for each
-// of the four 32-element groups G of the half, the 16 elements
-// 128h + 32G + 16hl .. +15 (one scale sub-block each). Bit layout as
+// Q6_K unit = column half hl of half h of a block: for each 32-element group
+// G of the half, the 16 elements 128h + 32G + 16hl .. +15 (one scale
+// sub-block each), activations in x-group gb + G. Bit layout as
 // dequantize_row_q6_K: q = (ql & 15 | ql >> 4) | qh bit pair << 4, value q - 32.
-template <int T, int RPT>
-__device__ __forceinline__ void unit_q6k(const u32x4 (&l0)[RPT], const u32x4 (&l1)[RPT], const u32x4 (&qh)[RPT],
-                                         const u32x2 (&sc)[RPT], const uint32_t (&dd)[RPT], int u, const uint8_t *xl,
-                                         int ldsT, const XqOff &o, float (&acc)[RPT][T]) {
-    const int h = (u >> 1) & 1, hl = u & 1, gb = 8 * (u >> 2) + 4 * h;
+template <int T>
+__device__ __forceinline__ void q6k_unit(const RawU &w, int hl, int gb, const uint8_t *xl, int ldsT, const XqOff &o,
+                                         float (&acc)[T]) {
+    const float d = xjd::f16_to_f32(w.f);
 #pragma unroll
     for (int G = 0; G < 4; G++) {
-        uint32_t q6[RPT][4];
-        float dsc[RPT];
+        uint32_t q6[4];
 #pragma unroll
-        for (int i = 0; i < RPT; i++) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t a0 = l0[i][j], a1 = l1[i][j], hb = qh[i][j];
-                q6[i][j] = G == 0 ? (a0 & 0x0F0F0F0Fu) | ((hb << 4) & 0x30303030u)
-                         : G == 1 ? (a1 & 0x0F0F0F0Fu) | ((hb << 2) & 0x30303030u)
-                         : G == 2 ? ((a0 >> 4) & 0x0F0F0F0Fu) | (hb & 0x30303030u)
-                                  : ((a1 >> 4) & 0x0F0F0F0Fu) | ((hb >> 2) & 0x30303030u);
-            }
-            const uint32_t sw = G < 2 ? sc[i].x : sc[i].y;
-            dsc[i] = xjd::f16_to_f32(dd[i]) * (float)(int8_t)byte_of(sw, 2 * (G & 1) + hl);
+        for (int j = 0; j < 4; j++) {
+            const uint32_t a0 = w.a[j], a1 = w.b[j], hb = w.c[j];
+            q6[j] = G == 0 ? (a0 & 0x0F0F0F0Fu) | ((hb << 4) & 0x30303030u)
+                  : G == 1 ? (a1 & 0x0F0F0F0Fu) | ((hb << 2) & 0x30303030u)
+                  : G == 2 ? ((a0 >> 4) & 0x0F0F0F0Fu) | (hb & 0x30303030u)
+                           : ((a1 >> 4) & 0x0F0F0F0Fu) | ((hb >> 2) & 0x30303030u);
         }
+        const uint32_t sw = G < 2 ? w.e.x : w.e.y;
+        const float dsc = d * (float)(int8_t)byte_of(sw, 2 * (G & 1) + hl);
         const int g = gb + G;
 #pragma unroll
         for (int t = 0; t < T; t++) {
@@ -215,11 +210,8 @@ __device__ __forceinline__ void unit_q6k(const u32x4 (&l0)[RPT], const u32x4 (&l
             planes<4>(xt + g * 96 + 16 * hl, pa, pb, pc);
             const float f = ((const float *)(xt + o.f_off))[g];
             const int sxh = ((const int *)(xt + o.sx_off))[2 * g + hl];
-#pragma unroll
-            for (int i = 0; i < RPT; i++) {
-                const int S = qdot<4>(q6[i], pa, pb, pc) - 32 * sxh;
-                acc[i][t] = fmaf((float)S * dsc[i], f, acc[i][t]);
-            }
+            const int S = qdot<4>(q6, pa, pb, pc) - 32 * sxh;
+            acc[t] = fmaf((float)S * dsc, f, acc[t]);
         }
     }
 }
@@ -252,20 +244,12 @@ __device__ __forceinline__ void unit_q80(const u32x4 (&qa)[RPT], const u32x4 (&q
 }
 
 // ---------------------------------------------------------- row loops --
-// Raw bytes of one 64-element unit of a Q4_K or Q6_K row:
-//   Q4_K  a = block header (d|dmin, 12 scale bytes), b, c = the pair's 32 nibble bytes
-//   Q6_K  a, b = ql columns (+0, +32), c = qh column, e = the half's 8 scales, f = d
-struct RawU {
-    u32x4 a, b, c;
-    u32x2 e;
-    uint32_t f;
-};
-
-// The same five loads for every type, addresses chosen without branches: a
-// load whose result reaches a register through a control-flow merge has to
-// complete before the merge, which would serialise the prefetch. Q4_K
-// re-reads header bytes for e and f, other types read the row's first bytes;
-// the extra values are ignored.
+// Unit u of a row, for either K-quant type, with the same five loads and
+// addresses chosen without branches (a load whose result reaches a register
+// through a control-flow merge must complete before the merge); used for the
+// window issued before a work-group's LDS setup. Q4_K re-reads header bytes
+// for e and f, other types read the row's first bytes; the extra values are
+// ignored.
 __device__ __forceinline__ RawU load_unit(uint32_t type, const uint8_t *__restrict__ W, int64_t nblk, int64_t rb, int u) {
     const bool q4 = type == XJ_Q4_K, q6 = type == XJ_Q6_K;
     const int h = (u >> 1) & 1, hl = u & 1;
@@ -285,25 +269,112 @@ __device__ __forceinline__ RawU load_unit(uint32_t type, const uint8_t *__restri
     return r;
 }
 
-// Q4_K / Q6_K rows: the lane's units u = lane, lane + TS, ... with the next
-// unit's loads in flight while the current one is computed; `cur` holds unit
-// `lane` on entry (loaded early by the caller).
-template <int T, int TS>
-__device__ __forceinline__ void rows_kq(uint32_t type, const uint8_t *__restrict__ W, int64_t nblk, int64_t rb, int nu,
-                                        int lane, RawU cur, const uint8_t *xl, int ldsT, const XqOff &o,
-                                        float (&acc)[1][T]) {
-    for (int u = lane; u < nu; u += TS) {
-        const RawU nxt = load_unit(type, W, nblk, rb, u + TS < nu ? u + TS : u);
-        if (type == XJ_Q4_K) {
-            const u32x4 h[1] = {cur.a}, q0[1] = {cur.b}, q1[1] = {cur.c};
-            unit_q4k<T, 1>(h, q0, q1, u, xl, ldsT, o, acc);
-        } else {
-            const u32x4 l0[1] = {cur.a}, l1[1] = {cur.b}, qh[1] = {cur.c};
-            const u32x2 sc[1] = {cur.e};
-            const uint32_t dd[1] = {cur.f};
-            unit_q6k<T, 1>(l0, l1, qh, sc, dd, u, xl, ldsT, o, acc);
+// Q4_K / Q6_K rows: lane `lane` takes units u = lane, lane + TS, ... Since
+// TS is a multiple of 4, the lane's position inside a block (Q4_K scale pair,
+// Q6_K half and column half) is the same for all its units, so every pointer
+// advances by a constant stride. `cur` holds unit `lane` on entry.
+//
+// MU > 0 (single-token launches, at most MU <= 4 units per lane): the loop over
+// the lane's units is unrolled, so every unit has its own registers and PD
+// units ahead of the one being computed are in flight; the loads are
+// unconditional (units past the row read the padding after the tensor,
+// kWeightPad) and only the arithmetic is predicated. A rolled loop that
+// rotated a register ring would have to wait for each load at the rotation.
+// MU == 0: rolled loop with the next unit in flight.
+__device__ __forceinline__ RawU ld_q4k(const uint8_t *blk, int p) {
+    RawU r;
+    r.a = ld16(blk);
+    r.b = ld16(blk + 16 + 32 * p);
+    r.c = ld16(blk + 32 + 32 * p);
+    return r;
+}
+
+struct Q6Ptr {
+    const uint8_t *ql, *qh, *sc, *dd;
+};
+
+// unit k steps (of TS/4 blocks) after the one q points at
+__device__ __forceinline__ RawU ld_q6k(const Q6Ptr &q, int64_t k) {
+    RawU r;
+    r.a = ld16(q.ql + k * 128);
+    r.b = ld16(q.ql + k * 128 + 32);
+    r.c = ld16(q.qh + k * 64);
+    r.e = *(const u32x2 *)(q.sc + k * 16);
+    r.f = *(const uint16_t *)(q.dd + k * 2);
+    return r;
+}
+
+// Units a lane has in flight ahead of the one it computes (MU > 0), and the
+// window of units loaded before the work-group's LDS setup.
+template <int MU>
+struct Win {
+    static constexpr int PD = MU <= 1 ? 0 : MU == 2 ? 1 : 2;   // MU <= 4 fits 168 VGPRs
+    static constexpr int N = PD + 1;
+};
+
+template <int T, int TS, int MU>
+__device__ __forceinline__ void rows_q4k(const uint8_t *__restrict__ W, int64_t rb, int nu, int lane,
+                                         const RawU (&win)[Win<MU>::N], const uint8_t *xl, int ldsT, const XqOff &o,
+                                         float (&acc)[T]) {
+    constexpr int DB = TS / 4;
+    const int p = lane & 3;
+    const int g0 = 8 * (lane >> 2) + 2 * p;
+    const uint8_t *blk = W + (rb + (lane >> 2)) * 144;
+    RawU cur = win[0];
+    if constexpr (MU > 0) {
+        constexpr int PD = Win<MU>::PD;
+        RawU r[MU];
+#pragma unroll
+        for (int m = 0; m <= PD; m++) r[m] = win[m];
+#pragma unroll
+        for (int m = 0; m < MU; m++) {
+            __builtin_amdgcn_sched_barrier(0);   // keep each prefetch in its step (register budget)
+            if (m + PD + 1 < MU) r[m + PD + 1] = ld_q4k(blk + (m + PD + 1) * DB * 144, p);
+            if (lane + m * TS < nu) q4k_unit<T>(r[m], p, g0 + 8 * DB * m, xl, ldsT, o, acc);
         }
-        cur = nxt;
+    } else {
+        int g = g0;
+        for (int u = lane; u < nu; u += TS) {
+            blk += DB * 144;
+            const RawU nxt = ld_q4k(blk, p);
+            q4k_unit<T>(cur, p, g, xl, ldsT, o, acc);
+            g += 8 * DB;
+            cur = nxt;
+        }
+    }
+}
+
+template <int T, int TS, int MU>
+__device__ __forceinline__ void rows_q6k(const uint8_t *__restrict__ W, int64_t nblk, int64_t rb, int nu, int lane,
+                                         const RawU (&win)[Win<MU>::N], const uint8_t *xl, int ldsT, const XqOff &o,
+                                         float (&acc)[T]) {
+    constexpr int DB = TS / 4;
+    const int h = (lane >> 1) & 1, hl = lane & 1;
+    const int64_t b = rb + (lane >> 2);
+    Q6Ptr q{W + b * 128 + 64 * h + 16 * hl, W + nblk * 128 + b * 64 + 32 * h + 16 * hl,
+            W + nblk * 192 + b * 16 + 8 * h, W + nblk * 208 + b * 2};
+    const int gb0 = 8 * (lane >> 2) + 4 * h;
+    RawU cur = win[0];
+    if constexpr (MU > 0) {
+        constexpr int PD = Win<MU>::PD;
+        RawU r[MU];
+#pragma unroll
+        for (int m = 0; m <= PD; m++) r[m] = win[m];
+#pragma unroll
+        for (int m = 0; m < MU; m++) {
+            __builtin_amdgcn_sched_barrier(0);   // keep each prefetch in its step (register budget)
+            if (m + PD + 1 < MU) r[m + PD + 1] = ld_q6k(q, (m + PD + 1) * DB);
+            if (lane + m * TS < nu) q6k_unit<T>(r[m], hl, gb0 + 8 * DB * m, xl, ldsT, o, acc);
+        }
+    } else {
+        int gb = gb0;
+        for (int u = lane; u < nu; u += TS) {
+            q.ql += DB * 128; q.qh += DB * 64; q.sc += DB * 16; q.dd += DB * 2;
+            const RawU nxt = ld_q6k(q, 0);
+            q6k_unit<T>(cur, hl, gb, xl, ldsT, o, acc);
+            gb += 8 * DB;
+            cur = nxt;
+        }
     }
 }
 
@@ -371,9 +442,37 @@ __device__ __forceinline__ int seg_of(const GArgs &a, int rg) {
 // Team-reduced results acc[i][t] of rows (rg - wg0) * ROWS + team * RPT + i:
 // lane i of the team stores row i (plain, residual add or conv + SiLU), and
 // the work-group's greedy argmax partial is written when the segment has one.
+// Operands of the epilogue of one row, loaded before the row's dot products
+// so their latency overlaps the weight stream: the residual (EPI_ADD) or,
+// for kernel sizes up to 4, the conv state and weights (EPI_CONV; larger
+// kernels load them in the epilogue).
+constexpr int kConvPre = 4;
+template <int T>
+struct EpiIn {
+    float y[T];
+    float st[kConvPre - 1], wc[kConvPre];
+};
+
+template <int T>
+__device__ __forceinline__ void epi_load(const GSeg &sg, int64_t r, bool mine, EpiIn<T> &e) {
+    if (!mine) return;
+    if (sg.epi == EPI_ADD) {
+#pragma unroll
+        for (int t = 0; t < T; t++) e.y[t] = sg.y[(int64_t)t * sg.ys + r];
+    } else if (sg.epi == EPI_CONV && sg.conv_k <= kConvPre) {
+        const int KC = sg.conv_k;
+#pragma unroll
+        for (int k = 0; k < kConvPre; k++) {
+            if (k + 1 < KC) e.st[k] = sg.conv_state[r * (KC - 1) + k];
+            if (k < KC) e.wc[k] = sg.conv_w[r * KC + k];
+        }
+    }
+}
+
 template <int T, int TS, int RPT>
 __device__ __forceinline__ void epilogue(const GArgs &a, const GSeg &sg, int rg, int team, int lane, int tid,
-                                         const float (&acc)[RPT][T], unsigned long long (*amax_sh)[T]) {
+                                         const float (&acc)[RPT][T], unsigned long long (*amax_sh)[T],
+                                         const EpiIn<T> &e) {
     constexpr int NT = 256 / TS, ROWS = NT * RPT;
     unsigned long long best[T];
 #pragma unroll
@@ -383,29 +482,47 @@ __device__ __forceinline__ void epilogue(const GArgs &a, const GSeg &sg, int rg,
         const int64_t r = (int64_t)(rg - sg.wg0) * ROWS + team * RPT + i;
         if (lane != i || r >= sg.n_rows) continue;
         if (sg.epi == EPI_CONV) {
+            // register arrays with compile-time indices only (KC is a runtime value <= 8)
             const int KC = sg.conv_k;
             float st[8], wc[8];
-            for (int k = 0; k + 1 < KC; k++) st[k] = sg.conv_state[r * (KC - 1) + k];
-            for (int k = 0; k < KC; k++) wc[k] = sg.conv_w[r * KC + k];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                if (KC <= kConvPre) {
+                    st[k] = k < kConvPre - 1 ? e.st[k < kConvPre - 1 ? k : 0] : 0.f;
+                    wc[k] = k < kConvPre ? e.wc[k < kConvPre ? k : 0] : 0.f;
+                } else {
+                    st[k] = k + 1 < KC ? sg.conv_state[r * (KC - 1) + k] : 0.f;
+                    wc[k] = k < KC ? sg.conv_w[r * KC + k] : 0.f;
+                }
+            }
+            float wl = 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) if (k == KC - 1) wl = wc[k];
 #pragma unroll
             for (int t = 0; t < T; t++) {
                 const float xv = acc[i][t];
                 float s = 0.f;
-                for (int k = 0; k + 1 < KC; k++) s = fmaf(st[k], wc[k], s);
-                s = fmaf(xv, wc[KC - 1], s);
-                for (int k = 0; k + 2 < KC; k++) st[k] = st[k + 1];
-                st[KC - 2] = xv;
+#pragma unroll
+                for (int k = 0; k < 7; k++) if (k + 1 < KC) s = fmaf(st[k], wc[k], s);
+                s = fmaf(xv, wl, s);
+#pragma unroll
+                for (int k = 0; k < 6; k++) if (k + 2 < KC) st[k] = st[k + 1];
+#pragma unroll
+                for (int k = 0; k < 7; k++) if (k == KC - 2) st[k] = xv;
                 sg.y[(int64_t)t * sg.ys + r] = xjd::silu(s);
                 const int ta = a.t0 + t;
                 if (ta < a.keep_n)
-                    for (int k = 0; k + 1 < KC; k++) sg.conv_ck[((int64_t)ta * sg.n_rows + r) * (KC - 1) + k] = st[k];
+#pragma unroll
+                    for (int k = 0; k < 7; k++)
+                        if (k + 1 < KC) sg.conv_ck[((int64_t)ta * sg.n_rows + r) * (KC - 1) + k] = st[k];
             }
-            for (int k = 0; k + 1 < KC; k++) sg.conv_state[r * (KC - 1) + k] = st[k];
+#pragma unroll
+            for (int k = 0; k < 7; k++) if (k + 1 < KC) sg.conv_state[r * (KC - 1) + k] = st[k];
         } else {
 #pragma unroll
             for (int t = 0; t < T; t++) {
                 float *yp = sg.y + (int64_t)t * sg.ys + r;
-                const float yv = sg.epi == EPI_ADD ? *yp + acc[i][t] : acc[i][t];
+                const float yv = sg.epi == EPI_ADD ? e.y[t] + acc[i][t] : acc[i][t];
                 if (a.post.mode != POST_NONE) xjd::store_sys(yp, yv);   // read by this launch's tail
                 else *yp = yv;
                 if (sg.amax) best[t] = xjd::argmax_key(acc[i][t], (uint32_t)r);
@@ -451,13 +568,25 @@ __device__ __forceinline__ void tail_swiglu(const GArgs &a, int rg, int *flag_sh
     xjd::emit_xq(v, k, in, a.post.xq + (int64_t)(in ? t : 0) * o.stride, o);
 }
 
-// Copy the T tokens' prepared activations (digits, scales, sums) into LDS.
+// Copy the T tokens' prepared activations (digits, scales, sums) into LDS,
+// eight 16-byte loads per thread in flight at a time.
 template <int T>
 __device__ __forceinline__ void stage_xq(const GArgs &a, const XqOff &o, u32x4 *lds_v) {
     const int n16 = o.v_off >> 4;
-    for (int i = threadIdx.x; i < T * n16; i += 256) {
-        const int t = i / n16, j = i - t * n16;
-        lds_v[i] = ld16(a.xq + (int64_t)t * o.stride + 16 * j);
+    for (int t = 0; t < T; t++) {
+        const uint8_t *src = a.xq + (int64_t)t * o.stride;
+        u32x4 *dst = lds_v + t * n16;
+        for (int i0 = threadIdx.x; i0 < n16; i0 += 256 * 8) {
+            u32x4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = i0 + 256 * j;
+                v[j] = ld16(src + 16 * (i < n16 ? i : n16 - 1));
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (i0 + 256 * j < n16) dst[i0 + 256 * j] = v[j];
+        }
     }
 }
 
@@ -504,14 +633,79 @@ __device__ __forceinline__ void prologue_rms(const GArgs &a, const XqOff &o, uin
     }
 }
 
+// Split-phase LDS setup for single-token launches. The setup loads (the
+// staged activations, or x and the norm weights of the RMSNorm prologue)
+// are issued before the weight window, so that waiting for them (vmcnt
+// drains in issue order) does not wait for the weights too. One register
+// buffer serves both: staging keeps 8 x 16 bytes per thread (v_off <= 32 KB),
+// the prologue keeps x and w of 16 inputs per thread (K <= 4096) as
+// sv[j] = {x[2j], x[2j+1], w[2j], w[2j+1]} (input k = tid + 256 * index).
+struct Setup1 {
+    u32x4 sv[8];
+};
+
+__device__ __forceinline__ bool setup1_fits(const GArgs &a, const XqOff &o) {
+    return a.pro == PRO_RMS ? a.K <= 256 * 16 : (o.v_off >> 4) <= 256 * 8;
+}
+
+__device__ __forceinline__ void setup1_issue(const GArgs &a, const XqOff &o, Setup1 &su) {
+    const int tid = threadIdx.x;
+    if (a.pro == PRO_RMS) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int k0 = tid + 256 * (2 * j), k1 = k0 + 256;
+            const int c0 = k0 < a.K ? k0 : a.K - 1, c1 = k1 < a.K ? k1 : a.K - 1;
+            su.sv[j] = u32x4{__float_as_uint(a.x[c0]), __float_as_uint(a.x[c1]), __float_as_uint(a.pro_w[c0]),
+                             __float_as_uint(a.pro_w[c1])};
+        }
+    } else {
+        const int n16 = o.v_off >> 4;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int i = tid + 256 * j;
+            su.sv[j] = ld16(a.xq + 16 * (i < n16 ? i : n16 - 1));
+        }
+    }
+}
+
+__device__ __forceinline__ void setup1_finish(const GArgs &a, const XqOff &o, const Setup1 &su, u32x4 *lds_v,
+                                              double *red) {
+    const int tid = threadIdx.x, K = a.K;
+    if (a.pro == PRO_RMS) {
+        double ss = 0;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const float xv = __uint_as_float(j & 1 ? su.sv[j >> 1].y : su.sv[j >> 1].x);
+            if (tid + 256 * j < K) ss += (double)xv * xv;
+        }
+        ss = xjd::block_sum_d(ss, red);
+        const float sc = 1.0f / sqrtf((float)(ss / K) + a.eps);
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int k = tid + 256 * j;
+            const float xv = __uint_as_float(j & 1 ? su.sv[j >> 1].y : su.sv[j >> 1].x);
+            const float wv = __uint_as_float(j & 1 ? su.sv[j >> 1].w : su.sv[j >> 1].z);
+            if (256 * j < K) xjd::emit_xq(xv * sc * wv, k, k < K, (uint8_t *)lds_v, o, false);
+        }
+    } else {
+        const int n16 = o.v_off >> 4;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (tid + 256 * j < n16) lds_v[tid + 256 * j] = su.sv[j];
+    }
+}
+
 // -------------------------------------------------------------- kernels --
-// A row group is 256/TS rows, one per team of TS lanes. The work-group
+// A row group is 256/TS rows, one per team of TS lanes; MU > 0: every lane
+// owns at most MU units of a row (single-token launches, which are kept to
+// three work-groups per CU so that a launch of up to 3 x CUs work-groups runs
+// in one wave). The work-group
 // issues the first unit of its first row group, stages the T tokens'
 // prepared activations in LDS meanwhile, then loops over row groups with
 // stride gridDim.x (prefetching each next group's first unit after the
 // previous group's epilogue).
-template <int T, int TS>
-__global__ __launch_bounds__(256) void gemv_kernel(const GArgs a) {
+template <int T, int TS, int MU>
+__global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a) {
     extern __shared__ u32x4 lds_v[];
     constexpr int NT = 256 / TS;
     __shared__ unsigned long long amax_sh[NT][T];
@@ -526,25 +720,45 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GArgs a) {
         return r < sg.n_rows ? r : (int64_t)sg.n_rows - 1;
     };
     auto blocks_per_row = [&](uint32_t type) { return (type == XJ_Q4_K || type == XJ_Q6_K) ? K / 256 : K / 32; };
-    auto first_unit = [&](int rg) {
+    // the lane's first units of row group rg, loaded before the work that
+    // precedes their use (units past the row read the tensor's padding)
+    constexpr int NW = Win<MU>::N;
+    RawU win[NW];
+    auto first_units = [&](int rg) {
         const GSeg &sg = a.seg[seg_of(a, rg)];
-        return load_unit(sg.type, sg.w, sg.nblk, row_of(sg, rg) * blocks_per_row(sg.type), lane < nu ? lane : nu - 1);
+        const int64_t rb = row_of(sg, rg) * blocks_per_row(sg.type);
+        const int u0 = lane < nu ? lane : nu - 1;
+#pragma unroll
+        for (int m = 0; m < NW; m++) win[m] = load_unit(sg.type, sg.w, sg.nblk, rb, u0 + m * TS);
     };
     int rg = blockIdx.x;
-    RawU pre = first_unit(rg);
-    if (a.pro == PRO_RMS) prologue_rms<T>(a, o, (uint8_t *)lds_v, red_sh);
-    else stage_xq<T>(a, o, lds_v);
+    if (T == 1 && setup1_fits(a, o)) {
+        Setup1 su;
+        setup1_issue(a, o, su);
+        __builtin_amdgcn_sched_barrier(0);
+        first_units(rg);
+        __builtin_amdgcn_sched_barrier(0);
+        setup1_finish(a, o, su, lds_v, red_sh);
+    } else {
+        first_units(rg);
+        if (a.pro == PRO_RMS) prologue_rms<T>(a, o, (uint8_t *)lds_v, red_sh);
+        else stage_xq<T>(a, o, lds_v);
+    }
     __syncthreads();
     const uint8_t *xl = (const uint8_t *)lds_v;
 
-    for (; rg < n_rg; rg += gridDim.x) {
+    for (;;) {
         const GSeg &sg = a.seg[seg_of(a, rg)];
         const int64_t row = row_of(sg, rg), rb = row * blocks_per_row(sg.type);
+        EpiIn<T> ein;
+        epi_load<T>(sg, row, lane == 0 && (int64_t)(rg - sg.wg0) * NT + team < sg.n_rows, ein);
         float acc[1][T];
 #pragma unroll
         for (int t = 0; t < T; t++) acc[0][t] = 0.f;
-        if (sg.type == XJ_Q4_K || sg.type == XJ_Q6_K) {
-            rows_kq<T, TS>(sg.type, sg.w, sg.nblk, rb, nu, lane, pre, xl, o.v_off, o, acc);
+        if (sg.type == XJ_Q4_K) {
+            rows_q4k<T, TS, MU>(sg.w, rb, nu, lane, win, xl, o.v_off, o, acc[0]);
+        } else if (sg.type == XJ_Q6_K) {
+            rows_q6k<T, TS, MU>(sg.w, sg.nblk, rb, nu, lane, win, xl, o.v_off, o, acc[0]);
         } else {
             const int64_t rr[1] = {row}, rbb[1] = {rb};
             if (sg.type == XJ_Q8_0) rows_q80<T, TS, 1>(sg.w, sg.nblk, rbb, K / 32, lane, xl, o.v_off, o, acc);
@@ -552,9 +766,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GArgs a) {
         }
 #pragma unroll
         for (int t = 0; t < T; t++) acc[0][t] = team_sum<TS>(acc[0][t]);
-        epilogue<T, TS, 1>(a, sg, rg, team, lane, tid, acc, amax_sh);
+        epilogue<T, TS, 1>(a, sg, rg, team, lane, tid, acc, amax_sh, ein);
         if (a.post.mode == POST_SWIGLU) tail_swiglu<T, NT>(a, rg, &flag_sh);
-        pre = first_unit(rg + (int)gridDim.x < n_rg ? rg + (int)gridDim.x : rg);
+        rg += gridDim.x;
+        if (rg >= n_rg) break;
+        first_units(rg);
     }
     if (a.inc_ptr && blockIdx.x == 0 && tid == 0) *a.inc_ptr += a.inc_by;
 }
@@ -600,16 +816,24 @@ int prep_launch(const GArgs &a, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-template <int T, int TS>
+template <int T, int TS, int MU = 0>
 static hipError_t launch_v(const GArgs &a, int grid, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_kernel<T, TS>), dim3(grid), dim3(256), (size_t)T * xq_off(a.K).v_off, st, a);
+    hipLaunchKernelGGL((gemv_kernel<T, TS, MU>), dim3(grid), dim3(256), (size_t)T * xq_off(a.K).v_off, st, a);
     return hipGetLastError();
 }
 
 template <int TS>
 static hipError_t launch_ts(const GArgs &a, int grid, hipStream_t st) {
+    const int upl = (a.K / 64 + TS - 1) / TS;   // 64-element units per lane
     switch (a.T) {
-    case 1: return launch_v<1, TS>(a, grid, st);
+    case 1:
+        switch (upl) {
+        case 1: return launch_v<1, TS, 1>(a, grid, st);
+        case 2: return launch_v<1, TS, 2>(a, grid, st);
+        case 3: return launch_v<1, TS, 3>(a, grid, st);
+        case 4: return launch_v<1, TS, 4>(a, grid, st);
+        default: return launch_v<1, TS, 0>(a, grid, st);
+        }
     case 2: return launch_v<2, TS>(a, grid, st);
     case 3: return launch_v<3, TS>(a, grid, st);
     case 4: return launch_v<4, TS>(a, grid, st);
@@ -656,9 +880,13 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
 
 template <int TS>
 static void raise_ts(int bytes) {
-    const void *f[] = {(const void *)gemv_kernel<1, TS>, (const void *)gemv_kernel<2, TS>, (const void *)gemv_kernel<3, TS>,
-                       (const void *)gemv_kernel<4, TS>, (const void *)gemv_kernel<5, TS>, (const void *)gemv_kernel<6, TS>,
-                       (const void *)gemv_kernel<7, TS>, (const void *)gemv_kernel<8, TS>};
+    const void *f[] = {(const void *)gemv_kernel<1, TS, 0>, (const void *)gemv_kernel<1, TS, 1>,
+                       (const void *)gemv_kernel<1, TS, 2>, (const void *)gemv_kernel<1, TS, 3>,
+                       (const void *)gemv_kernel<1, TS, 4>,
+                       (const void *)gemv_kernel<2, TS, 0>, (const void *)gemv_kernel<3, TS, 0>,
+                       (const void *)gemv_kernel<4, TS, 0>, (const void *)gemv_kernel<5, TS, 0>,
+                       (const void *)gemv_kernel<6, TS, 0>, (const void *)gemv_kernel<7, TS, 0>,
+                       (const void *)gemv_kernel<8, TS, 0>};
     for (const void *k : f) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 

@@ -18,6 +18,9 @@ namespace xjk {
 
 constexpr int kMaxSeg = 4;
 constexpr int kTileT = 8;        // tokens per GEMV launch (larger T is tiled)
+// Bytes allocated after every weight tensor: the GEMV prefetches each lane's
+// next units unconditionally, reading up to 3 * 16 + 1 Q4_K blocks past a row.
+constexpr size_t kWeightPad = 16384;
 
 enum Pro { PRO_NONE = 0, PRO_RMS = 1, PRO_SWIGLU = 2, PRO_GATED_RMS = 3 };
 enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_CONV = 2 };

@@ -109,7 +109,7 @@ bool upload(HStage *S, const xj_w &w, DevW *out, char *err, size_t errlen) {
         snprintf(err, errlen, "tensor type %s is not supported by the HIP backend", xj_type_name(w.type));
         return false;
     }
-    uint8_t *p = dalloc<uint8_t>(S, w.nbytes, err, errlen);
+    uint8_t *p = dalloc<uint8_t>(S, w.nbytes + kWeightPad, err, errlen);
     if (!p || upload_repack(w.type, w.data, w.ne1, w.ne0, p, S->st, err, errlen)) return false;
     out->p = p; out->type = w.type; out->n_rows = w.ne1; out->k = w.ne0; out->bytes = w.nbytes;
     S->wcache[w.data] = *out;
@@ -1055,7 +1055,7 @@ extern "C" void *xjh_upload_weight(uint32_t type, const void *host, int64_t n_ro
     if (!gemv_type_ok(type)) { snprintf(err, errlen, "type %s has no device layout", xj_type_name(type)); return nullptr; }
     const uint64_t bytes = xj_row_bytes(type, k) * (uint64_t)n_rows;
     void *p = nullptr;
-    if (hipMalloc(&p, bytes) != hipSuccess) { snprintf(err, errlen, "hipMalloc failed"); return nullptr; }
+    if (hipMalloc(&p, bytes + kWeightPad) != hipSuccess) { snprintf(err, errlen, "hipMalloc failed"); return nullptr; }
     if (upload_repack(type, host, n_rows, k, (uint8_t *)p, g_stream, err, errlen)) { (void)hipFree(p); return nullptr; }
     return p;
 }
