@@ -68,7 +68,13 @@ __global__ __launch_bounds__(256) void prep_kernel(const GArgs a) {
     float v = 0.f;
     if (a.pro == PRO_RMS) {
         double ss = 0;
-        for (int i = tid; i < K; i += 256) ss += (double)x[i] * x[i];
+        for (int i0 = tid; i0 < K; i0 += 256 * 8) {   // eight loads in flight per thread, same order
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = i0 + 256 * j < K ? x[i0 + 256 * j] : 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) ss += (double)v[j] * v[j];
+        }
         ss = xjd::block_sum_d(ss, red);
         const float sc = 1.0f / sqrtf((float)(ss / K) + a.eps);
         if (in) v = x[k] * sc * a.pro_w[k];

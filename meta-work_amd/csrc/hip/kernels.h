@@ -113,6 +113,7 @@ struct AttnArgs {
     const float *qnorm_w, *knorm_w;
     const float *inv_freq;               // [n_rot/2]
     const int32_t *npast;
+    float *qr;                           // normalised, rotated queries [T][H][D] (written by kv_store)
     float *scores;                       // split partials [T][H][n_split][D+2]
     float *out;                          // [T][H*D]
     int32_t T, H, Hkv, D, n_rot, n_ctx, n_split;

@@ -37,9 +37,12 @@ __global__ __launch_bounds__(256) void finalize_kernel(const unsigned long long 
     const int t = blockIdx.x, tid = threadIdx.x;
     __shared__ unsigned long long red[256];
     unsigned long long m = 0ull;
-    for (int i = tid; i < n_part; i += 256) {
-        const unsigned long long k = amax[(int64_t)t * n_part + i];
-        m = k > m ? k : m;
+    for (int i0 = tid; i0 < n_part; i0 += 256 * 8) {   // eight loads in flight per thread
+        unsigned long long k[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) k[j] = i0 + 256 * j < n_part ? amax[(int64_t)t * n_part + i0 + 256 * j] : 0ull;
+#pragma unroll
+        for (int j = 0; j < 8; j++) m = k[j] > m ? k[j] : m;
     }
     red[tid] = m;
     __syncthreads();

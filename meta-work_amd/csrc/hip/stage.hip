@@ -58,7 +58,8 @@ struct HStage {
     DevW output, tok_embd;
     const float *out_norm = nullptr;
     float *x = nullptr, *qkv = nullptr, *kb = nullptr, *vb = nullptr, *z = nullptr, *beta = nullptr,
-          *alpha = nullptr, *o = nullptr, *g = nullptr, *u = nullptr, *scores = nullptr, *logits = nullptr;
+          *alpha = nullptr, *o = nullptr, *g = nullptr, *u = nullptr, *qr = nullptr, *scores = nullptr,
+          *logits = nullptr;
     unsigned long long *amax = nullptr;
     int head_nwg = 0;
     int32_t *npast = nullptr;
@@ -280,7 +281,7 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
         }
         if (p.run(T, st)) return -1;
         at.kc = L.kc; at.vc = L.vc; at.qnorm_w = L.q_norm; at.knorm_w = L.k_norm; at.inv_freq = S->inv_freq;
-        at.npast = S->npast; at.scores = S->scores; at.out = S->o;
+        at.npast = S->npast; at.qr = S->qr; at.scores = S->scores; at.out = S->o;
         at.T = T; at.H = Hq; at.Hkv = Hkv; at.D = D; at.n_rot = hp.n_rot; at.n_ctx = S->s.n_ctx;
         at.n_split = attn_splits(S->s.n_ctx);
         at.eps = hp.eps; at.scale = 1.0f / sqrtf((float)D);
@@ -519,6 +520,7 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
     if (any_rec && (hp.conv_k < 2 || hp.conv_k > 8)) { snprintf(err, errlen, "conv kernel %d not supported", hp.conv_k); return nullptr; }
     if (hp.n_embd % 256 || hp.n_ff % 32) { snprintf(err, errlen, "n_embd must be a multiple of 256"); return nullptr; }
     if (hp.n_head_kv < 1 || hp.n_head % hp.n_head_kv) { snprintf(err, errlen, "n_head must be a multiple of n_head_kv"); return nullptr; }
+    if (hp.n_head / hp.n_head_kv > 8) { snprintf(err, errlen, "at most 8 query heads per kv head are supported"); return nullptr; }
     {   // every tensor a kernel reads must have the shape the kernel assumes
         const int64_t E = hp.n_embd, FF = hp.n_ff, D = hp.head_dim, nq = 2 * (int64_t)hp.n_head * D, nk = (int64_t)hp.n_head_kv * D;
         auto bad = [&](const xj_w &w, int64_t ne0, int64_t ne1, const char *what, int il) {
@@ -617,6 +619,7 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
     S->o = dalloc<float>(S, mb * sf, err, errlen);
     S->g = dalloc<float>(S, mb * sf, err, errlen);
     S->u = dalloc<float>(S, mb * sf, err, errlen);
+    S->qr = dalloc<float>(S, mb * hp.n_head * (size_t)hp.head_dim, err, errlen);
     S->scores = dalloc<float>(S, mb * hp.n_head * (size_t)attn_splits(n_ctx) * (hp.head_dim + 2), err, errlen);
     S->npast = dalloc<int32_t>(S, 1, err, errlen);
     {
@@ -635,7 +638,7 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
     const int half = hp.n_rot / 2 > 0 ? hp.n_rot / 2 : 1;
     S->inv_freq = dalloc<float>(S, half, err, errlen);
     if (!S->x || !S->qkv || !S->kb || !S->vb || !S->z || !S->beta || !S->alpha || !S->o || !S->g || !S->u ||
-        !S->scores || !S->npast || !S->inv_freq)
+        !S->qr || !S->scores || !S->npast || !S->inv_freq)
         return fail();
     if (has_head) {
         S->logits = dalloc<float>(S, mb * (size_t)S->output.n_rows, err, errlen);
