@@ -66,18 +66,12 @@ __global__ __launch_bounds__(256) void prep_kernel(const GArgs a) {
     __shared__ double red[4];
     const float *x = a.x + (int64_t)t * a.xs;
     float v = 0.f;
-    if (a.pro == PRO_RMS) {
-        double ss = 0;
-        for (int i0 = tid; i0 < K; i0 += 256 * 8) {   // eight loads in flight per thread, same order
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = i0 + 256 * j < K ? x[i0 + 256 * j] : 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; j++) ss += (double)v[j] * v[j];
+    float xr = 0.f;   // PRO_RMSU: the raw input, for the group's sum of squares
+    if (a.pro == PRO_RMSU) {
+        if (in) {
+            xr = x[k];
+            v = xr * a.pro_w[k];
         }
-        ss = xjd::block_sum_d(ss, red);
-        const float sc = 1.0f / sqrtf((float)(ss / K) + a.eps);
-        if (in) v = x[k] * sc * a.pro_w[k];
     } else if (a.pro == PRO_SWIGLU) {
         if (in) v = xjd::silu(x[k]) * a.x2[(int64_t)t * a.x2s + k];
     } else if (a.pro == PRO_GATED_RMS) {
@@ -103,7 +97,12 @@ __global__ __launch_bounds__(256) void prep_kernel(const GArgs a) {
     } else {
         if (in) v = x[k];
     }
-    xjd::emit_xq(v, k, in, a.xq + (int64_t)t * o.stride, o);
+    uint8_t *dst = a.xq + (int64_t)t * o.stride;
+    xjd::emit_xq(v, k, in, dst, o);
+    if (a.pro == PRO_RMSU) {
+        const double ss = xjd::group_ss(xr);
+        if (in && (k & 31) == 0) ((double *)(dst + o.ss_off))[k >> 5] = ss;
+    }
 }
 
 // -------------------------------------------------------- unit kernels --
@@ -596,109 +595,140 @@ __device__ __forceinline__ void stage_xq(const GArgs &a, const XqOff &o, u32x4 *
     }
 }
 
-// In-work-group prologue for inputs on the residual stream: the prepared
-// activations of RMSNorm(x[t]) * w (xj_cpu.c:56-61: double sum of squares,
-// x * sc * w) for the T tokens, built straight into LDS. Each thread holds
-// its K/256 inputs in registers between the sum and the conversion.
-template <int T>
-__device__ __forceinline__ void prologue_rms(const GArgs &a, const XqOff &o, uint8_t *xl, double *red) {
-    constexpr int NJ = 16;   // K <= 4096 from registers; larger K re-reads x
-    const int K = a.K, tid = threadIdx.x;
-    for (int t = 0; t < T; t++) {
-        const float *x = a.x + (int64_t)t * a.xs;
-        uint8_t *dst = xl + t * o.v_off;
-        if (K <= 256 * NJ) {
-            float xv[NJ], wv[NJ];
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                const int k = tid + 256 * j;
-                xv[j] = k < K ? x[k] : 0.f;
-                wv[j] = k < K ? a.pro_w[k] : 0.f;
-            }
-            double ss = 0;
-#pragma unroll
-            for (int j = 0; j < NJ; j++) ss += (double)xv[j] * xv[j];
-            ss = xjd::block_sum_d(ss, red);
-            const float sc = 1.0f / sqrtf((float)(ss / K) + a.eps);
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                const int k = tid + 256 * j;
-                if (256 * j < K) xjd::emit_xq(xv[j] * sc * wv[j], k, k < K, dst, o, false);
-            }
-        } else {
-            double ss = 0;
-            for (int k = tid; k < K; k += 256) ss += (double)x[k] * x[k];
-            ss = xjd::block_sum_d(ss, red);
-            const float sc = 1.0f / sqrtf((float)(ss / K) + a.eps);
-            for (int k0 = 0; k0 < K; k0 += 256) {
-                const int k = k0 + tid;
-                xjd::emit_xq(k < K ? x[k] * sc * a.pro_w[k] : 0.f, k, k < K, dst, o, false);
-            }
-        }
-        __syncthreads();   // red is reused by the next token
-    }
-}
-
-// Split-phase LDS setup for single-token launches. The setup loads (the
-// staged activations, or x and the norm weights of the RMSNorm prologue)
-// are issued before the weight window, so that waiting for them (vmcnt
-// drains in issue order) does not wait for the weights too. One register
-// buffer serves both: staging keeps 8 x 16 bytes per thread (v_off <= 32 KB),
-// the prologue keeps x and w of 16 inputs per thread (K <= 4096) as
-// sv[j] = {x[2j], x[2j+1], w[2j], w[2j+1]} (input k = tid + 256 * index).
+// Split-phase LDS staging for single-token launches: the staging loads are
+// issued before the weight window, so that waiting for them (vmcnt drains in
+// issue order) does not wait for the weights too. 8 x 16 bytes per thread
+// (v_off <= 32 KB).
 struct Setup1 {
     u32x4 sv[8];
 };
 
-__device__ __forceinline__ bool setup1_fits(const GArgs &a, const XqOff &o) {
-    return a.pro == PRO_RMS ? a.K <= 256 * 16 : (o.v_off >> 4) <= 256 * 8;
-}
+__device__ __forceinline__ bool setup1_fits(const XqOff &o) { return (o.v_off >> 4) <= 256 * 8; }
 
 __device__ __forceinline__ void setup1_issue(const GArgs &a, const XqOff &o, Setup1 &su) {
-    const int tid = threadIdx.x;
-    if (a.pro == PRO_RMS) {
+    const int n16 = o.v_off >> 4;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int k0 = tid + 256 * (2 * j), k1 = k0 + 256;
-            const int c0 = k0 < a.K ? k0 : a.K - 1, c1 = k1 < a.K ? k1 : a.K - 1;
-            su.sv[j] = u32x4{__float_as_uint(a.x[c0]), __float_as_uint(a.x[c1]), __float_as_uint(a.pro_w[c0]),
-                             __float_as_uint(a.pro_w[c1])};
-        }
-    } else {
-        const int n16 = o.v_off >> 4;
+    for (int j = 0; j < 8; j++) {
+        const int i = threadIdx.x + 256 * j;
+        su.sv[j] = ld16(a.xq + 16 * (i < n16 ? i : n16 - 1));
+    }
+}
+
+__device__ __forceinline__ void setup1_finish(const XqOff &o, const Setup1 &su, u32x4 *lds_v) {
+    const int n16 = o.v_off >> 4;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int i = tid + 256 * j;
-            su.sv[j] = ld16(a.xq + 16 * (i < n16 ? i : n16 - 1));
+    for (int j = 0; j < 8; j++)
+        if (threadIdx.x + 256 * j < n16) lds_v[threadIdx.x + 256 * j] = su.sv[j];
+}
+
+// PRO_RMSU_X: four consecutive inputs k..k+3 of one token, u = x * w, into
+// its LDS copy at dst: the digits, scale and half-group sums that emit_xq
+// gives for u, and the group's sum of x^2. Called by all 64 lanes of a
+// wavefront with k = k0 + 4 * lane (8 lanes per 32-element group); lanes with
+// in == false (whole groups, since K % 32 == 0) store nothing.
+__device__ __forceinline__ void emit4_rmsu(const f32x4 &x, const f32x4 &w, int k, bool in, uint8_t *dst,
+                                           const XqOff &o) {
+    const float u[4] = {x.x * w.x, x.y * w.y, x.z * w.z, x.w * w.w};
+    float m = fmaxf(fmaxf(fabsf(u[0]), fabsf(u[1])), fmaxf(fabsf(u[2]), fabsf(u[3])));
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    int E = 0;
+    (void)frexpf(m, &E);
+    if (E < -100) E = -100;
+    const float sc = ldexpf(1.0f, 20 - E);
+    uint32_t pa = 0, pb = 0, pc = 0;
+    int sx = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int X = (int)rintf(u[c] * sc);
+        const int dc = ((X + 64) & 127) - 64;
+        const int X1 = (X - dc) / 128;
+        const int db = ((X1 + 64) & 127) - 64;
+        const int da = (X1 - db) / 128;
+        pa |= ((uint32_t)da & 0xFFu) << (8 * c);
+        pb |= ((uint32_t)db & 0xFFu) << (8 * c);
+        pc |= ((uint32_t)dc & 0xFFu) << (8 * c);
+        sx += X;
+    }
+    sx += __shfl_xor(sx, 1, 64);
+    sx += __shfl_xor(sx, 2, 64);
+    double ss = ((double)x.x * x.x + (double)x.y * x.y) + ((double)x.z * x.z + (double)x.w * x.w);
+    ss += __shfl_xor(ss, 1, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    ss += __shfl_xor(ss, 4, 64);
+    if (!in) return;
+    const int g = k >> 5, l = k & 31;
+    *(uint32_t *)(dst + g * 96 + l) = pa;
+    *(uint32_t *)(dst + g * 96 + 32 + l) = pb;
+    *(uint32_t *)(dst + g * 96 + 64 + l) = pc;
+    if (l == 0) {
+        ((float *)(dst + o.f_off))[g] = ldexpf(1.0f, E - 20);
+        ((double *)(dst + o.ss_off))[g] = ss;
+    }
+    if ((k & 15) == 0) ((int *)(dst + o.sx_off))[k >> 4] = sx;
+}
+
+__device__ __forceinline__ f32x4 ld4f(const float *p) { return *(const f32x4 *)p; }
+
+// Split-phase PRO_RMSU_X setup of a single-token launch with K <= 4096: the
+// x and w loads are issued before the weight window, then converted into LDS.
+struct RmsX1 {
+    f32x4 x[4], w[4];
+};
+
+__device__ __forceinline__ void rmsx1_issue(const GArgs &a, RmsX1 &r) {
+    const int n4 = a.K >> 2;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int i = threadIdx.x + 256 * j, ic = i < n4 ? i : n4 - 1;
+        r.x[j] = ld4f(a.x + 4 * ic);
+        r.w[j] = ld4f(a.pro_w + 4 * ic);
+    }
+}
+
+__device__ __forceinline__ void rmsx1_finish(const GArgs &a, const XqOff &o, const RmsX1 &r, uint8_t *xl) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int k = 4 * (threadIdx.x + 256 * j);
+        emit4_rmsu(r.x[j], r.w[j], k, k < a.K, xl, o);
+    }
+}
+
+// PRO_RMSU_X setup for T tokens and any K, loads after the weight window.
+template <int T>
+__device__ __forceinline__ void rmsx_stage(const GArgs &a, const XqOff &o, uint8_t *xl) {
+    const int n4 = a.K >> 2;
+    for (int t = 0; t < T; t++) {
+        const float *x = a.x + (int64_t)t * a.xs;
+        for (int i0 = 0; i0 < n4; i0 += 1024) {
+            f32x4 xv[4], wv[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = i0 + threadIdx.x + 256 * j, ic = i < n4 ? i : n4 - 1;
+                xv[j] = ld4f(x + 4 * ic);
+                wv[j] = ld4f(a.pro_w + 4 * ic);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int k = 4 * (i0 + threadIdx.x + 256 * j);
+                emit4_rmsu(xv[j], wv[j], k, k < a.K, xl + t * o.v_off, o);
+            }
         }
     }
 }
 
-__device__ __forceinline__ void setup1_finish(const GArgs &a, const XqOff &o, const Setup1 &su, u32x4 *lds_v,
-                                              double *red) {
-    const int tid = threadIdx.x, K = a.K;
-    if (a.pro == PRO_RMS) {
-        double ss = 0;
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const float xv = __uint_as_float(j & 1 ? su.sv[j >> 1].y : su.sv[j >> 1].x);
-            if (tid + 256 * j < K) ss += (double)xv * xv;
-        }
-        ss = xjd::block_sum_d(ss, red);
-        const float sc = 1.0f / sqrtf((float)(ss / K) + a.eps);
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const int k = tid + 256 * j;
-            const float xv = __uint_as_float(j & 1 ? su.sv[j >> 1].y : su.sv[j >> 1].x);
-            const float wv = __uint_as_float(j & 1 ? su.sv[j >> 1].w : su.sv[j >> 1].z);
-            if (256 * j < K) xjd::emit_xq(xv * sc * wv, k, k < K, (uint8_t *)lds_v, o, false);
-        }
-    } else {
-        const int n16 = o.v_off >> 4;
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (tid + 256 * j < n16) lds_v[tid + 256 * j] = su.sv[j];
-    }
+// PRO_RMSU / PRO_RMSU_X: the norm scale of staged token t from its group sums of x^2
+// (double, fixed order). Called by every lane of a wavefront; each wavefront
+// computes it for itself and keeps it in a scalar register.
+__device__ __forceinline__ float rmsu_scale(const GArgs &a, const XqOff &o, const uint8_t *xl, int t) {
+    const double *ss = (const double *)(xl + t * o.v_off + o.ss_off);
+    const int lane = threadIdx.x & 63;
+    double s = 0;
+    for (int g = lane; g < o.G; g += 64) s += ss[g];
+    s = xjd::wave_sum_d(s);
+    const float sc = 1.0f / sqrtf((float)(s / a.K) + a.eps);
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sc)));
 }
 
 // -------------------------------------------------------------- kernels --
@@ -716,7 +746,6 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
     constexpr int NT = 256 / TS;
     __shared__ unsigned long long amax_sh[NT][T];
     __shared__ int flag_sh;
-    __shared__ double red_sh[4];
     const int K = a.K, nu = K / 64;
     const XqOff o = xq_off(K);
     const int tid = threadIdx.x, team = tid / TS, lane = tid % TS;
@@ -738,20 +767,34 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         for (int m = 0; m < NW; m++) win[m] = load_unit(sg.type, sg.w, sg.nblk, rb, u0 + m * TS);
     };
     int rg = blockIdx.x;
-    if (T == 1 && setup1_fits(a, o)) {
+    if (a.pro == PRO_RMSU_X) {
+        if (T == 1 && K <= 4096) {
+            RmsX1 r;
+            rmsx1_issue(a, r);
+            __builtin_amdgcn_sched_barrier(0);
+            first_units(rg);
+            __builtin_amdgcn_sched_barrier(0);
+            rmsx1_finish(a, o, r, (uint8_t *)lds_v);
+        } else {
+            first_units(rg);
+            rmsx_stage<T>(a, o, (uint8_t *)lds_v);
+        }
+    } else if (T == 1 && setup1_fits(o)) {
         Setup1 su;
         setup1_issue(a, o, su);
         __builtin_amdgcn_sched_barrier(0);
         first_units(rg);
         __builtin_amdgcn_sched_barrier(0);
-        setup1_finish(a, o, su, lds_v, red_sh);
+        setup1_finish(o, su, lds_v);
     } else {
         first_units(rg);
-        if (a.pro == PRO_RMS) prologue_rms<T>(a, o, (uint8_t *)lds_v, red_sh);
-        else stage_xq<T>(a, o, lds_v);
+        stage_xq<T>(a, o, lds_v);
     }
     __syncthreads();
     const uint8_t *xl = (const uint8_t *)lds_v;
+    float sc[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) sc[t] = a.pro == PRO_RMSU || a.pro == PRO_RMSU_X ? rmsu_scale(a, o, xl, t) : 1.f;
 
     for (;;) {
         const GSeg &sg = a.seg[seg_of(a, rg)];
@@ -771,7 +814,10 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
             else rows_f32<T, TS, 1>(sg.w, rr, K, lane, a.xq, o, acc);
         }
 #pragma unroll
-        for (int t = 0; t < T; t++) acc[0][t] = team_sum<TS>(acc[0][t]);
+        for (int t = 0; t < T; t++) {
+            acc[0][t] = team_sum<TS>(acc[0][t]);
+            acc[0][t] *= sc[t];
+        }
         epilogue<T, TS, 1>(a, sg, rg, team, lane, tid, acc, amax_sh, ein);
         if (a.post.mode == POST_SWIGLU) tail_swiglu<T, NT>(a, rg, &flag_sh);
         rg += gridDim.x;
@@ -818,6 +864,7 @@ size_t gemv_xq_bytes(int K) { return (size_t)(gemv_max_tile(K) > 0 ? gemv_max_ti
 int prep_launch(const GArgs &a, hipStream_t st) {
     if (a.T < 1 || a.K < 32 || a.K % 32 || !a.xq) return -1;
     if (a.pro == PRO_GATED_RMS && (a.group < 1 || a.K % a.group)) return -1;
+    if ((a.pro == PRO_RMSU || a.pro == PRO_GATED_RMS) && !a.pro_w) return -1;
     hipLaunchKernelGGL(prep_kernel, dim3((a.K + 255) / 256, a.T), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
@@ -861,14 +908,15 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
         const GSeg &s = a.seg[i];
         if ((s.type == XJ_Q4_K || s.type == XJ_Q6_K) && a.K % 256) return -1;
         if (s.type != XJ_Q4_K && s.type != XJ_Q6_K && s.type != XJ_Q8_0 && s.type != XJ_F32) return -1;
-        if (s.type == XJ_F32 && a.pro == PRO_RMS) return -1;   // F32 rows read v from a prep launch's xq
         if (s.n_rows < 1 || s.nwg != (s.n_rows + p.rows_per_group - 1) / p.rows_per_group) return -1;
         if (s.wg0 != (i ? a.seg[i - 1].wg0 + a.seg[i - 1].nwg : 0)) return -1;
         if (s.epi == EPI_CONV && (s.conv_k < 2 || s.conv_k > 8)) return -1;
+        if (s.type == XJ_F32 && a.pro == PRO_RMSU_X) return -1;   // F32 rows read v from a prep launch's xq
     }
     if (a.post.mode != POST_NONE && a.post.mode != POST_SWIGLU) return -1;
-    if (a.pro != PRO_NONE && a.pro != PRO_RMS) return -1;   // other prologues come prepared
-    if (a.pro == PRO_RMS && (!a.x || !a.pro_w)) return -1;
+    if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_RMSU_X) return -1;   // other prologues come prepared
+    if (a.pro == PRO_RMSU_X && (!a.x || !a.pro_w || ((uintptr_t)a.x & 15) || ((uintptr_t)a.pro_w & 15) || (a.xs & 3)))
+        return -1;
     if (a.post.mode == POST_SWIGLU &&
         (!a.post.xq || !a.post.cnt || a.nseg != 2 || a.seg[0].n_rows != a.seg[1].n_rows || a.seg[0].n_rows % 32 ||
          32 % p.rows_per_group)) return -1;

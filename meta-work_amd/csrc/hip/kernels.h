@@ -22,7 +22,12 @@ constexpr int kTileT = 8;        // tokens per GEMV launch (larger T is tiled)
 // next units unconditionally, reading up to 3 * 16 + 1 Q4_K blocks past a row.
 constexpr size_t kWeightPad = 16384;
 
-enum Pro { PRO_NONE = 0, PRO_RMS = 1, PRO_SWIGLU = 2, PRO_GATED_RMS = 3 };
+// Prologues. RMSNorm(x) * w = sc * (x * w) with sc = 1/sqrt(mean(x^2) + eps):
+// the activations are prepared from u = x * w with the per-group sums of x^2,
+// and the GEMV scales each row's dot product by sc.
+//   PRO_RMSU    the GEMV stages them from a prep launch's xq
+//   PRO_RMSU_X  the GEMV's work-groups build them from x in LDS (no prep launch)
+enum Pro { PRO_NONE = 0, PRO_SWIGLU = 2, PRO_GATED_RMS = 3, PRO_RMSU = 4, PRO_RMSU_X = 5 };
 enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_CONV = 2 };
 
 struct DevW {
@@ -50,7 +55,7 @@ struct GSeg {
     unsigned long long *amax;
 };
 
-// Tail that leaves the next GEMV's prepared activations (xq.h) behind, so the
+// Tails that leave the next GEMV's prepared activations (xq.h) behind, so the
 // next GEMV needs no prep launch:
 //   POST_SWIGLU  per 32-index group, the last of the work-groups that wrote
 //                its gate rows (segment 0) and up rows (segment 1) emits
@@ -59,13 +64,11 @@ enum Post { POST_NONE = 0, POST_SWIGLU = 2 };
 struct PostPrep {
     int32_t mode;
     uint8_t *xq;                   // token 0 of this tile
-    const float *w; float eps;
-    int32_t *cnt;                  // zero between launches; POST_SWIGLU: one per group
+    int32_t *cnt;                  // zero between launches, one per group
 };
 
 struct GArgs {
-    // prologue inputs: read by the prep kernel, or, with pro == PRO_RMS, by
-    // the GEMV itself (each work-group builds the activations in LDS)
+    // prologue inputs (read by the prep kernel, and by the GEMV for PRO_RMSU_X)
     const float *x;  int32_t xs;   // input rows x[t * xs + k]
     const float *x2; int32_t x2s;  // second input (SwiGLU up, gated-RMS z)
     int32_t pro;

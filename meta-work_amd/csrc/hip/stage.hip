@@ -154,9 +154,9 @@ struct Profile {
 };
 
 // One fused GEMV: segments sharing the input, its prepared activations
-// (built by the GEMV's own work-groups for an RMSNorm prologue, else by a
-// prep launch unless `prepared`), an optional tail that leaves the next
-// GEMV's activations behind, tiled over T. Token t of the tile that starts at
+// (built by a prep launch unless `prepared`, or, for an RMSNorm prologue over
+// quantized rows, by the GEMV's own work-groups), an optional tail that leaves
+// the next GEMV's activations behind, tiled over T. Token t of the tile that starts at
 // t0 uses xq + (t0 + t) * stride, so every buffer holds max_batch tokens.
 struct Gemv {
     GArgs a{};
@@ -173,8 +173,8 @@ struct Gemv {
         a.nseg++;
         return *this;
     }
-    Gemv &post(int mode, uint8_t *xq, int32_t *cnt, const float *w = nullptr, float eps = 0.f) {
-        a.post = PostPrep{mode, xq, w, eps, cnt};
+    Gemv &post(int mode, uint8_t *xq, int32_t *cnt) {
+        a.post = PostPrep{mode, xq, cnt};
         return *this;
     }
     // work-group ranges of the segments under the launch plan for (K, all rows)
@@ -202,8 +202,8 @@ struct Gemv {
             }
             a.inc_ptr = nullptr;
         }
-        // RMSNorm prologues run inside the GEMV's work-groups (F32 rows need a prep launch's xq)
-        bool inwg = a.pro == PRO_RMS && !prepared;
+        // RMSNorm prologues run inside the GEMV's work-groups (F32 rows read a prep launch's xq)
+        bool inwg = a.pro == PRO_RMSU && !prepared && !((uintptr_t)a.x & 15) && !(a.xs & 3) && !((uintptr_t)a.pro_w & 15);
         for (int i = 0; i < a.nseg; i++) inwg = inwg && a.seg[i].type != XJ_F32;
         const int64_t xs_in = xq_off(a.K).stride;
         const int64_t xs_out = a.post.mode != POST_NONE ? xq_off(a.seg[0].n_rows).stride : 0;
@@ -220,9 +220,11 @@ struct Gemv {
                 if (a.seg[i].amax) b.seg[i].amax = a.seg[i].amax + (int64_t)t0 * a.seg[i].nwg;
             }
             if (t0 + b.T < T) b.inc_ptr = nullptr;
-            if (!inwg) {
+            if (inwg) {
+                b.pro = PRO_RMSU_X;
+            } else {
                 if (!prof && !prepared && prep_launch(b, st)) return -1;
-                b.pro = PRO_NONE;   // the GEMV reads xq
+                if (b.pro != PRO_RMSU) b.pro = PRO_NONE;   // the GEMV reads xq
             }
             if (gemv_launch(b, st)) return -1;
         }
@@ -232,16 +234,16 @@ struct Gemv {
 
 // --------------------------------------------------------------- layers --
 
-// Layer il on T tokens of x. The GEMVs that read the residual stream apply
-// their RMSNorm inside their own work-groups; every other prologue is
-// produced by the kernel before its GEMV: the down input by gate|up, the
-// ssm_out input by the DeltaNet kernel, the wo input by attention.
+// Layer il on T tokens of x. The GEMVs that read the residual stream build
+// their RMSNorm activations inside their own work-groups; every other
+// prologue is produced by the kernel before its GEMV: the down input by
+// gate|up, the ssm_out input by the DeltaNet kernel, the wo input by attention.
 int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, hipStream_t st, Profile *pf = nullptr) {
     const xj_hparams &hp = S->s.m->hp;
     HLayer &L = S->L[il - S->s.l0];
     const int E = hp.n_embd, FF = hp.n_ff;
     auto rms_in = [&](Gemv &g, const float *w) {
-        g.a.x = x; g.a.xs = E; g.a.pro = PRO_RMS; g.a.pro_w = w; g.a.eps = hp.eps;
+        g.a.x = x; g.a.xs = E; g.a.pro = PRO_RMSU; g.a.pro_w = w; g.a.eps = hp.eps;
     };
     if (L.rec) {
         const int CD = hp.conv_dim, DI = hp.d_inner, Hv = hp.h_v;
@@ -313,7 +315,7 @@ int enqueue_layers(HStage *S, float *x, int T, int keep_n, bool inc, hipStream_t
 int enqueue_head(HStage *S, const float *x, int T, float *logits, hipStream_t st, Profile *pf = nullptr) {
     const xj_hparams &hp = S->s.m->hp;
     Gemv h(S->xq_e, pf);
-    h.a.x = x; h.a.xs = hp.n_embd; h.a.pro = PRO_RMS; h.a.pro_w = S->out_norm; h.a.eps = hp.eps;
+    h.a.x = x; h.a.xs = hp.n_embd; h.a.pro = PRO_RMSU; h.a.pro_w = S->out_norm; h.a.eps = hp.eps;
     h.seg(S->output, logits, (int)S->output.n_rows, EPI_STORE);
     h.a.seg[0].amax = S->amax;
     return h.run(T, st);

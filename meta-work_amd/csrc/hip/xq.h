@@ -9,6 +9,8 @@
 //                         |X| <= 2^20, |a| <= 64, b, c in [-64, 63]
 //   f   [G] float         2^(E_g - 20), where max|v| over the group < 2^E_g
 //   sx  [2G] int32        sum of X over each 16-element half of the group
+//   ss  [G] double        for an RMSNorm input stored as u = x * w: sum of x^2
+//                         over the group (the consumer forms the norm's scale)
 //   v   [K] float         v itself (read by F32 rows only)
 // Integer dot products of quantized weights with X are exact in 32 bits for
 // every block type, so sub-block sums do not depend on the summation order.
@@ -20,14 +22,15 @@
 namespace xjk {
 
 struct XqOff {
-    int G, f_off, sx_off, v_off, stride;   // bytes; v_off = the LDS bytes per token
+    int G, f_off, sx_off, ss_off, v_off, stride;   // bytes; v_off = the LDS bytes per token
 };
 __host__ __device__ inline XqOff xq_off(int K) {
     XqOff o;
     o.G = K / 32;
     o.f_off = o.G * 96;
     o.sx_off = o.f_off + ((o.G * 4 + 15) & ~15);
-    o.v_off = o.sx_off + ((o.G * 8 + 15) & ~15);
+    o.ss_off = o.sx_off + ((o.G * 8 + 15) & ~15);
+    o.v_off = o.ss_off + ((o.G * 8 + 15) & ~15);
     o.stride = (o.v_off + K * 4 + 255) & ~255;
     return o;
 }
@@ -75,6 +78,14 @@ __device__ __forceinline__ void emit_xq(float v, int k, bool in, uint8_t *dst, c
     if (l == 0) ((float *)(dst + o.f_off))[g] = ldexpf(1.0f, E - 20);
     if ((k & 15) == 0) ((int *)(dst + o.sx_off))[k >> 4] = sx;
     if (with_v) ((float *)(dst + o.v_off))[k] = v;
+}
+
+// Sum of x^2 (double) over the 32 lanes of a half-wavefront, in a fixed
+// butterfly order; every lane of the half gets the sum.
+__device__ __forceinline__ double group_ss(float x) {
+    double s = (double)x * x;
+    for (int off = 1; off < 32; off <<= 1) s += __shfl_xor(s, off, 64);
+    return s;
 }
 
 // Cross-work-group hand-off inside one launch. The producers store the
