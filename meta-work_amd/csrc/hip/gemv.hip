@@ -573,52 +573,45 @@ __device__ __forceinline__ void tail_swiglu(const GArgs &a, int rg, int *flag_sh
     xjd::emit_xq(v, k, in, a.post.xq + (int64_t)(in ? t : 0) * o.stride, o);
 }
 
-// Copy the T tokens' prepared activations (digits, scales, sums) into LDS,
-// eight 16-byte loads per thread in flight at a time.
+// Asynchronous global -> LDS copy of n16 16-byte chunks by the work-group
+// (global_load_lds_dwordx4: lane l of a wavefront writes LDS base + 16 * l).
+// Issued before the weight window, the copies hold no registers, and waiting
+// for them (vmcnt drains in issue order) does not wait for the weights.
+// Completion: the caller's wait for vmcnt and barrier.
+__device__ __forceinline__ void dma_lds(const uint8_t *src, uint8_t *lds, int n16) {
+    const int w = threadIdx.x >> 6;
+    for (int j0 = 0; j0 < n16; j0 += 256) {
+        const int i = j0 + threadIdx.x;
+        if (i < n16)
+            __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1))) *)(src + 16 * (int64_t)i),
+                                             (void __attribute__((address_space(3))) *)(lds + 16 * (j0 + 64 * w)),
+                                             16, 0, 0);
+    }
+}
+
+// Waits until at most N vector-memory operations of the wavefront are
+// outstanding (gfx9 s_waitcnt encoding; expcnt and lgkmcnt not waited for).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Work-group barrier without a memory fence (which would wait for every
+// outstanding load, the weight window included); the LDS-DMA data it
+// publishes is complete once each wavefront's vmcnt covers it.
+__device__ __forceinline__ void barrier_raw() { asm volatile("s_barrier" ::: "memory"); }
+// Work-group barrier ordering LDS accesses only.
+__device__ __forceinline__ void barrier_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// The T tokens' prepared activations, [0, v_off) of each, into LDS.
 template <int T>
-__device__ __forceinline__ void stage_xq(const GArgs &a, const XqOff &o, u32x4 *lds_v) {
-    const int n16 = o.v_off >> 4;
-    for (int t = 0; t < T; t++) {
-        const uint8_t *src = a.xq + (int64_t)t * o.stride;
-        u32x4 *dst = lds_v + t * n16;
-        for (int i0 = threadIdx.x; i0 < n16; i0 += 256 * 8) {
-            u32x4 v[8];
+__device__ __forceinline__ void dma_xq(const GArgs &a, const XqOff &o, uint8_t *lds) {
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int i = i0 + 256 * j;
-                v[j] = ld16(src + 16 * (i < n16 ? i : n16 - 1));
-            }
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                if (i0 + 256 * j < n16) dst[i0 + 256 * j] = v[j];
-        }
-    }
-}
-
-// Split-phase LDS staging for single-token launches: the staging loads are
-// issued before the weight window, so that waiting for them (vmcnt drains in
-// issue order) does not wait for the weights too. 8 x 16 bytes per thread
-// (v_off <= 32 KB).
-struct Setup1 {
-    u32x4 sv[8];
-};
-
-__device__ __forceinline__ bool setup1_fits(const XqOff &o) { return (o.v_off >> 4) <= 256 * 8; }
-
-__device__ __forceinline__ void setup1_issue(const GArgs &a, const XqOff &o, Setup1 &su) {
-    const int n16 = o.v_off >> 4;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int i = threadIdx.x + 256 * j;
-        su.sv[j] = ld16(a.xq + 16 * (i < n16 ? i : n16 - 1));
-    }
-}
-
-__device__ __forceinline__ void setup1_finish(const XqOff &o, const Setup1 &su, u32x4 *lds_v) {
-    const int n16 = o.v_off >> 4;
-#pragma unroll
-    for (int j = 0; j < 8; j++)
-        if (threadIdx.x + 256 * j < n16) lds_v[threadIdx.x + 256 * j] = su.sv[j];
+    for (int t = 0; t < T; t++) dma_lds(a.xq + (int64_t)t * o.stride, lds + t * o.v_off, o.v_off >> 4);
 }
 
 // PRO_RMSU_X: four consecutive inputs k..k+3 of one token, u = x * w, into
@@ -671,27 +664,19 @@ __device__ __forceinline__ void emit4_rmsu(const f32x4 &x, const f32x4 &w, int k
 
 __device__ __forceinline__ f32x4 ld4f(const float *p) { return *(const f32x4 *)p; }
 
-// Split-phase PRO_RMSU_X setup of a single-token launch with K <= 4096: the
-// x and w loads are issued before the weight window, then converted into LDS.
-struct RmsX1 {
-    f32x4 x[4], w[4];
-};
-
-__device__ __forceinline__ void rmsx1_issue(const GArgs &a, RmsX1 &r) {
-    const int n4 = a.K >> 2;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int i = threadIdx.x + 256 * j, ic = i < n4 ? i : n4 - 1;
-        r.x[j] = ld4f(a.x + 4 * ic);
-        r.w[j] = ld4f(a.pro_w + 4 * ic);
-    }
+// PRO_RMSU_X for a single token: x and w are copied into LDS after the
+// activations' area (at xl + v_off, 8 K bytes), then converted into it.
+__device__ __forceinline__ void rmsx1_issue(const GArgs &a, const XqOff &o, uint8_t *xl) {
+    dma_lds((const uint8_t *)a.x, xl + o.v_off, a.K >> 2);
+    dma_lds((const uint8_t *)a.pro_w, xl + o.v_off + 4 * a.K, a.K >> 2);
 }
 
-__device__ __forceinline__ void rmsx1_finish(const GArgs &a, const XqOff &o, const RmsX1 &r, uint8_t *xl) {
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int k = 4 * (threadIdx.x + 256 * j);
-        emit4_rmsu(r.x[j], r.w[j], k, k < a.K, xl, o);
+__device__ __forceinline__ void rmsx1_finish(const GArgs &a, const XqOff &o, uint8_t *xl) {
+    const f32x4 *xs = (const f32x4 *)(xl + o.v_off), *ws = (const f32x4 *)(xl + o.v_off + 4 * a.K);
+    const int n4 = a.K >> 2;
+    for (int i0 = 0; i0 < n4; i0 += 256) {
+        const int i = i0 + threadIdx.x, ic = i < n4 ? i : n4 - 1;
+        emit4_rmsu(xs[ic], ws[ic], 4 * i, i < n4, xl, o);
     }
 }
 
@@ -767,30 +752,26 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         for (int m = 0; m < NW; m++) win[m] = load_unit(sg.type, sg.w, sg.nblk, rb, u0 + m * TS);
     };
     int rg = blockIdx.x;
-    if (a.pro == PRO_RMSU_X) {
-        if (T == 1 && K <= 4096) {
-            RmsX1 r;
-            rmsx1_issue(a, r);
-            __builtin_amdgcn_sched_barrier(0);
-            first_units(rg);
-            __builtin_amdgcn_sched_barrier(0);
-            rmsx1_finish(a, o, r, (uint8_t *)lds_v);
-        } else {
-            first_units(rg);
-            rmsx_stage<T>(a, o, (uint8_t *)lds_v);
-        }
-    } else if (T == 1 && setup1_fits(o)) {
-        Setup1 su;
-        setup1_issue(a, o, su);
-        __builtin_amdgcn_sched_barrier(0);
+    uint8_t *lds = (uint8_t *)lds_v;
+    if (a.pro == PRO_RMSU_X && T > 1) {
         first_units(rg);
-        __builtin_amdgcn_sched_barrier(0);
-        setup1_finish(o, su, lds_v);
+        rmsx_stage<T>(a, o, lds);
+        __syncthreads();
     } else {
+        // LDS copies first, then the window's 5 * NW loads (load_unit issues
+        // five): waiting for vmcnt <= 5 * NW completes the copies only
+        if (a.pro == PRO_RMSU_X) rmsx1_issue(a, o, lds);
+        else dma_xq<T>(a, o, lds);
+        __builtin_amdgcn_sched_barrier(0);
         first_units(rg);
-        stage_xq<T>(a, o, lds_v);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm<5 * NW>();
+        barrier_raw();
+        if (a.pro == PRO_RMSU_X) {
+            rmsx1_finish(a, o, lds);
+            barrier_lds();
+        }
     }
-    __syncthreads();
     const uint8_t *xl = (const uint8_t *)lds_v;
     float sc[T];
 #pragma unroll
@@ -869,9 +850,16 @@ int prep_launch(const GArgs &a, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// Dynamic LDS of a launch: the T tokens' activations, and for a single-token
+// PRO_RMSU_X launch the copies of x and w after them.
+static size_t gemv_lds_bytes(const GArgs &a) {
+    const size_t b = (size_t)a.T * xq_off(a.K).v_off;
+    return a.pro == PRO_RMSU_X && a.T == 1 ? b + 8 * (size_t)a.K : b;
+}
+
 template <int T, int TS, int MU = 0>
 static hipError_t launch_v(const GArgs &a, int grid, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_kernel<T, TS, MU>), dim3(grid), dim3(256), (size_t)T * xq_off(a.K).v_off, st, a);
+    hipLaunchKernelGGL((gemv_kernel<T, TS, MU>), dim3(grid), dim3(256), gemv_lds_bytes(a), st, a);
     return hipGetLastError();
 }
 
@@ -900,7 +888,7 @@ static hipError_t launch_ts(const GArgs &a, int grid, hipStream_t st) {
 
 int gemv_launch(const GArgs &a, hipStream_t st) {
     if (a.T < 1 || a.T > kTileT || a.nseg < 1 || a.nseg > kMaxSeg || a.K < 32 || a.K % 32 || !a.xq) return -1;
-    if ((size_t)a.T * xq_off(a.K).v_off > (size_t)g_lds_max) return -1;
+    if (gemv_lds_bytes(a) > (size_t)g_lds_max) return -1;
     int64_t total = 0;
     for (int i = 0; i < a.nseg; i++) total += a.seg[i].n_rows;
     const GemvPlan p = gemv_plan(a.K, total);
