@@ -175,7 +175,7 @@ __device__ __forceinline__ void q4k_unit(const RawU &w, int p, int g0, const uin
         for (int t = 0; t < T; t++) {
             const uint8_t *xt = xl + t * ldsT;
             u32x4 pa[2], pb[2], pc[2];
-            planes<8>(xt + g * 96, pa, pb, pc);
+            planes<8>(xt + g * kDigStride, pa, pb, pc);
             const float f = ((const float *)(xt + o.f_off))[g];
             const int2 sxp = ((const int2 *)(xt + o.sx_off))[g];
             const float SX = (float)(sxp.x + sxp.y);
@@ -212,7 +212,7 @@ __device__ __forceinline__ void q6k_unit(const RawU &w, int hl, int gb, const ui
         for (int t = 0; t < T; t++) {
             const uint8_t *xt = xl + t * ldsT;
             u32x4 pa[1], pb[1], pc[1];
-            planes<4>(xt + g * 96 + 16 * hl, pa, pb, pc);
+            planes<4>(xt + g * kDigStride + 16 * hl, pa, pb, pc);
             const float f = ((const float *)(xt + o.f_off))[g];
             const int sxh = ((const int *)(xt + o.sx_off))[2 * g + hl];
             const int S = qdot<4>(q6, pa, pb, pc) - 32 * sxh;
@@ -230,7 +230,7 @@ __device__ __forceinline__ void unit_q80(const u32x4 (&qa)[RPT], const u32x4 (&q
     for (int t = 0; t < T; t++) {
         const uint8_t *xt = xl + t * ldsT;
         u32x4 pa[2], pb[2], pc[2];
-        planes<8>(xt + u * 96, pa, pb, pc);
+        planes<8>(xt + u * kDigStride, pa, pb, pc);
         const float f = ((const float *)(xt + o.f_off))[u];
 #pragma unroll
         for (int i = 0; i < RPT; i++) {
@@ -254,8 +254,19 @@ __device__ __forceinline__ void unit_q80(const u32x4 (&qa)[RPT], const u32x4 (&q
 // through a control-flow merge must complete before the merge); used for the
 // window issued before a work-group's LDS setup. Q4_K re-reads header bytes
 // for e and f, other types read the row's first bytes; the extra values are
-// ignored.
+// ignored. Q4 (a launch whose rows are all Q4_K): the three Q4_K loads only.
+template <bool Q4>
 __device__ __forceinline__ RawU load_unit(uint32_t type, const uint8_t *__restrict__ W, int64_t nblk, int64_t rb, int u) {
+    if constexpr (Q4) {
+        const uint8_t *blk = W + (rb + (u >> 2)) * 144;
+        RawU r;
+        r.a = ld16(blk);
+        r.b = ld16(blk + 16 + 32 * (u & 3));
+        r.c = ld16(blk + 32 + 32 * (u & 3));
+        r.e = u32x2{0u, 0u};
+        r.f = 0u;
+        return r;
+    }
     const bool q4 = type == XJ_Q4_K, q6 = type == XJ_Q6_K;
     const int h = (u >> 1) & 1, hl = u & 1;
     const int64_t b = rb + (u >> 2);
@@ -310,16 +321,20 @@ __device__ __forceinline__ RawU ld_q6k(const Q6Ptr &q, int64_t k) {
 }
 
 // Units a lane has in flight ahead of the one it computes (MU > 0), and the
-// window of units loaded before the work-group's LDS setup.
-template <int MU>
+// window of units loaded before the work-group's LDS setup. Two units: deeper
+// windows (up to all MU units up front) measured slower on decode-sized
+// launches, whose activation copies then queue behind more weight requests.
+// Q4 (Q4_K-only launches): three loads per unit instead of five.
+template <int MU, bool Q4>
 struct Win {
-    static constexpr int PD = MU <= 1 ? 0 : MU == 2 ? 1 : 2;   // MU <= 4 fits 168 VGPRs
+    static constexpr int PD = MU <= 1 ? 0 : 1;
     static constexpr int N = PD + 1;
+    static constexpr int LOADS = (Q4 ? 3 : 5) * N;   // vector-memory instructions of the window
 };
 
-template <int T, int TS, int MU>
+template <int T, int TS, int MU, bool Q4>
 __device__ __forceinline__ void rows_q4k(const uint8_t *__restrict__ W, int64_t rb, int nu, int lane,
-                                         const RawU (&win)[Win<MU>::N], const uint8_t *xl, int ldsT, const XqOff &o,
+                                         const RawU (&win)[Win<MU, Q4>::N], const uint8_t *xl, int ldsT, const XqOff &o,
                                          float (&acc)[T]) {
     constexpr int DB = TS / 4;
     const int p = lane & 3;
@@ -327,7 +342,7 @@ __device__ __forceinline__ void rows_q4k(const uint8_t *__restrict__ W, int64_t 
     const uint8_t *blk = W + (rb + (lane >> 2)) * 144;
     RawU cur = win[0];
     if constexpr (MU > 0) {
-        constexpr int PD = Win<MU>::PD;
+        constexpr int PD = Win<MU, Q4>::PD;
         RawU r[MU];
 #pragma unroll
         for (int m = 0; m <= PD; m++) r[m] = win[m];
@@ -351,7 +366,7 @@ __device__ __forceinline__ void rows_q4k(const uint8_t *__restrict__ W, int64_t 
 
 template <int T, int TS, int MU>
 __device__ __forceinline__ void rows_q6k(const uint8_t *__restrict__ W, int64_t nblk, int64_t rb, int nu, int lane,
-                                         const RawU (&win)[Win<MU>::N], const uint8_t *xl, int ldsT, const XqOff &o,
+                                         const RawU (&win)[Win<MU, false>::N], const uint8_t *xl, int ldsT, const XqOff &o,
                                          float (&acc)[T]) {
     constexpr int DB = TS / 4;
     const int h = (lane >> 1) & 1, hl = lane & 1;
@@ -361,7 +376,7 @@ __device__ __forceinline__ void rows_q6k(const uint8_t *__restrict__ W, int64_t 
     const int gb0 = 8 * (lane >> 2) + 4 * h;
     RawU cur = win[0];
     if constexpr (MU > 0) {
-        constexpr int PD = Win<MU>::PD;
+        constexpr int PD = Win<MU, false>::PD;
         RawU r[MU];
 #pragma unroll
         for (int m = 0; m <= PD; m++) r[m] = win[m];
@@ -459,18 +474,21 @@ struct EpiIn {
 };
 
 template <int T>
-__device__ __forceinline__ void epi_load(const GSeg &sg, int64_t r, bool mine, EpiIn<T> &e) {
-    if (!mine) return;
-    if (sg.epi == EPI_ADD) {
+__device__ __forceinline__ void epi_load(const GSeg &sg, int64_t r, EpiIn<T> &e) {
+    // Unconditional loads at clamped in-row addresses (a loaded value that
+    // reaches its register through a branch would make the first use of the
+    // weight window wait for every outstanding load); values an epilogue does
+    // not use are ignored. y is valid memory for every epilogue.
+    const bool conv = sg.epi == EPI_CONV && sg.conv_k <= kConvPre;
+    const int KC = conv ? sg.conv_k : 2;
+    const float *ps = conv ? sg.conv_state + r * (KC - 1) : sg.y + r;
+    const float *pw = conv ? sg.conv_w + r * KC : sg.y + r;
 #pragma unroll
-        for (int t = 0; t < T; t++) e.y[t] = sg.y[(int64_t)t * sg.ys + r];
-    } else if (sg.epi == EPI_CONV && sg.conv_k <= kConvPre) {
-        const int KC = sg.conv_k;
+    for (int t = 0; t < T; t++) e.y[t] = sg.y[(int64_t)t * sg.ys + r];
 #pragma unroll
-        for (int k = 0; k < kConvPre; k++) {
-            if (k + 1 < KC) e.st[k] = sg.conv_state[r * (KC - 1) + k];
-            if (k < KC) e.wc[k] = sg.conv_w[r * KC + k];
-        }
+    for (int k = 0; k < kConvPre; k++) {
+        if (k < kConvPre - 1) e.st[k < kConvPre - 1 ? k : 0] = ps[k < KC - 2 ? k : KC - 2];
+        e.wc[k] = pw[k < KC - 1 ? k : KC - 1];
     }
 }
 
@@ -623,9 +641,11 @@ __device__ __forceinline__ void emit4_rmsu(const f32x4 &x, const f32x4 &w, int k
                                            const XqOff &o) {
     const float u[4] = {x.x * w.x, x.y * w.y, x.z * w.z, x.w * w.w};
     float m = fmaxf(fmaxf(fabsf(u[0]), fabsf(u[1])), fmaxf(fabsf(u[2]), fabsf(u[3])));
-    m = fmaxf(m, __shfl_xor(m, 1, 64));
-    m = fmaxf(m, __shfl_xor(m, 2, 64));
-    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    // reductions over the 8 lanes of the group (quad butterflies, then the
+    // half-row mirror joins the two quads), over its 4 lanes for sx
+    m = fmaxf(m, xjd::dpp<0xB1>(m));
+    m = fmaxf(m, xjd::dpp<0x4E>(m));
+    m = fmaxf(m, xjd::dpp<0x141>(m));
     int E = 0;
     (void)frexpf(m, &E);
     if (E < -100) E = -100;
@@ -644,17 +664,17 @@ __device__ __forceinline__ void emit4_rmsu(const f32x4 &x, const f32x4 &w, int k
         pc |= ((uint32_t)dc & 0xFFu) << (8 * c);
         sx += X;
     }
-    sx += __shfl_xor(sx, 1, 64);
-    sx += __shfl_xor(sx, 2, 64);
+    sx += xjd::dpp_i<0xB1>(sx);
+    sx += xjd::dpp_i<0x4E>(sx);
     double ss = ((double)x.x * x.x + (double)x.y * x.y) + ((double)x.z * x.z + (double)x.w * x.w);
-    ss += __shfl_xor(ss, 1, 64);
-    ss += __shfl_xor(ss, 2, 64);
-    ss += __shfl_xor(ss, 4, 64);
+    ss += xjd::dpp_d<0xB1>(ss);
+    ss += xjd::dpp_d<0x4E>(ss);
+    ss += xjd::dpp_d<0x141>(ss);
     if (!in) return;
     const int g = k >> 5, l = k & 31;
-    *(uint32_t *)(dst + g * 96 + l) = pa;
-    *(uint32_t *)(dst + g * 96 + 32 + l) = pb;
-    *(uint32_t *)(dst + g * 96 + 64 + l) = pc;
+    *(uint32_t *)(dst + g * kDigStride + l) = pa;
+    *(uint32_t *)(dst + g * kDigStride + 32 + l) = pb;
+    *(uint32_t *)(dst + g * kDigStride + 64 + l) = pc;
     if (l == 0) {
         ((float *)(dst + o.f_off))[g] = ldexpf(1.0f, E - 20);
         ((double *)(dst + o.ss_off))[g] = ss;
@@ -711,21 +731,20 @@ __device__ __forceinline__ float rmsu_scale(const GArgs &a, const XqOff &o, cons
     const int lane = threadIdx.x & 63;
     double s = 0;
     for (int g = lane; g < o.G; g += 64) s += ss[g];
-    s = xjd::wave_sum_d(s);
-    const float sc = 1.0f / sqrtf((float)(s / a.K) + a.eps);
-    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sc)));
+    s = xjd::wave_sum_d(s);   // uniform: the wavefront's scale lives in scalar registers
+    return 1.0f / sqrtf((float)(s / a.K) + a.eps);
 }
 
 // -------------------------------------------------------------- kernels --
-// A row group is 256/TS rows, one per team of TS lanes; MU > 0: every lane
-// owns at most MU units of a row (single-token launches, which are kept to
-// three work-groups per CU so that a launch of up to 3 x CUs work-groups runs
-// in one wave). The work-group
-// issues the first unit of its first row group, stages the T tokens'
-// prepared activations in LDS meanwhile, then loops over row groups with
-// stride gridDim.x (prefetching each next group's first unit after the
-// previous group's epilogue).
-template <int T, int TS, int MU>
+// A row group is 256/TS rows, one per team of TS lanes. MU > 0 (single-token
+// launches with one work-group per row group, kept to three work-groups per
+// CU so that up to 3 x CUs of them run in one wave): every lane owns at most
+// MU units of its row, and the work-group issues the weight window of its row
+// group while the T tokens' activations are copied into LDS. MU == 0: the
+// same for the first unit, then a loop over row groups with stride gridDim.x
+// that prefetches each next group's first unit after the previous group's
+// epilogue.
+template <int T, int TS, int MU, bool Q4>
 __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a) {
     extern __shared__ u32x4 lds_v[];
     constexpr int NT = 256 / TS;
@@ -742,14 +761,14 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
     auto blocks_per_row = [&](uint32_t type) { return (type == XJ_Q4_K || type == XJ_Q6_K) ? K / 256 : K / 32; };
     // the lane's first units of row group rg, loaded before the work that
     // precedes their use (units past the row read the tensor's padding)
-    constexpr int NW = Win<MU>::N;
+    constexpr int NW = Win<MU, Q4>::N;
     RawU win[NW];
     auto first_units = [&](int rg) {
         const GSeg &sg = a.seg[seg_of(a, rg)];
         const int64_t rb = row_of(sg, rg) * blocks_per_row(sg.type);
         const int u0 = lane < nu ? lane : nu - 1;
 #pragma unroll
-        for (int m = 0; m < NW; m++) win[m] = load_unit(sg.type, sg.w, sg.nblk, rb, u0 + m * TS);
+        for (int m = 0; m < NW; m++) win[m] = load_unit<Q4>(sg.type, sg.w, sg.nblk, rb, u0 + m * TS);
     };
     int rg = blockIdx.x;
     uint8_t *lds = (uint8_t *)lds_v;
@@ -758,14 +777,14 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         rmsx_stage<T>(a, o, lds);
         __syncthreads();
     } else {
-        // LDS copies first, then the window's 5 * NW loads (load_unit issues
-        // five): waiting for vmcnt <= 5 * NW completes the copies only
+        // LDS copies first, then the window's loads: waiting for vmcnt <=
+        // their number completes the copies only
         if (a.pro == PRO_RMSU_X) rmsx1_issue(a, o, lds);
         else dma_xq<T>(a, o, lds);
         __builtin_amdgcn_sched_barrier(0);
         first_units(rg);
         __builtin_amdgcn_sched_barrier(0);
-        wait_vm<5 * NW>();
+        wait_vm<Win<MU, Q4>::LOADS>();
         barrier_raw();
         if (a.pro == PRO_RMSU_X) {
             rmsx1_finish(a, o, lds);
@@ -781,12 +800,13 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         const GSeg &sg = a.seg[seg_of(a, rg)];
         const int64_t row = row_of(sg, rg), rb = row * blocks_per_row(sg.type);
         EpiIn<T> ein;
-        epi_load<T>(sg, row, lane == 0 && (int64_t)(rg - sg.wg0) * NT + team < sg.n_rows, ein);
+        epi_load<T>(sg, row, ein);
         float acc[1][T];
 #pragma unroll
         for (int t = 0; t < T; t++) acc[0][t] = 0.f;
-        if (sg.type == XJ_Q4_K) {
-            rows_q4k<T, TS, MU>(sg.w, rb, nu, lane, win, xl, o.v_off, o, acc[0]);
+        if (Q4 || sg.type == XJ_Q4_K) {
+            rows_q4k<T, TS, MU, Q4>(sg.w, rb, nu, lane, win, xl, o.v_off, o, acc[0]);
+        } else if constexpr (Q4) {
         } else if (sg.type == XJ_Q6_K) {
             rows_q6k<T, TS, MU>(sg.w, sg.nblk, rb, nu, lane, win, xl, o.v_off, o, acc[0]);
         } else {
@@ -802,7 +822,9 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         epilogue<T, TS, 1>(a, sg, rg, team, lane, tid, acc, amax_sh, ein);
         if (a.post.mode == POST_SWIGLU) tail_swiglu<T, NT>(a, rg, &flag_sh);
         rg += gridDim.x;
-        if (rg >= n_rg) break;
+        // MU > 0: one row group per work-group (the launch covers them all), so
+        // no window is carried around a loop edge
+        if (MU > 0 || rg >= n_rg) break;
         first_units(rg);
     }
     if (a.inc_ptr && blockIdx.x == 0 && tid == 0) *a.inc_ptr += a.inc_by;
@@ -857,17 +879,32 @@ static size_t gemv_lds_bytes(const GArgs &a) {
     return a.pro == PRO_RMSU_X && a.T == 1 ? b + 8 * (size_t)a.K : b;
 }
 
-template <int T, int TS, int MU = 0>
+template <int T, int TS, int MU = 0, bool Q4 = false>
 static hipError_t launch_v(const GArgs &a, int grid, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_kernel<T, TS, MU>), dim3(grid), dim3(256), gemv_lds_bytes(a), st, a);
+    hipLaunchKernelGGL((gemv_kernel<T, TS, MU, Q4>), dim3(grid), dim3(256), gemv_lds_bytes(a), st, a);
     return hipGetLastError();
+}
+
+static bool all_q4k(const GArgs &a) {
+    for (int i = 0; i < a.nseg; i++)
+        if (a.seg[i].type != XJ_Q4_K) return false;
+    return true;
 }
 
 template <int TS>
 static hipError_t launch_ts(const GArgs &a, int grid, hipStream_t st) {
     const int upl = (a.K / 64 + TS - 1) / TS;   // 64-element units per lane
+    const int n_rg = a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg;
     switch (a.T) {
     case 1:
+        if (grid < n_rg) return launch_v<1, TS, 0>(a, grid, st);   // work-groups loop over row groups
+        if (all_q4k(a) && upl <= 5) switch (upl) {
+            case 1: return launch_v<1, TS, 1, true>(a, grid, st);
+            case 2: return launch_v<1, TS, 2, true>(a, grid, st);
+            case 3: return launch_v<1, TS, 3, true>(a, grid, st);
+            case 4: return launch_v<1, TS, 4, true>(a, grid, st);
+            default: return launch_v<1, TS, 5, true>(a, grid, st);
+        }
         switch (upl) {
         case 1: return launch_v<1, TS, 1>(a, grid, st);
         case 2: return launch_v<1, TS, 2>(a, grid, st);
@@ -922,13 +959,16 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
 
 template <int TS>
 static void raise_ts(int bytes) {
-    const void *f[] = {(const void *)gemv_kernel<1, TS, 0>, (const void *)gemv_kernel<1, TS, 1>,
-                       (const void *)gemv_kernel<1, TS, 2>, (const void *)gemv_kernel<1, TS, 3>,
-                       (const void *)gemv_kernel<1, TS, 4>,
-                       (const void *)gemv_kernel<2, TS, 0>, (const void *)gemv_kernel<3, TS, 0>,
-                       (const void *)gemv_kernel<4, TS, 0>, (const void *)gemv_kernel<5, TS, 0>,
-                       (const void *)gemv_kernel<6, TS, 0>, (const void *)gemv_kernel<7, TS, 0>,
-                       (const void *)gemv_kernel<8, TS, 0>};
+    const void *f[] = {(const void *)gemv_kernel<1, TS, 0, false>, (const void *)gemv_kernel<1, TS, 1, false>,
+                       (const void *)gemv_kernel<1, TS, 2, false>, (const void *)gemv_kernel<1, TS, 3, false>,
+                       (const void *)gemv_kernel<1, TS, 4, false>,
+                       (const void *)gemv_kernel<1, TS, 1, true>, (const void *)gemv_kernel<1, TS, 2, true>,
+                       (const void *)gemv_kernel<1, TS, 3, true>, (const void *)gemv_kernel<1, TS, 4, true>,
+                       (const void *)gemv_kernel<1, TS, 5, true>,
+                       (const void *)gemv_kernel<2, TS, 0, false>, (const void *)gemv_kernel<3, TS, 0, false>,
+                       (const void *)gemv_kernel<4, TS, 0, false>, (const void *)gemv_kernel<5, TS, 0, false>,
+                       (const void *)gemv_kernel<6, TS, 0, false>, (const void *)gemv_kernel<7, TS, 0, false>,
+                       (const void *)gemv_kernel<8, TS, 0, false>};
     for (const void *k : f) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 

@@ -21,13 +21,16 @@
 
 namespace xjk {
 
+// Bytes per group of digits (the three planes).
+constexpr int kDigStride = 96;
+
 struct XqOff {
     int G, f_off, sx_off, ss_off, v_off, stride;   // bytes; v_off = the LDS bytes per token
 };
 __host__ __device__ inline XqOff xq_off(int K) {
     XqOff o;
     o.G = K / 32;
-    o.f_off = o.G * 96;
+    o.f_off = o.G * kDigStride;
     o.sx_off = o.f_off + ((o.G * 4 + 15) & ~15);
     o.ss_off = o.sx_off + ((o.G * 8 + 15) & ~15);
     o.v_off = o.ss_off + ((o.G * 8 + 15) & ~15);
@@ -72,9 +75,9 @@ __device__ __forceinline__ void emit_xq(float v, int k, bool in, uint8_t *dst, c
     const int sx = row16_sum_i(X);
     if (!in) return;
     const int g = k >> 5, l = k & 31;
-    dst[g * 96 + l] = (uint8_t)(int8_t)a;
-    dst[g * 96 + 32 + l] = (uint8_t)(int8_t)b;
-    dst[g * 96 + 64 + l] = (uint8_t)(int8_t)c;
+    dst[g * xjk::kDigStride + l] = (uint8_t)(int8_t)a;
+    dst[g * xjk::kDigStride + 32 + l] = (uint8_t)(int8_t)b;
+    dst[g * xjk::kDigStride + 64 + l] = (uint8_t)(int8_t)c;
     if (l == 0) ((float *)(dst + o.f_off))[g] = ldexpf(1.0f, E - 20);
     if ((k & 15) == 0) ((int *)(dst + o.sx_off))[k >> 4] = sx;
     if (with_v) ((float *)(dst + o.v_off))[k] = v;
