@@ -105,6 +105,26 @@ __device__ __forceinline__ double block_sum_d(double v, double *red) {
     for (int i = 0; i < nw; i++) s += red[i];
     return s;
 }
+// Two block-wide sums with one exchange (same order as two block_sum_d calls);
+// red must hold 2 * blockDim.x/64 doubles.
+__device__ __forceinline__ void block_sum2_d(double &a, double &b, double *red) {
+    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    a = wave_sum_d(a);
+    b = wave_sum_d(b);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+        red[w] = a;
+        red[nw + w] = b;
+    }
+    __syncthreads();
+    double s = 0, t = 0;
+    for (int i = 0; i < nw; i++) {
+        s += red[i];
+        t += red[nw + i];
+    }
+    a = s;
+    b = t;
+}
 __device__ __forceinline__ float block_max(float v, float *red) {
     const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     v = wave_max(v);

@@ -1,18 +1,18 @@
 // Gated DeltaNet recurrent update (gfx950).
 //
-// delta_kernel: the per-token body of attn_linear (src/xiaoju-pipe/core/xj_cpu.c:183-219)
+// delta_head_kernel: the per-token body of attn_linear (src/xiaoju-pipe/core/xj_cpu.c:183-219)
 // after the conv (which the qkv GEMV epilogue already applied): L2-normalise
 // q and k of key head hk = hv % Hk (double sum, x / sqrt(sum + eps)), then for
 // every value row j of head hv
 //     S_j <- exp(softplus(alpha + dt) * A) * S_j
 //     delta_j = (v_j - S_j . k) * sigmoid(beta)
 //     S_j <- S_j + k * delta_j,   o_j = (S_j . q) / sqrt(S)
-// With a.xq set, the last work-group of each head also applies the gated
-// RMSNorm of o (xj_cpu.c:215-217) and writes the ssm_out GEMV's prepared
-// activations, so that GEMV needs no prep launch.
+// With a.xq set, the kernel also applies the gated RMSNorm of o
+// (xj_cpu.c:215-217) and writes the ssm_out GEMV's prepared activations, so
+// that GEMV needs no prep launch.
 //
-// Mapping: work-group (hv, 16 value rows); a 16-lane team owns one row j and
-// each lane keeps S/16 consecutive entries of it in registers across all T
+// Mapping: one work-group per value head; a 16-lane team owns S/64 rows, and
+// each lane keeps S/16 consecutive entries of each in registers across all T
 // tokens, so the 64 KB (S=128) head state is read and written once per call.
 // Per element the updates are the reference's own: m*eg, fma(m, k, sk),
 // fma(k, delta, m), fma(m, q, acc); only the 16 lane partial sums are combined
@@ -68,56 +68,66 @@ __device__ __forceinline__ float rule_step(float (&m)[S / 16], const float *ks, 
     return xjd::row16_sum(acc);
 }
 
+// 1024 threads: team r16 = tid / 16 (of 64) owns rows j = r16 + 64 * r,
+// r < S / 64, so 16 wavefronts share the head's latency; every operand of a
+// token is loaded at once. The work-group holds all of the head's outputs, so
+// the gated RMSNorm needs no hand-off between work-groups.
 template <int S>
-__global__ __launch_bounds__(256) void delta_kernel(const DeltaArgs a) {
-    constexpr int IPL = S / 16;
-    const int hv = blockIdx.x, tid = threadIdx.x;
-    const int j = blockIdx.y * 16 + (tid >> 4), l16 = tid & 15, i0 = l16 * IPL;
+__global__ __launch_bounds__(1024) void delta_head_kernel(const DeltaArgs a) {
+    constexpr int IPL = S / 16, NR = S / 64, NW = 1024 / 64;
+    const int hv = blockIdx.x, tid = threadIdx.x, r16 = tid >> 4, l16 = tid & 15, i0 = l16 * IPL;
     const int hk = hv % a.Hk;
-    __shared__ float qs[S], ks[S];
-    __shared__ double red[2][4];
-    float m[IPL];
-    float *Mp = a.state + ((int64_t)hv * S + j) * S + i0;
-    load_row<S>(Mp, m);
+    __shared__ float qs[S], ks[S], os[S];
+    __shared__ double red[2 * NW];
+    float m[NR][IPL];
+#pragma unroll
+    for (int r = 0; r < NR; r++) load_row<S>(a.state + ((int64_t)hv * S + r16 + 64 * r) * S + i0, m[r]);
+    const float dt = a.dt[hv], A = a.A[hv];
+    const bool in = tid < S;
+    const float nw = a.norm_w && in ? a.norm_w[tid] : 0.f;
     for (int t = 0; t < a.T; t++) {
         const float *row = a.qkv + (int64_t)t * a.qkv_s;
-        const float qv = tid < S ? row[hk * S + tid] : 0.f, kv = tid < S ? row[a.k_off + hk * S + tid] : 0.f;
-        const double sq = xjd::block_sum_d((double)qv * qv, red[0]);
-        const double sk2 = xjd::block_sum_d((double)kv * kv, red[1]);
-        if (tid < S) {
+        const float qv = in ? row[hk * S + tid] : 0.f, kv = in ? row[a.k_off + hk * S + tid] : 0.f;
+        const float bt = a.beta[(int64_t)t * a.beta_s + hv], al = a.alpha[(int64_t)t * a.alpha_s + hv];
+        float vj[NR];
+#pragma unroll
+        for (int r = 0; r < NR; r++) vj[r] = row[a.v_off + hv * S + r16 + 64 * r];
+        const float zv = a.xq && in ? a.z[(int64_t)t * a.z_s + hv * S + tid] : 0.f;
+        double sq = (double)qv * qv, sk2 = (double)kv * kv;
+        xjd::block_sum2_d(sq, sk2, red);
+        if (in) {
             qs[tid] = qv * (1.0f / sqrtf((float)sq + a.eps));
             ks[tid] = kv * (1.0f / sqrtf((float)sk2 + a.eps));
         }
+        const float b = xjd::sigm(bt);
+        const float eg = expf(xjd::softplus(al + dt) * A);
         __syncthreads();
-        const float b = xjd::sigm(a.beta[(int64_t)t * a.beta_s + hv]);
-        const float g = xjd::softplus(a.alpha[(int64_t)t * a.alpha_s + hv] + a.dt[hv]) * a.A[hv];
-        const float eg = expf(g);
-        const float vj = row[a.v_off + hv * S + j];
-        const float o = rule_step<S>(m, ks, qs, i0, eg, b, vj);
-        if (l16 == 0) {
-            float *op = a.out + (int64_t)t * a.out_s + hv * S + j;
-            if (a.xq) xjd::store_sys(op, o * a.qscale);   // read by the head's last work-group
-            else *op = o * a.qscale;
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const float o = rule_step<S>(m[r], ks, qs, i0, eg, b, vj[r]) * a.qscale;
+            const int j = r16 + 64 * r;
+            if (l16 == 0) {
+                os[j] = o;
+                a.out[(int64_t)t * a.out_s + hv * S + j] = o;
+            }
+            if (t < a.keep_n) store_row<S>(a.ck + (((int64_t)t * a.Hv + hv) * S + j) * S + i0, m[r]);
         }
-        if (t < a.keep_n) store_row<S>(a.ck + (((int64_t)t * a.Hv + hv) * S + j) * S + i0, m);
         __syncthreads();
+        if (a.xq) {
+            // gated RMSNorm (xj_cpu.c:215-217) of the head's outputs into the
+            // ssm_out GEMV's prepared activations
+            const float ov = in ? os[tid] : 0.f;
+            const double ss = xjd::block_sum_d((double)ov * ov, red);
+            const float gsc = 1.0f / sqrtf((float)(ss / S) + a.eps);
+            if (tid < (S + 63) / 64 * 64) {   // wavefronts holding outputs
+                const XqOff o = xq_off(a.Hv * S);
+                const float v = in ? ov * gsc * nw * xjd::silu(zv) : 0.f;
+                xjd::emit_xq(v, hv * S + tid, in, a.xq + (int64_t)t * o.stride, o);
+            }
+        }
     }
-    store_row<S>(Mp, m);
-    if (!a.xq) return;
-    // gated RMSNorm tail: the last of the head's S/16 work-groups emits the
-    // ssm_out GEMV's activations norm(o) * norm_w * silu(z) for every token
-    __shared__ int flag_sh;
-    if (!xjd::arrive_last(a.cnt + hv, S / 16, &flag_sh)) return;
-    const XqOff o = xq_off(a.Hv * S);
-    const bool in = tid < S;
-    for (int t = 0; t < a.T; t++) {
-        const float ov = in ? xjd::load_sys(a.out + (int64_t)t * a.out_s + hv * S + tid) : 0.f;
-        const double ss = xjd::block_sum_d((double)ov * ov, red[0]);
-        const float gsc = 1.0f / sqrtf((float)(ss / S) + a.eps);
-        const float v = in ? ov * gsc * a.norm_w[tid] * xjd::silu(a.z[(int64_t)t * a.z_s + hv * S + tid]) : 0.f;
-        xjd::emit_xq(v, hv * S + tid, in, a.xq + (int64_t)t * o.stride, o);
-        __syncthreads();
-    }
+#pragma unroll
+    for (int r = 0; r < NR; r++) store_row<S>(a.state + ((int64_t)hv * S + r16 + 64 * r) * S + i0, m[r]);
 }
 
 template <int S>
@@ -143,9 +153,9 @@ __global__ __launch_bounds__(256) void delta_rec_kernel(int H, int T, const floa
 }
 
 int delta_launch(const DeltaArgs &a, hipStream_t st) {
-    if (a.xq && (!a.cnt || !a.z || !a.norm_w)) return -1;
-    if (a.S == 128) hipLaunchKernelGGL(delta_kernel<128>, dim3(a.Hv, 128 / 16), dim3(256), 0, st, a);
-    else if (a.S == 64) hipLaunchKernelGGL(delta_kernel<64>, dim3(a.Hv, 64 / 16), dim3(256), 0, st, a);
+    if (a.xq && (!a.z || !a.norm_w)) return -1;
+    if (a.S == 128) hipLaunchKernelGGL(delta_head_kernel<128>, dim3(a.Hv), dim3(1024), 0, st, a);
+    else if (a.S == 64) hipLaunchKernelGGL(delta_head_kernel<64>, dim3(a.Hv), dim3(1024), 0, st, a);
     else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -332,9 +332,9 @@ struct Win {
     static constexpr int LOADS = (Q4 ? 3 : 5) * N;   // vector-memory instructions of the window
 };
 
-template <int T, int TS, int MU, bool Q4>
+template <int T, int TS, int MU, int PD>
 __device__ __forceinline__ void rows_q4k(const uint8_t *__restrict__ W, int64_t rb, int nu, int lane,
-                                         const RawU (&win)[Win<MU, Q4>::N], const uint8_t *xl, int ldsT, const XqOff &o,
+                                         const RawU (&win)[PD + 1], const uint8_t *xl, int ldsT, const XqOff &o,
                                          float (&acc)[T]) {
     constexpr int DB = TS / 4;
     const int p = lane & 3;
@@ -342,7 +342,6 @@ __device__ __forceinline__ void rows_q4k(const uint8_t *__restrict__ W, int64_t 
     const uint8_t *blk = W + (rb + (lane >> 2)) * 144;
     RawU cur = win[0];
     if constexpr (MU > 0) {
-        constexpr int PD = Win<MU, Q4>::PD;
         RawU r[MU];
 #pragma unroll
         for (int m = 0; m <= PD; m++) r[m] = win[m];
@@ -364,9 +363,9 @@ __device__ __forceinline__ void rows_q4k(const uint8_t *__restrict__ W, int64_t 
     }
 }
 
-template <int T, int TS, int MU>
+template <int T, int TS, int MU, int PD>
 __device__ __forceinline__ void rows_q6k(const uint8_t *__restrict__ W, int64_t nblk, int64_t rb, int nu, int lane,
-                                         const RawU (&win)[Win<MU, false>::N], const uint8_t *xl, int ldsT, const XqOff &o,
+                                         const RawU (&win)[PD + 1], const uint8_t *xl, int ldsT, const XqOff &o,
                                          float (&acc)[T]) {
     constexpr int DB = TS / 4;
     const int h = (lane >> 1) & 1, hl = lane & 1;
@@ -376,7 +375,6 @@ __device__ __forceinline__ void rows_q6k(const uint8_t *__restrict__ W, int64_t 
     const int gb0 = 8 * (lane >> 2) + 4 * h;
     RawU cur = win[0];
     if constexpr (MU > 0) {
-        constexpr int PD = Win<MU, false>::PD;
         RawU r[MU];
 #pragma unroll
         for (int m = 0; m <= PD; m++) r[m] = win[m];
@@ -492,6 +490,58 @@ __device__ __forceinline__ void epi_load(const GSeg &sg, int64_t r, EpiIn<T> &e)
     }
 }
 
+// Epilogue of row r (one lane): conv + SiLU, residual add or plain store.
+template <int T>
+__device__ __forceinline__ void epi_row(const GArgs &a, const GSeg &sg, int64_t r, const float (&acc)[T],
+                                        const EpiIn<T> &e) {
+    if (sg.epi == EPI_CONV) {
+        // register arrays with compile-time indices only (KC is a runtime value <= 8)
+        const int KC = sg.conv_k;
+        float st[8], wc[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            if (KC <= kConvPre) {
+                st[k] = k < kConvPre - 1 ? e.st[k < kConvPre - 1 ? k : 0] : 0.f;
+                wc[k] = k < kConvPre ? e.wc[k < kConvPre ? k : 0] : 0.f;
+            } else {
+                st[k] = k + 1 < KC ? sg.conv_state[r * (KC - 1) + k] : 0.f;
+                wc[k] = k < KC ? sg.conv_w[r * KC + k] : 0.f;
+            }
+        }
+        float wl = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) if (k == KC - 1) wl = wc[k];
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const float xv = acc[t];
+            float s = 0.f;
+#pragma unroll
+            for (int k = 0; k < 7; k++) if (k + 1 < KC) s = fmaf(st[k], wc[k], s);
+            s = fmaf(xv, wl, s);
+#pragma unroll
+            for (int k = 0; k < 6; k++) if (k + 2 < KC) st[k] = st[k + 1];
+#pragma unroll
+            for (int k = 0; k < 7; k++) if (k == KC - 2) st[k] = xv;
+            sg.y[(int64_t)t * sg.ys + r] = xjd::silu(s);
+            const int ta = a.t0 + t;
+            if (ta < a.keep_n)
+#pragma unroll
+                for (int k = 0; k < 7; k++)
+                    if (k + 1 < KC) sg.conv_ck[((int64_t)ta * sg.n_rows + r) * (KC - 1) + k] = st[k];
+        }
+#pragma unroll
+        for (int k = 0; k < 7; k++) if (k + 1 < KC) sg.conv_state[r * (KC - 1) + k] = st[k];
+    } else {
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            float *yp = sg.y + (int64_t)t * sg.ys + r;
+            const float yv = sg.epi == EPI_ADD ? e.y[t] + acc[t] : acc[t];
+            if (a.post.mode != POST_NONE) xjd::store_sys(yp, yv);   // read by this launch's tail
+            else *yp = yv;
+        }
+    }
+}
+
 template <int T, int TS, int RPT>
 __device__ __forceinline__ void epilogue(const GArgs &a, const GSeg &sg, int rg, int team, int lane, int tid,
                                          const float (&acc)[RPT][T], unsigned long long (*amax_sh)[T],
@@ -504,53 +554,10 @@ __device__ __forceinline__ void epilogue(const GArgs &a, const GSeg &sg, int rg,
     for (int i = 0; i < RPT; i++) {
         const int64_t r = (int64_t)(rg - sg.wg0) * ROWS + team * RPT + i;
         if (lane != i || r >= sg.n_rows) continue;
-        if (sg.epi == EPI_CONV) {
-            // register arrays with compile-time indices only (KC is a runtime value <= 8)
-            const int KC = sg.conv_k;
-            float st[8], wc[8];
+        epi_row<T>(a, sg, r, acc[i], e);
+        if (sg.amax)
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                if (KC <= kConvPre) {
-                    st[k] = k < kConvPre - 1 ? e.st[k < kConvPre - 1 ? k : 0] : 0.f;
-                    wc[k] = k < kConvPre ? e.wc[k < kConvPre ? k : 0] : 0.f;
-                } else {
-                    st[k] = k + 1 < KC ? sg.conv_state[r * (KC - 1) + k] : 0.f;
-                    wc[k] = k < KC ? sg.conv_w[r * KC + k] : 0.f;
-                }
-            }
-            float wl = 0.f;
-#pragma unroll
-            for (int k = 0; k < 8; k++) if (k == KC - 1) wl = wc[k];
-#pragma unroll
-            for (int t = 0; t < T; t++) {
-                const float xv = acc[i][t];
-                float s = 0.f;
-#pragma unroll
-                for (int k = 0; k < 7; k++) if (k + 1 < KC) s = fmaf(st[k], wc[k], s);
-                s = fmaf(xv, wl, s);
-#pragma unroll
-                for (int k = 0; k < 6; k++) if (k + 2 < KC) st[k] = st[k + 1];
-#pragma unroll
-                for (int k = 0; k < 7; k++) if (k == KC - 2) st[k] = xv;
-                sg.y[(int64_t)t * sg.ys + r] = xjd::silu(s);
-                const int ta = a.t0 + t;
-                if (ta < a.keep_n)
-#pragma unroll
-                    for (int k = 0; k < 7; k++)
-                        if (k + 1 < KC) sg.conv_ck[((int64_t)ta * sg.n_rows + r) * (KC - 1) + k] = st[k];
-            }
-#pragma unroll
-            for (int k = 0; k < 7; k++) if (k + 1 < KC) sg.conv_state[r * (KC - 1) + k] = st[k];
-        } else {
-#pragma unroll
-            for (int t = 0; t < T; t++) {
-                float *yp = sg.y + (int64_t)t * sg.ys + r;
-                const float yv = sg.epi == EPI_ADD ? e.y[t] + acc[i][t] : acc[i][t];
-                if (a.post.mode != POST_NONE) xjd::store_sys(yp, yv);   // read by this launch's tail
-                else *yp = yv;
-                if (sg.amax) best[t] = xjd::argmax_key(acc[i][t], (uint32_t)r);
-            }
-        }
+            for (int t = 0; t < T; t++) best[t] = xjd::argmax_key(acc[i][t], (uint32_t)r);
     }
     if (sg.amax) {  // uniform per work-group
         // lanes 0..RPT-1 of each team hold one row's key each: reduce them first
@@ -598,7 +605,7 @@ __device__ __forceinline__ void tail_swiglu(const GArgs &a, int rg, int *flag_sh
 // Completion: the caller's wait for vmcnt and barrier.
 __device__ __forceinline__ void dma_lds(const uint8_t *src, uint8_t *lds, int n16) {
     const int w = threadIdx.x >> 6;
-    for (int j0 = 0; j0 < n16; j0 += 256) {
+    for (int j0 = 0; j0 < n16; j0 += blockDim.x) {
         const int i = j0 + threadIdx.x;
         if (i < n16)
             __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1))) *)(src + 16 * (int64_t)i),
@@ -694,7 +701,7 @@ __device__ __forceinline__ void rmsx1_issue(const GArgs &a, const XqOff &o, uint
 __device__ __forceinline__ void rmsx1_finish(const GArgs &a, const XqOff &o, uint8_t *xl) {
     const f32x4 *xs = (const f32x4 *)(xl + o.v_off), *ws = (const f32x4 *)(xl + o.v_off + 4 * a.K);
     const int n4 = a.K >> 2;
-    for (int i0 = 0; i0 < n4; i0 += 256) {
+    for (int i0 = 0; i0 < n4; i0 += blockDim.x) {
         const int i = i0 + threadIdx.x, ic = i < n4 ? i : n4 - 1;
         emit4_rmsu(xs[ic], ws[ic], 4 * i, i < n4, xl, o);
     }
@@ -781,7 +788,7 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         // their number completes the copies only
         if (a.pro == PRO_RMSU_X) rmsx1_issue(a, o, lds);
         else dma_xq<T>(a, o, lds);
-        __builtin_amdgcn_sched_barrier(0);
+        barrier_raw();   // the group's copies are queued ahead of its weight requests
         first_units(rg);
         __builtin_amdgcn_sched_barrier(0);
         wait_vm<Win<MU, Q4>::LOADS>();
@@ -805,10 +812,10 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
 #pragma unroll
         for (int t = 0; t < T; t++) acc[0][t] = 0.f;
         if (Q4 || sg.type == XJ_Q4_K) {
-            rows_q4k<T, TS, MU, Q4>(sg.w, rb, nu, lane, win, xl, o.v_off, o, acc[0]);
+            rows_q4k<T, TS, MU, Win<MU, Q4>::PD>(sg.w, rb, nu, lane, win, xl, o.v_off, o, acc[0]);
         } else if constexpr (Q4) {
         } else if (sg.type == XJ_Q6_K) {
-            rows_q6k<T, TS, MU>(sg.w, sg.nblk, rb, nu, lane, win, xl, o.v_off, o, acc[0]);
+            rows_q6k<T, TS, MU, Win<MU, false>::PD>(sg.w, sg.nblk, rb, nu, lane, win, xl, o.v_off, o, acc[0]);
         } else {
             const int64_t rr[1] = {row}, rbb[1] = {rb};
             if (sg.type == XJ_Q8_0) rows_q80<T, TS, 1>(sg.w, sg.nblk, rbb, K / 32, lane, xl, o.v_off, o, acc);
@@ -827,6 +834,49 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         if (MU > 0 || rg >= n_rg) break;
         first_units(rg);
     }
+    if (a.inc_ptr && blockIdx.x == 0 && tid == 0) *a.inc_ptr += a.inc_by;
+}
+
+// Single-token launch of a prepared input with one work-group per CU:
+// work-group g of segment i (g in [wg0, wg0 + nwg)) takes rows
+// (g - wg0) * rpw + team, one per team of TS lanes (blockDim.x / TS >= rpw
+// teams; the others repeat a valid row and store nothing). The activations
+// are copied into LDS once per CU, then every lane requests its MU units at
+// once. No tails and no argmax partials.
+template <int TS, int MU, bool Q4>
+__global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
+    extern __shared__ u32x4 lds_v[];
+    constexpr int PD = MU - 1;
+    const int K = a.K, nu = K / 64;
+    const XqOff o = xq_off(K);
+    const int tid = threadIdx.x, team = tid / TS, lane = tid % TS;
+    const int rg = blockIdx.x;
+    const GSeg &sg = a.seg[seg_of(a, rg)];
+    const int64_t r0 = (int64_t)(rg - sg.wg0) * a.rpw + team;
+    const bool mine = team < a.rpw && r0 < sg.n_rows;
+    const int64_t row = mine ? r0 : (int64_t)sg.n_rows - 1;
+    const int64_t rb = row * (K / 256);
+    uint8_t *lds = (uint8_t *)lds_v;
+    // the activations first, complete before any weight request: queued
+    // behind the weight stream they would arrive with its last bytes
+    dma_xq<1>(a, o, lds);
+    wait_vm<0>();
+    barrier_raw();
+    RawU win[MU];
+    const int u0 = lane < nu ? lane : nu - 1;
+#pragma unroll
+    for (int m = 0; m < MU; m++) win[m] = load_unit<Q4>(sg.type, sg.w, sg.nblk, rb, u0 + m * TS);
+    const float sc = a.pro == PRO_RMSU ? rmsu_scale(a, o, lds, 0) : 1.f;
+    EpiIn<1> ein;
+    epi_load<1>(sg, row, ein);
+    float acc[1] = {0.f};
+    if (Q4 || sg.type == XJ_Q4_K) {
+        rows_q4k<1, TS, MU, PD>(sg.w, rb, nu, lane, win, lds, o.v_off, o, acc);
+    } else if constexpr (!Q4) {
+        rows_q6k<1, TS, MU, PD>(sg.w, sg.nblk, rb, nu, lane, win, lds, o.v_off, o, acc);
+    }
+    acc[0] = team_sum<TS>(acc[0]) * sc;
+    if (mine && lane == 0) epi_row<1>(a, sg, row, acc, ein);
     if (a.inc_ptr && blockIdx.x == 0 && tid == 0) *a.inc_ptr += a.inc_by;
 }
 
@@ -923,6 +973,82 @@ static hipError_t launch_ts(const GArgs &a, int grid, hipStream_t st) {
     }
 }
 
+// Per-CU launch (gemv_cu_kernel) of a single-token GEMV when its rows fit
+// one work-group per CU: lanes per row TS with at most 5 units per lane,
+// rows per work-group rpw with rpw * TS <= 1024 and every segment's
+// work-groups counted, at most one per CU in total. Returns 1 when not
+// applicable.
+template <int TS>
+static int launch_cu_ts(GArgs b, int rpw, int upl, bool q4, hipStream_t st) {
+    int wg = 0;
+    for (int i = 0; i < b.nseg; i++) {
+        b.seg[i].wg0 = wg;
+        b.seg[i].nwg = (b.seg[i].n_rows + rpw - 1) / rpw;
+        wg += b.seg[i].nwg;
+    }
+    b.rpw = rpw;
+    const int threads = (rpw * TS + 63) / 64 * 64;
+    size_t lds = gemv_lds_bytes(b);
+    // more than half of a CU's LDS keeps each work-group on a CU of its own
+    if (g_lds_max > 80 * 1024 && lds < 80 * 1024 + 256) lds = 80 * 1024 + 256;
+    void (*k)(GArgs) = nullptr;
+    if (q4) {
+        switch (upl) {
+        case 1: k = gemv_cu_kernel<TS, 1, true>; break;
+        case 2: k = gemv_cu_kernel<TS, 2, true>; break;
+        case 3: k = gemv_cu_kernel<TS, 3, true>; break;
+        case 4: k = gemv_cu_kernel<TS, 4, true>; break;
+        default: k = gemv_cu_kernel<TS, 5, true>; break;
+        }
+    } else {
+        switch (upl) {
+        case 1: k = gemv_cu_kernel<TS, 1, false>; break;
+        case 2: k = gemv_cu_kernel<TS, 2, false>; break;
+        case 3: k = gemv_cu_kernel<TS, 3, false>; break;
+        case 4: k = gemv_cu_kernel<TS, 4, false>; break;
+        default: k = gemv_cu_kernel<TS, 5, false>; break;
+        }
+    }
+    hipLaunchKernelGGL(k, dim3(wg), dim3(threads), lds, st, b);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+static int gemv_launch_cu(const GArgs &a, hipStream_t st) {
+    static const bool on = env_or("XJ_GEMV_CU", 1) != 0;
+    if (!on || a.T != 1 || a.post.mode != POST_NONE) return 1;
+    if (a.pro != PRO_NONE && a.pro != PRO_RMSU) return 1;   // RMSNorm built in LDS: many work-groups share it
+    int64_t total = 0;
+    bool q4 = true;
+    for (int i = 0; i < a.nseg; i++) {
+        const GSeg &s = a.seg[i];
+        if ((s.type != XJ_Q4_K && s.type != XJ_Q6_K) || s.amax || s.n_rows < 1) return 1;
+        if (s.epi == EPI_CONV && (s.conv_k < 2 || s.conv_k > 8)) return 1;
+        q4 = q4 && s.type == XJ_Q4_K;
+        total += s.n_rows;
+    }
+    if (a.K % 256 || a.K > 16384 || gemv_lds_bytes(a) > (size_t)g_lds_max) return 1;
+    // the fewest rows per work-group whose work-groups fit one per CU
+    int rpw = (int)((total + g_cus - 1) / g_cus);
+    for (;; rpw++) {
+        int64_t wg = 0;
+        for (int i = 0; i < a.nseg; i++) wg += (a.seg[i].n_rows + rpw - 1) / rpw;
+        if (wg <= g_cus) break;
+    }
+    // the most lanes per row (more wavefronts) with at most 5 units per lane
+    const int nu = a.K / 64;
+    for (int ts = 64; ts >= 8; ts /= 2) {
+        const int upl = (nu + ts - 1) / ts;
+        if (upl > 5 || rpw * ts > 1024) continue;
+        switch (ts) {
+        case 8: return launch_cu_ts<8>(a, rpw, upl, q4, st);
+        case 16: return launch_cu_ts<16>(a, rpw, upl, q4, st);
+        case 32: return launch_cu_ts<32>(a, rpw, upl, q4, st);
+        default: return launch_cu_ts<64>(a, rpw, upl, q4, st);
+        }
+    }
+    return 1;
+}
+
 int gemv_launch(const GArgs &a, hipStream_t st) {
     if (a.T < 1 || a.T > kTileT || a.nseg < 1 || a.nseg > kMaxSeg || a.K < 32 || a.K % 32 || !a.xq) return -1;
     if (gemv_lds_bytes(a) > (size_t)g_lds_max) return -1;
@@ -945,6 +1071,10 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
     if (a.post.mode == POST_SWIGLU &&
         (!a.post.xq || !a.post.cnt || a.nseg != 2 || a.seg[0].n_rows != a.seg[1].n_rows || a.seg[0].n_rows % 32 ||
          32 % p.rows_per_group)) return -1;
+    if (a.T == 1) {
+        const int rc = gemv_launch_cu(a, st);
+        if (rc <= 0) return rc;
+    }
     const int n_rg = a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg;
     const int grid = n_rg < g_grid_cap ? n_rg : g_grid_cap;
     hipError_t e;
@@ -972,6 +1102,16 @@ static void raise_ts(int bytes) {
     for (const void *k : f) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 
+template <int TS>
+static void raise_cu(int bytes) {
+    const void *f[] = {(const void *)gemv_cu_kernel<TS, 1, true>, (const void *)gemv_cu_kernel<TS, 2, true>,
+                       (const void *)gemv_cu_kernel<TS, 3, true>, (const void *)gemv_cu_kernel<TS, 4, true>,
+                       (const void *)gemv_cu_kernel<TS, 5, true>, (const void *)gemv_cu_kernel<TS, 1, false>,
+                       (const void *)gemv_cu_kernel<TS, 2, false>, (const void *)gemv_cu_kernel<TS, 3, false>,
+                       (const void *)gemv_cu_kernel<TS, 4, false>, (const void *)gemv_cu_kernel<TS, 5, false>};
+    for (const void *k : f) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
+
 int gemv_init(char *err, size_t errlen) {
     static bool done = false;
     if (done) return 0;
@@ -986,6 +1126,7 @@ int gemv_init(char *err, size_t errlen) {
     // keep 4 KB for the static reduction buffers
     int want = lds > 65536 ? lds - 4096 : 65536 - 4096;
     raise_ts<8>(want); raise_ts<16>(want); raise_ts<32>(want); raise_ts<64>(want);
+    raise_cu<8>(want); raise_cu<16>(want); raise_cu<32>(want); raise_cu<64>(want);
     (void)hipGetLastError();
     g_lds_max = want;
     done = true;

@@ -79,6 +79,7 @@ struct GArgs {
     int32_t keep_n;                // conv checkpoints for absolute tokens t < keep_n
     int32_t *inc_ptr; int32_t inc_by;
     PostPrep post;
+    int32_t rpw;                   // rows per work-group (set by the launcher for per-CU launches)
     int32_t nseg;
     GSeg seg[kMaxSeg];
 };
@@ -137,13 +138,11 @@ struct DeltaArgs {
     float *out; int32_t out_s;           // [T][Hv*S]
     int32_t T, Hk, Hv, S, keep_n;
     float eps, qscale;
-    // optional tail: per head, the last of its work-groups writes the
-    // prepared activations of norm(out) * norm_w * silu(z) (gated RMSNorm,
-    // xj_cpu.c:215-217) into xq (token stride xq_off(Hv*S).stride)
+    // optional: the prepared activations of norm(out) * norm_w * silu(z)
+    // (gated RMSNorm, xj_cpu.c:215-217) into xq (token stride xq_off(Hv*S).stride)
     uint8_t *xq;
     const float *z; int32_t z_s;
     const float *norm_w;
-    int32_t *cnt;                        // [Hv], zero between launches
 };
 int delta_launch(const DeltaArgs &a, hipStream_t st);
 

@@ -68,7 +68,7 @@ struct HStage {
     // n_head*head_dim (wo) and n_ff (down)
     uint8_t *xq_e = nullptr, *xq_di = nullptr, *xq_att = nullptr, *xq_ff = nullptr;
     // arrival counters of the producer tails (zero between launches)
-    int32_t *cnt_grp = nullptr, *cnt_head = nullptr;
+    int32_t *cnt_grp = nullptr;
     float *inv_freq = nullptr;
     float *h_x = nullptr;            // pinned staging [max_batch][n_embd]
     int32_t *h_i = nullptr;          // pinned scalar
@@ -261,7 +261,7 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
         d.state = L.ssm; d.ck = L.ck_ssm; d.out = S->o; d.out_s = DI;
         d.T = T; d.Hk = hp.h_k; d.Hv = Hv; d.S = hp.s_k; d.keep_n = keep_n; d.eps = hp.eps;
         d.qscale = 1.0f / sqrtf((float)hp.s_k);
-        d.xq = S->xq_di; d.z = S->z; d.z_s = DI; d.norm_w = L.ssm_norm; d.cnt = S->cnt_head;
+        d.xq = S->xq_di; d.z = S->z; d.z_s = DI; d.norm_w = L.ssm_norm;
         if (!pf && delta_launch(d, st)) return -1;
         Gemv q(S->xq_di, pf);
         q.prepared = true;
@@ -630,12 +630,11 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
         S->xq_di = dalloc<uint8_t>(S, xqb(hp.d_inner), err, errlen);
         S->xq_att = dalloc<uint8_t>(S, xqb(hp.n_head * hp.head_dim), err, errlen);
         S->xq_ff = dalloc<uint8_t>(S, xqb(hp.n_ff), err, errlen);
-        const size_t nc = (size_t)(hp.n_ff / 32) + (size_t)(hp.h_v > 0 ? hp.h_v : 1);
+        const size_t nc = (size_t)(hp.n_ff / 32) + 1;
         int32_t *cnt = dalloc<int32_t>(S, nc, err, errlen);
         if (!S->xq_e || !S->xq_di || !S->xq_att || !S->xq_ff || !cnt) return fail();
         XJ_CHECK(hipMemset(cnt, 0, nc * 4), err, errlen, fail());
         S->cnt_grp = cnt;
-        S->cnt_head = cnt + hp.n_ff / 32;
     }
     const int half = hp.n_rot / 2 > 0 ? hp.n_rot / 2 : 1;
     S->inv_freq = dalloc<float>(S, half, err, errlen);
