@@ -5,16 +5,17 @@
 // (xj_kernels.metal:440-452):
 //   kv_store_kernel  one work-group per (token, kv head): RMSNorm(k_norm) of the
 //                    new key (double sum, x*sc*w), NeoX RoPE of the first n_rot
-//                    dims (xj_cpu.c:68-77; theta = pos * inv_freq[i] with
-//                    inv_freq = base^(-2i/n_rot) computed on the host exactly as
-//                    the reference's powf, cos/sin of theta evaluated in double),
-//                    then k and v rounded to fp16 (RNE) and stored at position
+//                    dims (xj_cpu.c:68-77; cos and sin of theta = pos * base^(-2i/n_rot)
+//                    from a table the host fills per position with the
+//                    reference's float powf, cosf and sinf), then k and v
+//                    rounded to fp16 (RNE) and stored at position
 //                    n_past + t; the same for the query heads that read this kv
 //                    head (q_norm, RoPE), kept in fp32 for the split kernel.
-//   attn_part_kernel one work-group per (query head, token, 64-position split):
-//                    scores q.k_j * scale (16-lane teams, one position per team),
-//                    the split's max, sum of exponentials and unnormalised
-//                    sum_j e_j v_j (8 dims x 8 position groups per thread row,
+//   attn_part_kernel one work-group per (kv head, token, 32-position split) for
+//                    the G query heads of the kv head: scores q.k_j * scale
+//                    (16-lane teams, two positions per team), per head the
+//                    split's max, sum of exponentials and unnormalised
+//                    sum_j e_j v_j (8 dims x position groups per thread row,
 //                    16-byte loads, position groups combined in a fixed order)
 //   attn_combine     merges the splits with the usual max rescaling, divides
 //                    by the total, applies sigmoid(gate) (xj_cpu.c:128-147:
@@ -53,10 +54,7 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const AttnArgs a) {
                           : a.qg[(int64_t)t * a.qg_s + (int64_t)(g * G + i - 1) * 2 * D + tid];
     }
     const float vv = in ? a.vn[(int64_t)t * a.vn_s + g * D + tid] : 0.f;
-    for (int i = tid; i < a.n_rot / 2; i += 256) {
-        const float theta = (float)pos * a.inv_freq[i];
-        cs[i] = float2{(float)cos((double)theta), (float)sin((double)theta)};
-    }
+    for (int i = tid; i < a.n_rot / 2; i += 256) cs[i] = a.rope[(int64_t)pos * (a.n_rot / 2) + i];
 #pragma unroll
     for (int i = 0; i <= kMaxGroup; i++) {
         const double ss = xjd::wave_sum_d((double)v[i] * v[i]);
@@ -86,100 +84,144 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const AttnArgs a) {
     }
 }
 
-// Split-K decode attention. Work-group (h, t, s) covers positions
-// [s*P, min(s*P+P, pos+1)) of query head h, token t: it writes the split's
-// maximum score m_s, l_s = sum_j exp(s_j - m_s) and the unnormalised
-// o_s = sum_j exp(s_j - m_s) v_j. Splits past pos exit.
-// The grid covers n_ctx, so one captured graph serves every decode position.
-constexpr int kSplitP = 64;
+// Split-K decode attention. Work-group (g, t, s) covers positions
+// [s*P, min(s*P+P, pos+1)) for the G query heads of kv head g, token t: it
+// writes, per head, the split's maximum score m_s, l_s = sum_j exp(s_j - m_s)
+// and the unnormalised o_s = sum_j exp(s_j - m_s) v_j. Splits past pos exit.
+// The keys and values of the split are requested at once and read once for
+// all G heads. The grid covers n_ctx, so one captured graph serves every
+// decode position.
+constexpr int kSplitP = 32;
 
-template <int D>
+template <int D, int G>
 __global__ __launch_bounds__(256) void attn_part_kernel(const AttnArgs a) {
-    constexpr int DL = D / 16;           // score dims per lane
+    constexpr int DL = D / 16;           // score dims per lane (16-lane teams, one position each)
+    constexpr int NPT = kSplitP / 16;    // positions per team
     constexpr int DG = D / 8;            // PV: 8-dim groups
     constexpr int PG = 256 / DG;         // PV: position groups
-    const int h = blockIdx.x, t = blockIdx.y, sp = blockIdx.z, tid = threadIdx.x;
+    constexpr int NPG = kSplitP / PG;    // PV: positions per group
+    constexpr int HC = G < 4 ? G : 4;    // PV: heads per LDS pass
+    static_assert(kSplitP % PG == 0 && NPG >= 1, "split size");
+    const int g = blockIdx.x, t = blockIdx.y, sp = blockIdx.z, tid = threadIdx.x;
     const int team = tid >> 4, l16 = tid & 15;
-    const int kvh = h / (a.H / a.Hkv), nk = a.Hkv * D;
+    const int nk = a.Hkv * D;
     const int pos = *a.npast + t, j0 = sp * kSplitP;
     if (j0 > pos) return;                       // uniform per work-group
     const int n = (j0 + kSplitP - 1 < pos ? j0 + kSplitP - 1 : pos) - j0 + 1;
-    __shared__ float q[D];
-    __shared__ float e[kSplitP];
-    __shared__ float redf[4];
-    __shared__ float po[PG][D];
-    for (int i = tid; i < D; i += 256) q[i] = a.qr[((int64_t)t * a.H + h) * D + i];
-    __syncthreads();
-    float qv[DL];
+    __shared__ float e[G][kSplitP];
+    __shared__ float ml[G][2];
+    __shared__ float po[PG][HC][D];
+    // every key and value of the split, clamped to valid positions
+    u32x4 kw[NPT][(DL + 7) / 8];
+    uint2 kw4[NPT];
 #pragma unroll
-    for (int d = 0; d < DL; d++) qv[d] = q[l16 * DL + d];
-    float mx = -INFINITY;
+    for (int r = 0; r < NPT; r++) {
+        const int jj = team + 16 * r, jc = jj < n ? jj : n - 1;
+        const uint16_t *kp = a.kc + (int64_t)(j0 + jc) * nk + g * D + l16 * DL;
+        if constexpr (DL % 8 == 0) {
 #pragma unroll
-    for (int r = 0; r < kSplitP / 16; r++) {
-        const int jj = team + 16 * r;
-        if (jj < n) {
-            const uint16_t *kp = a.kc + (int64_t)(j0 + jj) * nk + kvh * D + l16 * DL;
-            float s = 0.f;
-            if constexpr (DL % 8 == 0) {
-#pragma unroll
-                for (int d = 0; d < DL; d += 8) {
-                    const u32x4 kw = *(const u32x4 *)(kp + d);
-#pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        const uint32_t w2 = kw[c];
-                        s = fmaf(qv[d + 2 * c], xjd::f16_to_f32(w2 & 0xFFFFu), s);
-                        s = fmaf(qv[d + 2 * c + 1], xjd::f16_to_f32(w2 >> 16), s);
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int d = 0; d < DL; d++) s = fmaf(qv[d], xjd::f16_to_f32(kp[d]), s);
-            }
-            s = xjd::row16_sum(s) * a.scale;
-            if (l16 == 0) e[jj] = s;
-            mx = fmaxf(mx, s);
+            for (int d = 0; d < DL / 8; d++) kw[r][d] = *(const u32x4 *)(kp + 8 * d);
+        } else {
+            kw4[r] = *(const uint2 *)kp;   // DL == 4
         }
     }
-    mx = xjd::block_max(mx, redf);
-    __syncthreads();
-    float lsum = 0.f;
-    if (tid < 64) {
-        const float ev = tid < n ? expf(e[tid] - mx) : 0.f;
-        if (tid < n) e[tid] = ev;
-        lsum = ev;
-        for (int off = 32; off > 0; off >>= 1) lsum += __shfl_xor(lsum, off, 64);
-    }
-    __syncthreads();
-    // PV: thread (pg, dg) sums positions pg, pg + PG, ... over dims 8dg..8dg+7
-    {
-        const int dg = tid % DG, pg = tid / DG;
-        float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        const uint16_t *vp = a.vc + (int64_t)j0 * nk + kvh * D + 8 * dg;
+    const int dg = tid % DG, pg = tid / DG;
+    u32x4 vw[NPG];
 #pragma unroll
-        for (int r = 0; r < kSplitP / PG; r++) {
-            const int jj = pg + PG * r;
-            if (jj < n) {
-                const u32x4 vw = *(const u32x4 *)(vp + (int64_t)jj * nk);
-                const float ej = e[jj];
+    for (int r = 0; r < NPG; r++) {
+        const int jj = pg + PG * r, jc = jj < n ? jj : n - 1;
+        vw[r] = *(const u32x4 *)(a.vc + (int64_t)(j0 + jc) * nk + g * D + 8 * dg);
+    }
+    float qv[G][DL];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        const float *qp = a.qr + ((int64_t)t * a.H + g * G + h) * D + l16 * DL;
+#pragma unroll
+        for (int d = 0; d < DL; d += 4) {
+            const float4 q4 = *(const float4 *)(qp + d);
+            qv[h][d] = q4.x; qv[h][d + 1] = q4.y; qv[h][d + 2] = q4.z; qv[h][d + 3] = q4.w;
+        }
+    }
+    // scores
+#pragma unroll
+    for (int r = 0; r < NPT; r++) {
+        const int jj = team + 16 * r;
+        float kf[DL];
+        if constexpr (DL % 8 == 0) {
+#pragma unroll
+            for (int d = 0; d < DL / 8; d++)
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
-                    o[2 * c] = fmaf(ej, xjd::f16_to_f32(vw[c] & 0xFFFFu), o[2 * c]);
-                    o[2 * c + 1] = fmaf(ej, xjd::f16_to_f32(vw[c] >> 16), o[2 * c + 1]);
+                    kf[8 * d + 2 * c] = xjd::f16_to_f32(kw[r][d][c] & 0xFFFFu);
+                    kf[8 * d + 2 * c + 1] = xjd::f16_to_f32(kw[r][d][c] >> 16);
                 }
-            }
+        } else {
+            kf[0] = xjd::f16_to_f32(kw4[r].x & 0xFFFFu); kf[1] = xjd::f16_to_f32(kw4[r].x >> 16);
+            kf[2] = xjd::f16_to_f32(kw4[r].y & 0xFFFFu); kf[3] = xjd::f16_to_f32(kw4[r].y >> 16);
         }
 #pragma unroll
-        for (int c = 0; c < 8; c++) po[pg][8 * dg + c] = o[c];
+        for (int h = 0; h < G; h++) {
+            float s = 0.f;
+#pragma unroll
+            for (int d = 0; d < DL; d++) s = fmaf(qv[h][d], kf[d], s);
+            s = xjd::row16_sum(s) * a.scale;
+            if (l16 == 0) e[h][jj] = jj < n ? s : -INFINITY;
+        }
     }
     __syncthreads();
-    float *part = a.scores + (((int64_t)t * a.H + h) * a.n_split + sp) * (D + 2);
-    for (int d = tid; d < D; d += 256) {
-        float o = 0.f;
-#pragma unroll
-        for (int g2 = 0; g2 < PG; g2++) o += po[g2][d];
-        part[2 + d] = o;
+    // per head: maximum, exponentials and their sum over the split (32 lanes per head)
+    if (tid < G * 32) {
+        const int h = tid >> 5, jj = tid & 31;
+        const float sv = e[h][jj];
+        float m = xjd::row16_max(sv);
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        const float ev = jj < n ? expf(sv - m) : 0.f;
+        e[h][jj] = ev;
+        float l = xjd::row16_sum(ev);
+        l += __shfl_xor(l, 16, 64);
+        if (jj == 0) { ml[h][0] = m; ml[h][1] = l; }
     }
-    if (tid == 0) { part[0] = mx; part[1] = lsum; }
+    __syncthreads();
+    // PV: thread (pg, dg) sums positions pg, pg + PG, ... over dims 8dg..8dg+7, HC heads per pass
+#pragma unroll
+    for (int h0 = 0; h0 < G; h0 += HC) {
+        float o[HC][8];
+#pragma unroll
+        for (int h = 0; h < HC; h++)
+#pragma unroll
+            for (int c = 0; c < 8; c++) o[h][c] = 0.f;
+#pragma unroll
+        for (int r = 0; r < NPG; r++) {
+            const int jj = pg + PG * r;
+            float vf[8];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                vf[2 * c] = xjd::f16_to_f32(vw[r][c] & 0xFFFFu);
+                vf[2 * c + 1] = xjd::f16_to_f32(vw[r][c] >> 16);
+            }
+#pragma unroll
+            for (int h = 0; h < HC; h++) {
+                const float ej = e[h0 + h][jj];   // 0 past n
+#pragma unroll
+                for (int c = 0; c < 8; c++) o[h][c] = fmaf(ej, vf[c], o[h][c]);
+            }
+        }
+        if (h0) __syncthreads();   // po of the previous pass consumed
+#pragma unroll
+        for (int h = 0; h < HC; h++)
+#pragma unroll
+            for (int c = 0; c < 8; c++) po[pg][h][8 * dg + c] = o[h][c];
+        __syncthreads();
+        for (int idx = tid; idx < HC * D; idx += 256) {
+            const int h = idx / D, d = idx % D;
+            float acc = 0.f;
+#pragma unroll
+            for (int g2 = 0; g2 < PG; g2++) acc += po[g2][h][d];
+            float *part = a.scores + (((int64_t)t * a.H + g * G + h0 + h) * a.n_split + sp) * (D + 2);
+            part[2 + d] = acc;
+            if (d == 0) { part[0] = ml[h0 + h][0]; part[1] = ml[h0 + h][1]; }
+        }
+    }
 }
 
 // out[t][h] = sigmoid(gate) * sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s
@@ -204,29 +246,33 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
         for (int s = 64; s < ns; s++) L = fmaf(expf(part[(int64_t)s * (D + 2)] - M), part[(int64_t)s * (D + 2) + 1], L);
         if (tid == 0) inv_l = 1.0f / L;
     }
-    __syncthreads();
     const float *qr = a.qg + (int64_t)t * a.qg_s + (int64_t)h * 2 * D;
     const int d = tid;   // D <= 256
     const bool in = d < D;
     float r = 0.f;
-    if (in) {
-        float o = 0.f, M2 = -INFINITY;
-        if (ns > 64)   // more splits than cached weights: recompute the maximum
+    if (ns <= 64) {
+        // every split's value of dim d requested before the weights are known
+        // (clamped addresses, so the loads need no branch), summed in order
+        const int dc = in ? d : D - 1;
+        float pv[64];
+#pragma unroll
+        for (int s = 0; s < 64; s++) pv[s] = part[(int64_t)(s < ns ? s : ns - 1) * (D + 2) + 2 + dc];
+        __syncthreads();
+        float o = 0.f;
+#pragma unroll
+        for (int s = 0; s < 64; s++) if (s < ns) o = fmaf(w[s], pv[s], o);
+        r = o * inv_l * (in ? xjd::sigm(qr[D + dc]) : 0.f);
+    } else {
+        __syncthreads();
+        if (in) {
+            // more splits than cached weights: recompute the maximum
+            float o = 0.f, M2 = -INFINITY;
             for (int s = 0; s < ns; s++) M2 = fmaxf(M2, part[(int64_t)s * (D + 2)]);
-        if (ns <= 64) {
-            for (int s0 = 0; s0 < ns; s0 += 8) {   // eight loads in flight, summed in order
-                float pv[8];
-#pragma unroll
-                for (int j = 0; j < 8; j++) pv[j] = s0 + j < ns ? part[(int64_t)(s0 + j) * (D + 2) + 2 + d] : 0.f;
-#pragma unroll
-                for (int j = 0; j < 8; j++) if (s0 + j < ns) o = fmaf(w[s0 + j], pv[j], o);
-            }
-        } else {
             for (int s = 0; s < ns; s++) o = fmaf(expf(part[(int64_t)s * (D + 2)] - M2), part[(int64_t)s * (D + 2) + 2 + d], o);
+            r = o * inv_l * xjd::sigm(qr[D + d]);
         }
-        r = o * inv_l * xjd::sigm(qr[D + d]);
-        a.out[(int64_t)t * a.H * D + (int64_t)h * D + d] = r;
     }
+    if (in) a.out[(int64_t)t * a.H * D + (int64_t)h * D + d] = r;
     // the wo GEMV's prepared activations (no prologue): groups of 32 lie inside the head
     if (a.xq) xjd::emit_xq(r, h * D + d, in, a.xq + (int64_t)t * xq_off(a.H * D).stride, xq_off(a.H * D));
 }
@@ -234,7 +280,13 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
 template <int D>
 static int launch_d(const AttnArgs &a, hipStream_t st) {
     hipLaunchKernelGGL(kv_store_kernel<D>, dim3(a.T, a.Hkv), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(attn_part_kernel<D>, dim3(a.H, a.T, a.n_split), dim3(256), 0, st, a);
+    switch (a.H / a.Hkv) {
+    case 1: hipLaunchKernelGGL((attn_part_kernel<D, 1>), dim3(a.Hkv, a.T, a.n_split), dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((attn_part_kernel<D, 2>), dim3(a.Hkv, a.T, a.n_split), dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((attn_part_kernel<D, 4>), dim3(a.Hkv, a.T, a.n_split), dim3(256), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((attn_part_kernel<D, 8>), dim3(a.Hkv, a.T, a.n_split), dim3(256), 0, st, a); break;
+    default: return -1;
+    }
     hipLaunchKernelGGL(attn_combine_kernel<D>, dim3(a.H, a.T), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
@@ -242,7 +294,9 @@ static int launch_d(const AttnArgs &a, hipStream_t st) {
 int attn_splits(int n_ctx) { return (n_ctx + kSplitP - 1) / kSplitP; }
 
 int attn_launch(const AttnArgs &a, hipStream_t st) {
-    if (a.H % a.Hkv || a.H / a.Hkv > kMaxGroup || a.n_rot > a.D || a.n_rot % 2 || a.n_split != attn_splits(a.n_ctx) ||
+    const int G = a.Hkv > 0 ? a.H / a.Hkv : 0;
+    if (a.Hkv < 1 || a.H % a.Hkv || (G != 1 && G != 2 && G != 4 && G != 8) || a.n_rot > a.D || a.n_rot % 2 ||
+        a.n_split != attn_splits(a.n_ctx) ||
         !a.qr)
         return -1;
     switch (a.D) {

@@ -115,7 +115,7 @@ struct AttnArgs {
     const float *vn; int32_t vn_s;
     uint16_t *kc, *vc;                   // fp16 caches [n_ctx][Hkv*D]
     const float *qnorm_w, *knorm_w;
-    const float *inv_freq;               // [n_rot/2]
+    const float2 *rope;                  // [n_ctx][n_rot/2] (cos, sin) of pos * base^(-2i/n_rot)
     const int32_t *npast;
     float *qr;                           // normalised, rotated queries [T][H][D] (written by kv_store)
     float *scores;                       // split partials [T][H][n_split][D+2]
@@ -125,7 +125,7 @@ struct AttnArgs {
     uint8_t *xq;                         // optional: prepared activations of out (no prologue)
 };
 int attn_launch(const AttnArgs &a, hipStream_t st);
-int attn_splits(int n_ctx);             // 64-position splits covering n_ctx
+int attn_splits(int n_ctx);             // 32-position splits covering n_ctx
 
 struct DeltaArgs {
     const float *qkv; int32_t qkv_s;    // conv+SiLU outputs [T][conv_dim]

@@ -69,7 +69,7 @@ struct HStage {
     uint8_t *xq_e = nullptr, *xq_di = nullptr, *xq_att = nullptr, *xq_ff = nullptr;
     // arrival counters of the producer tails (zero between launches)
     int32_t *cnt_grp = nullptr;
-    float *inv_freq = nullptr;
+    float2 *rope = nullptr;
     float *h_x = nullptr;            // pinned staging [max_batch][n_embd]
     int32_t *h_i = nullptr;          // pinned scalar
     int n_ck = 0;
@@ -282,7 +282,7 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
             at.qg = S->qkv; at.qg_s = nq; at.kn = S->kb; at.kn_s = nk; at.vn = S->vb; at.vn_s = nk;
         }
         if (p.run(T, st)) return -1;
-        at.kc = L.kc; at.vc = L.vc; at.qnorm_w = L.q_norm; at.knorm_w = L.k_norm; at.inv_freq = S->inv_freq;
+        at.kc = L.kc; at.vc = L.vc; at.qnorm_w = L.q_norm; at.knorm_w = L.k_norm; at.rope = S->rope;
         at.npast = S->npast; at.qr = S->qr; at.scores = S->scores; at.out = S->o;
         at.T = T; at.H = Hq; at.Hkv = Hkv; at.D = D; at.n_rot = hp.n_rot; at.n_ctx = S->s.n_ctx;
         at.n_split = attn_splits(S->s.n_ctx);
@@ -637,9 +637,9 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
         S->cnt_grp = cnt;
     }
     const int half = hp.n_rot / 2 > 0 ? hp.n_rot / 2 : 1;
-    S->inv_freq = dalloc<float>(S, half, err, errlen);
+    S->rope = dalloc<float2>(S, (size_t)n_ctx * half, err, errlen);
     if (!S->x || !S->qkv || !S->kb || !S->vb || !S->z || !S->beta || !S->alpha || !S->o || !S->g || !S->u ||
-        !S->qr || !S->scores || !S->npast || !S->inv_freq)
+        !S->qr || !S->scores || !S->npast || !S->rope)
         return fail();
     if (has_head) {
         S->logits = dalloc<float>(S, mb * (size_t)S->output.n_rows, err, errlen);
@@ -648,10 +648,15 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
         S->amax = dalloc<unsigned long long>(S, mb * (size_t)S->head_nwg, err, errlen);
         if (!S->logits || !S->amax) return fail();
     }
-    {   // theta_i = pos * base^(-2i/n_rot), the exponent evaluated as the reference does (xj_cpu.c:71)
-        std::vector<float> f(half, 0.f);
-        for (int i = 0; i < hp.n_rot / 2; i++) f[i] = powf(hp.rope_base, -2.0f * i / hp.n_rot);
-        XJ_CHECK(hipMemcpy(S->inv_freq, f.data(), half * 4, hipMemcpyHostToDevice), err, errlen, fail());
+    {   // cos and sin of theta = pos * base^(-2i/n_rot) for every position, in float as the
+        // reference's rope evaluates them (xj_cpu.c:68-77)
+        std::vector<float2> cs((size_t)n_ctx * half, float2{1.f, 0.f});
+        for (int p = 0; p < n_ctx; p++)
+            for (int i = 0; i < hp.n_rot / 2; i++) {
+                const float theta = p * powf(hp.rope_base, -2.0f * i / hp.n_rot);
+                cs[(size_t)p * half + i] = float2{cosf(theta), sinf(theta)};
+            }
+        XJ_CHECK(hipMemcpy(S->rope, cs.data(), cs.size() * sizeof(float2), hipMemcpyHostToDevice), err, errlen, fail());
     }
     XJ_CHECK(hipHostMalloc((void **)&S->h_x, sizeof(float) * mb * E, hipHostMallocDefault), err, errlen, fail());
     XJ_CHECK(hipHostMalloc((void **)&S->h_i, 64, hipHostMallocDefault), err, errlen, fail());
