@@ -1,8 +1,8 @@
 // Bit-exact decode of one 32-element chunk of a row in the device layout
 // (see kernels.h). Same products in the same order as xj_dequant_row
-// (src/xiaoju-pipe/core/xj_quant.h:61-118): Q4_K (d*sc)*q - dmin*m,
-// Q6_K (d*sc)*q, Q8_0 d*q. Used by the dequant check kernel and by the
-// device-side embedding lookup.
+// (src/xiaoju-pipe/core/xj_quant.h:57-118): F16 / BF16 widened, Q4_K and
+// Q5_K (d*sc)*q - dmin*m, Q6_K (d*sc)*q, Q8_0 d*q. Used by the dequant
+// check kernel and by the device-side embedding lookup.
 #pragma once
 #include "common.h"
 #include "xj_abi.h"
@@ -15,6 +15,31 @@ __device__ __forceinline__ void dequant_chunk(const uint8_t *__restrict__ W, uin
     if (type == XJ_F32) {
         const float *src = (const float *)W + row * K + c * 32;
         for (int l = 0; l < 32; l++) out[l] = src[l];
+    } else if (type == XJ_F16 || type == XJ_BF16) {
+        const uint16_t *src = (const uint16_t *)W + row * K + c * 32;
+        for (int l = 0; l < 32; l++)
+            out[l] = type == XJ_F16 ? f16_to_f32(src[l]) : __uint_as_float((uint32_t)src[l] << 16);
+    } else if (type == XJ_Q5_K) {
+        // as Q4_K, with bit j of qh[l] (j = the sub-block) as the fifth bit of element l
+        const int64_t b = c >> 3;
+        const int j = (int)(c & 7), p = j >> 1, hi = j & 1;
+        const uint8_t *blk = W + (row * (K / 256) + b) * 176;
+        const float d = f16_to_f32(*(const uint16_t *)blk), dmin = f16_to_f32(*(const uint16_t *)(blk + 2));
+        const uint8_t *s = blk + 4;
+        uint32_t sc, mn;
+        if (j < 4) {
+            sc = s[j] & 63;
+            mn = s[j + 4] & 63;
+        } else {
+            sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+            mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+        }
+        const float dj = d * (float)sc, mj = dmin * (float)mn;
+        const uint8_t *qh = blk + 16, *ql = blk + 48 + 32 * p;
+        for (int l = 0; l < 32; l++) {
+            const int q = (hi ? (ql[l] >> 4) : (ql[l] & 0xF)) + (((qh[l] >> j) & 1) << 4);
+            out[l] = dj * (float)q - mj;
+        }
     } else if (type == XJ_Q8_0) {
         const int64_t g = row * (K / 32) + c;
         const float d = f16_to_f32(*(const uint16_t *)(W + nblk * 32 + g * 2));

@@ -439,6 +439,79 @@ __device__ __forceinline__ void rows_f32(const uint8_t *__restrict__ W, const in
     }
 }
 
+// F16 / BF16 rows (no configuration uses them): widened exactly, fp32
+// products with the prepared v, read from global memory.
+template <int T, int TS, int RPT>
+__device__ __forceinline__ void rows_h16(const uint8_t *__restrict__ W, const int64_t (&row)[RPT], int K, int lane,
+                                         bool bf, const uint8_t *xq, const XqOff &o, float (&acc)[RPT][T]) {
+    for (int c = lane; c < K / 32; c += TS) {
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const float *v = (const float *)(xq + (int64_t)t * o.stride + o.v_off) + c * 32;
+#pragma unroll
+            for (int i = 0; i < RPT; i++) {
+                const uint8_t *w = W + (row[i] * K + c * 32) * 2;
+                float s = acc[i][t];
+#pragma unroll
+                for (int e = 0; e < 32; e += 8) {
+                    const u32x4 wv = ld16(w + 2 * e);
+                    const f32x4 x0 = *(const f32x4 *)(v + e), x1 = *(const f32x4 *)(v + e + 4);
+                    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                    for (int h = 0; h < 8; h++) {
+                        const uint32_t b = (wv[h >> 1] >> (16 * (h & 1))) & 0xFFFFu;
+                        s = fmaf(bf ? __uint_as_float(b << 16) : xjd::f16_to_f32(b), xs[h], s);
+                    }
+                }
+                acc[i][t] = s;
+            }
+        }
+    }
+}
+
+// Q5_K rows (no configuration uses them): a unit is scale pair p of a block,
+// as for Q4_K, with bit j of qh[l] as the fifth bit of element l of sub-block
+// j (xj_quant.h:83-98). |q| <= 31 keeps the digit-plane sums within 32 bits.
+// Blocks stay in the GGUF layout (176 bytes: d, dmin, scales[12], qh[32], qs[128]).
+template <int T, int TS>
+__device__ __forceinline__ void rows_q5k(const uint8_t *__restrict__ W, int64_t rb, int nu, int lane,
+                                         const uint8_t *xl, int ldsT, const XqOff &o, float (&acc)[T]) {
+    for (int u = lane; u < nu; u += TS) {
+        const int p = u & 3, jm = (2 * p) & 3;
+        const bool hi4 = p >= 2;
+        const uint8_t *blk = W + (rb + (u >> 2)) * 176;
+        const u32x4 hdr = ld16(blk), h0 = ld16(blk + 16), h1 = ld16(blk + 32);
+        const u32x4 qa = ld16(blk + 48 + 32 * p), qb = ld16(blk + 64 + 32 * p);
+        const float d = xjd::f16_to_f32(hdr.x & 0xFFFFu), dmin = xjd::f16_to_f32(hdr.x >> 16);
+        const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        const uint32_t hb[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        const int g0 = 8 * (u >> 2) + 2 * p;
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++) {
+            const uint32_t A = byte_of(hdr.y, jm + sb), B = byte_of(hdr.z, jm + sb), C = byte_of(hdr.w, jm + sb);
+            const uint32_t sc = hi4 ? ((C & 0xF) | ((A >> 6) << 4)) : (A & 63);
+            const uint32_t mn = hi4 ? ((C >> 4) | ((B >> 6) << 4)) : (B & 63);
+            const float ds = d * (float)sc, dm = dmin * (float)mn;
+            const int j = 2 * p + sb;
+            uint32_t q5[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                q5[k] = (sb ? (q[k] >> 4) & 0x0F0F0F0Fu : q[k] & 0x0F0F0F0Fu) | (((hb[k] >> j) & 0x01010101u) << 4);
+            const int g = g0 + sb;
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+                const uint8_t *xt = xl + t * ldsT;
+                u32x4 pa[2], pb[2], pc[2];
+                planes<8>(xt + g * kDigStride, pa, pb, pc);
+                const float f = ((const float *)(xt + o.f_off))[g];
+                const int2 sxp = ((const int2 *)(xt + o.sx_off))[g];
+                const int S = qdot<8>(q5, pa, pb, pc);
+                acc[t] = fmaf((float)S * ds - (float)(sxp.x + sxp.y) * dm, f, acc[t]);
+            }
+        }
+    }
+}
+
 // Team reduction over TS lanes (8, 16, 32 or 64) in a fixed order.
 template <int TS>
 __device__ __forceinline__ float team_sum(float v) {
@@ -765,7 +838,9 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         const int64_t r = (int64_t)(rg - sg.wg0) * NT + team;
         return r < sg.n_rows ? r : (int64_t)sg.n_rows - 1;
     };
-    auto blocks_per_row = [&](uint32_t type) { return (type == XJ_Q4_K || type == XJ_Q6_K) ? K / 256 : K / 32; };
+    auto blocks_per_row = [&](uint32_t type) {
+        return (type == XJ_Q4_K || type == XJ_Q6_K || type == XJ_Q5_K) ? K / 256 : K / 32;
+    };
     // the lane's first units of row group rg, loaded before the work that
     // precedes their use (units past the row read the tensor's padding)
     constexpr int NW = Win<MU, Q4>::N;
@@ -819,6 +894,8 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         } else {
             const int64_t rr[1] = {row}, rbb[1] = {rb};
             if (sg.type == XJ_Q8_0) rows_q80<T, TS, 1>(sg.w, sg.nblk, rbb, K / 32, lane, xl, o.v_off, o, acc);
+            else if (sg.type == XJ_Q5_K) rows_q5k<T, TS>(sg.w, rb, nu, lane, xl, o.v_off, o, acc[0]);
+            else if (sg.type == XJ_F16 || sg.type == XJ_BF16) rows_h16<T, TS, 1>(sg.w, rr, K, lane, sg.type == XJ_BF16, a.xq, o, acc);
             else rows_f32<T, TS, 1>(sg.w, rr, K, lane, a.xq, o, acc);
         }
 #pragma unroll
@@ -1057,12 +1134,15 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
     const GemvPlan p = gemv_plan(a.K, total);
     for (int i = 0; i < a.nseg; i++) {
         const GSeg &s = a.seg[i];
-        if ((s.type == XJ_Q4_K || s.type == XJ_Q6_K) && a.K % 256) return -1;
-        if (s.type != XJ_Q4_K && s.type != XJ_Q6_K && s.type != XJ_Q8_0 && s.type != XJ_F32) return -1;
+        if ((s.type == XJ_Q4_K || s.type == XJ_Q6_K || s.type == XJ_Q5_K) && a.K % 256) return -1;
+        if (s.type != XJ_Q4_K && s.type != XJ_Q6_K && s.type != XJ_Q8_0 && s.type != XJ_F32 && s.type != XJ_Q5_K &&
+            s.type != XJ_F16 && s.type != XJ_BF16)
+            return -1;
         if (s.n_rows < 1 || s.nwg != (s.n_rows + p.rows_per_group - 1) / p.rows_per_group) return -1;
         if (s.wg0 != (i ? a.seg[i - 1].wg0 + a.seg[i - 1].nwg : 0)) return -1;
         if (s.epi == EPI_CONV && (s.conv_k < 2 || s.conv_k > 8)) return -1;
-        if (s.type == XJ_F32 && a.pro == PRO_RMSU_X) return -1;   // F32 rows read v from a prep launch's xq
+        // float rows read v from a prep launch's xq
+        if ((s.type == XJ_F32 || s.type == XJ_F16 || s.type == XJ_BF16) && a.pro == PRO_RMSU_X) return -1;
     }
     if (a.post.mode != POST_NONE && a.post.mode != POST_SWIGLU) return -1;
     if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_RMSU_X) return -1;   // other prologues come prepared
@@ -1138,7 +1218,7 @@ int upload_repack(uint32_t type, const void *src, int64_t n_rows, int64_t k, uin
                   char *err, size_t errlen) {
     const uint8_t *s = (const uint8_t *)src;
     const uint64_t bytes = xj_row_bytes(type, k) * (uint64_t)n_rows;
-    if (type == XJ_F32 || type == XJ_Q4_K) {
+    if (type == XJ_F32 || type == XJ_F16 || type == XJ_BF16 || type == XJ_Q4_K || type == XJ_Q5_K) {
         XJ_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st), err, errlen, -1);
         XJ_CHECK(hipStreamSynchronize(st), err, errlen, -1);
         return 0;

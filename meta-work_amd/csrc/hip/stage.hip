@@ -99,7 +99,9 @@ T *dalloc(HStage *S, size_t n, char *err, size_t errlen) {
     return (T *)p;
 }
 
-bool gemv_type_ok(uint32_t t) { return t == XJ_F32 || t == XJ_Q4_K || t == XJ_Q6_K || t == XJ_Q8_0; }
+bool gemv_type_ok(uint32_t t) {
+    return t == XJ_F32 || t == XJ_F16 || t == XJ_BF16 || t == XJ_Q4_K || t == XJ_Q5_K || t == XJ_Q6_K || t == XJ_Q8_0;
+}
 
 bool upload(HStage *S, const xj_w &w, DevW *out, char *err, size_t errlen) {
     *out = DevW();
@@ -204,7 +206,8 @@ struct Gemv {
         }
         // RMSNorm prologues run inside the GEMV's work-groups (F32 rows read a prep launch's xq)
         bool inwg = a.pro == PRO_RMSU && !prepared && !((uintptr_t)a.x & 15) && !(a.xs & 3) && !((uintptr_t)a.pro_w & 15);
-        for (int i = 0; i < a.nseg; i++) inwg = inwg && a.seg[i].type != XJ_F32;
+        for (int i = 0; i < a.nseg; i++)
+            inwg = inwg && a.seg[i].type != XJ_F32 && a.seg[i].type != XJ_F16 && a.seg[i].type != XJ_BF16;
         const int64_t xs_in = xq_off(a.K).stride;
         const int64_t xs_out = a.post.mode != POST_NONE ? xq_off(a.seg[0].n_rows).stride : 0;
         for (int t0 = 0; t0 < T; t0 += tile) {
@@ -1102,7 +1105,8 @@ static int gemv_enqueue(uint32_t type, const void *dw, int64_t n_rows, int64_t k
 extern "C" int xjh_gemv(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T, float *y, int add,
                         char *err, size_t errlen) {
     if (!ops_stream()) return -1;
-    if (!gemv_type_ok(type) || T < 1 || n_rows < 1 || k % 32 || ((type == XJ_Q4_K || type == XJ_Q6_K) && k % 256)) {
+    if (!gemv_type_ok(type) || T < 1 || n_rows < 1 || k % 32 ||
+        ((type == XJ_Q4_K || type == XJ_Q6_K || type == XJ_Q5_K) && k % 256)) {
         snprintf(err, errlen, "unsupported GEMV shape/type"); return -1;
     }
     if (gemv_enqueue(type, dw, n_rows, k, x, T, y, add, g_stream)) { snprintf(err, errlen, "GEMV launch failed"); return -1; }

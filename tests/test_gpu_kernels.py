@@ -16,7 +16,7 @@ from helpers import random_blocks
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("t", [xp.Q4_K, xp.Q6_K, xp.Q8_0])
+@pytest.mark.parametrize("t", [xp.Q4_K, xp.Q6_K, xp.Q8_0, xp.Q5_K, xp.F16, xp.BF16])
 def test_dequant_bit_exact_random_blocks(t):
     rows, k = 96, 1024
     blob = random_blocks(t, rows, k, 11 + t)
@@ -64,6 +64,43 @@ def test_gemv_matches_oracle(t, rows, k, T):
     ref64 = xs.astype(np.float64) @ wd.T
     assert rel_l2(got, ref64) < 1e-5
     assert rel_l2(want, ref64) < 1e-5
+
+
+def _secondary_weights(t, rows, k, seed):
+    """Finite weights of the types no configuration uses: F16 / BF16 rounded
+    (RNE) from normal samples; Q5_K blocks with every field random except d and
+    dmin, drawn from a few ordinary fp16 scales (no quantizer for Q5_K exists)."""
+    rng = np.random.default_rng(seed)
+    if t in (xp.F16, xp.BF16):
+        x = (rng.standard_normal((rows, k)) * 0.05).astype(np.float32)
+        if t == xp.F16:
+            return x.astype(np.float16).view(np.uint8).reshape(-1).copy()
+        b = x.view(np.uint32).astype(np.uint64)
+        b = (b + 0x7FFF + ((b >> 16) & 1)) >> 16   # round to nearest even (finite inputs)
+        return b.astype(np.uint16).view(np.uint8).reshape(-1).copy()
+    rb = xp.row_bytes(t, k)
+    blob = rng.integers(0, 256, rows * rb, dtype=np.uint8)
+    blocks = blob.reshape(-1, 176)
+    scales = np.array([0.004, 0.002, 0.0015, 0.003], np.float16).view(np.uint16)
+    h = scales[rng.integers(0, len(scales), (blocks.shape[0], 2))]
+    blocks[:, 0:4] = h.view(np.uint8).reshape(-1, 4)
+    return blob
+
+
+@pytest.mark.parametrize("t,rows,k", [(xp.Q5_K, 700, 2560), (xp.F16, 300, 1024), (xp.BF16, 257, 512)])
+@pytest.mark.parametrize("T", [1, 3, 5])
+def test_gemv_secondary_types(t, rows, k, T):
+    blob = _secondary_weights(t, rows, k, 300 + t)
+    xs = xp.fill_normal(T * k, 90 + T, 1.0).reshape(T, k)
+    w = xp.DevWeight(t, blob, rows, k)
+    got = xp.gemv(w, xs)
+    want = orc.matmul(t, blob, k, rows, xs)
+    assert rel_l2(got, want) < 1e-3
+    wd = orc.dequant_rows(t, blob, rows, k).astype(np.float64)
+    assert np.isfinite(wd).all()
+    ref64 = xs.astype(np.float64) @ wd.T
+    assert rel_l2(got, ref64) < 1e-5
+    assert np.array_equal(xp.dequant(w).view(np.uint32), orc.dequant_rows(t, blob, rows, k).view(np.uint32))
 
 
 @pytest.mark.parametrize("t", [xp.Q4_K, xp.Q6_K, xp.Q8_0])
