@@ -730,20 +730,22 @@ __device__ __forceinline__ void emit4_rmsu(const f32x4 &x, const f32x4 &w, int k
     (void)frexpf(m, &E);
     if (E < -100) E = -100;
     const float sc = ldexpf(1.0f, 20 - E);
+    // digits of X + 64 * (2^14 + 2^7 + 1) >= 0 are the balanced digits + 64:
+    // packed as bytes, then each byte d' becomes d' - 64 (two's complement)
     uint32_t pa = 0, pb = 0, pc = 0;
     int sx = 0;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         const int X = (int)rintf(u[c] * sc);
-        const int dc = ((X + 64) & 127) - 64;
-        const int X1 = (X - dc) / 128;
-        const int db = ((X1 + 64) & 127) - 64;
-        const int da = (X1 - db) / 128;
-        pa |= ((uint32_t)da & 0xFFu) << (8 * c);
-        pb |= ((uint32_t)db & 0xFFu) << (8 * c);
-        pc |= ((uint32_t)dc & 0xFFu) << (8 * c);
+        const uint32_t Xb = (uint32_t)(X + 1056832);
+        pc |= (Xb & 127u) << (8 * c);
+        pb |= ((Xb >> 7) & 127u) << (8 * c);
+        pa |= (Xb >> 14) << (8 * c);
         sx += X;
     }
+    pa = xjd::unbias_bytes(pa);
+    pb = xjd::unbias_bytes(pb);
+    pc = xjd::unbias_bytes(pc);
     sx += xjd::dpp_i<0xB1>(sx);
     sx += xjd::dpp_i<0x4E>(sx);
     double ss = ((double)x.x * x.x + (double)x.y * x.y) + ((double)x.z * x.z + (double)x.w * x.w);
@@ -894,9 +896,12 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         } else {
             const int64_t rr[1] = {row}, rbb[1] = {rb};
             if (sg.type == XJ_Q8_0) rows_q80<T, TS, 1>(sg.w, sg.nblk, rbb, K / 32, lane, xl, o.v_off, o, acc);
-            else if (sg.type == XJ_Q5_K) rows_q5k<T, TS>(sg.w, rb, nu, lane, xl, o.v_off, o, acc[0]);
-            else if (sg.type == XJ_F16 || sg.type == XJ_BF16) rows_h16<T, TS, 1>(sg.w, rr, K, lane, sg.type == XJ_BF16, a.xq, o, acc);
-            else rows_f32<T, TS, 1>(sg.w, rr, K, lane, a.xq, o, acc);
+            // the types no configuration uses come one token per launch (their
+            // loops would raise the register count of every multi-token kernel)
+            else if (sg.type == XJ_Q5_K) { if constexpr (T == 1) rows_q5k<T, TS>(sg.w, rb, nu, lane, xl, o.v_off, o, acc[0]); }
+            else if (sg.type == XJ_F16 || sg.type == XJ_BF16) {
+                if constexpr (T == 1) rows_h16<T, TS, 1>(sg.w, rr, K, lane, sg.type == XJ_BF16, a.xq, o, acc);
+            } else rows_f32<T, TS, 1>(sg.w, rr, K, lane, a.xq, o, acc);
         }
 #pragma unroll
         for (int t = 0; t < T; t++) {
@@ -1151,6 +1156,30 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
     if (a.post.mode == POST_SWIGLU &&
         (!a.post.xq || !a.post.cnt || a.nseg != 2 || a.seg[0].n_rows != a.seg[1].n_rows || a.seg[0].n_rows % 32 ||
          32 % p.rows_per_group)) return -1;
+    if (a.T > 1) {
+        bool secondary = false;
+        for (int i = 0; i < a.nseg; i++)
+            secondary = secondary || a.seg[i].type == XJ_Q5_K || a.seg[i].type == XJ_F16 || a.seg[i].type == XJ_BF16;
+        if (secondary) {   // one launch per token (multi-token kernels carry no Q5_K / F16 / BF16 rows)
+            const int64_t xs = xq_off(a.K).stride;
+            for (int t = 0; t < a.T; t++) {
+                GArgs b = a;
+                b.T = 1;
+                b.t0 = a.t0 + t;
+                b.xq = a.xq + t * xs;
+                if (a.x) b.x = a.x + (int64_t)t * a.xs;
+                if (a.x2) b.x2 = a.x2 + (int64_t)t * a.x2s;
+                if (a.post.mode != POST_NONE) b.post.xq = a.post.xq + t * xq_off(a.seg[0].n_rows).stride;
+                for (int i = 0; i < a.nseg; i++) {
+                    b.seg[i].y = a.seg[i].y + (int64_t)t * a.seg[i].ys;
+                    if (a.seg[i].amax) b.seg[i].amax = a.seg[i].amax + (int64_t)t * a.seg[i].nwg;
+                }
+                if (t + 1 < a.T) b.inc_ptr = nullptr;
+                if (gemv_launch(b, st)) return -1;
+            }
+            return 0;
+        }
+    }
     if (a.T == 1) {
         const int rc = gemv_launch_cu(a, st);
         if (rc <= 0) return rc;

@@ -55,6 +55,10 @@ __device__ __forceinline__ int row16_sum_i(int v) {
     return v;
 }
 
+// Bytes d' in [0, 128] -> d' - 64 as int8, in every byte of a word: d' ^ 0xC0
+// is d' - 64 when bit 6 of d' is clear; bit 6 set flips bit 7 back.
+__device__ __forceinline__ uint32_t unbias_bytes(uint32_t p) { return p ^ 0xC0C0C0C0u ^ ((p << 1) & 0x80808080u); }
+
 // Writes element k (value v) of one token's xq at dst. Called by all 64
 // lanes of a wavefront with k = k0 + lane, k0 a multiple of 64, so that each
 // half-wavefront holds one 32-element group; lanes with in == false (k >= K,
@@ -68,10 +72,10 @@ __device__ __forceinline__ void emit_xq(float v, int k, bool in, uint8_t *dst, c
     (void)frexpf(m, &E);
     if (E < -100) E = -100;
     const int X = (int)rintf(v * ldexpf(1.0f, 20 - E));
-    const int c = ((X + 64) & 127) - 64;
-    const int X1 = (X - c) / 128;
-    const int b = ((X1 + 64) & 127) - 64;
-    const int a = (X1 - b) / 128;
+    // X + 64 * (2^14 + 2^7 + 1) >= 0 (|X| <= 2^20): its base-128 digits are the
+    // balanced digits + 64
+    const int Xb = X + 1056832;
+    const int c = (Xb & 127) - 64, b = ((Xb >> 7) & 127) - 64, a = (Xb >> 14) - 64;
     const int sx = row16_sum_i(X);
     if (!in) return;
     const int g = k >> 5, l = k & 31;
