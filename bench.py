@@ -147,7 +147,7 @@ def main():
             traffic = json.load(f).get("bytes_per_launch")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "gemv_kernel<1,lanes> (fused dequant-GEMV, T=1, with its prologue/tails)",
+                "kernel": "gemv_kernel<1,...> / gemv_cu_kernel (fused dequant-GEMV, T=1, with its prologues/tails)",
                 "bytes_per_launch": round(g_bytes / g_launch), "launches_per_step": g_launch,
                 "us_per_launch": round(g_ms * 1e3 / g_launch, 3), "gemv_share_of_step": round(g_ms / r["gpu_ms"], 3)}
     log(f"GEMV leg: {g_launch} launches/step, {g_bytes / 1e9:.3f} GB/step, {g_ms:.3f} ms -> {achieved:.0f} GB/s")

@@ -9,6 +9,9 @@ traffic  HBM bytes per single-token GEMV launch from FETCH_SIZE / WRITE_SIZE
          (KiB per dispatch), each scaled by the factor that makes the same
          counter read the known size of the calibration copy (the largest
          runtime copy-kernel dispatch of the run)
+
+Single-token GEMV launches are the gemv_kernel<1, ...> and gemv_cu_kernel
+dispatches (the two launch forms of the same fused dequant-GEMV).
 """
 import collections
 import csv
@@ -28,6 +31,10 @@ def _one(d, suffix):
 
 def _short(name):
     return name.split("(")[0].replace("void ", "")
+
+
+def _gemv1(name):
+    return name.startswith("void xjk::gemv_kernel<1,") or name.startswith("void xjk::gemv_cu_kernel<")
 
 
 def trace(d):
@@ -62,7 +69,7 @@ def trace(d):
         n = v[0][1]
         out.append(f"| `{k}` | {n} | {t:.1f} | {t / n:.2f} |")
     g1 = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for seg in steps for r in seg
-          if r["Kernel_Name"].startswith("void xjk::gemv_kernel<1,")]
+          if _gemv1(r["Kernel_Name"])]
     if g1:
         out += ["", f"Single-token GEMV launches in the decode steps: {len(g1)}, average duration "
                 f"{sum(g1) / len(g1) / 1e3:.3f} us."]
@@ -80,11 +87,11 @@ def traffic(dfetch, dwrite, copy_bytes, out_json=None):
         vals = _counter(d, name)
         copies = [v for k, v in vals if k.startswith("__amd_rocclr_copyBuffer")]
         factor = copy_bytes / (max(copies) * 1024.0)
-        g1 = [v for k, v in vals if k.startswith("void xjk::gemv_kernel<1,")]
+        g1 = [v for k, v in vals if _gemv1(k)]
         res[name] = {"factor": factor, "launches": len(g1), "kib_per_launch_raw": sum(g1) / len(g1),
                      "bytes_per_launch": sum(g1) / len(g1) * 1024.0 * factor}
     total = res["FETCH_SIZE"]["bytes_per_launch"] + res["WRITE_SIZE"]["bytes_per_launch"]
-    doc = {"kernel": "gemv_kernel<1,lanes> (single-token GEMV launches of the decode step)",
+    doc = {"kernel": "gemv_kernel<1,...> / gemv_cu_kernel (single-token GEMV launches of the decode step)",
            "bytes_per_launch": round(total), "fetch": res["FETCH_SIZE"], "write": res["WRITE_SIZE"],
            "calibration_copy_bytes": copy_bytes}
     if out_json:
