@@ -105,6 +105,23 @@ __device__ __forceinline__ double block_sum_d(double v, double *red) {
     for (int i = 0; i < nw; i++) s += red[i];
     return s;
 }
+// Sum over the first NW wavefronts of the work-group (threads beyond hold
+// nothing): those wavefronts reduce, every thread gets the total. red must
+// hold NW doubles; all threads must call it.
+template <int NW>
+__device__ __forceinline__ double head_sum_d(double v, double *red) {
+    const int w = threadIdx.x >> 6;
+    if (w < NW) {
+        v = wave_sum_d(v);
+        if ((threadIdx.x & 63) == 0) red[w] = v;
+    }
+    __syncthreads();
+    double s = 0;
+#pragma unroll
+    for (int i = 0; i < NW; i++) s += red[i];
+    return s;
+}
+
 // Two block-wide sums with one exchange (same order as two block_sum_d calls);
 // red must hold 2 * blockDim.x/64 doubles.
 __device__ __forceinline__ void block_sum2_d(double &a, double &b, double *red) {

@@ -93,8 +93,10 @@ __global__ __launch_bounds__(1024) void delta_head_kernel(const DeltaArgs a) {
 #pragma unroll
         for (int r = 0; r < NR; r++) vj[r] = row[a.v_off + hv * S + r16 + 64 * r];
         const float zv = a.xq && in ? a.z[(int64_t)t * a.z_s + hv * S + tid] : 0.f;
-        double sq = (double)qv * qv, sk2 = (double)kv * kv;
-        xjd::block_sum2_d(sq, sk2, red);
+        // the q and k sums over the S threads that hold them (S / 64 wavefronts)
+        __syncthreads();   // red and qs / ks of the previous token consumed
+        const double sq = xjd::head_sum_d<(S + 63) / 64>((double)qv * qv, red);
+        const double sk2 = xjd::head_sum_d<(S + 63) / 64>((double)kv * kv, red + 4);
         if (in) {
             qs[tid] = qv * (1.0f / sqrtf((float)sq + a.eps));
             ks[tid] = kv * (1.0f / sqrtf((float)sk2 + a.eps));
@@ -117,7 +119,7 @@ __global__ __launch_bounds__(1024) void delta_head_kernel(const DeltaArgs a) {
             // gated RMSNorm (xj_cpu.c:215-217) of the head's outputs into the
             // ssm_out GEMV's prepared activations
             const float ov = in ? os[tid] : 0.f;
-            const double ss = xjd::block_sum_d((double)ov * ov, red);
+            const double ss = xjd::head_sum_d<(S + 63) / 64>((double)ov * ov, red + 8);
             const float gsc = 1.0f / sqrtf((float)(ss / S) + a.eps);
             if (tid < (S + 63) / 64 * 64) {   // wavefronts holding outputs
                 const XqOff o = xq_off(a.Hv * S);
