@@ -919,16 +919,55 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
     if (a.inc_ptr && blockIdx.x == 0 && tid == 0) *a.inc_ptr += a.inc_by;
 }
 
-// Single-token launch of a prepared input with one work-group per CU:
-// work-group g of segment i (g in [wg0, wg0 + nwg)) takes rows
+// POST_SWIGLU tail of a single-token per-CU launch (rpw rows per work-group,
+// gate = segment 0, up = segment 1): the work-group arrives once on every
+// 32-index group its rows touch; the last of the group's work-groups (those
+// of both segments covering its 32 rows) emits silu(gate) * up
+// (xj_cpu.c:273). At most 8 groups per work-group (rpw <= 226).
+__device__ __forceinline__ void tail_swiglu_cu(const GArgs &a, int rg, const GSeg &sg) {
+    __shared__ int last_sh[8];
+    const int tid = threadIdx.x, j = rg - sg.wg0;
+    const int r_lo = j * a.rpw, r_hi = (r_lo + a.rpw < sg.n_rows ? r_lo + a.rpw : sg.n_rows) - 1;
+    const int ga = r_lo / 32, ng = r_hi / 32 - ga + 1;
+    __builtin_amdgcn_s_waitcnt(0);   // this group's system-scope stores of y are complete
+    __syncthreads();
+    if (tid < ng) {
+        const int grp = ga + tid;
+        const int target = 2 * ((32 * grp + 31) / a.rpw - (32 * grp) / a.rpw + 1);
+        const int n = __hip_atomic_fetch_add(a.post.cnt + grp, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = n == target - 1;
+        if (last) __hip_atomic_store(a.post.cnt + grp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_sh[tid] = last;
+    }
+    __syncthreads();
+    const GSeg &g = a.seg[0], &u = a.seg[1];
+    const XqOff o = xq_off(g.n_rows);
+    for (int i = 0; i < ng; i++) {
+        if (!last_sh[i]) continue;   // uniform
+        if (tid < 64) {
+            const int k = 32 * (ga + i) + (tid & 31);
+            const bool in = tid < 32;
+            const float v = in ? xjd::silu(xjd::load_sys(g.y + k)) * xjd::load_sys(u.y + k) : 0.f;
+            xjd::emit_xq(v, k, in, a.post.xq, o);
+        }
+    }
+}
+
+// Single-token launch with one work-group per CU (per-segment ranges of
+// work-groups): work-group g of segment i (g in [wg0, wg0 + nwg)) takes rows
 // (g - wg0) * rpw + team, one per team of TS lanes (blockDim.x / TS >= rpw
 // teams; the others repeat a valid row and store nothing). The activations
-// are copied into LDS once per CU, then every lane requests its MU units at
-// once. No tails and no argmax partials.
-template <int TS, int MU, bool Q4>
+// (prepared, or x and w of an RMSNorm input) are copied into LDS once per
+// CU; WF (RMSNorm inputs) requests two units of every lane right behind the
+// copies and converts x and w while they arrive, otherwise the copies
+// complete first and every lane then requests all its MU units. The gate|up
+// launch ends with the SwiGLU tail; no argmax partials.
+template <int TS, int MU, bool Q4, bool WF>
 __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
     extern __shared__ u32x4 lds_v[];
-    constexpr int PD = MU - 1;
+    // WF: two units requested right behind the activation copies, the rest
+    // from the unit loop; otherwise the copies complete first, then all units
+    constexpr int NW = WF ? (MU < 2 ? MU : 2) : MU, PD = NW - 1;
     const int K = a.K, nu = K / 64;
     const XqOff o = xq_off(K);
     const int tid = threadIdx.x, team = tid / TS, lane = tid % TS;
@@ -939,16 +978,24 @@ __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
     const int64_t row = mine ? r0 : (int64_t)sg.n_rows - 1;
     const int64_t rb = row * (K / 256);
     uint8_t *lds = (uint8_t *)lds_v;
-    // the activations first, complete before any weight request: queued
-    // behind the weight stream they would arrive with its last bytes
-    dma_xq<1>(a, o, lds);
-    wait_vm<0>();
+    if (a.pro == PRO_RMSU_X) rmsx1_issue(a, o, lds);
+    else dma_xq<1>(a, o, lds);
+    if (!WF) wait_vm<0>();   // the activations complete before any weight request
     barrier_raw();
-    RawU win[MU];
+    RawU win[NW];
     const int u0 = lane < nu ? lane : nu - 1;
 #pragma unroll
-    for (int m = 0; m < MU; m++) win[m] = load_unit<Q4>(sg.type, sg.w, sg.nblk, rb, u0 + m * TS);
-    const float sc = a.pro == PRO_RMSU ? rmsu_scale(a, o, lds, 0) : 1.f;
+    for (int m = 0; m < NW; m++) win[m] = load_unit<Q4>(sg.type, sg.w, sg.nblk, rb, u0 + m * TS);
+    if (WF) {
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm<(Q4 ? 3 : 5) * NW>();
+        barrier_raw();
+    }
+    if (a.pro == PRO_RMSU_X) {
+        rmsx1_finish(a, o, lds);
+        barrier_lds();
+    }
+    const float sc = a.pro == PRO_RMSU || a.pro == PRO_RMSU_X ? rmsu_scale(a, o, lds, 0) : 1.f;
     EpiIn<1> ein;
     epi_load<1>(sg, row, ein);
     float acc[1] = {0.f};
@@ -959,6 +1006,7 @@ __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
     }
     acc[0] = team_sum<TS>(acc[0]) * sc;
     if (mine && lane == 0) epi_row<1>(a, sg, row, acc, ein);
+    if (a.post.mode == POST_SWIGLU) tail_swiglu_cu(a, rg, sg);
     if (a.inc_ptr && blockIdx.x == 0 && tid == 0) *a.inc_ptr += a.inc_by;
 }
 
@@ -1061,7 +1109,7 @@ static hipError_t launch_ts(const GArgs &a, int grid, hipStream_t st) {
 // work-groups counted, at most one per CU in total. Returns 1 when not
 // applicable.
 template <int TS>
-static int launch_cu_ts(GArgs b, int rpw, int upl, bool q4, hipStream_t st) {
+static int launch_cu_ts(GArgs b, int rpw, int upl, bool q4, bool wf, hipStream_t st) {
     int wg = 0;
     for (int i = 0; i < b.nseg; i++) {
         b.seg[i].wg0 = wg;
@@ -1069,36 +1117,46 @@ static int launch_cu_ts(GArgs b, int rpw, int upl, bool q4, hipStream_t st) {
         wg += b.seg[i].nwg;
     }
     b.rpw = rpw;
-    const int threads = (rpw * TS + 63) / 64 * 64;
+    int threads = (rpw * TS + 63) / 64 * 64;
+    // an RMSNorm input is converted four elements per thread in one pass
+    if (b.pro == PRO_RMSU_X && threads < b.K / 4 && b.K / 4 <= 1024) threads = (b.K / 4 + 63) / 64 * 64;
     size_t lds = gemv_lds_bytes(b);
     // more than half of a CU's LDS keeps each work-group on a CU of its own
-    if (g_lds_max > 80 * 1024 && lds < 80 * 1024 + 256) lds = 80 * 1024 + 256;
+    if (!wf && g_lds_max > 80 * 1024 && lds < 80 * 1024 + 256) lds = 80 * 1024 + 256;
     void (*k)(GArgs) = nullptr;
-    if (q4) {
-        switch (upl) {
-        case 1: k = gemv_cu_kernel<TS, 1, true>; break;
-        case 2: k = gemv_cu_kernel<TS, 2, true>; break;
-        case 3: k = gemv_cu_kernel<TS, 3, true>; break;
-        case 4: k = gemv_cu_kernel<TS, 4, true>; break;
-        default: k = gemv_cu_kernel<TS, 5, true>; break;
-        }
-    } else {
-        switch (upl) {
-        case 1: k = gemv_cu_kernel<TS, 1, false>; break;
-        case 2: k = gemv_cu_kernel<TS, 2, false>; break;
-        case 3: k = gemv_cu_kernel<TS, 3, false>; break;
-        case 4: k = gemv_cu_kernel<TS, 4, false>; break;
-        default: k = gemv_cu_kernel<TS, 5, false>; break;
-        }
+#define XJ_CU_K(Q, W)                                          \
+    switch (upl) {                                              \
+    case 1: k = gemv_cu_kernel<TS, 1, Q, W>; break;            \
+    case 2: k = gemv_cu_kernel<TS, 2, Q, W>; break;            \
+    case 3: k = gemv_cu_kernel<TS, 3, Q, W>; break;            \
+    case 4: k = gemv_cu_kernel<TS, 4, Q, W>; break;            \
+    default: k = gemv_cu_kernel<TS, 5, Q, W>; break;           \
     }
+    if (q4 && wf) { XJ_CU_K(true, true) }
+    else if (q4) { XJ_CU_K(true, false) }
+    else if (wf) { XJ_CU_K(false, true) }
+    else { XJ_CU_K(false, false) }
+#undef XJ_CU_K
     hipLaunchKernelGGL(k, dim3(wg), dim3(threads), lds, st, b);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 static int gemv_launch_cu(const GArgs &a, hipStream_t st) {
     static const bool on = env_or("XJ_GEMV_CU", 1) != 0;
-    if (!on || a.T != 1 || a.post.mode != POST_NONE) return 1;
-    if (a.pro != PRO_NONE && a.pro != PRO_RMSU) return 1;   // RMSNorm built in LDS: many work-groups share it
+    static const int rms_k = env_or("XJ_GEMV_RMS_WG_PER_CU", 1);
+    if (!on || a.T != 1) return 1;
+    if (a.post.mode == POST_SWIGLU) {
+        if (!a.post.xq || !a.post.cnt || a.nseg != 2 || a.seg[0].n_rows != a.seg[1].n_rows || a.seg[0].n_rows % 32)
+            return 1;
+    } else if (a.post.mode != POST_NONE) {
+        return 1;
+    }
+    if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_RMSU_X) return 1;
+    // RMSNorm inputs: rms_k balanced work-groups per CU, the weight window
+    // requested right behind the copies of x and w
+    const bool wf = a.pro == PRO_RMSU_X;
+    if (wf && (rms_k < 1 || !a.x || !a.pro_w || ((uintptr_t)a.x & 15) || ((uintptr_t)a.pro_w & 15))) return 1;
+    const int nwg_max = wf ? rms_k * g_cus : g_cus;
     int64_t total = 0;
     bool q4 = true;
     for (int i = 0; i < a.nseg; i++) {
@@ -1109,23 +1167,23 @@ static int gemv_launch_cu(const GArgs &a, hipStream_t st) {
         total += s.n_rows;
     }
     if (a.K % 256 || a.K > 16384 || gemv_lds_bytes(a) > (size_t)g_lds_max) return 1;
-    // the fewest rows per work-group whose work-groups fit one per CU
-    int rpw = (int)((total + g_cus - 1) / g_cus);
+    // the fewest rows per work-group whose work-groups fit nwg_max
+    int rpw = (int)((total + nwg_max - 1) / nwg_max);
     for (;; rpw++) {
         int64_t wg = 0;
         for (int i = 0; i < a.nseg; i++) wg += (a.seg[i].n_rows + rpw - 1) / rpw;
-        if (wg <= g_cus) break;
+        if (wg <= nwg_max) break;
     }
     // the most lanes per row (more wavefronts) with at most 5 units per lane
     const int nu = a.K / 64;
     for (int ts = 64; ts >= 8; ts /= 2) {
         const int upl = (nu + ts - 1) / ts;
-        if (upl > 5 || rpw * ts > 1024) continue;
+        if (upl > 5 || rpw * ts > 1024 || (a.post.mode == POST_SWIGLU && rpw > 226)) continue;
         switch (ts) {
-        case 8: return launch_cu_ts<8>(a, rpw, upl, q4, st);
-        case 16: return launch_cu_ts<16>(a, rpw, upl, q4, st);
-        case 32: return launch_cu_ts<32>(a, rpw, upl, q4, st);
-        default: return launch_cu_ts<64>(a, rpw, upl, q4, st);
+        case 8: return launch_cu_ts<8>(a, rpw, upl, q4, wf, st);
+        case 16: return launch_cu_ts<16>(a, rpw, upl, q4, wf, st);
+        case 32: return launch_cu_ts<32>(a, rpw, upl, q4, wf, st);
+        default: return launch_cu_ts<64>(a, rpw, upl, q4, wf, st);
         }
     }
     return 1;
@@ -1211,14 +1269,19 @@ static void raise_ts(int bytes) {
     for (const void *k : f) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 
+template <int TS, bool WF>
+static void raise_cu_wf(int bytes) {
+    const void *f[] = {(const void *)gemv_cu_kernel<TS, 1, true, WF>, (const void *)gemv_cu_kernel<TS, 2, true, WF>,
+                       (const void *)gemv_cu_kernel<TS, 3, true, WF>, (const void *)gemv_cu_kernel<TS, 4, true, WF>,
+                       (const void *)gemv_cu_kernel<TS, 5, true, WF>, (const void *)gemv_cu_kernel<TS, 1, false, WF>,
+                       (const void *)gemv_cu_kernel<TS, 2, false, WF>, (const void *)gemv_cu_kernel<TS, 3, false, WF>,
+                       (const void *)gemv_cu_kernel<TS, 4, false, WF>, (const void *)gemv_cu_kernel<TS, 5, false, WF>};
+    for (const void *k : f) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
 template <int TS>
 static void raise_cu(int bytes) {
-    const void *f[] = {(const void *)gemv_cu_kernel<TS, 1, true>, (const void *)gemv_cu_kernel<TS, 2, true>,
-                       (const void *)gemv_cu_kernel<TS, 3, true>, (const void *)gemv_cu_kernel<TS, 4, true>,
-                       (const void *)gemv_cu_kernel<TS, 5, true>, (const void *)gemv_cu_kernel<TS, 1, false>,
-                       (const void *)gemv_cu_kernel<TS, 2, false>, (const void *)gemv_cu_kernel<TS, 3, false>,
-                       (const void *)gemv_cu_kernel<TS, 4, false>, (const void *)gemv_cu_kernel<TS, 5, false>};
-    for (const void *k : f) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    raise_cu_wf<TS, false>(bytes);
+    raise_cu_wf<TS, true>(bytes);
 }
 
 int gemv_init(char *err, size_t errlen) {
