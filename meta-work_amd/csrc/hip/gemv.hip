@@ -712,94 +712,135 @@ __device__ __forceinline__ void dma_xq(const GArgs &a, const XqOff &o, uint8_t *
     for (int t = 0; t < T; t++) dma_lds(a.xq + (int64_t)t * o.stride, lds + t * o.v_off, o.v_off >> 4);
 }
 
-// PRO_RMSU_X: four consecutive inputs k..k+3 of one token, u = x * w, into
-// its LDS copy at dst: the digits, scale and half-group sums that emit_xq
-// gives for u, and the group's sum of x^2. Called by all 64 lanes of a
-// wavefront with k = k0 + 4 * lane (8 lanes per 32-element group); lanes with
-// in == false (whole groups, since K % 32 == 0) store nothing.
-__device__ __forceinline__ void emit4_rmsu(const f32x4 &x, const f32x4 &w, int k, bool in, uint8_t *dst,
-                                           const XqOff &o) {
-    const float u[4] = {x.x * w.x, x.y * w.y, x.z * w.z, x.w * w.w};
-    float m = fmaxf(fmaxf(fabsf(u[0]), fabsf(u[1])), fmaxf(fabsf(u[2]), fabsf(u[3])));
-    // reductions over the 8 lanes of the group (quad butterflies, then the
-    // half-row mirror joins the two quads), over its 4 lanes for sx
-    m = fmaxf(m, xjd::dpp<0xB1>(m));
+// PRO_RMSU_X / PRO_X: eight consecutive inputs k..k+7 of one token (u = x * w,
+// or u = x for PRO_X) into its LDS copy at dst: the digits, scale and
+// half-group sums that emit_xq gives for u, and (RMS) the group's sum of x^2.
+// Called by all 64 lanes of a wavefront with k = k0 + 8 * lane (4 lanes per
+// 32-element group, 2 per half); lanes with in == false (whole groups, since
+// K % 32 == 0) store nothing.
+template <bool RMS>
+__device__ __forceinline__ void emit8(const f32x4 (&x)[2], const f32x4 (&w)[2], int k, bool in, uint8_t *dst,
+                                      const XqOff &o) {
+    const float xv[8] = {x[0].x, x[0].y, x[0].z, x[0].w, x[1].x, x[1].y, x[1].z, x[1].w};
+    float u[8];
+    if (RMS) {
+        const float wv[8] = {w[0].x, w[0].y, w[0].z, w[0].w, w[1].x, w[1].y, w[1].z, w[1].w};
+#pragma unroll
+        for (int c = 0; c < 8; c++) u[c] = xv[c] * wv[c];
+    } else {
+#pragma unroll
+        for (int c = 0; c < 8; c++) u[c] = xv[c];
+    }
+    float m = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; c++) m = fmaxf(m, fabsf(u[c]));
+    m = fmaxf(m, xjd::dpp<0xB1>(m));   // the group's 4 lanes (one quad)
     m = fmaxf(m, xjd::dpp<0x4E>(m));
-    m = fmaxf(m, xjd::dpp<0x141>(m));
     int E = 0;
     (void)frexpf(m, &E);
     if (E < -100) E = -100;
     const float sc = ldexpf(1.0f, 20 - E);
-    // digits of X + 64 * (2^14 + 2^7 + 1) >= 0 are the balanced digits + 64:
-    // packed as bytes, then each byte d' becomes d' - 64 (two's complement)
-    uint32_t pa = 0, pb = 0, pc = 0;
-    int sx = 0;
+    // X = rint(u * sc), |X| <= 2^20: u * sc + 1.5 * 2^23 rounds once (to
+    // nearest even) to an integer whose float bits are 0x4B400000 + X. The
+    // base-128 digits of Xb = X + 64 * (2^14 + 2^7 + 1) >= 0 are the balanced
+    // digits + 64.
+    constexpr uint32_t kBias = 0x102040u;
+    uint32_t xb[8], sum = 0;
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const int X = (int)rintf(u[c] * sc);
-        const uint32_t Xb = (uint32_t)(X + 1056832);
-        pc |= (Xb & 127u) << (8 * c);
-        pb |= ((Xb >> 7) & 127u) << (8 * c);
-        pa |= (Xb >> 14) << (8 * c);
-        sx += X;
+    for (int c = 0; c < 8; c++) {
+        xb[c] = __float_as_uint(__builtin_fmaf(u[c], sc, 12582912.0f)) - (0x4B400000u - kBias);
+        sum += xb[c];
     }
-    pa = xjd::unbias_bytes(pa);
-    pb = xjd::unbias_bytes(pb);
-    pc = xjd::unbias_bytes(pc);
-    sx += xjd::dpp_i<0xB1>(sx);
-    sx += xjd::dpp_i<0x4E>(sx);
-    double ss = ((double)x.x * x.x + (double)x.y * x.y) + ((double)x.z * x.z + (double)x.w * x.w);
-    ss += xjd::dpp_d<0xB1>(ss);
-    ss += xjd::dpp_d<0x4E>(ss);
-    ss += xjd::dpp_d<0x141>(ss);
+    int sx = (int)sum - 8 * (int)kBias;
+    sx += xjd::dpp_i<0xB1>(sx);   // the 16-element half (2 lanes)
+    // digit bytes of four inputs: t = the low 16 bits of two Xb side by side,
+    // s = bits 8..23; c = bits 0..6, b = bits 7..13, a = bits 14..21 of Xb
+    uint32_t pa[2], pb[2], pc[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t *q = xb + 4 * h;
+        const uint32_t t01 = __builtin_amdgcn_perm(q[1], q[0], 0x05040100u);
+        const uint32_t t23 = __builtin_amdgcn_perm(q[3], q[2], 0x05040100u);
+        const uint32_t s01 = __builtin_amdgcn_perm(q[1], q[0], 0x06050201u);
+        const uint32_t s23 = __builtin_amdgcn_perm(q[3], q[2], 0x06050201u);
+        pc[h] = xjd::unbias_bytes(__builtin_amdgcn_perm(t23, t01, 0x06040200u) & 0x7F7F7F7Fu);
+        pb[h] = xjd::unbias_bytes(__builtin_amdgcn_perm(t23 >> 7, t01 >> 7, 0x06040200u) & 0x7F7F7F7Fu);
+        pa[h] = xjd::unbias_bytes(__builtin_amdgcn_perm(s23 >> 6, s01 >> 6, 0x06040200u));
+    }
+    double ss = 0;
+    if (RMS) {
+        double q[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) q[c] = (double)xv[2 * c] * xv[2 * c] + (double)xv[2 * c + 1] * xv[2 * c + 1];
+        ss = (q[0] + q[1]) + (q[2] + q[3]);
+        ss += xjd::dpp_d<0xB1>(ss);
+        ss += xjd::dpp_d<0x4E>(ss);
+    }
     if (!in) return;
     const int g = k >> 5, l = k & 31;
-    *(uint32_t *)(dst + g * kDigStride + l) = pa;
-    *(uint32_t *)(dst + g * kDigStride + 32 + l) = pb;
-    *(uint32_t *)(dst + g * kDigStride + 64 + l) = pc;
+    uint8_t *d = dst + g * kDigStride + l;
+    *(uint2 *)d = make_uint2(pa[0], pa[1]);
+    *(uint2 *)(d + 32) = make_uint2(pb[0], pb[1]);
+    *(uint2 *)(d + 64) = make_uint2(pc[0], pc[1]);
     if (l == 0) {
         ((float *)(dst + o.f_off))[g] = ldexpf(1.0f, E - 20);
-        ((double *)(dst + o.ss_off))[g] = ss;
+        if (RMS) ((double *)(dst + o.ss_off))[g] = ss;
     }
     if ((k & 15) == 0) ((int *)(dst + o.sx_off))[k >> 4] = sx;
 }
 
 __device__ __forceinline__ f32x4 ld4f(const float *p) { return *(const f32x4 *)p; }
 
-// PRO_RMSU_X for a single token: x and w are copied into LDS after the
-// activations' area (at xl + v_off, 8 K bytes), then converted into it.
+// Prologues whose activations the GEMV's work-groups build from x in LDS.
+__device__ __forceinline__ bool pro_inwg(int pro) { return pro == PRO_RMSU_X || pro == PRO_X; }
+
+// PRO_RMSU_X / PRO_X for a single token: x (and w) are copied into LDS after
+// the activations' area (at xl + v_off, 4 K bytes each), then converted into
+// it (PRO_X: u = x * 1, exact).
 __device__ __forceinline__ void rmsx1_issue(const GArgs &a, const XqOff &o, uint8_t *xl) {
     dma_lds((const uint8_t *)a.x, xl + o.v_off, a.K >> 2);
-    dma_lds((const uint8_t *)a.pro_w, xl + o.v_off + 4 * a.K, a.K >> 2);
+    if (a.pro == PRO_RMSU_X) dma_lds((const uint8_t *)a.pro_w, xl + o.v_off + 4 * a.K, a.K >> 2);
 }
 
 __device__ __forceinline__ void rmsx1_finish(const GArgs &a, const XqOff &o, uint8_t *xl) {
     const f32x4 *xs = (const f32x4 *)(xl + o.v_off), *ws = (const f32x4 *)(xl + o.v_off + 4 * a.K);
-    const int n4 = a.K >> 2;
-    for (int i0 = 0; i0 < n4; i0 += blockDim.x) {
-        const int i = i0 + threadIdx.x, ic = i < n4 ? i : n4 - 1;
-        emit4_rmsu(xs[ic], ws[ic], 4 * i, i < n4, xl, o);
+    const int n8 = a.K >> 3;
+    for (int i0 = 0; i0 < n8; i0 += blockDim.x) {
+        const int i = i0 + threadIdx.x, ic = i < n8 ? i : n8 - 1;
+        const f32x4 x[2] = {xs[2 * ic], xs[2 * ic + 1]};
+        if (a.pro == PRO_X) {
+            emit8<false>(x, x, 8 * i, i < n8, xl, o);
+        } else {
+            const f32x4 w[2] = {ws[2 * ic], ws[2 * ic + 1]};
+            emit8<true>(x, w, 8 * i, i < n8, xl, o);
+        }
     }
 }
 
-// PRO_RMSU_X setup for T tokens and any K, loads after the weight window.
+// PRO_RMSU_X / PRO_X setup for T tokens and any K, loads after the weight window.
 template <int T>
 __device__ __forceinline__ void rmsx_stage(const GArgs &a, const XqOff &o, uint8_t *xl) {
-    const int n4 = a.K >> 2;
+    const int n8 = a.K >> 3;
+    const bool rms = a.pro == PRO_RMSU_X;
     for (int t = 0; t < T; t++) {
         const float *x = a.x + (int64_t)t * a.xs;
-        for (int i0 = 0; i0 < n4; i0 += 1024) {
-            f32x4 xv[4], wv[4];
+        for (int i0 = 0; i0 < n8; i0 += 512) {
+            f32x4 xv[2][2], wv[2][2];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int i = i0 + threadIdx.x + 256 * j, ic = i < n4 ? i : n4 - 1;
-                xv[j] = ld4f(x + 4 * ic);
-                wv[j] = ld4f(a.pro_w + 4 * ic);
+            for (int j = 0; j < 2; j++) {
+                const int i = i0 + threadIdx.x + 256 * j, ic = i < n8 ? i : n8 - 1;
+                xv[j][0] = ld4f(x + 8 * ic);
+                xv[j][1] = ld4f(x + 8 * ic + 4);
+                if (rms) {
+                    wv[j][0] = ld4f(a.pro_w + 8 * ic);
+                    wv[j][1] = ld4f(a.pro_w + 8 * ic + 4);
+                }
             }
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int k = 4 * (i0 + threadIdx.x + 256 * j);
-                emit4_rmsu(xv[j], wv[j], k, k < a.K, xl + t * o.v_off, o);
+            for (int j = 0; j < 2; j++) {
+                const int i = i0 + threadIdx.x + 256 * j;
+                if (rms) emit8<true>(xv[j], wv[j], 8 * i, i < n8, xl + t * o.v_off, o);
+                else emit8<false>(xv[j], xv[j], 8 * i, i < n8, xl + t * o.v_off, o);
             }
         }
     }
@@ -856,21 +897,21 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
     };
     int rg = blockIdx.x;
     uint8_t *lds = (uint8_t *)lds_v;
-    if (a.pro == PRO_RMSU_X && T > 1) {
+    if (pro_inwg(a.pro) && T > 1) {
         first_units(rg);
         rmsx_stage<T>(a, o, lds);
         __syncthreads();
     } else {
         // LDS copies first, then the window's loads: waiting for vmcnt <=
         // their number completes the copies only
-        if (a.pro == PRO_RMSU_X) rmsx1_issue(a, o, lds);
+        if (pro_inwg(a.pro)) rmsx1_issue(a, o, lds);
         else dma_xq<T>(a, o, lds);
         barrier_raw();   // the group's copies are queued ahead of its weight requests
         first_units(rg);
         __builtin_amdgcn_sched_barrier(0);
         wait_vm<Win<MU, Q4>::LOADS>();
         barrier_raw();
-        if (a.pro == PRO_RMSU_X) {
+        if (pro_inwg(a.pro)) {
             rmsx1_finish(a, o, lds);
             barrier_lds();
         }
@@ -953,15 +994,31 @@ __device__ __forceinline__ void tail_swiglu_cu(const GArgs &a, int rg, const GSe
     }
 }
 
+// POST_SWIGLU_H: the gate results of the work-group's rows (teams [0, rpw))
+// and the up results of the same rows (teams [ho, ho + rpw)) meet in LDS, and
+// silu(gate) * up (xj_cpu.c:273) is stored for each row.
+__device__ __forceinline__ void swiglu_h_cu(const GArgs &a, int rg, int ho, int team, int lane, float y) {
+    __shared__ float ys[128];   // one per team (TS >= 8)
+    if (lane == 0) ys[team] = y;
+    barrier_lds();
+    const int i = threadIdx.x;
+    const int64_t r = (int64_t)rg * a.rpw + i;
+    if (i < a.rpw && r < a.seg[0].n_rows) a.post.h[r] = xjd::silu(ys[i]) * ys[ho + i];
+}
+
 // Single-token launch with one work-group per CU (per-segment ranges of
 // work-groups): work-group g of segment i (g in [wg0, wg0 + nwg)) takes rows
 // (g - wg0) * rpw + team, one per team of TS lanes (blockDim.x / TS >= rpw
-// teams; the others repeat a valid row and store nothing). The activations
-// (prepared, or x and w of an RMSNorm input) are copied into LDS once per
-// CU; WF (RMSNorm inputs) requests two units of every lane right behind the
-// copies and converts x and w while they arrive, otherwise the copies
-// complete first and every lane then requests all its MU units. The gate|up
-// launch ends with the SwiGLU tail; no argmax partials.
+// teams; the others repeat a valid row and store nothing). POST_SWIGLU_H:
+// work-group g takes rows g * rpw + team of the gate (segment 0) in teams
+// [0, rpw) and the same rows of the up (segment 1) in teams [ho, ho + rpw),
+// ho = rpw rounded up to whole wavefronts. The activations (prepared, or
+// the x (and w) of an input built in the work-group: PRO_RMSU_X, PRO_X) are
+// copied into LDS once per CU; WF (inputs built in the work-group) requests
+// two units of every lane right behind the copies and converts x while they
+// arrive, otherwise the copies complete first and every lane then requests
+// all its MU units. The gate|up launch ends with the SwiGLU tail (or its
+// work-group-local form, POST_SWIGLU_H); no argmax partials.
 template <int TS, int MU, bool Q4, bool WF>
 __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
     extern __shared__ u32x4 lds_v[];
@@ -972,13 +1029,20 @@ __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
     const XqOff o = xq_off(K);
     const int tid = threadIdx.x, team = tid / TS, lane = tid % TS;
     const int rg = blockIdx.x;
-    const GSeg &sg = a.seg[seg_of(a, rg)];
-    const int64_t r0 = (int64_t)(rg - sg.wg0) * a.rpw + team;
-    const bool mine = team < a.rpw && r0 < sg.n_rows;
+    const bool H = a.post.mode == POST_SWIGLU_H;
+    constexpr int TPW = 64 / TS;   // teams per wavefront
+    const int ho = (a.rpw + TPW - 1) / TPW * TPW;
+    // uniform over the wavefront (ho is a multiple of TPW)
+    const int si = H ? __builtin_amdgcn_readfirstlane((int)(team >= ho)) : seg_of(a, rg);
+    const GSeg &sg = a.seg[si];
+    const int tr = H && si ? team - ho : team;
+    const int64_t r0 = (int64_t)(rg - sg.wg0) * a.rpw + tr;
+    const bool mine = tr < a.rpw && r0 < sg.n_rows;
     const int64_t row = mine ? r0 : (int64_t)sg.n_rows - 1;
     const int64_t rb = row * (K / 256);
     uint8_t *lds = (uint8_t *)lds_v;
-    if (a.pro == PRO_RMSU_X) rmsx1_issue(a, o, lds);
+    const bool inwg = pro_inwg(a.pro);
+    if (inwg) rmsx1_issue(a, o, lds);
     else dma_xq<1>(a, o, lds);
     if (!WF) wait_vm<0>();   // the activations complete before any weight request
     barrier_raw();
@@ -986,12 +1050,12 @@ __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
     const int u0 = lane < nu ? lane : nu - 1;
 #pragma unroll
     for (int m = 0; m < NW; m++) win[m] = load_unit<Q4>(sg.type, sg.w, sg.nblk, rb, u0 + m * TS);
-    if (WF) {
+    if (WF) {   // the copies complete, the window's loads stay in flight
         __builtin_amdgcn_sched_barrier(0);
         wait_vm<(Q4 ? 3 : 5) * NW>();
         barrier_raw();
     }
-    if (a.pro == PRO_RMSU_X) {
+    if (inwg) {
         rmsx1_finish(a, o, lds);
         barrier_lds();
     }
@@ -1005,8 +1069,12 @@ __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
         rows_q6k<1, TS, MU, PD>(sg.w, sg.nblk, rb, nu, lane, win, lds, o.v_off, o, acc);
     }
     acc[0] = team_sum<TS>(acc[0]) * sc;
-    if (mine && lane == 0) epi_row<1>(a, sg, row, acc, ein);
-    if (a.post.mode == POST_SWIGLU) tail_swiglu_cu(a, rg, sg);
+    if (H) {
+        swiglu_h_cu(a, rg, ho, team, lane, acc[0]);
+    } else {
+        if (mine && lane == 0) epi_row<1>(a, sg, row, acc, ein);
+        if (a.post.mode == POST_SWIGLU) tail_swiglu_cu(a, rg, sg);
+    }
     if (a.inc_ptr && blockIdx.x == 0 && tid == 0) *a.inc_ptr += a.inc_by;
 }
 
@@ -1053,10 +1121,11 @@ int prep_launch(const GArgs &a, hipStream_t st) {
 }
 
 // Dynamic LDS of a launch: the T tokens' activations, and for a single-token
-// PRO_RMSU_X launch the copies of x and w after them.
+// PRO_RMSU_X (PRO_X) launch the copies of x and w (x) after them.
 static size_t gemv_lds_bytes(const GArgs &a) {
     const size_t b = (size_t)a.T * xq_off(a.K).v_off;
-    return a.pro == PRO_RMSU_X && a.T == 1 ? b + 8 * (size_t)a.K : b;
+    if (a.T > 1) return b;
+    return a.pro == PRO_RMSU_X ? b + 8 * (size_t)a.K : a.pro == PRO_X ? b + 4 * (size_t)a.K : b;
 }
 
 template <int T, int TS, int MU = 0, bool Q4 = false>
@@ -1103,26 +1172,48 @@ static hipError_t launch_ts(const GArgs &a, int grid, hipStream_t st) {
     }
 }
 
-// Per-CU launch (gemv_cu_kernel) of a single-token GEMV when its rows fit
-// one work-group per CU: lanes per row TS with at most 5 units per lane,
-// rows per work-group rpw with rpw * TS <= 1024 and every segment's
-// work-groups counted, at most one per CU in total. Returns 1 when not
-// applicable.
+// Threads of a per-CU work-group whose teams need `need`: an input built in
+// the work-group is converted eight elements per thread, in one round where a
+// work-group of K / 8 threads is allowed.
+static int cu_threads(const GArgs &a, int need) {
+    int t = (need + 63) / 64 * 64;
+    if (a.pro == PRO_RMSU_X || a.pro == PRO_X) {
+        const int one = (a.K / 8 + 63) / 64 * 64;
+        if (t < one && one <= 1024) t = one;
+    }
+    return t;
+}
+
+// Teams of a per-CU work-group with rpw rows (POST_SWIGLU_H: rpw gate rows
+// from team 0 and rpw up rows from the first whole wavefront after them).
+static int cu_teams(int rpw, int ts, bool h) {
+    const int tpw = 64 / ts;
+    return h ? (rpw + tpw - 1) / tpw * tpw + rpw : rpw;
+}
+
+// Per-CU launch (gemv_cu_kernel) of a single-token GEMV under its plan
+// (cu_plan): lanes per row TS with at most 5 units per lane, rows per
+// work-group rpw with teams * TS <= 1024, every segment's work-groups counted
+// (POST_SWIGLU_H: shared by both segments), at most one per CU in total.
 template <int TS>
 static int launch_cu_ts(GArgs b, int rpw, int upl, bool q4, bool wf, hipStream_t st) {
-    int wg = 0;
-    for (int i = 0; i < b.nseg; i++) {
-        b.seg[i].wg0 = wg;
-        b.seg[i].nwg = (b.seg[i].n_rows + rpw - 1) / rpw;
-        wg += b.seg[i].nwg;
+    int wg = 0, teams = rpw;
+    if (b.post.mode == POST_SWIGLU_H) {   // gate and up rows of the same indices in each work-group
+        wg = (b.seg[0].n_rows + rpw - 1) / rpw;
+        for (int i = 0; i < 2; i++) b.seg[i].wg0 = 0, b.seg[i].nwg = wg;
+        teams = cu_teams(rpw, TS, true);
+    } else {
+        for (int i = 0; i < b.nseg; i++) {
+            b.seg[i].wg0 = wg;
+            b.seg[i].nwg = (b.seg[i].n_rows + rpw - 1) / rpw;
+            wg += b.seg[i].nwg;
+        }
     }
     b.rpw = rpw;
-    int threads = (rpw * TS + 63) / 64 * 64;
-    // an RMSNorm input is converted four elements per thread in one pass
-    if (b.pro == PRO_RMSU_X && threads < b.K / 4 && b.K / 4 <= 1024) threads = (b.K / 4 + 63) / 64 * 64;
+    const int threads = cu_threads(b, teams * TS);
     size_t lds = gemv_lds_bytes(b);
     // more than half of a CU's LDS keeps each work-group on a CU of its own
-    if (!wf && g_lds_max > 80 * 1024 && lds < 80 * 1024 + 256) lds = 80 * 1024 + 256;
+    if (b.pro != PRO_RMSU_X && g_lds_max > 80 * 1024 && lds < 80 * 1024 + 256) lds = 80 * 1024 + 256;
     void (*k)(GArgs) = nullptr;
 #define XJ_CU_K(Q, W)                                          \
     switch (upl) {                                              \
@@ -1141,52 +1232,86 @@ static int launch_cu_ts(GArgs b, int rpw, int upl, bool q4, bool wf, hipStream_t
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-static int gemv_launch_cu(const GArgs &a, hipStream_t st) {
+// Per-CU plan of a single-token launch: rows per work-group (per segment
+// for POST_SWIGLU_H), lanes per row, units per lane, all-Q4_K, and whether
+// the weight window is requested behind the activation copies.
+struct CuPlan {
+    int rpw, ts, upl;
+    bool q4, wf;
+};
+
+static bool cu_plan(const GArgs &a, CuPlan &p) {
     static const bool on = env_or("XJ_GEMV_CU", 1) != 0;
     static const int rms_k = env_or("XJ_GEMV_RMS_WG_PER_CU", 1);
-    if (!on || a.T != 1) return 1;
+    if (!on || a.T != 1) return false;
+    const bool H = a.post.mode == POST_SWIGLU_H;
     if (a.post.mode == POST_SWIGLU) {
         if (!a.post.xq || !a.post.cnt || a.nseg != 2 || a.seg[0].n_rows != a.seg[1].n_rows || a.seg[0].n_rows % 32)
-            return 1;
+            return false;
+    } else if (H) {
+        if (!a.post.h || a.nseg != 2 || a.seg[0].n_rows != a.seg[1].n_rows || a.seg[0].type != a.seg[1].type ||
+            a.seg[0].epi != EPI_STORE || a.seg[1].epi != EPI_STORE)
+            return false;
     } else if (a.post.mode != POST_NONE) {
-        return 1;
+        return false;
     }
-    if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_RMSU_X) return 1;
-    // RMSNorm inputs: rms_k balanced work-groups per CU, the weight window
-    // requested right behind the copies of x and w
-    const bool wf = a.pro == PRO_RMSU_X;
-    if (wf && (rms_k < 1 || !a.x || !a.pro_w || ((uintptr_t)a.x & 15) || ((uintptr_t)a.pro_w & 15))) return 1;
-    const int nwg_max = wf ? rms_k * g_cus : g_cus;
+    if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_RMSU_X && a.pro != PRO_X) return false;
+    if ((a.pro == PRO_RMSU_X || a.pro == PRO_X) && (!a.x || ((uintptr_t)a.x & 15))) return false;
+    // inputs built in the work-group: the weight window requested right
+    // behind the copies of x (and w); RMSNorm inputs: rms_k balanced
+    // work-groups per CU
+    const bool wf = a.pro == PRO_RMSU_X || a.pro == PRO_X;
+    if (a.pro == PRO_RMSU_X && (rms_k < 1 || !a.pro_w || ((uintptr_t)a.pro_w & 15))) return false;
+    const int nwg_max = a.pro == PRO_RMSU_X ? rms_k * g_cus : g_cus;
     int64_t total = 0;
     bool q4 = true;
     for (int i = 0; i < a.nseg; i++) {
         const GSeg &s = a.seg[i];
-        if ((s.type != XJ_Q4_K && s.type != XJ_Q6_K) || s.amax || s.n_rows < 1) return 1;
-        if (s.epi == EPI_CONV && (s.conv_k < 2 || s.conv_k > 8)) return 1;
+        if ((s.type != XJ_Q4_K && s.type != XJ_Q6_K) || s.amax || s.n_rows < 1) return false;
+        if (s.epi == EPI_CONV && (s.conv_k < 2 || s.conv_k > 8)) return false;
         q4 = q4 && s.type == XJ_Q4_K;
         total += s.n_rows;
     }
-    if (a.K % 256 || a.K > 16384 || gemv_lds_bytes(a) > (size_t)g_lds_max) return 1;
+    if (a.K % 256 || a.K > 16384 || gemv_lds_bytes(a) > (size_t)g_lds_max) return false;
     // the fewest rows per work-group whose work-groups fit nwg_max
-    int rpw = (int)((total + nwg_max - 1) / nwg_max);
-    for (;; rpw++) {
-        int64_t wg = 0;
-        for (int i = 0; i < a.nseg; i++) wg += (a.seg[i].n_rows + rpw - 1) / rpw;
-        if (wg <= nwg_max) break;
+    int rpw;
+    if (H) {
+        rpw = (a.seg[0].n_rows + nwg_max - 1) / nwg_max;
+    } else {
+        rpw = (int)((total + nwg_max - 1) / nwg_max);
+        for (;; rpw++) {
+            int64_t wg = 0;
+            for (int i = 0; i < a.nseg; i++) wg += (a.seg[i].n_rows + rpw - 1) / rpw;
+            if (wg <= nwg_max) break;
+        }
     }
     // the most lanes per row (more wavefronts) with at most 5 units per lane
     const int nu = a.K / 64;
     for (int ts = 64; ts >= 8; ts /= 2) {
         const int upl = (nu + ts - 1) / ts;
-        if (upl > 5 || rpw * ts > 1024 || (a.post.mode == POST_SWIGLU && rpw > 226)) continue;
-        switch (ts) {
-        case 8: return launch_cu_ts<8>(a, rpw, upl, q4, wf, st);
-        case 16: return launch_cu_ts<16>(a, rpw, upl, q4, wf, st);
-        case 32: return launch_cu_ts<32>(a, rpw, upl, q4, wf, st);
-        default: return launch_cu_ts<64>(a, rpw, upl, q4, wf, st);
-        }
+        if (upl > 5 || cu_teams(rpw, ts, H) * ts > 1024 || (a.post.mode == POST_SWIGLU && rpw > 226)) continue;
+        p = CuPlan{rpw, ts, upl, q4, wf};
+        return true;
     }
-    return 1;
+    return false;
+}
+
+// Returns 1 when no per-CU plan applies.
+static int gemv_launch_cu(const GArgs &a, hipStream_t st) {
+    CuPlan p;
+    if (!cu_plan(a, p)) return 1;
+    switch (p.ts) {
+    case 8: return launch_cu_ts<8>(a, p.rpw, p.upl, p.q4, p.wf, st);
+    case 16: return launch_cu_ts<16>(a, p.rpw, p.upl, p.q4, p.wf, st);
+    case 32: return launch_cu_ts<32>(a, p.rpw, p.upl, p.q4, p.wf, st);
+    default: return launch_cu_ts<64>(a, p.rpw, p.upl, p.q4, p.wf, st);
+    }
+}
+
+bool gemv_swiglu_h_ok(const GArgs &a) {
+    static const bool on = env_or("XJ_GEMV_SWIGLU_H", 1) != 0;
+    CuPlan p;
+    return on && a.post.mode == POST_SWIGLU_H && cu_plan(a, p);
 }
 
 int gemv_launch(const GArgs &a, hipStream_t st) {
@@ -1205,12 +1330,16 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
         if (s.wg0 != (i ? a.seg[i - 1].wg0 + a.seg[i - 1].nwg : 0)) return -1;
         if (s.epi == EPI_CONV && (s.conv_k < 2 || s.conv_k > 8)) return -1;
         // float rows read v from a prep launch's xq
-        if ((s.type == XJ_F32 || s.type == XJ_F16 || s.type == XJ_BF16) && a.pro == PRO_RMSU_X) return -1;
+        if ((s.type == XJ_F32 || s.type == XJ_F16 || s.type == XJ_BF16) && (a.pro == PRO_RMSU_X || a.pro == PRO_X))
+            return -1;
     }
-    if (a.post.mode != POST_NONE && a.post.mode != POST_SWIGLU) return -1;
-    if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_RMSU_X) return -1;   // other prologues come prepared
-    if (a.pro == PRO_RMSU_X && (!a.x || !a.pro_w || ((uintptr_t)a.x & 15) || ((uintptr_t)a.pro_w & 15) || (a.xs & 3)))
-        return -1;
+    if (a.post.mode != POST_NONE && a.post.mode != POST_SWIGLU && a.post.mode != POST_SWIGLU_H) return -1;
+    // other prologues come prepared
+    if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_RMSU_X && a.pro != PRO_X) return -1;
+    if ((a.pro == PRO_RMSU_X || a.pro == PRO_X) && (!a.x || ((uintptr_t)a.x & 15) || (a.xs & 3))) return -1;
+    if (a.pro == PRO_RMSU_X && (!a.pro_w || ((uintptr_t)a.pro_w & 15))) return -1;
+    // POST_SWIGLU_H exists in the per-CU launch only
+    if (a.post.mode == POST_SWIGLU_H) return gemv_launch_cu(a, st) == 0 ? 0 : -1;
     if (a.post.mode == POST_SWIGLU &&
         (!a.post.xq || !a.post.cnt || a.nseg != 2 || a.seg[0].n_rows != a.seg[1].n_rows || a.seg[0].n_rows % 32 ||
          32 % p.rows_per_group)) return -1;

@@ -27,7 +27,9 @@ constexpr size_t kWeightPad = 16384;
 // and the GEMV scales each row's dot product by sc.
 //   PRO_RMSU    the GEMV stages them from a prep launch's xq
 //   PRO_RMSU_X  the GEMV's work-groups build them from x in LDS (no prep launch)
-enum Pro { PRO_NONE = 0, PRO_SWIGLU = 2, PRO_GATED_RMS = 3, PRO_RMSU = 4, PRO_RMSU_X = 5 };
+//   PRO_X       the GEMV's work-groups build them from the plain input x in
+//               LDS (no norm), e.g. the SwiGLU values left by POST_SWIGLU_H
+enum Pro { PRO_NONE = 0, PRO_SWIGLU = 2, PRO_GATED_RMS = 3, PRO_RMSU = 4, PRO_RMSU_X = 5, PRO_X = 6 };
 enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_CONV = 2 };
 
 struct DevW {
@@ -60,11 +62,16 @@ struct GSeg {
 //   POST_SWIGLU  per 32-index group, the last of the work-groups that wrote
 //                its gate rows (segment 0) and up rows (segment 1) emits
 //                silu(gate) * up
-enum Post { POST_NONE = 0, POST_SWIGLU = 2 };
+//   POST_SWIGLU_H  single token, per-CU launch: every work-group computes the
+//                gate and up rows of the same indices and stores
+//                silu(gate) * up as floats into h (the down GEMV reads them
+//                with PRO_X); no hand-off between work-groups
+enum Post { POST_NONE = 0, POST_SWIGLU = 2, POST_SWIGLU_H = 3 };
 struct PostPrep {
     int32_t mode;
     uint8_t *xq;                   // token 0 of this tile
     int32_t *cnt;                  // zero between launches, one per group
+    float *h;                      // POST_SWIGLU_H output [n_rows]
 };
 
 struct GArgs {
@@ -98,6 +105,9 @@ int prep_launch(const GArgs &a, hipStream_t st);
 // covers row groups [wg0, wg0+nwg) with nwg = ceil(n_rows / rows_per_group)
 // of gemv_plan(K, total rows of all segments).
 int gemv_launch(const GArgs &a, hipStream_t st);
+// Whether gemv_launch serves `a` (one token, post.mode = POST_SWIGLU_H,
+// gate = segment 0, up = segment 1) with a per-CU launch.
+bool gemv_swiglu_h_ok(const GArgs &a);
 int gemv_init(char *err, size_t errlen);       // raise the dynamic-LDS limit once
 int gemv_max_tile(int K);                       // largest T tile whose activations fit in LDS
 size_t gemv_xq_bytes(int K);                    // xq bytes for the largest tile of this K

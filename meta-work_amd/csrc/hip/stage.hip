@@ -176,8 +176,25 @@ struct Gemv {
         return *this;
     }
     Gemv &post(int mode, uint8_t *xq, int32_t *cnt) {
-        a.post = PostPrep{mode, xq, cnt};
+        a.post = PostPrep{mode, xq, cnt, nullptr};
         return *this;
+    }
+    // RMSNorm prologues run inside the GEMV's work-groups (F32 rows read a prep launch's xq)
+    bool inwg() const {
+        bool ok = a.pro == PRO_RMSU && !prepared && !((uintptr_t)a.x & 15) && !(a.xs & 3) && !((uintptr_t)a.pro_w & 15);
+        for (int i = 0; i < a.nseg; i++)
+            ok = ok && a.seg[i].type != XJ_F32 && a.seg[i].type != XJ_F16 && a.seg[i].type != XJ_BF16;
+        return ok;
+    }
+    // One token of gate|up: POST_SWIGLU_H into h when the per-CU launch serves it.
+    bool swiglu_h(float *h) {
+        GArgs b = a;
+        b.T = 1;
+        b.post = PostPrep{POST_SWIGLU_H, nullptr, nullptr, h};
+        if (inwg()) b.pro = PRO_RMSU_X;
+        if (!gemv_swiglu_h_ok(b)) return false;
+        a.post = b.post;
+        return true;
     }
     // work-group ranges of the segments under the launch plan for (K, all rows)
     void place() {
@@ -204,12 +221,10 @@ struct Gemv {
             }
             a.inc_ptr = nullptr;
         }
-        // RMSNorm prologues run inside the GEMV's work-groups (F32 rows read a prep launch's xq)
-        bool inwg = a.pro == PRO_RMSU && !prepared && !((uintptr_t)a.x & 15) && !(a.xs & 3) && !((uintptr_t)a.pro_w & 15);
-        for (int i = 0; i < a.nseg; i++)
-            inwg = inwg && a.seg[i].type != XJ_F32 && a.seg[i].type != XJ_F16 && a.seg[i].type != XJ_BF16;
+        const bool in_wg = inwg();
         const int64_t xs_in = xq_off(a.K).stride;
-        const int64_t xs_out = a.post.mode != POST_NONE ? xq_off(a.seg[0].n_rows).stride : 0;
+        const int64_t xs_out = a.post.mode == POST_SWIGLU ? xq_off(a.seg[0].n_rows).stride : 0;
+        if (a.post.mode == POST_SWIGLU_H && T != 1) return -1;
         for (int t0 = 0; t0 < T; t0 += tile) {
             GArgs b = a;
             b.T = T - t0 < tile ? T - t0 : tile;
@@ -217,15 +232,15 @@ struct Gemv {
             b.x = a.x ? a.x + (int64_t)t0 * a.xs : nullptr;
             if (a.x2) b.x2 = a.x2 + (int64_t)t0 * a.x2s;
             b.xq = a.xq + t0 * xs_in;
-            if (a.post.mode != POST_NONE) b.post.xq = a.post.xq + t0 * xs_out;
+            if (a.post.mode == POST_SWIGLU) b.post.xq = a.post.xq + t0 * xs_out;
             for (int i = 0; i < a.nseg; i++) {
                 b.seg[i].y = a.seg[i].y + (int64_t)t0 * a.seg[i].ys;
                 if (a.seg[i].amax) b.seg[i].amax = a.seg[i].amax + (int64_t)t0 * a.seg[i].nwg;
             }
             if (t0 + b.T < T) b.inc_ptr = nullptr;
-            if (inwg) {
+            if (in_wg) {
                 b.pro = PRO_RMSU_X;
-            } else {
+            } else if (a.pro != PRO_X) {   // PRO_X: built from x inside the GEMV
                 if (!prof && !prepared && prep_launch(b, st)) return -1;
                 if (b.pro != PRO_RMSU) b.pro = PRO_NONE;   // the GEMV reads xq
             }
@@ -299,10 +314,20 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
     }
     Gemv f(S->xq_e, pf);
     rms_in(f, L.post_norm);
-    f.seg(L.ffn_gate, S->g, FF, EPI_STORE).seg(L.ffn_up, S->u, FF, EPI_STORE).post(POST_SWIGLU, S->xq_ff, S->cnt_grp);
+    f.seg(L.ffn_gate, S->g, FF, EPI_STORE).seg(L.ffn_up, S->u, FF, EPI_STORE);
+    // one token: every work-group of gate|up leaves silu(gate) * up of its
+    // rows in g, and down builds its activations from them (float rows of
+    // down read a prepared xq instead)
+    const uint32_t dt = L.ffn_down.type;
+    const bool h = T == 1 && dt != XJ_F32 && dt != XJ_F16 && dt != XJ_BF16 && f.swiglu_h(S->g);
+    if (!h) f.post(POST_SWIGLU, S->xq_ff, S->cnt_grp);
     if (f.run(T, st)) return -1;
     Gemv dn(S->xq_ff, pf);
-    dn.prepared = true;
+    if (h) {
+        dn.a.x = S->g; dn.a.xs = FF; dn.a.pro = PRO_X;
+    } else {
+        dn.prepared = true;
+    }
     dn.a.inc_ptr = inc; dn.a.inc_by = T;
     dn.seg(L.ffn_down, x, E, EPI_ADD);
     return dn.run(T, st);
