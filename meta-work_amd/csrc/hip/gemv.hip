@@ -1015,16 +1015,18 @@ __device__ __forceinline__ void swiglu_h_cu(const GArgs &a, int rg, int ho, int 
 // ho = rpw rounded up to whole wavefronts. The activations (prepared, or
 // the x (and w) of an input built in the work-group: PRO_RMSU_X, PRO_X) are
 // copied into LDS once per CU; WF (inputs built in the work-group) requests
-// two units of every lane right behind the copies and converts x while they
-// arrive, otherwise the copies complete first and every lane then requests
+// one unit of every lane right behind the copies and converts x while it
+// arrives, otherwise the copies complete first and every lane then requests
 // all its MU units. The gate|up launch ends with the SwiGLU tail (or its
 // work-group-local form, POST_SWIGLU_H); no argmax partials.
 template <int TS, int MU, bool Q4, bool WF>
 __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
     extern __shared__ u32x4 lds_v[];
-    // WF: two units requested right behind the activation copies, the rest
-    // from the unit loop; otherwise the copies complete first, then all units
-    constexpr int NW = WF ? (MU < 2 ? MU : 2) : MU, PD = NW - 1;
+    // WF: one unit requested right behind the activation copies, the rest
+    // from the unit loop one ahead (more in flight before the conversion
+    // delays it, more ahead in the loop congests: both measured slower);
+    // otherwise the copies complete first, then all units
+    constexpr int NW = WF ? 1 : MU, PD = NW - 1;
     const int K = a.K, nu = K / 64;
     const XqOff o = xq_off(K);
     const int tid = threadIdx.x, team = tid / TS, lane = tid % TS;
