@@ -21,9 +21,12 @@ Also reported, on the same run:
   decode_0_8b   the same measurement on the 0.8B-shape model.
 
 usage: python bench.py [--gpus 1] [--steps 512] [--warmup 16] [--no-cpu] [--no-extra]
-                       [--copy-calibration MB]
+                       [--copy-calibration MB] [--delta-c3]
 --copy-calibration MB first copies MB megabytes device-to-device (one runtime
 copy kernel of known size, to calibrate the HBM byte counters of a profiler run).
+--delta-c3 runs only the Gated DeltaNet prefill comparison (16 heads, d=128,
+2048 tokens: chunk-wise MFMA kernels vs the token-by-token kernel) and prints
+its JSON line.
 """
 import argparse
 import json
@@ -110,6 +113,36 @@ def gemv_leg(t, rows, k, copies, iters):
             "GBps": round(by / (ms * 1e-3) / 1e9, 1), "frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
 
 
+def delta_c3(reps=3):
+    """Gated DeltaNet prefill on the c3 shape (16 heads, d=128, 2048 tokens from a zero state): the chunk-wise
+    MFMA kernels (chunk 64) next to the token-by-token kernel. Wall ms per call include the host copies; the
+    kernel durations come from a rocprofv3 trace of `bench.py --delta-c3`."""
+    T, H, S = 2048, 16, 128
+    rng = np.random.default_rng(20261109)
+    q = rng.standard_normal((T, H, S)).astype(np.float32)
+    k = rng.standard_normal((T, H, S)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rng.standard_normal((T, H, S)).astype(np.float32)
+    dec = (1 / (1 + np.exp(-rng.standard_normal((T, H))))).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((T, H))))).astype(np.float32)
+    st = np.zeros((H, S, S), np.float32)
+    res = {}
+    for name, chunk in (("chunked", 64), ("recurrent", 0)):
+        best = None
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            o, s = xp.delta(q, k, v, dec, beta, st, 1 / np.sqrt(S), chunk=chunk)
+            dt = (time.perf_counter() - t0) * 1e3
+            best = dt if best is None else min(best, dt)
+        res[name] = (o, s, best)
+    rel = lambda a, b: float(np.linalg.norm(a - b) / np.linalg.norm(b))
+    return {"shape": "H=16 d=128 T=2048 chunk 64", "chunked_wall_ms": round(res["chunked"][2], 2),
+            "recurrent_wall_ms": round(res["recurrent"][2], 2),
+            "out_rel_l2": rel(res["chunked"][0], res["recurrent"][0]),
+            "state_rel_l2": rel(res["chunked"][1], res["recurrent"][1])}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -118,6 +151,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the 0.8B run and the GEMV legs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB")
+    ap.add_argument("--delta-c3", action="store_true", help="only the chunked vs token-by-token DeltaNet prefill")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the token loop on a single MI355X and has no "
@@ -125,6 +159,9 @@ def main():
         sys.exit(2)
 
     log(f"device: {xp.device_name()}")
+    if args.delta_c3:
+        print(json.dumps(delta_c3()), flush=True)
+        return
     if args.copy_calibration:
         n = args.copy_calibration << 20
         src, dst = xp.Dev(nbytes=n), xp.Dev(nbytes=n)

@@ -13,16 +13,29 @@
 // Decay ratios are formed as exp of differences of cumulative logs, so 64
 // steps of small decays never underflow a product.
 //
-// Phase 1 (all chunks and heads in parallel) builds W = X diag(e^lg) K,
-// U = X V, P and the decay vectors; phase 2 walks the chunks in order, one
-// work-group per (head, 16 value rows), since the value rows of the state are
-// independent: delta = U - W M0^T, O, M_C.
+// Every chunk-level dense product runs on the matrix cores in fp32
+// (v_mfma_f32_16x16x4f32: fp32 products, fp32 sums). Phase 1 (all chunks and
+// heads in parallel) forms K K^T and Q K^T, solves for X (one wavefront, row
+// by row, while the others finish P), then W = X diag(e^lg) K and U = X V.
+// Phase 2 walks the chunks in order, one work-group per (head, 16 value rows)
+// since the value rows of the state are independent: delta = U - W M0^T, O,
+// M_C.
 #include "common.h"
 #include "kernels.h"
 
 namespace xjk {
 
 constexpr int kC = 64;
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// D (16x16) += A (16x4) B (4x16) on the matrix cores. Lane l supplies
+// A[l%16][l/16] and B[l/16][l%16]; element r of lane l is D[4*(l/16) + r][l%16].
+// Tiles below walk an inner dimension in blocks of 16: lane group l/16 takes
+// inner indices 16b + 4*(l/16) + s, s = 0..3 (one MFMA per s).
+__device__ __forceinline__ v4f mma(v4f c, float a, float b) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v4f ld4(const float *p) { return *(const v4f *)p; }
 
 template <int S>
 struct WorkLayout {
@@ -31,19 +44,34 @@ struct WorkLayout {
 };
 
 template <int S>
+constexpr size_t prep_lds_bytes() { return (size_t)(2 * kC * (S + 4) + kC * (kC + 4)) * 4; }
+template <int S>
+constexpr size_t scan_lds_bytes() { return (size_t)((16 + kC) * (S + 4) + kC * 20) * 4; }
+
+template <int S>
 __global__ __launch_bounds__(256) void dc_prep(int H, int T, const float *__restrict__ q, const float *__restrict__ k,
                                                const float *__restrict__ v, const float *__restrict__ decay,
                                                const float *__restrict__ beta, float *__restrict__ work) {
     using WL = WorkLayout<S>;
+    constexpr int KS = S + 4, XS = kC + 4;   // LDS row strides (floats)
+    extern __shared__ __align__(16) float sm[];
+    float *Ks = sm;                // [kC][KS] the chunk's k rows (zero past T)
+    float *Vs = Ks + kC * KS;      // [kC][KS] v rows
+    float *AX = Vs + kC * KS;      // [kC][XS] A, then X in place
+    __shared__ float lg[kC], bb[kC];
+    __shared__ __align__(16) float gam[kC];
     const int n = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-    __shared__ float Ks[kC][S];
-    __shared__ float AX[kC][kC + 1];
-    __shared__ float lg[kC], bb[kC], gam[kC];
-    __shared__ float rowtmp[kC];
+    const int w = tid >> 6, l = tid & 63, lr = l & 15, lq = l >> 4;
     float *wk = work + ((int64_t)n * H + h) * WL::SIZE;
-    for (int idx = tid; idx < kC * S; idx += 256) {
-        const int t = idx / S, i = idx % S, tok = n * kC + t;
-        Ks[t][i] = tok < T ? k[((int64_t)tok * H + h) * S + i] : 0.f;
+    for (int idx = tid; idx < kC * S / 4; idx += 256) {
+        const int t = idx / (S / 4), c = 4 * (idx % (S / 4)), tok = n * kC + t;
+        v4f kv = {0.f, 0.f, 0.f, 0.f}, vv = kv;
+        if (tok < T) {
+            kv = ld4(k + ((int64_t)tok * H + h) * S + c);
+            vv = ld4(v + ((int64_t)tok * H + h) * S + c);
+        }
+        *(v4f *)(Ks + t * KS + c) = kv;
+        *(v4f *)(Vs + t * KS + c) = vv;
     }
     if (tid < kC) {
         const int tok = n * kC + tid;
@@ -57,58 +85,79 @@ __global__ __launch_bounds__(256) void dc_prep(int H, int T, const float *__rest
     }
     __syncthreads();
     if (tid < kC) gam[tid] = expf(lg[tid]);
-    // A (strictly lower) = beta_s e^(lg_s-lg_r) k_s.k_r
-    for (int idx = tid; idx < kC * kC; idx += 256) {
-        const int s = idx / kC, r = idx % kC;
-        float a = 0.f;
-        if (r < s) {
-            float dsum = 0.f;
-            for (int i = 0; i < S; i++) dsum = fmaf(Ks[s][i], Ks[r][i], dsum);
-            a = bb[s] * expf(lg[s] - lg[r]) * dsum;
+    // A (strictly lower) = beta_s e^(lg_s - lg_r) k_s.k_r: wavefront w takes
+    // rows 16w..16w+15, tiles on and below the diagonal
+    for (int J = 0; J < 4; J++) {
+        v4f kk = {0.f, 0.f, 0.f, 0.f};
+        if (J <= w) {
+            for (int b = 0; b < S / 16; b++) {
+                const int c = 16 * b + 4 * lq;
+                const v4f ka = ld4(Ks + (16 * w + lr) * KS + c), kb = ld4(Ks + (16 * J + lr) * KS + c);
+#pragma unroll
+                for (int s = 0; s < 4; s++) kk = mma(kk, ka[s], kb[s]);
+            }
         }
-        AX[s][r] = a;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int s_ = 16 * w + 4 * lq + r, r_ = 16 * J + lr;
+            AX[s_ * XS + r_] = r_ < s_ ? bb[s_] * expf(lg[s_] - lg[r_]) * kk[r] : 0.f;
+        }
     }
     __syncthreads();
-    // X = (I + A)^-1 diag(beta), in place, row by row (unit lower triangular solve)
-    for (int s = 0; s < kC; s++) {
-        if (tid < kC) {
-            const int r = tid;
+    if (w == 0) {
+        // X = (I + A)^-1 diag(beta), row by row in place; lane l owns column l.
+        // One wavefront: its LDS reads of row s precede its writes of row s.
+        for (int s = 0; s < kC; s++) {
             float x = 0.f;
-            if (r < s) {
-                for (int m = r; m < s; m++) x = fmaf(-AX[s][m], AX[m][r], x);
-            } else if (r == s) {
-                x = bb[s];
+            for (int m = 0; m < s; m++) x = fmaf(-AX[s * XS + m], AX[m * XS + l], x);
+            AX[s * XS + l] = l < s ? x : l == s ? bb[s] : 0.f;
+        }
+    } else {
+        // P[t][r] = e^(lg_t - lg_r) q_t.k_r for r <= t (zero elsewhere and past T):
+        // the 10 tiles on and below the diagonal over wavefronts 1..3
+        for (int tile = w - 1; tile < 16; tile += 3) {
+            const int I = tile / 4, J = tile % 4;
+            v4f qk = {0.f, 0.f, 0.f, 0.f};
+            const int tokA = n * kC + 16 * I + lr;
+            if (J <= I) {
+                const float *qa = q + ((int64_t)tokA * H + h) * S;
+                for (int b = 0; b < S / 16; b++) {
+                    const int c = 16 * b + 4 * lq;
+                    const v4f a4 = tokA < T ? ld4(qa + c) : v4f{0.f, 0.f, 0.f, 0.f};
+                    const v4f kb = ld4(Ks + (16 * J + lr) * KS + c);
+#pragma unroll
+                    for (int s = 0; s < 4; s++) qk = mma(qk, a4[s], kb[s]);
+                }
             }
-            rowtmp[r] = x;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t_ = 16 * I + 4 * lq + r, r_ = 16 * J + lr;
+                wk[WL::P + t_ * kC + r_] = r_ <= t_ && n * kC + t_ < T ? expf(lg[t_] - lg[r_]) * qk[r] : 0.f;
+            }
         }
-        __syncthreads();
-        if (tid < kC) AX[s][tid] = rowtmp[tid];
-        __syncthreads();
     }
-    // W = X diag(gam) K and U = X V
-    for (int idx = tid; idx < kC * S; idx += 256) {
-        const int s = idx / S, i = idx % S;
-        float w = 0.f, u = 0.f;
-        for (int r = 0; r <= s; r++) {
-            const int tok = n * kC + r;
-            const float vr = tok < T ? v[((int64_t)tok * H + h) * S + i] : 0.f;
-            w = fmaf(AX[s][r] * gam[r], Ks[r][i], w);
-            u = fmaf(AX[s][r], vr, u);
+    __syncthreads();
+    // W = X diag(gam) K and U = X V: wavefront w takes key/value column blocks
+    // w, w + 4, ...; X is lower triangular, so row block I needs inner blocks <= I
+    for (int J = w; J < S / 16; J += 4) {
+        for (int I = 0; I < 4; I++) {
+            v4f aw = {0.f, 0.f, 0.f, 0.f}, au = aw;
+            for (int b = 0; b <= I; b++) {
+                const int c = 16 * b + 4 * lq;
+                const v4f xa = ld4(AX + (16 * I + lr) * XS + c), g = ld4(gam + c);
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    aw = mma(aw, xa[s] * g[s], Ks[(c + s) * KS + 16 * J + lr]);
+                    au = mma(au, xa[s], Vs[(c + s) * KS + 16 * J + lr]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int s_ = 16 * I + 4 * lq + r, i_ = 16 * J + lr;
+                wk[WL::W + s_ * S + i_] = aw[r];
+                wk[WL::U + s_ * S + i_] = au[r];
+            }
         }
-        wk[WL::W + idx] = w;
-        wk[WL::U + idx] = u;
-    }
-    // P[t][r] = e^(lg_t - lg_r) q_t . k_r for r <= t
-    for (int idx = tid; idx < kC * kC; idx += 256) {
-        const int t = idx / kC, r = idx % kC, tok = n * kC + t;
-        float p = 0.f;
-        if (r <= t && tok < T) {
-            const float *qt = q + ((int64_t)tok * H + h) * S;
-            float dsum = 0.f;
-            for (int i = 0; i < S; i++) dsum = fmaf(qt[i], Ks[r][i], dsum);
-            p = expf(lg[t] - lg[r]) * dsum;
-        }
-        wk[WL::P + idx] = p;
     }
     if (tid < kC) {
         wk[WL::GAM + tid] = gam[tid];
@@ -122,49 +171,98 @@ __global__ __launch_bounds__(256) void dc_scan(int H, int T, const float *__rest
                                                const float *__restrict__ work, float qscale, float *__restrict__ state,
                                                float *__restrict__ out) {
     using WL = WorkLayout<S>;
-    constexpr int JB = 16;
+    constexpr int JB = 16, KS = S + 4, DS = JB + 4;
+    extern __shared__ __align__(16) float sm[];
+    float *Mb = sm;                // [JB][KS] state rows j0..j0+15 (value) x key
+    float *Kc = Mb + JB * KS;      // [kC][KS] the chunk's k rows (zero past T)
+    float *dl = Kc + kC * KS;      // [kC][DS] delta[s][j]
     const int h = blockIdx.x, j0 = blockIdx.y * JB, tid = threadIdx.x;
-    __shared__ float Mb[JB][S + 4];
-    __shared__ float dl[kC][JB + 1];
-    for (int idx = tid; idx < JB * S; idx += 256) Mb[idx / S][idx % S] = state[((int64_t)h * S + j0 + idx / S) * S + idx % S];
-    __syncthreads();
+    const int w = tid >> 6, l = tid & 63, lr = l & 15, lq = l >> 4;
+    for (int idx = tid; idx < JB * S / 4; idx += 256) {
+        const int j = idx / (S / 4), c = 4 * (idx % (S / 4));
+        *(v4f *)(Mb + j * KS + c) = ld4(state + ((int64_t)h * S + j0 + j) * S + c);
+    }
     const int nch = (T + kC - 1) / kC;
-    const int jj = tid % JB, sg = tid / JB;   // (row group, value row) for delta and O
     for (int n = 0; n < nch; n++) {
         const float *wk = work + ((int64_t)n * H + h) * WL::SIZE;
-        for (int s = sg; s < kC; s += 256 / JB) {
-            const float *Wr = wk + WL::W + s * S;
-            float d = 0.f;
-            for (int i = 0; i < S; i++) d = fmaf(Wr[i], Mb[jj][i], d);
-            dl[s][jj] = wk[WL::U + s * S + j0 + jj] - d;
+        for (int idx = tid; idx < kC * S / 4; idx += 256) {
+            const int t = idx / (S / 4), c = 4 * (idx % (S / 4)), tok = n * kC + t;
+            *(v4f *)(Kc + t * KS + c) = tok < T ? ld4(k + ((int64_t)tok * H + h) * S + c) : v4f{0.f, 0.f, 0.f, 0.f};
         }
-        __syncthreads();
-        for (int t = sg; t < kC; t += 256 / JB) {
-            const int tok = n * kC + t;
-            if (tok >= T) continue;
-            const float *qt = q + ((int64_t)tok * H + h) * S;
-            float a = 0.f;
-            for (int i = 0; i < S; i++) a = fmaf(qt[i], Mb[jj][i], a);
-            float o = wk[WL::GAM + t] * a;
-            const float *Pr = wk + WL::P + t * kC;
-            for (int r = 0; r <= t; r++) o = fmaf(Pr[r], dl[r][jj], o);
-            out[((int64_t)tok * H + h) * S + j0 + jj] = o * qscale;
-        }
-        __syncthreads();
-        const float gC = wk[WL::GC];
-        for (int idx = tid; idx < JB * S; idx += 256) {
-            const int r0 = idx / S, i = idx % S;
-            float m = gC * Mb[r0][i];
-            for (int r = 0; r < kC; r++) {
-                const int tok = n * kC + r;
-                const float kr = tok < T ? k[((int64_t)tok * H + h) * S + i] : 0.f;
-                m = fmaf(wk[WL::GEND + r] * dl[r][r0], kr, m);
+        __syncthreads();   // M0 (first chunk) and this chunk's k rows in place
+        // delta = U - W M0^T: wavefront w takes rows 16w..16w+15
+        {
+            v4f acc = {0.f, 0.f, 0.f, 0.f};
+            const float *Wr = wk + WL::W + (16 * w + lr) * S;
+            for (int b = 0; b < S / 16; b++) {
+                const int c = 16 * b + 4 * lq;
+                const v4f wa = ld4(Wr + c), mb = ld4(Mb + lr * KS + c);
+#pragma unroll
+                for (int s = 0; s < 4; s++) acc = mma(acc, wa[s], mb[s]);
             }
-            Mb[r0][i] = m;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int s_ = 16 * w + 4 * lq + r;
+                dl[s_ * DS + lr] = wk[WL::U + s_ * S + j0 + lr] - acc[r];
+            }
         }
         __syncthreads();
+        // O = diag(gam) Q M0^T + P delta: wavefront w takes tokens 16w..16w+15
+        {
+            v4f aq = {0.f, 0.f, 0.f, 0.f}, ap = aq;
+            const int tokA = n * kC + 16 * w + lr;
+            const float *qa = q + ((int64_t)tokA * H + h) * S;
+            for (int b = 0; b < S / 16; b++) {
+                const int c = 16 * b + 4 * lq;
+                const v4f a4 = tokA < T ? ld4(qa + c) : v4f{0.f, 0.f, 0.f, 0.f};
+                const v4f mb = ld4(Mb + lr * KS + c);
+#pragma unroll
+                for (int s = 0; s < 4; s++) aq = mma(aq, a4[s], mb[s]);
+            }
+            const float *Pr = wk + WL::P + (16 * w + lr) * kC;
+            for (int b = 0; b <= w; b++) {   // P is zero above the diagonal
+                const int c = 16 * b + 4 * lq;
+                const v4f pa = ld4(Pr + c);
+#pragma unroll
+                for (int s = 0; s < 4; s++) ap = mma(ap, pa[s], dl[(c + s) * DS + lr]);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t_ = 16 * w + 4 * lq + r, tok = n * kC + t_;
+                if (tok < T) out[((int64_t)tok * H + h) * S + j0 + lr] = (wk[WL::GAM + t_] * aq[r] + ap[r]) * qscale;
+            }
+        }
+        // M_C = gam_C M0 + (delta o gend)^T K: wavefront w takes key blocks w, w + 4, ...
+        v4f mc[S / 64];
+#pragma unroll
+        for (int jj = 0; jj < S / 64; jj++) {
+            const int J = w + 4 * jj;
+            v4f acc = {0.f, 0.f, 0.f, 0.f};
+            for (int b = 0; b < kC / 16; b++) {
+                const int c = 16 * b + 4 * lq;
+                const v4f ge = ld4(wk + WL::GEND + c);
+#pragma unroll
+                for (int s = 0; s < 4; s++) acc = mma(acc, dl[(c + s) * DS + lr] * ge[s], Kc[(c + s) * KS + 16 * J + lr]);
+            }
+            mc[jj] = acc;
+        }
+        __syncthreads();   // every wavefront has finished reading M0
+        const float gC = wk[WL::GC];
+#pragma unroll
+        for (int jj = 0; jj < S / 64; jj++) {
+            const int J = w + 4 * jj;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float *m = Mb + (4 * lq + r) * KS + 16 * J + lr;
+                *m = gC * *m + mc[jj][r];
+            }
+        }
+        __syncthreads();   // M_C complete; Kc and dl free for the next chunk
     }
-    for (int idx = tid; idx < JB * S; idx += 256) state[((int64_t)h * S + j0 + idx / S) * S + idx % S] = Mb[idx / S][idx % S];
+    for (int idx = tid; idx < JB * S / 4; idx += 256) {
+        const int j = idx / (S / 4), c = 4 * (idx % (S / 4));
+        *(v4f *)(state + ((int64_t)h * S + j0 + j) * S + c) = ld4(Mb + j * KS + c);
+    }
 }
 
 size_t delta_chunked_work_bytes(int H, int S, int T, int chunk) {
@@ -175,21 +273,32 @@ size_t delta_chunked_work_bytes(int H, int S, int T, int chunk) {
     return 0;
 }
 
+template <int S>
+static int dc_launch(int H, int T, const float *q, const float *k, const float *v, const float *decay,
+                     const float *beta, float qscale, float *state, float *out, float *work, hipStream_t st) {
+    static const bool raised =
+        hipFuncSetAttribute((const void *)dc_prep<S>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)prep_lds_bytes<S>()) == hipSuccess &&
+        hipFuncSetAttribute((const void *)dc_scan<S>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)scan_lds_bytes<S>()) == hipSuccess;
+    if (!raised) return -1;
+    const int nch = (T + kC - 1) / kC;
+    hipLaunchKernelGGL(dc_prep<S>, dim3(nch, H), dim3(256), prep_lds_bytes<S>(), st, H, T, q, k, v, decay, beta, work);
+    hipLaunchKernelGGL(dc_scan<S>, dim3(H, S / 16), dim3(256), scan_lds_bytes<S>(), st, H, T, q, k, work, qscale, state,
+                       out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 int delta_chunked_launch(int H, int S, int T, int chunk, const float *q, const float *k, const float *v,
                          const float *decay, const float *beta, float qscale, float *state, float *out, float *work,
                          hipStream_t st) {
-    if (chunk != kC) return -1;
-    const int nch = (T + kC - 1) / kC;
-    if (S == 128) {
-        hipLaunchKernelGGL(dc_prep<128>, dim3(nch, H), dim3(256), 0, st, H, T, q, k, v, decay, beta, work);
-        hipLaunchKernelGGL(dc_scan<128>, dim3(H, 128 / 16), dim3(256), 0, st, H, T, q, k, work, qscale, state, out);
-    } else if (S == 64) {
-        hipLaunchKernelGGL(dc_prep<64>, dim3(nch, H), dim3(256), 0, st, H, T, q, k, v, decay, beta, work);
-        hipLaunchKernelGGL(dc_scan<64>, dim3(H, 64 / 16), dim3(256), 0, st, H, T, q, k, work, qscale, state, out);
-    } else {
-        return -1;
-    }
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    if (chunk != kC || T < 1 || H < 1) return -1;
+    // the row loads are 16-byte vectors
+    for (const void *p : {(const void *)q, (const void *)k, (const void *)v, (const void *)state, (const void *)work})
+        if ((uintptr_t)p & 15) return -1;
+    if (S == 128) return dc_launch<128>(H, T, q, k, v, decay, beta, qscale, state, out, work, st);
+    if (S == 64) return dc_launch<64>(H, T, q, k, v, decay, beta, qscale, state, out, work, st);
+    return -1;
 }
 
 }  // namespace xjk

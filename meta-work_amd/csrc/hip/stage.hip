@@ -1191,7 +1191,7 @@ extern "C" int xjh_delta_chunked(int H, int S, int T, int chunk, const float *q,
     void *work = nullptr;
     if (hipMalloc(&work, wb) != hipSuccess) { snprintf(err, errlen, "hipMalloc failed"); return -1; }
     int rc = delta_chunked_launch(H, S, T, chunk, q, k, v, decay, beta, qscale, state, out, (float *)work, g_stream);
-    if (rc) snprintf(err, errlen, "chunked delta launch failed");
+    if (rc) snprintf(err, errlen, "chunked delta launch failed (q, k, v and state must be 16-byte aligned)");
     else rc = ops_done(err, errlen);
     (void)hipFree(work);
     return rc;
