@@ -19,6 +19,8 @@
 // in a fixed butterfly instead of one running sum. With keep, the state after
 // each token t < keep_n is written to checkpoint t (xj_cpu.c:218).
 //
+// delta_part_kernel: the same per row, split over 32-row work-groups (below).
+//
 // delta_rec_kernel: the same rule with decay and beta given per token and head
 // (the standalone layer test), q and k used as given.
 #include "common.h"
@@ -132,6 +134,65 @@ __global__ __launch_bounds__(1024) void delta_head_kernel(const DeltaArgs a) {
     for (int r = 0; r < NR; r++) store_row<S>(a.state + ((int64_t)hv * S + r16 + 64 * r) * S + i0, m[r]);
 }
 
+// The same update split over value rows: work-group (hv, p) owns the 32 rows
+// p*32 .. p*32+31 of head hv (one activation group), 16 lanes per row; q and
+// k are normalised by every work-group of the head. The gated RMSNorm couples
+// the head's rows, so with a.xq set each work-group writes the digits of
+// u_j = o_j * norm_w_j * silu(z_j) for its group and the group's sum of o_j^2
+// (double, fixed order) into the group's ss field; the ssm_out GEMV
+// (PRO_HEADRMS) folds 1/sqrt(sum over the head's groups / S + eps) into the
+// head's group scales - the same product in another order.
+template <int S>
+__global__ __launch_bounds__(512) void delta_part_kernel(const DeltaArgs a) {
+    constexpr int IPL = S / 16, RW = 32;
+    const int hv = blockIdx.x, p = blockIdx.y, tid = threadIdx.x, team = tid >> 4, l16 = tid & 15, i0 = l16 * IPL;
+    const int hk = hv % a.Hk, j = p * RW + team;
+    __shared__ float qs[S], ks[S], os[RW];
+    __shared__ double red[16];
+    float m[IPL];
+    load_row<S>(a.state + ((int64_t)hv * S + j) * S + i0, m);
+    const float dt = a.dt[hv], A = a.A[hv];
+    const bool in = tid < S;
+    const bool emit = a.xq && tid < RW;   // lanes of wavefront 0 that emit the group
+    const float nw = emit ? a.norm_w[p * RW + tid] : 0.f;
+    for (int t = 0; t < a.T; t++) {
+        const float *row = a.qkv + (int64_t)t * a.qkv_s;
+        const float qv = in ? row[hk * S + tid] : 0.f, kv = in ? row[a.k_off + hk * S + tid] : 0.f;
+        const float bt = a.beta[(int64_t)t * a.beta_s + hv], al = a.alpha[(int64_t)t * a.alpha_s + hv];
+        const float vj = row[a.v_off + hv * S + j];
+        const float zv = emit ? a.z[(int64_t)t * a.z_s + hv * S + p * RW + tid] : 0.f;
+        __syncthreads();   // red and qs / ks / os of the previous token consumed
+        const double sq = xjd::head_sum_d<(S + 63) / 64>((double)qv * qv, red);
+        const double sk2 = xjd::head_sum_d<(S + 63) / 64>((double)kv * kv, red + 4);
+        if (in) {
+            qs[tid] = qv * (1.0f / sqrtf((float)sq + a.eps));
+            ks[tid] = kv * (1.0f / sqrtf((float)sk2 + a.eps));
+        }
+        const float b = xjd::sigm(bt);
+        const float eg = expf(xjd::softplus(al + dt) * A);
+        __syncthreads();
+        const float o = rule_step<S>(m, ks, qs, i0, eg, b, vj) * a.qscale;
+        if (l16 == 0) {
+            os[team] = o;
+            a.out[(int64_t)t * a.out_s + hv * S + j] = o;
+        }
+        if (t < a.keep_n) store_row<S>(a.ck + (((int64_t)t * a.Hv + hv) * S + j) * S + i0, m);
+        if (a.xq) {
+            __syncthreads();
+            if (tid < 64) {   // wavefront 0: lanes 0..31 hold the group
+                const XqOff o = xq_off(a.Hv * S);
+                const float ov = emit ? os[tid] : 0.f;
+                const double ss = xjd::group_ss(ov);
+                const int k = hv * S + p * RW + tid;
+                uint8_t *dst = a.xq + (int64_t)t * o.stride;
+                xjd::emit_xq(emit ? ov * nw * xjd::silu(zv) : 0.f, k, emit, dst, o);
+                if (tid == 0) ((double *)(dst + o.ss_off))[k >> 5] = ss;
+            }
+        }
+    }
+    store_row<S>(a.state + ((int64_t)hv * S + j) * S + i0, m);
+}
+
 template <int S>
 __global__ __launch_bounds__(256) void delta_rec_kernel(int H, int T, const float *q, const float *k, const float *v,
                                                         const float *decay, const float *beta, float qscale,
@@ -156,9 +217,17 @@ __global__ __launch_bounds__(256) void delta_rec_kernel(int H, int T, const floa
 
 int delta_launch(const DeltaArgs &a, hipStream_t st) {
     if (a.xq && (!a.z || !a.norm_w)) return -1;
-    if (a.S == 128) hipLaunchKernelGGL(delta_head_kernel<128>, dim3(a.Hv), dim3(1024), 0, st, a);
-    else if (a.S == 64) hipLaunchKernelGGL(delta_head_kernel<64>, dim3(a.Hv), dim3(1024), 0, st, a);
-    else return -1;
+    if (a.split) {   // one work-group per 32 value rows; the norm's scale is left to the consumer
+        if (a.S == 128) hipLaunchKernelGGL(delta_part_kernel<128>, dim3(a.Hv, 4), dim3(512), 0, st, a);
+        else if (a.S == 64) hipLaunchKernelGGL(delta_part_kernel<64>, dim3(a.Hv, 2), dim3(512), 0, st, a);
+        else return -1;
+    } else if (a.S == 128) {
+        hipLaunchKernelGGL(delta_head_kernel<128>, dim3(a.Hv), dim3(1024), 0, st, a);
+    } else if (a.S == 64) {
+        hipLaunchKernelGGL(delta_head_kernel<64>, dim3(a.Hv), dim3(1024), 0, st, a);
+    } else {
+        return -1;
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -846,6 +846,21 @@ __device__ __forceinline__ void rmsx_stage(const GArgs &a, const XqOff &o, uint8
     }
 }
 
+// PRO_HEADRMS: every head of a.group elements of staged token t gets the
+// scale 1/sqrt(sum of its groups' ss / group + eps), folded into the f of
+// each of its groups (each thread sums the head's doubles in the same order).
+// Completion: the caller's barrier.
+__device__ __forceinline__ void head_scale(const GArgs &a, const XqOff &o, uint8_t *xl, int t) {
+    uint8_t *x = xl + t * o.v_off;
+    const int gph = a.group >> 5;
+    for (int g = threadIdx.x; g < o.G; g += blockDim.x) {
+        const double *ss = (const double *)(x + o.ss_off) + g / gph * gph;
+        double s = 0;
+        for (int i = 0; i < gph; i++) s += ss[i];
+        ((float *)(x + o.f_off))[g] *= 1.0f / sqrtf((float)(s / a.group) + a.eps);
+    }
+}
+
 // PRO_RMSU / PRO_RMSU_X: the norm scale of staged token t from its group sums of x^2
 // (double, fixed order). Called by every lane of a wavefront; each wavefront
 // computes it for itself and keeps it in a scalar register.
@@ -913,6 +928,11 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         barrier_raw();
         if (pro_inwg(a.pro)) {
             rmsx1_finish(a, o, lds);
+            barrier_lds();
+        }
+        if (a.pro == PRO_HEADRMS) {
+#pragma unroll
+            for (int t = 0; t < T; t++) head_scale(a, o, lds, t);
             barrier_lds();
         }
     }
@@ -1059,6 +1079,10 @@ __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
     }
     if (inwg) {
         rmsx1_finish(a, o, lds);
+        barrier_lds();
+    }
+    if (a.pro == PRO_HEADRMS) {   // prepared: the copies completed before the weight requests
+        head_scale(a, o, lds, 0);
         barrier_lds();
     }
     const float sc = a.pro == PRO_RMSU || a.pro == PRO_RMSU_X ? rmsu_scale(a, o, lds, 0) : 1.f;
@@ -1257,7 +1281,8 @@ static bool cu_plan(const GArgs &a, CuPlan &p) {
     } else if (a.post.mode != POST_NONE) {
         return false;
     }
-    if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_RMSU_X && a.pro != PRO_X) return false;
+    if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_RMSU_X && a.pro != PRO_X && a.pro != PRO_HEADRMS)
+        return false;
     if ((a.pro == PRO_RMSU_X || a.pro == PRO_X) && (!a.x || ((uintptr_t)a.x & 15))) return false;
     // inputs built in the work-group: the weight window requested right
     // behind the copies of x (and w); RMSNorm inputs: rms_k balanced
@@ -1337,7 +1362,9 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
     }
     if (a.post.mode != POST_NONE && a.post.mode != POST_SWIGLU && a.post.mode != POST_SWIGLU_H) return -1;
     // other prologues come prepared
-    if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_RMSU_X && a.pro != PRO_X) return -1;
+    if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_RMSU_X && a.pro != PRO_X && a.pro != PRO_HEADRMS)
+        return -1;
+    if (a.pro == PRO_HEADRMS && (a.group < 32 || a.group % 32 || a.K % a.group)) return -1;
     if ((a.pro == PRO_RMSU_X || a.pro == PRO_X) && (!a.x || ((uintptr_t)a.x & 15) || (a.xs & 3))) return -1;
     if (a.pro == PRO_RMSU_X && (!a.pro_w || ((uintptr_t)a.pro_w & 15))) return -1;
     // POST_SWIGLU_H exists in the per-CU launch only

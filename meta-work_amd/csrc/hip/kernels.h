@@ -29,7 +29,11 @@ constexpr size_t kWeightPad = 16384;
 //   PRO_RMSU_X  the GEMV's work-groups build them from x in LDS (no prep launch)
 //   PRO_X       the GEMV's work-groups build them from the plain input x in
 //               LDS (no norm), e.g. the SwiGLU values left by POST_SWIGLU_H
-enum Pro { PRO_NONE = 0, PRO_SWIGLU = 2, PRO_GATED_RMS = 3, PRO_RMSU = 4, PRO_RMSU_X = 5, PRO_X = 6 };
+//   PRO_HEADRMS prepared digits of u = o * w * silu(z) whose groups carry the
+//               sum of o^2 in ss: every head of `group` elements is scaled by
+//               1/sqrt(sum over its groups / group + eps) (a gated RMSNorm per
+//               head whose rows were produced by different work-groups)
+enum Pro { PRO_NONE = 0, PRO_SWIGLU = 2, PRO_GATED_RMS = 3, PRO_RMSU = 4, PRO_RMSU_X = 5, PRO_X = 6, PRO_HEADRMS = 7 };
 enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_CONV = 2 };
 
 struct DevW {
@@ -153,6 +157,9 @@ struct DeltaArgs {
     uint8_t *xq;
     const float *z; int32_t z_s;
     const float *norm_w;
+    // split: one work-group per 32 value rows, xq holding the digits of
+    // out * norm_w * silu(z) and each group's sum of out^2 (PRO_HEADRMS input)
+    int32_t split;
 };
 int delta_launch(const DeltaArgs &a, hipStream_t st);
 

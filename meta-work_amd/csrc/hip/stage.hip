@@ -242,7 +242,7 @@ struct Gemv {
                 b.pro = PRO_RMSU_X;
             } else if (a.pro != PRO_X) {   // PRO_X: built from x inside the GEMV
                 if (!prof && !prepared && prep_launch(b, st)) return -1;
-                if (b.pro != PRO_RMSU) b.pro = PRO_NONE;   // the GEMV reads xq
+                if (b.pro != PRO_RMSU && b.pro != PRO_HEADRMS) b.pro = PRO_NONE;   // the GEMV reads xq
             }
             if (gemv_launch(b, st)) return -1;
         }
@@ -280,9 +280,17 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
         d.T = T; d.Hk = hp.h_k; d.Hv = Hv; d.S = hp.s_k; d.keep_n = keep_n; d.eps = hp.eps;
         d.qscale = 1.0f / sqrtf((float)hp.s_k);
         d.xq = S->xq_di; d.z = S->z; d.z_s = DI; d.norm_w = L.ssm_norm;
+        // one work-group per 32 value rows, the norm's per-head scale applied
+        // by the ssm_out GEMV (its float rows read v, which must be final)
+        const uint32_t ot = L.ssm_out.type;
+        static const bool split_on = env_int("XJ_DELTA_SPLIT", 1) != 0;
+        d.split = split_on && ot != XJ_F32 && ot != XJ_F16 && ot != XJ_BF16 && hp.s_k % 32 == 0;
         if (!pf && delta_launch(d, st)) return -1;
         Gemv q(S->xq_di, pf);
         q.prepared = true;
+        if (d.split) {
+            q.a.pro = PRO_HEADRMS; q.a.group = hp.s_k; q.a.eps = hp.eps;
+        }
         q.seg(L.ssm_out, x, E, EPI_ADD);
         if (q.run(T, st)) return -1;
     } else {
