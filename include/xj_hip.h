@@ -59,6 +59,11 @@ uint64_t    xj_hip_stage_state_bytes(const xj_model *m, int l0, int l1, int n_ct
  * which the reference's keep/rollback (one forward call only) cannot. */
 int xj_hip_stage_snapshot(xj_stage *s, int slot, char *err, size_t errlen);
 int xj_hip_stage_restore(xj_stage *s, int slot, int n_past, char *err, size_t errlen);
+/* Test hook, no counterpart in the reference: fill every attention layer's K
+ * and V cache from position pos0 to n_ctx with the fp16 pattern `bits`
+ * (e.g. 0x7E00, a NaN), standing for stale memory that a decode step must
+ * never read before writing it. */
+int xj_hip_stage_fill_kv(xj_stage *s, int pos0, uint16_t bits, char *err, size_t errlen);
 
 /* -------------------------------------------------------- host loader -- */
 

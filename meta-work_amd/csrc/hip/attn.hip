@@ -3,7 +3,8 @@
 // Computes attn_full of src/xiaoju-pipe/core/xj_cpu.c:83-151 after the q/k/v
 // projections, with the cache in fp16 as the Metal backend keeps it
 // (xj_kernels.metal:440-452):
-//   kv_store_kernel  one work-group per (token, kv head): RMSNorm(k_norm) of the
+//   kv_store_kernel  one work-group per (token, kv head) (several tokens; a single
+//                    token leaves this to attn_part_kernel): RMSNorm(k_norm) of the
 //                    new key (double sum, x*sc*w), NeoX RoPE of the first n_rot
 //                    dims (xj_cpu.c:68-77; cos and sin of theta = pos * base^(-2i/n_rot)
 //                    from a table the host fills per position with the
@@ -93,7 +94,20 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const AttnArgs a) {
 // decode position.
 constexpr int kSplitP = 32;
 
-template <int D, int G>
+// Work-group barrier ordering LDS accesses only (global loads in flight stay
+// in flight).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// F (single token): the work-group also does kv_store's work for itself -
+// the G queries normalised and rotated into LDS, and in the split holding pos
+// the new key (stored to the cache with its value, and used in place of the
+// cache bytes read for pos) - with kv_store's arithmetic, so the results are
+// those of kv_store + attn_part bit for bit.
+template <int D, int G, bool F>
 __global__ __launch_bounds__(256) void attn_part_kernel(const AttnArgs a) {
     constexpr int DL = D / 16;           // score dims per lane (16-lane teams, one position each)
     constexpr int NPT = kSplitP / 16;    // positions per team
@@ -111,6 +125,22 @@ __global__ __launch_bounds__(256) void attn_part_kernel(const AttnArgs a) {
     __shared__ float e[G][kSplitP];
     __shared__ float ml[G][2];
     __shared__ float po[PG][HC][D];
+    // F: the token's raw queries (and in the split holding pos its key and
+    // value), requested ahead of the cache so that their use waits for them only
+    const bool last = F && pos - j0 < kSplitP;   // this split holds pos (uniform)
+    float v[G + 1], vv = 0.f;
+    float2 csv = {0.f, 0.f};
+    float qnw = 0.f, knw = 0.f;
+    if constexpr (F) {
+        const bool in = tid < D;
+        qnw = in ? a.qnorm_w[tid] : 0.f;
+        knw = in && last ? a.knorm_w[tid] : 0.f;
+#pragma unroll
+        for (int i = 0; i < G; i++) v[i] = in ? a.qg[(int64_t)(g * G + i) * 2 * D + tid] : 0.f;
+        v[G] = in && last ? a.kn[g * D + tid] : 0.f;
+        vv = in && last ? a.vn[g * D + tid] : 0.f;
+        if (tid < a.n_rot / 2) csv = a.rope[(int64_t)pos * (a.n_rot / 2) + tid];   // n_rot <= D <= 256
+    }
     // every key and value of the split, clamped to valid positions
     u32x4 kw[NPT][(DL + 7) / 8];
     uint2 kw4[NPT];
@@ -133,13 +163,76 @@ __global__ __launch_bounds__(256) void attn_part_kernel(const AttnArgs a) {
         vw[r] = *(const u32x4 *)(a.vc + (int64_t)(j0 + jc) * nk + g * D + 8 * dg);
     }
     float qv[G][DL];
+    if constexpr (F) {
+        __shared__ float buf[G + 1][D];   // vectors 0..G-1 = queries, G = the new key
+        __shared__ float2 cs[D / 2];
+        __shared__ double red[4][G + 1];
+        __shared__ __align__(16) uint16_t kv16[2][D];   // the new key and value in fp16
+        const int NV = last ? G + 1 : G, w = tid >> 6;
+        const bool in = tid < D;
+        if (tid < a.n_rot / 2) cs[tid] = csv;
 #pragma unroll
-    for (int h = 0; h < G; h++) {
-        const float *qp = a.qr + ((int64_t)t * a.H + g * G + h) * D + l16 * DL;
+        for (int i = 0; i <= G; i++) {
+            const double ss = xjd::wave_sum_d((double)v[i] * v[i]);
+            if ((tid & 63) == 0 && i < NV) red[w][i] = ss;
+        }
+        lds_barrier();
 #pragma unroll
-        for (int d = 0; d < DL; d += 4) {
-            const float4 q4 = *(const float4 *)(qp + d);
-            qv[h][d] = q4.x; qv[h][d + 1] = q4.y; qv[h][d + 2] = q4.z; qv[h][d + 3] = q4.w;
+        for (int i = 0; i <= G; i++) {
+            if (i >= NV) break;
+            const double ss = red[0][i] + red[1][i] + red[2][i] + red[3][i];
+            const float sc = 1.0f / sqrtf((float)(ss / D) + a.eps);
+            if (in) buf[i][tid] = v[i] * sc * (i == G ? knw : qnw);
+        }
+        lds_barrier();
+        const int half = a.n_rot / 2;
+        for (int idx = tid; idx < NV * half; idx += 256) {
+            const int i = idx / half, j = idx % half;
+            const float x0 = buf[i][j], x1 = buf[i][j + half];
+            buf[i][j] = x0 * cs[j].x - x1 * cs[j].y;
+            buf[i][j + half] = x0 * cs[j].y + x1 * cs[j].x;
+        }
+        lds_barrier();
+        if (last && in) {
+            const uint16_t k16 = xjd::f32_to_f16(buf[G][tid]), v16 = xjd::f32_to_f16(vv);
+            a.kc[(int64_t)pos * nk + g * D + tid] = k16;
+            a.vc[(int64_t)pos * nk + g * D + tid] = v16;
+            kv16[0][tid] = k16;
+            kv16[1][tid] = v16;
+        }
+        lds_barrier();
+#pragma unroll
+        for (int h = 0; h < G; h++)
+#pragma unroll
+            for (int d = 0; d < DL; d++) qv[h][d] = buf[h][l16 * DL + d];
+        if (last) {   // the cache bytes read for pos (every clamped entry past it too) were stale
+#pragma unroll
+            for (int r = 0; r < NPT; r++) {
+                const int jj = team + 16 * r, jc = jj < n ? jj : n - 1;
+                if (j0 + jc != pos) continue;
+                const uint16_t *kp = &kv16[0][l16 * DL];
+                if constexpr (DL % 8 == 0) {
+#pragma unroll
+                    for (int d = 0; d < DL / 8; d++) kw[r][d] = *(const u32x4 *)(kp + 8 * d);
+                } else {
+                    kw4[r] = *(const uint2 *)kp;
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < NPG; r++) {
+                const int jj = pg + PG * r, jc = jj < n ? jj : n - 1;
+                if (j0 + jc == pos) vw[r] = *(const u32x4 *)&kv16[1][8 * dg];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            const float *qp = a.qr + ((int64_t)t * a.H + g * G + h) * D + l16 * DL;
+#pragma unroll
+            for (int d = 0; d < DL; d += 4) {
+                const float4 q4 = *(const float4 *)(qp + d);
+                qv[h][d] = q4.x; qv[h][d + 1] = q4.y; qv[h][d + 2] = q4.z; qv[h][d + 3] = q4.w;
+            }
         }
     }
     // scores
@@ -277,15 +370,26 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
     if (a.xq) xjd::emit_xq(r, h * D + d, in, a.xq + (int64_t)t * xq_off(a.H * D).stride, xq_off(a.H * D));
 }
 
+template <int D, bool F>
+static void launch_part(const AttnArgs &a, hipStream_t st) {
+    switch (a.H / a.Hkv) {
+    case 1: hipLaunchKernelGGL((attn_part_kernel<D, 1, F>), dim3(a.Hkv, a.T, a.n_split), dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((attn_part_kernel<D, 2, F>), dim3(a.Hkv, a.T, a.n_split), dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((attn_part_kernel<D, 4, F>), dim3(a.Hkv, a.T, a.n_split), dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((attn_part_kernel<D, 8, F>), dim3(a.Hkv, a.T, a.n_split), dim3(256), 0, st, a); break;
+    }
+}
+
+// A single token: kv_store's work inside the split kernel (XJ_ATTN_FUSE=0
+// keeps the separate kv_store launch).
 template <int D>
 static int launch_d(const AttnArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(kv_store_kernel<D>, dim3(a.T, a.Hkv), dim3(256), 0, st, a);
-    switch (a.H / a.Hkv) {
-    case 1: hipLaunchKernelGGL((attn_part_kernel<D, 1>), dim3(a.Hkv, a.T, a.n_split), dim3(256), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((attn_part_kernel<D, 2>), dim3(a.Hkv, a.T, a.n_split), dim3(256), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((attn_part_kernel<D, 4>), dim3(a.Hkv, a.T, a.n_split), dim3(256), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((attn_part_kernel<D, 8>), dim3(a.Hkv, a.T, a.n_split), dim3(256), 0, st, a); break;
-    default: return -1;
+    static const bool fuse = getenv("XJ_ATTN_FUSE") == nullptr || atoi(getenv("XJ_ATTN_FUSE")) != 0;
+    if (a.T == 1 && fuse) {
+        launch_part<D, true>(a, st);
+    } else {
+        hipLaunchKernelGGL(kv_store_kernel<D>, dim3(a.T, a.Hkv), dim3(256), 0, st, a);
+        launch_part<D, false>(a, st);
     }
     hipLaunchKernelGGL(attn_combine_kernel<D>, dim3(a.H, a.T), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;

@@ -725,6 +725,22 @@ extern "C" int xj_hip_stage_snapshot(xj_stage *s, int slot, char *err, size_t er
     return 0;
 }
 
+extern "C" int xj_hip_stage_fill_kv(xj_stage *s, int pos0, uint16_t bits, char *err, size_t errlen) {
+    HStage *S = H(s);
+    if (pos0 < 0 || pos0 > s->n_ctx) { snprintf(err, errlen, "bad position %d", pos0); return -1; }
+    const xj_hparams &hp = S->s.m->hp;
+    const size_t nk = (size_t)hp.n_head_kv * hp.head_dim, n = (size_t)(s->n_ctx - pos0) * nk;
+    for (auto &L : S->L) {
+        if (L.rec || !L.kc || !n) continue;
+        if (hipMemsetD16Async((hipDeviceptr_t)(L.kc + pos0 * nk), bits, n, S->st) != hipSuccess ||
+            hipMemsetD16Async((hipDeviceptr_t)(L.vc + pos0 * nk), bits, n, S->st) != hipSuccess) {
+            snprintf(err, errlen, "cache fill failed");
+            return -1;
+        }
+    }
+    return sync_check(S, err, errlen);
+}
+
 extern "C" int xj_hip_stage_restore(xj_stage *s, int slot, int n_past, char *err, size_t errlen) {
     HStage *S = H(s);
     if (slot < 0 || slot >= kSnapSlots) { snprintf(err, errlen, "snapshot slot %d out of range", slot); return -1; }

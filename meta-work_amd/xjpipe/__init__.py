@@ -127,6 +127,7 @@ def lib():
     _sig(L, "xj_hip_stage_state_bytes", U64, C.POINTER(XjModel), I, I, I, I)
     _sig(L, "xj_hip_stage_snapshot", I, PS, I, CP, S)
     _sig(L, "xj_hip_stage_restore", I, PS, I, I, CP, S)
+    _sig(L, "xj_hip_stage_fill_kv", I, PS, I, C.c_uint16, CP, S)
     _sig(L, "xj_type_block", I, U32, C.POINTER(I))
     _sig(L, "xj_row_bytes", U64, U32, I64)
     _sig(L, "xj_type_name", CP, U32)
@@ -329,6 +330,11 @@ class HipStage:
     def restore(self, slot, n_past):
         err = _err()
         _check(lib().xj_hip_stage_restore(self.ptr, slot, n_past, err, ERR), err, "restore")
+
+    def fill_kv(self, pos0, bits):
+        """Test hook: the fp16 pattern `bits` in every K/V cache slot from pos0 on."""
+        err = _err()
+        _check(lib().xj_hip_stage_fill_kv(self.ptr, pos0, bits, err, ERR), err, "fill_kv")
 
     def destroy(self):
         if self.ptr:

@@ -138,6 +138,25 @@ def test_chain_greedy_matches_oracle(tiny):
     c.destroy()
 
 
+def test_decode_never_reads_unwritten_cache(tiny):
+    """The cache slots at and past the decode position hold whatever the memory held (here an fp16 NaN in
+    every slot) until a step writes them; a single-token step writes its own slot inside the attention
+    kernel, so it must not combine those bytes, not even with a zero weight (0 * NaN = NaN)."""
+    m, L = tiny, tiny.hp.n_layer
+    prompt = prompt_ids(m, 21, 6)
+    g = xp.HipStage(m, 0, L, 256, 8, True)
+    ch = xp.Chain([g])
+    first = ch.eval(prompt)
+    g.fill_kv(len(prompt), 0x7E00)
+    toks = np.concatenate([first, ch.decode(40)])
+    c = orc.CpuStage(m.ptr, 0, L, 256, 8, True, kv_f16=True)
+    want, margins = orc.greedy([c], prompt, 41)
+    assert np.array_equal(toks, want), (toks, want, margins)
+    ch.free()
+    g.destroy()
+    c.destroy()
+
+
 def test_chain_split_and_vtable_agree(tiny):
     """Two chained stages on the device give the same tokens as the host-driven vtable loop."""
     m, L = tiny, tiny.hp.n_layer
