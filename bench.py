@@ -17,7 +17,8 @@ Also reported, on the same run:
                 (oracle/_ref, OpenMP on this host's cores) on a bounded sample
                 of the same workload; the oracle's C restatement if that
                 library is absent.
-  gemv_*        stand-alone cold-cache GEMV legs (Q4_K / Q6_K LM-head shapes).
+  gemv_*        stand-alone cold-cache GEMV legs (Q4_K / Q6_K LM-head shapes), and
+                the gate|up and down shapes at T = 1..5 activation rows.
   decode_0_8b   the same measurement on the 0.8B-shape model.
 
 usage: python bench.py [--gpus 1] [--steps 512] [--warmup 16] [--no-cpu] [--no-extra]
@@ -113,6 +114,22 @@ def gemv_leg(t, rows, k, copies, iters):
             "GBps": round(by / (ms * 1e-3) / 1e9, 1), "frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
 
 
+def gemv_tokens(t, rows, k, copies=12, iters=200):
+    """One weight shape at T = 1..5 activation rows (the speculative-verify widths), cold weights:
+    us per launch and weight GB/s."""
+    blob = xp.quantize(t, xp.fill_normal(rows * k, 17, 0.02).reshape(rows, k))
+    ws = [xp.DevWeight(t, blob, rows, k) for _ in range(copies)]
+    by = rows * xp.row_bytes(t, k)
+    out = []
+    for T in range(1, 6):
+        xs = np.stack([xp.fill_normal(k, 5 + i, 1.0) for i in range(T)])
+        ms = xp.gemv_time(ws, xs, iters)
+        out.append({"T": T, "us": round(ms * 1e3, 2), "GBps": round(by / (ms * 1e-3) / 1e9, 1)})
+    for w in ws:
+        w.free()
+    return {"shape": f"{xp.TYPE_NAMES[t]} {rows}x{k}", "by_T": out}
+
+
 def delta_c3(reps=3):
     """Gated DeltaNet prefill on the c3 shape (16 heads, d=128, 2048 tokens from a zero state): the chunk-wise
     MFMA kernels (chunk 64) next to the token-by-token kernel. Wall ms per call include the host copies; the
@@ -200,6 +217,7 @@ def main():
         r8["st"].destroy()
         extra["gemv_legs"] = [gemv_leg(xp.Q4_K, 151936, 1024, 8, 64), gemv_leg(xp.Q6_K, 151936, 2560, 3, 24),
                               gemv_leg(xp.Q4_K, 4096, 1024, 256, 512)]
+        extra["gemv_tokens"] = [gemv_tokens(xp.Q4_K, 18432, 2560), gemv_tokens(xp.Q6_K, 2560, 9216)]
         log(f"extra: {extra}")
 
     cpu = None

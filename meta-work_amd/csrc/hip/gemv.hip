@@ -44,6 +44,7 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 static int g_lds_max = 64 * 1024;
+constexpr int kCuMaxT = 5;   // tokens of a per-CU launch (speculative verify widths)
 static int g_cus = 256;
 static int g_grid_cap = 256 * 8;
 
@@ -794,25 +795,36 @@ __device__ __forceinline__ f32x4 ld4f(const float *p) { return *(const f32x4 *)p
 // Prologues whose activations the GEMV's work-groups build from x in LDS.
 __device__ __forceinline__ bool pro_inwg(int pro) { return pro == PRO_RMSU_X || pro == PRO_X; }
 
-// PRO_RMSU_X / PRO_X for a single token: x (and w) are copied into LDS after
-// the activations' area (at xl + v_off, 4 K bytes each), then converted into
-// it (PRO_X: u = x * 1, exact).
+// PRO_RMSU_X / PRO_X for T tokens of a per-CU launch (or one token of the
+// 256-thread form): x of token t is copied into LDS after the T tokens'
+// activations (at xl + T * v_off + t * 4K bytes), w after those copies (at
+// xl + T * v_off + T * 4K), then converted into token t's activations
+// (PRO_X: u = x * 1, exact).
+template <int T>
 __device__ __forceinline__ void rmsx1_issue(const GArgs &a, const XqOff &o, uint8_t *xl) {
-    dma_lds((const uint8_t *)a.x, xl + o.v_off, a.K >> 2);
-    if (a.pro == PRO_RMSU_X) dma_lds((const uint8_t *)a.pro_w, xl + o.v_off + 4 * a.K, a.K >> 2);
+    uint8_t *base = xl + T * o.v_off;
+#pragma unroll
+    for (int t = 0; t < T; t++) dma_lds((const uint8_t *)(a.x + (int64_t)t * a.xs), base + t * 4 * a.K, a.K >> 2);
+    if (a.pro == PRO_RMSU_X) dma_lds((const uint8_t *)a.pro_w, base + T * 4 * a.K, a.K >> 2);
 }
 
+template <int T>
 __device__ __forceinline__ void rmsx1_finish(const GArgs &a, const XqOff &o, uint8_t *xl) {
-    const f32x4 *xs = (const f32x4 *)(xl + o.v_off), *ws = (const f32x4 *)(xl + o.v_off + 4 * a.K);
+    const uint8_t *base = xl + T * o.v_off;
+    const f32x4 *ws = (const f32x4 *)(base + T * 4 * a.K);
     const int n8 = a.K >> 3;
-    for (int i0 = 0; i0 < n8; i0 += blockDim.x) {
-        const int i = i0 + threadIdx.x, ic = i < n8 ? i : n8 - 1;
-        const f32x4 x[2] = {xs[2 * ic], xs[2 * ic + 1]};
-        if (a.pro == PRO_X) {
-            emit8<false>(x, x, 8 * i, i < n8, xl, o);
-        } else {
-            const f32x4 w[2] = {ws[2 * ic], ws[2 * ic + 1]};
-            emit8<true>(x, w, 8 * i, i < n8, xl, o);
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        const f32x4 *xs = (const f32x4 *)(base + t * 4 * a.K);
+        for (int i0 = 0; i0 < n8; i0 += blockDim.x) {
+            const int i = i0 + threadIdx.x, ic = i < n8 ? i : n8 - 1;
+            const f32x4 x[2] = {xs[2 * ic], xs[2 * ic + 1]};
+            if (a.pro == PRO_X) {
+                emit8<false>(x, x, 8 * i, i < n8, xl + t * o.v_off, o);
+            } else {
+                const f32x4 w[2] = {ws[2 * ic], ws[2 * ic + 1]};
+                emit8<true>(x, w, 8 * i, i < n8, xl + t * o.v_off, o);
+            }
         }
     }
 }
@@ -919,7 +931,7 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
     } else {
         // LDS copies first, then the window's loads: waiting for vmcnt <=
         // their number completes the copies only
-        if (pro_inwg(a.pro)) rmsx1_issue(a, o, lds);
+        if (pro_inwg(a.pro)) rmsx1_issue<1>(a, o, lds);
         else dma_xq<T>(a, o, lds);
         barrier_raw();   // the group's copies are queued ahead of its weight requests
         first_units(rg);
@@ -927,7 +939,7 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         wait_vm<Win<MU, Q4>::LOADS>();
         barrier_raw();
         if (pro_inwg(a.pro)) {
-            rmsx1_finish(a, o, lds);
+            rmsx1_finish<1>(a, o, lds);
             barrier_lds();
         }
         if (a.pro == PRO_HEADRMS) {
@@ -980,11 +992,12 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
     if (a.inc_ptr && blockIdx.x == 0 && tid == 0) *a.inc_ptr += a.inc_by;
 }
 
-// POST_SWIGLU tail of a single-token per-CU launch (rpw rows per work-group,
+// POST_SWIGLU tail of a per-CU launch over T tokens (rpw rows per work-group,
 // gate = segment 0, up = segment 1): the work-group arrives once on every
 // 32-index group its rows touch; the last of the group's work-groups (those
 // of both segments covering its 32 rows) emits silu(gate) * up
 // (xj_cpu.c:273). At most 8 groups per work-group (rpw <= 226).
+template <int T>
 __device__ __forceinline__ void tail_swiglu_cu(const GArgs &a, int rg, const GSeg &sg) {
     __shared__ int last_sh[8];
     const int tid = threadIdx.x, j = rg - sg.wg0;
@@ -1008,8 +1021,13 @@ __device__ __forceinline__ void tail_swiglu_cu(const GArgs &a, int rg, const GSe
         if (tid < 64) {
             const int k = 32 * (ga + i) + (tid & 31);
             const bool in = tid < 32;
-            const float v = in ? xjd::silu(xjd::load_sys(g.y + k)) * xjd::load_sys(u.y + k) : 0.f;
-            xjd::emit_xq(v, k, in, a.post.xq, o);
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+                const float v = in ? xjd::silu(xjd::load_sys(g.y + (int64_t)t * g.ys + k)) *
+                                         xjd::load_sys(u.y + (int64_t)t * u.ys + k)
+                                   : 0.f;
+                xjd::emit_xq(v, k, in, a.post.xq + (int64_t)t * o.stride, o);
+            }
         }
     }
 }
@@ -1039,14 +1057,15 @@ __device__ __forceinline__ void swiglu_h_cu(const GArgs &a, int rg, int ho, int 
 // arrives, otherwise the copies complete first and every lane then requests
 // all its MU units. The gate|up launch ends with the SwiGLU tail (or its
 // work-group-local form, POST_SWIGLU_H); no argmax partials.
-template <int TS, int MU, bool Q4, bool WF>
+template <int T, int TS, int MU, bool Q4, bool WF>
 __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
     extern __shared__ u32x4 lds_v[];
     // WF: one unit requested right behind the activation copies, the rest
     // from the unit loop one ahead (more in flight before the conversion
     // delays it, more ahead in the loop congests: both measured slower);
-    // otherwise the copies complete first, then all units
-    constexpr int NW = WF ? 1 : MU, PD = NW - 1;
+    // otherwise the copies complete first, then all units. MU == 0 (several
+    // tokens): a rolled unit loop with the next unit in flight.
+    constexpr int NW = WF || MU == 0 ? 1 : MU, PD = NW - 1;
     const int K = a.K, nu = K / 64;
     const XqOff o = xq_off(K);
     const int tid = threadIdx.x, team = tid / TS, lane = tid % TS;
@@ -1064,8 +1083,8 @@ __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
     const int64_t rb = row * (K / 256);
     uint8_t *lds = (uint8_t *)lds_v;
     const bool inwg = pro_inwg(a.pro);
-    if (inwg) rmsx1_issue(a, o, lds);
-    else dma_xq<1>(a, o, lds);
+    if (inwg) rmsx1_issue<T>(a, o, lds);
+    else dma_xq<T>(a, o, lds);
     if (!WF) wait_vm<0>();   // the activations complete before any weight request
     barrier_raw();
     RawU win[NW];
@@ -1078,28 +1097,34 @@ __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
         barrier_raw();
     }
     if (inwg) {
-        rmsx1_finish(a, o, lds);
+        rmsx1_finish<T>(a, o, lds);
         barrier_lds();
     }
     if (a.pro == PRO_HEADRMS) {   // prepared: the copies completed before the weight requests
-        head_scale(a, o, lds, 0);
+#pragma unroll
+        for (int t = 0; t < T; t++) head_scale(a, o, lds, t);
         barrier_lds();
     }
-    const float sc = a.pro == PRO_RMSU || a.pro == PRO_RMSU_X ? rmsu_scale(a, o, lds, 0) : 1.f;
-    EpiIn<1> ein;
-    epi_load<1>(sg, row, ein);
-    float acc[1] = {0.f};
+    float sc[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) sc[t] = a.pro == PRO_RMSU || a.pro == PRO_RMSU_X ? rmsu_scale(a, o, lds, t) : 1.f;
+    EpiIn<T> ein;
+    epi_load<T>(sg, row, ein);
+    float acc[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) acc[t] = 0.f;
     if (Q4 || sg.type == XJ_Q4_K) {
-        rows_q4k<1, TS, MU, PD>(sg.w, rb, nu, lane, win, lds, o.v_off, o, acc);
+        rows_q4k<T, TS, MU, PD>(sg.w, rb, nu, lane, win, lds, o.v_off, o, acc);
     } else if constexpr (!Q4) {
-        rows_q6k<1, TS, MU, PD>(sg.w, sg.nblk, rb, nu, lane, win, lds, o.v_off, o, acc);
+        rows_q6k<T, TS, MU, PD>(sg.w, sg.nblk, rb, nu, lane, win, lds, o.v_off, o, acc);
     }
-    acc[0] = team_sum<TS>(acc[0]) * sc;
-    if (H) {
+#pragma unroll
+    for (int t = 0; t < T; t++) acc[t] = team_sum<TS>(acc[t]) * sc[t];
+    if (T == 1 && H) {
         swiglu_h_cu(a, rg, ho, team, lane, acc[0]);
     } else {
-        if (mine && lane == 0) epi_row<1>(a, sg, row, acc, ein);
-        if (a.post.mode == POST_SWIGLU) tail_swiglu_cu(a, rg, sg);
+        if (mine && lane == 0) epi_row<T>(a, sg, row, acc, ein);
+        if (a.post.mode == POST_SWIGLU) tail_swiglu_cu<T>(a, rg, sg);
     }
     if (a.inc_ptr && blockIdx.x == 0 && tid == 0) *a.inc_ptr += a.inc_by;
 }
@@ -1210,6 +1235,13 @@ static int cu_threads(const GArgs &a, int need) {
     return t;
 }
 
+// Dynamic LDS of a per-CU launch: the T tokens' activations, and for an
+// input built in the work-group the copies of x (one per token) and of w.
+static size_t cu_lds_bytes(const GArgs &a) {
+    const size_t b = (size_t)a.T * xq_off(a.K).v_off;
+    return a.pro == PRO_RMSU_X ? b + (size_t)(a.T + 1) * 4 * a.K : a.pro == PRO_X ? b + (size_t)a.T * 4 * a.K : b;
+}
+
 // Teams of a per-CU work-group with rpw rows (POST_SWIGLU_H: rpw gate rows
 // from team 0 and rpw up rows from the first whole wavefront after them).
 static int cu_teams(int rpw, int ts, bool h) {
@@ -1237,17 +1269,25 @@ static int launch_cu_ts(GArgs b, int rpw, int upl, bool q4, bool wf, hipStream_t
     }
     b.rpw = rpw;
     const int threads = cu_threads(b, teams * TS);
-    size_t lds = gemv_lds_bytes(b);
+    size_t lds = cu_lds_bytes(b);
     // more than half of a CU's LDS keeps each work-group on a CU of its own
     if (b.pro != PRO_RMSU_X && g_lds_max > 80 * 1024 && lds < 80 * 1024 + 256) lds = 80 * 1024 + 256;
     void (*k)(GArgs) = nullptr;
-#define XJ_CU_K(Q, W)                                          \
-    switch (upl) {                                              \
-    case 1: k = gemv_cu_kernel<TS, 1, Q, W>; break;            \
-    case 2: k = gemv_cu_kernel<TS, 2, Q, W>; break;            \
-    case 3: k = gemv_cu_kernel<TS, 3, Q, W>; break;            \
-    case 4: k = gemv_cu_kernel<TS, 4, Q, W>; break;            \
-    default: k = gemv_cu_kernel<TS, 5, Q, W>; break;           \
+#define XJ_CU_K(Q, W)                                                   \
+    switch (b.T) {                                                       \
+    case 1:                                                              \
+        switch (upl) {                                                   \
+        case 1: k = gemv_cu_kernel<1, TS, 1, Q, W>; break;               \
+        case 2: k = gemv_cu_kernel<1, TS, 2, Q, W>; break;               \
+        case 3: k = gemv_cu_kernel<1, TS, 3, Q, W>; break;               \
+        case 4: k = gemv_cu_kernel<1, TS, 4, Q, W>; break;               \
+        default: k = gemv_cu_kernel<1, TS, 5, Q, W>; break;              \
+        }                                                                \
+        break;                                                           \
+    case 2: k = gemv_cu_kernel<2, TS, 0, Q, W>; break;                   \
+    case 3: k = gemv_cu_kernel<3, TS, 0, Q, W>; break;                   \
+    case 4: k = gemv_cu_kernel<4, TS, 0, Q, W>; break;                   \
+    default: k = gemv_cu_kernel<5, TS, 0, Q, W>; break;                  \
     }
     if (q4 && wf) { XJ_CU_K(true, true) }
     else if (q4) { XJ_CU_K(true, false) }
@@ -1269,8 +1309,9 @@ struct CuPlan {
 static bool cu_plan(const GArgs &a, CuPlan &p) {
     static const bool on = env_or("XJ_GEMV_CU", 1) != 0;
     static const int rms_k = env_or("XJ_GEMV_RMS_WG_PER_CU", 1);
-    if (!on || a.T != 1) return false;
+    if (!on || a.T < 1 || a.T > kCuMaxT) return false;
     const bool H = a.post.mode == POST_SWIGLU_H;
+    if (H && a.T != 1) return false;
     if (a.post.mode == POST_SWIGLU) {
         if (!a.post.xq || !a.post.cnt || a.nseg != 2 || a.seg[0].n_rows != a.seg[1].n_rows || a.seg[0].n_rows % 32)
             return false;
@@ -1299,7 +1340,7 @@ static bool cu_plan(const GArgs &a, CuPlan &p) {
         q4 = q4 && s.type == XJ_Q4_K;
         total += s.n_rows;
     }
-    if (a.K % 256 || a.K > 16384 || gemv_lds_bytes(a) > (size_t)g_lds_max) return false;
+    if (a.K % 256 || a.K > 16384 || cu_lds_bytes(a) > (size_t)g_lds_max) return false;
     // the fewest rows per work-group whose work-groups fit nwg_max
     int rpw;
     if (H) {
@@ -1396,7 +1437,7 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
             return 0;
         }
     }
-    if (a.T == 1) {
+    if (a.T <= kCuMaxT) {
         const int rc = gemv_launch_cu(a, st);
         if (rc <= 0) return rc;
     }
@@ -1429,11 +1470,15 @@ static void raise_ts(int bytes) {
 
 template <int TS, bool WF>
 static void raise_cu_wf(int bytes) {
-    const void *f[] = {(const void *)gemv_cu_kernel<TS, 1, true, WF>, (const void *)gemv_cu_kernel<TS, 2, true, WF>,
-                       (const void *)gemv_cu_kernel<TS, 3, true, WF>, (const void *)gemv_cu_kernel<TS, 4, true, WF>,
-                       (const void *)gemv_cu_kernel<TS, 5, true, WF>, (const void *)gemv_cu_kernel<TS, 1, false, WF>,
-                       (const void *)gemv_cu_kernel<TS, 2, false, WF>, (const void *)gemv_cu_kernel<TS, 3, false, WF>,
-                       (const void *)gemv_cu_kernel<TS, 4, false, WF>, (const void *)gemv_cu_kernel<TS, 5, false, WF>};
+    const void *f[] = {(const void *)gemv_cu_kernel<1, TS, 1, true, WF>, (const void *)gemv_cu_kernel<1, TS, 2, true, WF>,
+                       (const void *)gemv_cu_kernel<1, TS, 3, true, WF>, (const void *)gemv_cu_kernel<1, TS, 4, true, WF>,
+                       (const void *)gemv_cu_kernel<1, TS, 5, true, WF>, (const void *)gemv_cu_kernel<1, TS, 1, false, WF>,
+                       (const void *)gemv_cu_kernel<1, TS, 2, false, WF>, (const void *)gemv_cu_kernel<1, TS, 3, false, WF>,
+                       (const void *)gemv_cu_kernel<1, TS, 4, false, WF>, (const void *)gemv_cu_kernel<1, TS, 5, false, WF>,
+                       (const void *)gemv_cu_kernel<2, TS, 0, true, WF>, (const void *)gemv_cu_kernel<3, TS, 0, true, WF>,
+                       (const void *)gemv_cu_kernel<4, TS, 0, true, WF>, (const void *)gemv_cu_kernel<5, TS, 0, true, WF>,
+                       (const void *)gemv_cu_kernel<2, TS, 0, false, WF>, (const void *)gemv_cu_kernel<3, TS, 0, false, WF>,
+                       (const void *)gemv_cu_kernel<4, TS, 0, false, WF>, (const void *)gemv_cu_kernel<5, TS, 0, false, WF>};
     for (const void *k : f) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 template <int TS>
