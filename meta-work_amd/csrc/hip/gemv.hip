@@ -1052,11 +1052,13 @@ __device__ __forceinline__ void swiglu_h_cu(const GArgs &a, int rg, int ho, int 
 // [0, rpw) and the same rows of the up (segment 1) in teams [ho, ho + rpw),
 // ho = rpw rounded up to whole wavefronts. The activations (prepared, or
 // the x (and w) of an input built in the work-group: PRO_RMSU_X, PRO_X) are
-// copied into LDS once per CU; WF (inputs built in the work-group) requests
-// one unit of every lane right behind the copies and converts x while it
-// arrives, otherwise the copies complete first and every lane then requests
-// all its MU units. The gate|up launch ends with the SwiGLU tail (or its
-// work-group-local form, POST_SWIGLU_H); no argmax partials.
+// copied into LDS once per CU; WF (inputs built in the work-group, and
+// prepared inputs without a tail) requests one unit of every lane right
+// behind the copies and converts x while it arrives; otherwise (a prepared
+// input with the cross-work-group tail) the copies complete first and every
+// lane then requests all its MU units. The gate|up launch ends with the
+// SwiGLU tail (or its work-group-local form, POST_SWIGLU_H); no argmax
+// partials.
 template <int T, int TS, int MU, bool Q4, bool WF>
 __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
     extern __shared__ u32x4 lds_v[];
@@ -1325,10 +1327,11 @@ static bool cu_plan(const GArgs &a, CuPlan &p) {
     if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_RMSU_X && a.pro != PRO_X && a.pro != PRO_HEADRMS)
         return false;
     if ((a.pro == PRO_RMSU_X || a.pro == PRO_X) && (!a.x || ((uintptr_t)a.x & 15))) return false;
-    // inputs built in the work-group: the weight window requested right
-    // behind the copies of x (and w); RMSNorm inputs: rms_k balanced
-    // work-groups per CU
-    const bool wf = a.pro == PRO_RMSU_X || a.pro == PRO_X;
+    // the weight window requested right behind the activation copies for
+    // inputs built in the work-group and for prepared inputs without a tail
+    // (before: the copies completed first; 702 vs 707 tok/s); RMSNorm inputs:
+    // rms_k balanced work-groups per CU
+    const bool wf = a.pro == PRO_RMSU_X || a.pro == PRO_X || a.post.mode == POST_NONE;
     if (a.pro == PRO_RMSU_X && (rms_k < 1 || !a.pro_w || ((uintptr_t)a.pro_w & 15))) return false;
     const int nwg_max = a.pro == PRO_RMSU_X ? rms_k * g_cus : g_cus;
     int64_t total = 0;
