@@ -1158,9 +1158,11 @@ GemvPlan gemv_plan(int K, int64_t rows) {
 }
 
 int gemv_max_tile(int K) {
+    static const int cap = env_or("XJ_GEMV_TILE", kCuMaxT);
     const int per_t = xq_off(K).v_off;
     int t = (int)(g_lds_max / per_t);
-    return t < 1 ? 0 : t > kTileT ? kTileT : t;
+    const int c = cap < 1 ? 1 : cap > kTileT ? kTileT : cap;
+    return t < 1 ? 0 : t > c ? c : t;
 }
 
 size_t gemv_xq_bytes(int K) { return (size_t)(gemv_max_tile(K) > 0 ? gemv_max_tile(K) : 1) * xq_off(K).stride; }
