@@ -190,6 +190,39 @@ double xjh_gemv_time(uint32_t type, void *const *dws, int n_copies, int64_t n_ro
 /* out[t] = rmsnorm(x[t]) * w  (mode 0) or x[t]/sqrt(sum x^2 + eps) (mode 1). */
 int xjh_norm(int mode, const float *x, const float *w, int n, int rows, float eps, float *out,
              char *err, size_t errlen);
+/* g[i] = silu(g[i]) * u[i] over n floats, in place.
+ * Replaces: src/xiaoju-pipe/metal/xj_kernels.metal:591-600 (xj_swiglu);
+ * CPU form xj_cpu.c:273. */
+int xjh_swiglu(float *g, const float *u, int64_t n, char *err, size_t errlen);
+/* NeoX RoPE in place: for token t < T and head h < n_heads, the pairs
+ * (i, i + n_rot/2) of x + t*tok_stride + h*head_stride are rotated by
+ * theta = (pos0 + t) * base^(-2i/n_rot) (cos and sin evaluated in float on the
+ * host, as xj_cpu.c:68-77 does).
+ * Replaces: src/xiaoju-pipe/metal/xj_kernels.metal:422-437 (xj_rope). */
+int xjh_rope(float *x, int T, int n_heads, int64_t tok_stride, int64_t head_stride, int n_rot,
+             int pos0, float base, char *err, size_t errlen);
+/* Depthwise causal conv + SiLU in place over x [T][C] (kernel K in 2..8,
+ * weights w [C][K], state [C][K-1] = the last K-1 inputs, oldest first,
+ * carried across calls); ck (may be NULL when ck_n == 0) receives the state
+ * after each of the first ck_n tokens, [ck_n][C][K-1]. The code is the qkv
+ * GEMV's conv epilogue.
+ * Replaces: src/xiaoju-pipe/metal/xj_kernels.metal:525-549 (xj_conv_silu);
+ * CPU form xj_cpu.c:172-182. */
+int xjh_conv_silu(float *x, float *state, const float *w, int C, int K, int T, float *ck, int ck_n,
+                  char *err, size_t errlen);
+/* Gated GQA attention of T new tokens at positions n_past .. n_past+T-1, after
+ * the projections, through the token loop's own kernels: qg [T][H][2D]
+ * (q | gate per head), k, v [T][Hkv*D] (raw projections); the new keys get
+ * RMSNorm(k_norm) + RoPE and are stored with the values into the fp16 caches
+ * kc, vc [n_ctx][Hkv*D] (IEEE half bits); out [T][H*D] = softmax(q'.K^T /
+ * sqrt(D)) V * sigmoid(gate) with q' = RoPE(RMSNorm(q) * q_norm). D in
+ * {64, 128, 256}, H/Hkv in {1, 2, 4, 8}.
+ * Replaces: src/xiaoju-pipe/metal/xj_kernels.metal:439-523 (xj_kv_store,
+ * xj_attn_scores, xj_softmax, xj_attn_out); CPU form xj_cpu.c:106-147. */
+int xjh_attn_decode(int T, int H, int Hkv, int D, int n_rot, float rope_base, float eps, int n_past,
+                    int n_ctx, const float *qg, const float *k, const float *v, const float *q_norm,
+                    const float *k_norm, uint16_t *kc, uint16_t *vc, float *out,
+                    char *err, size_t errlen);
 /* First index of the maximum of each of T rows of n floats. */
 int xjh_argmax(const float *x, int n, int T, int32_t *out_host, char *err, size_t errlen);
 /* Gated delta rule (standalone, decay and beta given per token and head):

@@ -395,6 +395,41 @@ static int launch_d(const AttnArgs &a, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// NeoX RoPE in place (xj_cpu.c:68-77) of T tokens x n_heads heads, one
+// thread per pair (i, i + n_rot/2), with cos and sin of position pos0 + t from
+// the same kind of table kv_store reads (cs[t][n_rot/2]).
+__global__ __launch_bounds__(256) void rope_kernel(float *x, const float2 *cs, int T, int nh, int64_t tok_s, int64_t head_s,
+                                                   int n_rot) {
+    const int half = n_rot / 2;
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gid >= (int64_t)T * nh * half) return;
+    const int i = (int)(gid % half), h = (int)((gid / half) % nh), t = (int)(gid / ((int64_t)half * nh));
+    const float2 c = cs[(int64_t)t * half + i];
+    float *p = x + t * tok_s + h * head_s;
+    const float x0 = p[i], x1 = p[i + half];
+    p[i] = x0 * c.x - x1 * c.y;
+    p[i + half] = x0 * c.y + x1 * c.x;
+}
+
+void rope_table(int pos0, int n, int n_rot, float base, float2 *out) {
+    const int half = n_rot / 2;
+    for (int p = 0; p < n; p++)
+        for (int i = 0; i < half; i++) {
+            const float theta = (pos0 + p) * powf(base, -2.0f * i / n_rot);
+            out[(size_t)p * half + i] = float2{cosf(theta), sinf(theta)};
+        }
+}
+
+int rope_launch(float *x, const float2 *cs, int T, int n_heads, int64_t tok_stride, int64_t head_stride, int n_rot,
+                hipStream_t st) {
+    if (T < 0 || n_heads < 0 || n_rot < 2 || n_rot % 2) return -1;
+    const int64_t n = (int64_t)T * n_heads * (n_rot / 2);
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, cs, T, n_heads, tok_stride,
+                       head_stride, n_rot);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 int attn_splits(int n_ctx) { return (n_ctx + kSplitP - 1) / kSplitP; }
 
 int attn_launch(const AttnArgs &a, hipStream_t st) {

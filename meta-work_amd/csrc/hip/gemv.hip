@@ -1561,6 +1561,39 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *__restrict_
     xjd::dequant_chunk(W, type, K, nblk, r0 + rr, c, y + rr * K + c * 32);
 }
 
+// Depthwise causal conv + SiLU of T tokens in place, one thread per channel,
+// tokens in order: the EPI_CONV epilogue's own code (epi_load / epi_row) with
+// the token's input as the row's dot product. Checkpoint t (t < keep_n) holds
+// the state after token t.
+__global__ __launch_bounds__(256) void conv_silu_kernel(const GArgs a, float *x, int T) {
+    const GSeg &sg0 = a.seg[0];
+    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r >= sg0.n_rows) return;
+    for (int t = 0; t < T; t++) {
+        GSeg sg = sg0;
+        sg.y = x + (int64_t)t * sg0.n_rows;
+        GArgs b = a;
+        b.t0 = t;
+        EpiIn<1> e;
+        epi_load<1>(sg, r, e);
+        const float acc[1] = {sg.y[r]};
+        epi_row<1>(b, sg, r, acc, e);
+    }
+}
+
+int conv_silu_launch(float *x, float *state, const float *w, int C, int K, int T, float *ck, int ck_n, hipStream_t st) {
+    if (C < 1 || T < 1 || K < 2 || K > 8 || ck_n < 0 || ck_n > T || (ck_n && !ck)) return -1;
+    GArgs a{};
+    a.keep_n = ck_n;
+    a.post.mode = POST_NONE;
+    a.nseg = 1;
+    GSeg &sg = a.seg[0];
+    sg.n_rows = C; sg.ys = C; sg.epi = EPI_CONV;
+    sg.conv_state = state; sg.conv_w = w; sg.conv_ck = ck; sg.conv_k = K;
+    hipLaunchKernelGGL(conv_silu_kernel, dim3((C + 255) / 256), dim3(256), 0, st, a, x, T);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 int dequant_launch(const DevW &w, int64_t r0, int64_t n, float *y, hipStream_t st) {
     const int64_t nch = w.k / 32, total = n * nch;
     const int64_t nblk = xjd::dev_nblk(w.type, w.n_rows, w.k);

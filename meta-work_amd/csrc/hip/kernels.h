@@ -187,5 +187,18 @@ int argmax_finalize_launch(const unsigned long long *amax, int n_part, int T, in
 // Plain argmax of T rows of n floats (first maximum).
 int argmax_rows_launch(const float *x, int n, int T, int32_t *out, hipStream_t st);
 int norm_launch(int mode, const float *x, const float *w, int n, int rows, float eps, float *out, hipStream_t st);
+// g = silu(g) * u over n floats.
+int swiglu_launch(float *g, const float *u, int64_t n, hipStream_t st);
+// NeoX RoPE in place of x[t * tok_stride + h * head_stride + i] for T tokens and
+// n_heads heads; cs[t][n_rot/2] holds (cos, sin) of token t's angles.
+int rope_launch(float *x, const float2 *cs, int T, int n_heads, int64_t tok_stride, int64_t head_stride, int n_rot,
+                hipStream_t st);
+// (cos, sin) of theta = pos * base^(-2i/n_rot) for positions pos0 .. pos0+n-1,
+// in float as the reference's rope evaluates them: out[p][n_rot/2].
+void rope_table(int pos0, int n, int n_rot, float base, float2 *out);
+// Depthwise causal conv (kernel K <= 8) + SiLU in place of x [T][C], state
+// [C][K-1] carried across calls, ck [ck_n][C][K-1] the state after each of the
+// first ck_n tokens (EPI_CONV's code).
+int conv_silu_launch(float *x, float *state, const float *w, int C, int K, int T, float *ck, int ck_n, hipStream_t st);
 
 }  // namespace xjk

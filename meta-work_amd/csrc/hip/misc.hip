@@ -9,6 +9,8 @@
 //                    advances the step counter (one work-group per token row).
 //   argmax_rows      plain first-maximum argmax of T rows (test entry point).
 //   norm_kernel      RMSNorm / L2 rows (xj_cpu.c:56-61, :185-193).
+//   swiglu_kernel    g = silu(g) * u (xj_cpu.c:273; test entry point: the
+//                    token loop applies SwiGLU inside the gate|up and down GEMVs).
 #include "common.h"
 #include "dequant.h"
 #include "kernels.h"
@@ -104,6 +106,18 @@ int argmax_finalize_launch(const unsigned long long *amax, int n_part, int T, in
 
 int argmax_rows_launch(const float *x, int n, int T, int32_t *out, hipStream_t st) {
     hipLaunchKernelGGL(argmax_rows_kernel, dim3(T), dim3(256), 0, st, x, n, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+__global__ __launch_bounds__(256) void swiglu_kernel(float *g, const float *u, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) g[i] = xjd::silu(g[i]) * u[i];
+}
+
+int swiglu_launch(float *g, const float *u, int64_t n, hipStream_t st) {
+    if (n < 0) return -1;
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, n);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

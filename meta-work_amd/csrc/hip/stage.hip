@@ -687,11 +687,7 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
     {   // cos and sin of theta = pos * base^(-2i/n_rot) for every position, in float as the
         // reference's rope evaluates them (xj_cpu.c:68-77)
         std::vector<float2> cs((size_t)n_ctx * half, float2{1.f, 0.f});
-        for (int p = 0; p < n_ctx; p++)
-            for (int i = 0; i < hp.n_rot / 2; i++) {
-                const float theta = p * powf(hp.rope_base, -2.0f * i / hp.n_rot);
-                cs[(size_t)p * half + i] = float2{cosf(theta), sinf(theta)};
-            }
+        rope_table(0, n_ctx, hp.n_rot, hp.rope_base, cs.data());
         XJ_CHECK(hipMemcpy(S->rope, cs.data(), cs.size() * sizeof(float2), hipMemcpyHostToDevice), err, errlen, fail());
     }
     XJ_CHECK(hipHostMalloc((void **)&S->h_x, sizeof(float) * mb * E, hipHostMallocDefault), err, errlen, fail());
@@ -1185,6 +1181,94 @@ extern "C" int xjh_norm(int mode, const float *x, const float *w, int n, int row
     if (!ops_stream()) return -1;
     if (norm_launch(mode, x, w, n, rows, eps, out, g_stream)) { snprintf(err, errlen, "norm launch failed"); return -1; }
     return ops_done(err, errlen);
+}
+
+extern "C" int xjh_swiglu(float *g, const float *u, int64_t n, char *err, size_t errlen) {
+    if (!ops_stream()) return -1;
+    if (swiglu_launch(g, u, n, g_stream)) { snprintf(err, errlen, "swiglu launch failed (n = %lld)", (long long)n); return -1; }
+    return ops_done(err, errlen);
+}
+
+extern "C" int xjh_rope(float *x, int T, int n_heads, int64_t tok_stride, int64_t head_stride, int n_rot, int pos0,
+                        float base, char *err, size_t errlen) {
+    if (!ops_stream()) return -1;
+    if (T < 0 || n_heads < 0 || n_rot < 2 || n_rot % 2 || pos0 < 0 || head_stride < n_rot) {
+        snprintf(err, errlen, "rope: bad shape (T=%d, heads=%d, n_rot=%d, pos0=%d)", T, n_heads, n_rot, pos0);
+        return -1;
+    }
+    if (!T || !n_heads) return 0;
+    const int half = n_rot / 2;
+    std::vector<float2> cs((size_t)T * half);
+    rope_table(pos0, T, n_rot, base, cs.data());
+    float2 *d = nullptr;
+    if (hipMalloc(&d, cs.size() * sizeof(float2)) != hipSuccess) { snprintf(err, errlen, "hipMalloc failed"); return -1; }
+    int rc = 0;
+    if (hipMemcpy(d, cs.data(), cs.size() * sizeof(float2), hipMemcpyHostToDevice) != hipSuccess ||
+        rope_launch(x, d, T, n_heads, tok_stride, head_stride, n_rot, g_stream)) {
+        snprintf(err, errlen, "rope launch failed");
+        rc = -1;
+    } else {
+        rc = ops_done(err, errlen);
+    }
+    (void)hipFree(d);
+    return rc;
+}
+
+extern "C" int xjh_conv_silu(float *x, float *state, const float *w, int C, int K, int T, float *ck, int ck_n,
+                             char *err, size_t errlen) {
+    if (!ops_stream()) return -1;
+    if (conv_silu_launch(x, state, w, C, K, T, ck, ck_n, g_stream)) {
+        snprintf(err, errlen, "conv_silu: bad shape (C=%d, K=%d (2..8), T=%d, ck_n=%d)", C, K, T, ck_n);
+        return -1;
+    }
+    return ops_done(err, errlen);
+}
+
+extern "C" int xjh_attn_decode(int T, int H, int Hkv, int D, int n_rot, float rope_base, float eps, int n_past, int n_ctx,
+                               const float *qg, const float *k, const float *v, const float *q_norm, const float *k_norm,
+                               uint16_t *kc, uint16_t *vc, float *out, char *err, size_t errlen) {
+    if (!ops_stream()) return -1;
+    const int G = Hkv > 0 ? H / Hkv : 0;
+    if (T < 1 || Hkv < 1 || H % Hkv || (G != 1 && G != 2 && G != 4 && G != 8) || (D != 64 && D != 128 && D != 256) ||
+        n_rot < 0 || n_rot % 2 || n_rot > D || n_past < 0 || n_past + T > n_ctx || ((uintptr_t)kc | (uintptr_t)vc) & 15) {
+        snprintf(err, errlen, "attn_decode: bad shape or unaligned cache (T=%d H=%d Hkv=%d D=%d n_rot=%d n_past=%d n_ctx=%d)",
+                 T, H, Hkv, D, n_rot, n_past, n_ctx);
+        return -1;
+    }
+    const int half = n_rot / 2 > 0 ? n_rot / 2 : 1;
+    std::vector<float2> cs((size_t)n_ctx * half, float2{1.f, 0.f});
+    rope_table(0, n_ctx, n_rot, rope_base, cs.data());
+    AttnArgs at{};
+    at.n_split = attn_splits(n_ctx);
+    // every region 256-byte aligned (the split kernel reads qr with 16-byte loads)
+    const size_t b_rope = (cs.size() * sizeof(float2) + 255) & ~(size_t)255, b_qr = ((size_t)T * H * D * 4 + 255) & ~(size_t)255,
+                 b_sc = (size_t)T * H * at.n_split * (D + 2) * 4;
+    uint8_t *buf = nullptr;
+    if (hipMalloc(&buf, 256 + b_rope + b_qr + b_sc) != hipSuccess) { snprintf(err, errlen, "hipMalloc failed"); return -1; }
+    int32_t *np = (int32_t *)buf;
+    float2 *rope = (float2 *)(buf + 256);
+    int rc = 0;
+    if (hipMemcpy(np, &n_past, 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(rope, cs.data(), cs.size() * sizeof(float2), hipMemcpyHostToDevice) != hipSuccess) {
+        snprintf(err, errlen, "attn_decode: copy failed");
+        rc = -1;
+    }
+    if (!rc) {
+        at.qg = qg; at.qg_s = 2 * H * D;
+        at.kn = k; at.kn_s = Hkv * D;
+        at.vn = v; at.vn_s = Hkv * D;
+        at.kc = kc; at.vc = vc; at.qnorm_w = q_norm; at.knorm_w = k_norm; at.rope = rope; at.npast = np;
+        at.qr = (float *)(buf + 256 + b_rope);
+        at.scores = (float *)(buf + 256 + b_rope + b_qr);
+        at.out = out;
+        at.T = T; at.H = H; at.Hkv = Hkv; at.D = D; at.n_rot = n_rot; at.n_ctx = n_ctx;
+        at.eps = eps; at.scale = 1.0f / sqrtf((float)D);
+        at.xq = nullptr;
+        if (attn_launch(at, g_stream)) { snprintf(err, errlen, "attn_decode launch failed"); rc = -1; }
+        else rc = ops_done(err, errlen);
+    }
+    (void)hipFree(buf);
+    return rc;
 }
 
 extern "C" int xjh_argmax(const float *x, int n, int T, int32_t *out_host, char *err, size_t errlen) {

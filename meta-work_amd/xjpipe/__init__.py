@@ -163,6 +163,10 @@ def lib():
     _sig(L, "xjh_argmax", I, P, I, I, P, CP, S)
     _sig(L, "xjh_delta_recurrent", I, I, I, I, P, P, P, P, P, F, P, P, CP, S)
     _sig(L, "xjh_delta_chunked", I, I, I, I, I, P, P, P, P, P, F, P, P, CP, S)
+    _sig(L, "xjh_swiglu", I, P, P, I64, CP, S)
+    _sig(L, "xjh_rope", I, P, I, I, I64, I64, I, I, F, CP, S)
+    _sig(L, "xjh_conv_silu", I, P, P, P, I, I, I, P, I, CP, S)
+    _sig(L, "xjh_attn_decode", I, I, I, I, I, I, F, F, I, I, P, P, P, P, P, P, P, P, CP, S)
     _lib = L
     return L
 
@@ -549,6 +553,62 @@ def delta(q, k, v, decay, beta, state, qscale, chunk=0):
                                        err, ERR)
     _check(rc, err, "delta")
     return do.get(np.float32, (T, H, S)), ds.get(np.float32, (H, S, S))
+
+
+def swiglu(g, u):
+    """silu(g) * u on the GPU (float32, any shape)."""
+    g = np.ascontiguousarray(g, np.float32)
+    dg, du = Dev(g), Dev(np.ascontiguousarray(u, np.float32))
+    err = _err()
+    _check(lib().xjh_swiglu(dg.ptr, du.ptr, g.size, err, ERR), err, "swiglu")
+    return dg.get(np.float32, g.shape)
+
+
+def rope(x, n_rot, pos0, base, head_stride=None):
+    """NeoX RoPE on the GPU of x [T][n_heads * head_stride] (the first n_rot
+    elements of each head's head_stride rotated), token t at position pos0 + t."""
+    x = np.ascontiguousarray(x, np.float32)
+    T = x.shape[0]
+    hs = head_stride or x.shape[1]
+    nh = x.shape[1] // hs
+    dx = Dev(x)
+    err = _err()
+    _check(lib().xjh_rope(dx.ptr, T, nh, x.shape[1], hs, n_rot, pos0, base, err, ERR), err, "rope")
+    return dx.get(np.float32, x.shape)
+
+
+def conv_silu(x, w, state, ck_n=0):
+    """Depthwise causal conv + SiLU on the GPU: x [T][C], w [C][K], state [C][K-1].
+    Returns (out, new_state, checkpoints [ck_n][C][K-1])."""
+    x = np.ascontiguousarray(x, np.float32)
+    T, Cn = x.shape
+    K = w.shape[1]
+    dx, dw, ds = Dev(x), Dev(np.ascontiguousarray(w, np.float32)), Dev(np.ascontiguousarray(state, np.float32))
+    dck = Dev(nbytes=max(1, ck_n * Cn * (K - 1) * 4))
+    err = _err()
+    _check(lib().xjh_conv_silu(dx.ptr, ds.ptr, dw.ptr, Cn, K, T, dck.ptr if ck_n else None, ck_n, err, ERR), err,
+           "conv_silu")
+    return (dx.get(np.float32, x.shape), ds.get(np.float32, (Cn, K - 1)),
+            dck.get(np.float32, (ck_n, Cn, K - 1)) if ck_n else None)
+
+
+def attn_decode(qg, k, v, q_norm, k_norm, kc, vc, n_past, n_rot, base, eps):
+    """Gated GQA attention on the GPU for T tokens at n_past.. (the token loop's
+    kernels). qg [T][H][2D], k, v [T][Hkv][D], kc, vc uint16 fp16 bits
+    [n_ctx][Hkv*D] (updated copies are returned). Returns (out [T][H*D], kc, vc)."""
+    qg = np.ascontiguousarray(qg, np.float32)
+    T, H, D2 = qg.shape
+    D = D2 // 2
+    Hkv = k.shape[1]
+    n_ctx = kc.shape[0]
+    dq, dk, dv = Dev(qg), Dev(np.ascontiguousarray(k, np.float32)), Dev(np.ascontiguousarray(v, np.float32))
+    dqn, dkn = Dev(np.ascontiguousarray(q_norm, np.float32)), Dev(np.ascontiguousarray(k_norm, np.float32))
+    dkc, dvc = Dev(np.ascontiguousarray(kc, np.uint16)), Dev(np.ascontiguousarray(vc, np.uint16))
+    do = Dev(nbytes=T * H * D * 4)
+    err = _err()
+    _check(lib().xjh_attn_decode(T, H, Hkv, D, n_rot, base, eps, n_past, n_ctx, dq.ptr, dk.ptr, dv.ptr, dqn.ptr,
+                                 dkn.ptr, dkc.ptr, dvc.ptr, do.ptr, err, ERR), err, "attn_decode")
+    return (do.get(np.float32, (T, H * D)), dkc.get(np.uint16, kc.shape), dvc.get(np.uint16, vc.shape))
 
 
 def device_name():

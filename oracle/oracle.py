@@ -56,6 +56,9 @@ def olib():
         _sig(L, "xjo_greedy", I, C.POINTER(PS), I, P, I, I, P, P, CP, S)
         _sig(L, "xjo_argmax", I, P, I)
         _sig(L, "xjo_delta_recurrent", None, I, I, I, P, P, P, P, P, F, P, P)
+        _sig(L, "xjo_conv_silu", None, I, I, P, P, P)
+        _sig(L, "xjo_swiglu", None, S, P, P)
+        _sig(L, "xjo_attn_decode", None, I, I, I, I, I, F, F, I, I, P, P, P, P, P, P, P, P)
         _sig(L, "xjo_abi_offsets", I, C.POINTER(C.c_long), I)
         _o = L
     return _o
@@ -135,6 +138,44 @@ def rope(v, n_rot, pos, base, ref=False):
     f = rlib().ref_rope if ref else olib().xjo_rope
     f(_ptr(v), n_rot, pos, base)
     return v
+
+
+def swiglu(g, u):
+    g = np.array(g, np.float32)
+    olib().xjo_swiglu(g.size, _ptr(g), _ptr(np.ascontiguousarray(u, np.float32)))
+    return g
+
+
+def conv_silu(x, w, state, ck_n=0):
+    """Tokens of x [T][C] in order through xjo_conv_silu; returns (out, state,
+    the state after each of the first ck_n tokens)."""
+    x = np.array(x, np.float32)
+    st = np.array(state, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    T, Cn = x.shape
+    K = w.shape[1]
+    ck = np.empty((ck_n, Cn, K - 1), np.float32)
+    for t in range(T):
+        olib().xjo_conv_silu(Cn, K, _ptr(x[t]), _ptr(w), _ptr(st))
+        if t < ck_n:
+            ck[t] = st
+    return x, st, ck
+
+
+def attn_decode(qg, k, v, q_norm, k_norm, kc, vc, n_past, n_rot, base, eps, kv_f16=True):
+    """xjo_attn_decode on float caches kc, vc [n_ctx][Hkv*D] (copies updated and
+    returned); qg [T][H][2D], k, v [T][Hkv][D]. Returns (out [T][H*D], kc, vc)."""
+    qg = np.ascontiguousarray(qg, np.float32)
+    T, H, D2 = qg.shape
+    D = D2 // 2
+    Hkv = k.shape[1]
+    k = np.array(k, np.float32)
+    kc, vc = np.array(kc, np.float32), np.array(vc, np.float32)
+    out = np.empty((T, H * D), np.float32)
+    olib().xjo_attn_decode(T, H, Hkv, D, n_rot, base, eps, n_past, int(kv_f16), _ptr(qg), _ptr(k),
+                           _ptr(np.ascontiguousarray(v, np.float32)), _ptr(np.ascontiguousarray(q_norm, np.float32)),
+                           _ptr(np.ascontiguousarray(k_norm, np.float32)), _ptr(kc), _ptr(vc), _ptr(out))
+    return out, kc, vc
 
 
 def delta_recurrent(q, k, v, decay, beta, state, qscale):

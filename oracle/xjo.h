@@ -5,6 +5,8 @@
  *
  *   xjo_f16 / xjo_to_f16 / xjo_dequant_row  <- src/xiaoju-pipe/core/xj_quant.h:9-122
  *   xjo_matmul, xjo_rmsnorm, xjo_rope,       <- src/xiaoju-pipe/core/xj_cpu.c:36-77
+ *   xjo_attn_decode                          <- src/xiaoju-pipe/core/xj_cpu.c:106-147 (attention
+ *                                               after the projections; the oracle stage uses it)
  *   xjo_stage_new (forward/logits/rollback/  <- src/xiaoju-pipe/core/xj_cpu.c:83-418
  *     reset/destroy, embed)
  *   xjo_greedy                               <- src/xiaoju-pipe/core/xj_net.c:532-559 (no-remote
@@ -52,6 +54,16 @@ int xjo_greedy(xj_stage **stages, int n_stages, const int32_t *prompt, int n_pro
 
 /* First index of the maximum (strict >), xj_spec.c:12-16. */
 int xjo_argmax(const float *x, int n);
+
+/* One token of the causal depthwise conv + SiLU (xj_cpu.c:172-182), x and
+ * state [C][KC-1] updated in place. */
+void xjo_conv_silu(int C, int KC, float *x, const float *w, float *state);
+/* g = silu(g) * u (xj_cpu.c:273). */
+void xjo_swiglu(size_t n, float *g, const float *u);
+/* Gated GQA attention after the projections (xj_cpu.c:106-147); see attn_core. */
+void xjo_attn_decode(int T, int H, int Hkv, int D, int n_rot, float base, float eps, int n_past, int kv_f16,
+                     const float *qg, float *k, const float *v, const float *qnw, const float *knw,
+                     float *kc, float *vc, float *att);
 
 void xjo_delta_recurrent(int H, int S, int T, const float *q, const float *k, const float *v,
                          const float *decay, const float *beta, float qscale, float *state, float *out);

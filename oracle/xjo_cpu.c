@@ -5,6 +5,9 @@
  *   xjo_rmsnorm       <- xj_cpu.c:56-61    double sum, x*sc*w
  *   xjo_rope          <- xj_cpu.c:68-77    NeoX pairs (i, i+n_rot/2), theta in fp32
  *   attn_full         <- xj_cpu.c:83-151   gated GQA: q|gate interleaved per head
+ *   xjo_attn_decode   <- xj_cpu.c:106-147  its part after the projections (attn_core)
+ *   xjo_conv_silu     <- xj_cpu.c:172-182  one token of the causal conv + SiLU
+ *   xjo_swiglu        <- xj_cpu.c:273
  *   attn_linear       <- xj_cpu.c:155-223  conv+SiLU, L2(q,k), gated delta rule, gated RMSNorm
  *   ensure_ck         <- xj_cpu.c:228-242
  *   stage_forward     <- xj_cpu.c:244-280
@@ -116,7 +119,73 @@ void xjo_rope(float *v, int n_rot, int pos, float base) {
 
 static const float *F32(const xj_w *w) { return (const float *)w->data; }
 
-static float kv_round(const ostage *o, float v) { return o->kv_f16 ? xjo_f16(xjo_to_f16(v)) : v; }
+
+/* The part of attn_full after the projections (xj_cpu.c:106-147): key
+ * norm + RoPE + store of each new key/value at n_past + t (rounded through
+ * fp16 when kv_f16), then for every token and query head the query norm +
+ * RoPE, softmax(q.K^T * scale) V over positions 0..n_past+t, times
+ * sigmoid(gate). qg [T][H][2D] (q | gate per head), k, v [T][Hkv][D] (k is
+ * normalised and rotated in place), caches [n_ctx][Hkv*D], att [T][H][D]. */
+static void attn_core(int T, int H, int Hkv, int D, int n_rot, float base, float eps, int n_past, int kv_f16,
+                      const float *qg, float *k, const float *v, const float *qnw, const float *knw,
+                      float *kc, float *vc, float *att) {
+    const int nq = 2 * H * D, nk = Hkv * D;
+    const float scale = 1.0f / sqrtf((float)D);
+    /* normalise + rotate the new keys and append the batch to the cache first,
+     * so token t of the batch sees tokens 0..t of it */
+    for (int t = 0; t < T; t++) {
+        const int pos = n_past + t;
+        float *kt = k + (size_t)t * nk;
+        const float *vt = v + (size_t)t * nk;
+        for (int g = 0; g < Hkv; g++) {
+            xjo_rmsnorm(kt + g * D, kt + g * D, knw, D, eps);
+            xjo_rope(kt + g * D, n_rot, pos, base);
+        }
+        float *kd = kc + (size_t)pos * nk, *vd = vc + (size_t)pos * nk;
+        for (int e = 0; e < nk; e++) {
+            kd[e] = kv_f16 ? xjo_f16(xjo_to_f16(kt[e])) : kt[e];
+            vd[e] = kv_f16 ? xjo_f16(xjo_to_f16(vt[e])) : vt[e];
+        }
+    }
+
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int t = 0; t < T; t++) {
+        for (int hh = 0; hh < H; hh++) {
+            const int pos = n_past + t, kvh = hh / (H / Hkv);
+            float q[1024];
+            const float *qr = qg + (size_t)t * nq + (size_t)hh * 2 * D;
+            xjo_rmsnorm(q, qr, qnw, D, eps);
+            xjo_rope(q, n_rot, pos, base);
+            float *sc = malloc(sizeof(float) * (size_t)(pos + 1));
+            float mx = -INFINITY;
+            for (int j = 0; j <= pos; j++) {
+                const float *kj = kc + (size_t)j * nk + (size_t)kvh * D;
+                float dsum = 0;
+                for (int i = 0; i < D; i++) dsum += q[i] * kj[i];
+                sc[j] = dsum * scale;
+                if (sc[j] > mx) mx = sc[j];
+            }
+            double sum = 0;
+            for (int j = 0; j <= pos; j++) { sc[j] = expf(sc[j] - mx); sum += sc[j]; }
+            float *oh = att + (size_t)t * H * D + (size_t)hh * D;
+            for (int i = 0; i < D; i++) oh[i] = 0;
+            for (int j = 0; j <= pos; j++) {
+                const float *vj = vc + (size_t)j * nk + (size_t)kvh * D;
+                const float p = (float)(sc[j] / sum);
+                for (int i = 0; i < D; i++) oh[i] += p * vj[i];
+            }
+            free(sc);
+            const float *gate = qr + D;
+            for (int i = 0; i < D; i++) oh[i] *= sigm(gate[i]);
+        }
+    }
+}
+
+void xjo_attn_decode(int T, int H, int Hkv, int D, int n_rot, float base, float eps, int n_past, int kv_f16,
+                     const float *qg, float *k, const float *v, const float *qnw, const float *knw,
+                     float *kc, float *vc, float *att) {
+    attn_core(T, H, Hkv, D, n_rot, base, eps, n_past, kv_f16, qg, k, v, qnw, knw, kc, vc, att);
+}
 
 static void attn_full(xj_stage *s, ostage *o, int il, const float *h, float *out, int T) {
     const xj_hparams *hp = &s->m->hp;
@@ -141,52 +210,31 @@ static void attn_full(xj_stage *s, ostage *o, int il, const float *h, float *out
         mm(o, &L->wv, h, v, T);
     }
 
-    const float scale = 1.0f / sqrtf((float)D);
-    /* normalise + rotate the new keys and append the batch to the cache first,
-     * so token t of the batch sees tokens 0..t of it */
-    for (int t = 0; t < T; t++) {
-        const int pos = s->n_past + t;
-        float *kt = k + (size_t)t * nk, *vt = v + (size_t)t * nk;
-        for (int g = 0; g < Hkv; g++) {
-            xjo_rmsnorm(kt + g * D, kt + g * D, F32(&L->k_norm), D, hp->eps);
-            xjo_rope(kt + g * D, hp->n_rot, pos, hp->rope_base);
-        }
-        float *kd = st->kc + (size_t)pos * nk, *vd = st->vc + (size_t)pos * nk;
-        for (int e = 0; e < nk; e++) { kd[e] = kv_round(o, kt[e]); vd[e] = kv_round(o, vt[e]); }
-    }
-
-#pragma omp parallel for collapse(2) schedule(static)
-    for (int t = 0; t < T; t++) {
-        for (int hh = 0; hh < H; hh++) {
-            const int pos = s->n_past + t, kvh = hh / (H / Hkv);
-            float q[1024];
-            const float *qr = qg + (size_t)t * nq + (size_t)hh * 2 * D;
-            xjo_rmsnorm(q, qr, F32(&L->q_norm), D, hp->eps);
-            xjo_rope(q, hp->n_rot, pos, hp->rope_base);
-            float *sc = malloc(sizeof(float) * (size_t)(pos + 1));
-            float mx = -INFINITY;
-            for (int j = 0; j <= pos; j++) {
-                const float *kj = st->kc + (size_t)j * nk + (size_t)kvh * D;
-                float dsum = 0;
-                for (int i = 0; i < D; i++) dsum += q[i] * kj[i];
-                sc[j] = dsum * scale;
-                if (sc[j] > mx) mx = sc[j];
-            }
-            double sum = 0;
-            for (int j = 0; j <= pos; j++) { sc[j] = expf(sc[j] - mx); sum += sc[j]; }
-            float *oh = att + (size_t)t * H * D + (size_t)hh * D;
-            for (int i = 0; i < D; i++) oh[i] = 0;
-            for (int j = 0; j <= pos; j++) {
-                const float *vj = st->vc + (size_t)j * nk + (size_t)kvh * D;
-                const float p = (float)(sc[j] / sum);
-                for (int i = 0; i < D; i++) oh[i] += p * vj[i];
-            }
-            free(sc);
-            const float *gate = qr + D;
-            for (int i = 0; i < D; i++) oh[i] *= sigm(gate[i]);
-        }
-    }
+    attn_core(T, H, Hkv, D, hp->n_rot, hp->rope_base, hp->eps, s->n_past, o->kv_f16, qg, k, v, F32(&L->q_norm),
+              F32(&L->k_norm), st->kc, st->vc, att);
     mm(o, &L->wo, att, out, T);
+}
+
+/* Causal depthwise conv of one token + SiLU (xj_cpu.c:172-182): for each of
+ * the C channels the window is the KC-1 stored inputs (state [C][KC-1],
+ * oldest first) followed by x[c]; the state shifts by one and keeps x[c];
+ * x[c] becomes silu(window . w[c][0..KC-1]). */
+void xjo_conv_silu(int C, int KC, float *x, const float *w, float *state) {
+    for (int c = 0; c < C; c++) {
+        float *cs = state + (size_t)c * (KC - 1);
+        const float *wc = w + (size_t)c * KC;
+        float acc = 0;
+        for (int kk = 0; kk < KC - 1; kk++) acc += cs[kk] * wc[kk];
+        acc += x[c] * wc[KC - 1];
+        for (int kk = 0; kk < KC - 2; kk++) cs[kk] = cs[kk + 1];
+        cs[KC - 2] = x[c];
+        x[c] = silu(acc);
+    }
+}
+
+/* g[i] = silu(g[i]) * u[i] (xj_cpu.c:273). */
+void xjo_swiglu(size_t n, float *g, const float *u) {
+    for (size_t i = 0; i < n; i++) g[i] = silu(g[i]) * u[i];
 }
 
 static void attn_linear(xj_stage *s, ostage *o, int il, const float *h, float *out, int T) {
@@ -206,17 +254,7 @@ static void attn_linear(xj_stage *s, ostage *o, int il, const float *h, float *o
 
     for (int t = 0; t < T; t++) {
         float *x = qkv + (size_t)t * CD;
-        /* causal depthwise conv: window = the KC-1 stored inputs + this input */
-        for (int c = 0; c < CD; c++) {
-            float *cs = st->conv + (size_t)c * (KC - 1);
-            const float *wc = cw + (size_t)c * KC;
-            float acc = 0;
-            for (int kk = 0; kk < KC - 1; kk++) acc += cs[kk] * wc[kk];
-            acc += x[c] * wc[KC - 1];
-            for (int kk = 0; kk < KC - 2; kk++) cs[kk] = cs[kk + 1];
-            cs[KC - 2] = x[c];
-            x[c] = silu(acc);
-        }
+        xjo_conv_silu(CD, KC, x, cw, st->conv);
         float *q = x, *k = x + hp->key_dim, *v = x + 2 * hp->key_dim;
         for (int g = 0; g < Hk; g++) {
             xjo_l2norm(q + g * S, S, hp->eps);
@@ -287,7 +325,7 @@ static int stage_forward(xj_stage *s, float *x, int T, char *err, size_t errlen)
         for (int t = 0; t < T; t++) xjo_rmsnorm(o->h + (size_t)t * E, x + (size_t)t * E, F32(&L->post_norm), E, hp->eps);
         mm(o, &L->ffn_gate, o->h, o->g, T);
         mm(o, &L->ffn_up, o->h, o->a, T);
-        for (size_t i = 0; i < (size_t)T * hp->n_ff; i++) o->g[i] = silu(o->g[i]) * o->a[i];
+        xjo_swiglu((size_t)T * hp->n_ff, o->g, o->a);
         mm(o, &L->ffn_down, o->g, o->u, T);
         for (size_t i = 0; i < (size_t)T * E; i++) x[i] += o->u[i];
     }

@@ -1,0 +1,143 @@
+"""Per-op entry points of the gfx950 library against the oracle (same seeded
+inputs): SwiGLU, NeoX RoPE, the causal conv + SiLU (the qkv GEMV's conv
+epilogue run on its own) and gated GQA attention through the token loop's
+attention kernels (fused single-token and kv_store + split paths, more than 64
+splits in the combine).
+
+Bars, written per test: elementwise results within a few float32 roundings
+(the device's expf and the compilers' fused multiply-adds differ from glibc's
+by an ulp or two); copied state (conv windows, fp16 values) bit-exact; fp16
+keys within one fp16 ulp; attention outputs within 1e-5 relative L2.
+"""
+import numpy as np
+import pytest
+
+import oracle as orc
+import xjpipe as xp
+from conftest import rel_l2
+from test_oracle import attn_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _close(got, want, rtol):
+    scale = np.maximum(np.abs(want), np.abs(want).max() * 1e-3)
+    return float(np.max(np.abs(got - want) / scale)) < rtol
+
+
+@pytest.mark.parametrize("n", [1, 255, 100003])
+def test_swiglu_matches_oracle(n):
+    rng = np.random.default_rng(n)
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    assert _close(xp.swiglu(g, u), orc.swiglu(g, u), 1e-6)
+
+
+@pytest.mark.parametrize("n_rot,D,pos0", [(64, 256, 0), (64, 256, 4093), (128, 128, 17)])
+def test_rope_matches_oracle(n_rot, D, pos0):
+    """Rows laid out as the attention queries are ([q(D) | gate(D)] per head):
+    only the first n_rot dims of each head's q rotate; everything else is left
+    bit for bit."""
+    rng = np.random.default_rng(pos0 + n_rot)
+    T, H = 5, 6
+    x = rng.standard_normal((T, H * 2 * D)).astype(np.float32)
+    got = xp.rope(x, n_rot, pos0, 1e7, head_stride=2 * D)
+    want = x.copy().reshape(T, H, 2 * D)
+    for t in range(T):
+        for h in range(H):
+            want[t, h, :D] = orc.rope(want[t, h, :D], n_rot, pos0 + t, 1e7)
+    want = want.reshape(T, -1)
+    assert _close(got, want, 1e-6)
+    rot = np.zeros((H, 2 * D), bool)
+    rot[:, :n_rot] = True
+    keep = ~np.tile(rot.reshape(-1), (T, 1))
+    assert np.array_equal(got[keep], x[keep])
+
+
+@pytest.mark.parametrize("K,Cn,T,ck_n", [(4, 8192, 1, 0), (4, 6144, 5, 4), (2, 1000, 3, 3), (6, 777, 17, 16)])
+def test_conv_silu_matches_oracle(K, Cn, T, ck_n):
+    rng = np.random.default_rng(K * 1000 + T)
+    x = rng.standard_normal((T, Cn)).astype(np.float32)
+    w = rng.standard_normal((Cn, K)).astype(np.float32)
+    st = rng.standard_normal((Cn, K - 1)).astype(np.float32)
+    got, gst, gck = xp.conv_silu(x, w, st, ck_n)
+    want, wst, wck = orc.conv_silu(x, w, st, ck_n)
+    # the K-term sums may cancel: bound the difference by the float32 rounding of
+    # a K-term dot product, K * eps * sum_k |w_k x_k| (silu' < 1.1), plus the
+    # rounding of silu itself
+    seq = np.abs(np.concatenate([st.T, x], axis=0)).astype(np.float64)
+    mag = np.stack([np.einsum("kc,ck->c", seq[t:t + K], np.abs(w).astype(np.float64)) for t in range(T)])
+    bound = 1.1 * K * 2.0**-23 * mag + 4 * 2.0**-24 * np.abs(want)
+    assert np.all(np.abs(got.astype(np.float64) - want) <= bound)
+    assert np.array_equal(gst, wst)
+    if ck_n:
+        assert np.array_equal(gck, wck)
+
+
+def test_conv_silu_state_carries_across_calls():
+    """Two calls of 3 and 4 tokens equal one call of 7."""
+    rng = np.random.default_rng(5)
+    K, Cn = 4, 512
+    x = rng.standard_normal((7, Cn)).astype(np.float32)
+    w = rng.standard_normal((Cn, K)).astype(np.float32)
+    st = np.zeros((Cn, K - 1), np.float32)
+    a, sa, _ = xp.conv_silu(x[:3], w, st)
+    b, sb, _ = xp.conv_silu(x[3:], w, sa)
+    c, sc, _ = xp.conv_silu(x, w, st)
+    assert np.array_equal(np.concatenate([a, b]), c) and np.array_equal(sb, sc)
+
+
+ATTN_CASES = [
+    # T, H, Hkv, D, n_rot, n_past, n_ctx
+    (1, 16, 4, 256, 64, 0, 64),        # first token
+    (1, 16, 4, 256, 64, 777, 1024),    # fused single-token path
+    (1, 8, 2, 256, 64, 2500, 4096),    # 79 splits (> 64) in the combine
+    (4, 16, 4, 256, 64, 2600, 4096),   # kv_store + split path
+    (3, 8, 2, 128, 128, 31, 128),      # the batch crosses a split boundary
+    (5, 8, 8, 64, 32, 60, 96),         # G = 1
+    (2, 8, 1, 64, 64, 10, 64),         # G = 8
+]
+
+
+@pytest.mark.parametrize("T,H,Hkv,D,n_rot,n_past,n_ctx", ATTN_CASES)
+def test_attn_decode_matches_oracle(T, H, Hkv, D, n_rot, n_past, n_ctx):
+    print(f"attn_decode T={T} H={H} Hkv={Hkv} D={D} n_past={n_past} n_ctx={n_ctx}", flush=True)
+    qg, k, v, qn, kn, kc, vc = attn_inputs(T, H, Hkv, D, n_past, n_ctx, 50 + n_past)
+    base, eps = 1e7, 1e-6
+    got, gkc, gvc = xp.attn_decode(qg, k, v, qn, kn, kc, vc, n_past, n_rot, base, eps)
+    f = lambda b: b.view(np.float16).astype(np.float32)
+    want, wkc, wvc = orc.attn_decode(qg, k, v, qn, kn, f(kc), f(vc), n_past, n_rot, base, eps)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, want) < 1e-5
+    new = slice(n_past, n_past + T)
+    assert np.array_equal(gvc[new], wvc[new].astype(np.float16).view(np.uint16))
+    kd = np.abs(gkc[new].astype(np.int32) - wkc[new].astype(np.float16).view(np.uint16).astype(np.int32))
+    assert kd.max() <= 1
+    # nothing else in the caches changed
+    assert np.array_equal(gkc[:n_past], kc[:n_past]) and np.array_equal(gkc[n_past + T:], kc[n_past + T:])
+    assert np.array_equal(gvc[:n_past], vc[:n_past]) and np.array_equal(gvc[n_past + T:], vc[n_past + T:])
+
+
+def test_attn_decode_token_by_token_equals_batch():
+    """Three single-token calls leave the same caches (bit for bit) and the same
+    outputs (to the fp32 reassociation of the two launch forms) as one call of 3."""
+    T, H, Hkv, D, n_past, n_ctx = 3, 16, 4, 256, 100, 256
+    qg, k, v, qn, kn, kc, vc = attn_inputs(T, H, Hkv, D, n_past, n_ctx, 77)
+    ob, kcb, vcb = xp.attn_decode(qg, k, v, qn, kn, kc, vc, n_past, 64, 1e7, 1e-6)
+    kcs, vcs, outs = kc, vc, []
+    for t in range(T):
+        o, kcs, vcs = xp.attn_decode(qg[t:t + 1], k[t:t + 1], v[t:t + 1], qn, kn, kcs, vcs, n_past + t, 64, 1e7, 1e-6)
+        outs.append(o)
+    assert np.array_equal(kcs, kcb) and np.array_equal(vcs, vcb)
+    assert rel_l2(np.concatenate(outs), ob) < 1e-6
+
+
+def test_per_op_entries_reject_bad_shapes():
+    with pytest.raises(xp.XjError):
+        xp.conv_silu(np.zeros((2, 8), np.float32), np.zeros((8, 9), np.float32), np.zeros((8, 8), np.float32))
+    qg, k, v, qn, kn, kc, vc = attn_inputs(2, 8, 2, 64, 62, 64, 1)
+    with pytest.raises(xp.XjError):   # n_past + T > n_ctx
+        xp.attn_decode(qg, k, v, qn, kn, kc, vc, 63, 64, 1e4, 1e-6)
+    qg, k, v, qn, kn, kc, vc = attn_inputs(1, 6, 2, 64, 0, 8, 1)
+    with pytest.raises(xp.XjError):   # H / Hkv = 3
+        xp.attn_decode(qg, k, v, qn, kn, kc, vc, 0, 64, 1e4, 1e-6)

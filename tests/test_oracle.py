@@ -8,7 +8,10 @@ compared with it:
     (tests/golden/*.npz|json, see gen_golden.py);
   * live bit-for-bit comparison with that reference build where it exists
     (oracle/_ref), including an -march=native build against the portable one;
-  * invariants the mathematics fixes for the delta rule.
+  * invariants the mathematics fixes for the delta rule;
+  * float64 brute force from the definitions for the per-op restatements
+    (SwiGLU, the causal conv + SiLU, gated GQA attention with its fp16 cache),
+    plus the closed form of attention over a single position.
 """
 import json
 import os
@@ -303,3 +306,128 @@ def test_kv_f16_cache_rounds_only_the_cache(tiny_path):
     a = orc.CpuStage(m.ptr, 0, L, 64, 16, True, kv_f16=False).forward(x.copy())
     b = orc.CpuStage(m.ptr, 0, L, 64, 16, True, kv_f16=True).forward(x.copy())
     assert 0 < rel_l2(b, a) < 5e-3
+
+
+# ------------------------------------------- per-op restatements, brute force --
+
+def _silu(x):
+    return x / (1.0 + np.exp(-x))
+
+
+def test_swiglu_matches_definition():
+    rng = np.random.default_rng(20)
+    g = (rng.standard_normal(4099) * 4).astype(np.float32)
+    u = rng.standard_normal(4099).astype(np.float32)
+    got = orc.swiglu(g, u)
+    want = _silu(g.astype(np.float64)) * u
+    assert np.max(np.abs(got - want) / (np.abs(want) + 1e-30)) < 1e-5
+
+
+@pytest.mark.parametrize("K", [2, 4, 6])
+def test_conv_silu_matches_sliding_window(K):
+    """out[t][c] = silu(sum_k w[c][k] * seq[t + k][c]) over seq = the K-1 stored
+    inputs followed by the new ones; the state keeps the last K-1 inputs and
+    checkpoint t is the state after token t."""
+    rng = np.random.default_rng(21 + K)
+    T, Cn = 9, 37
+    x = rng.standard_normal((T, Cn)).astype(np.float32)
+    w = rng.standard_normal((Cn, K)).astype(np.float32)
+    st = rng.standard_normal((Cn, K - 1)).astype(np.float32)
+    out, st2, ck = orc.conv_silu(x, w, st, ck_n=T - 1)
+    seq = np.concatenate([st.T, x], axis=0).astype(np.float64)   # [K-1+T][C]
+    want = np.stack([_silu(np.einsum("kc,ck->c", seq[t:t + K], w.astype(np.float64))) for t in range(T)])
+    assert np.max(np.abs(out - want)) < 1e-5
+    assert np.array_equal(st2, seq[T:T + K - 1].T.astype(np.float32))
+    for t in range(T - 1):
+        assert np.array_equal(ck[t], seq[t + 1:t + K].T.astype(np.float32))
+
+
+def _np_rms(x, w, eps):
+    return x / np.sqrt(np.mean(x * x) + eps) * w
+
+
+def _np_rope(x, n_rot, pos, base):
+    """NeoX RoPE with the angle formed in float32 as the reference does
+    (theta = pos * powf(base, -2i/n_rot)), the rotation in float64."""
+    x = x.copy()
+    half = n_rot // 2
+    i = np.arange(half, dtype=np.float32)
+    inv = np.power(np.float32(base), np.float32(-2.0) * i / np.float32(n_rot), dtype=np.float32)
+    th = (np.float32(pos) * inv).astype(np.float64)
+    c, s = np.cos(th), np.sin(th)
+    x0, x1 = x[:half].copy(), x[half:n_rot].copy()
+    x[:half] = x0 * c - x1 * s
+    x[half:n_rot] = x0 * s + x1 * c
+    return x
+
+
+def np_attn_decode(qg, k, v, qn, kn, kc, vc, n_past, n_rot, base, eps):
+    """Gated GQA attention from its definition in float64, with the new keys and
+    values rounded to fp16 in the cache."""
+    T, H, D2 = qg.shape
+    D, Hkv = D2 // 2, k.shape[1]
+    kc, vc = kc.astype(np.float64), vc.astype(np.float64)
+    for t in range(T):
+        pos = n_past + t
+        for g in range(Hkv):
+            kk = _np_rope(_np_rms(k[t, g].astype(np.float64), kn, eps), n_rot, pos, base)
+            kc[pos, g * D:(g + 1) * D] = kk.astype(np.float32).astype(np.float16)
+            vc[pos, g * D:(g + 1) * D] = v[t, g].astype(np.float16)
+    out = np.zeros((T, H * D))
+    for t in range(T):
+        pos = n_past + t
+        for h in range(H):
+            g = h // (H // Hkv)
+            q = _np_rope(_np_rms(qg[t, h, :D].astype(np.float64), qn, eps), n_rot, pos, base)
+            s = kc[:pos + 1, g * D:(g + 1) * D] @ q / np.sqrt(D)
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            out[t, h * D:(h + 1) * D] = (p @ vc[:pos + 1, g * D:(g + 1) * D]) / (1.0 + np.exp(-qg[t, h, D:].astype(np.float64)))
+    return out, kc, vc
+
+
+def attn_inputs(T, H, Hkv, D, n_past, n_ctx, seed):
+    """Seeded inputs for one attention call: the cache below n_past holds fp16
+    values; positions at and past n_past hold 0x7E00 (a NaN) so a read of an
+    unwritten slot shows."""
+    rng = np.random.default_rng(seed)
+    qg = rng.standard_normal((T, H, 2 * D)).astype(np.float32)
+    k = rng.standard_normal((T, Hkv, D)).astype(np.float32)
+    v = rng.standard_normal((T, Hkv, D)).astype(np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    kc = np.full((n_ctx, Hkv * D), 0x7E00, np.uint16)
+    vc = np.full((n_ctx, Hkv * D), 0x7E00, np.uint16)
+    kc[:n_past] = (rng.standard_normal((n_past, Hkv * D)) * 2).astype(np.float16).view(np.uint16)
+    vc[:n_past] = rng.standard_normal((n_past, Hkv * D)).astype(np.float16).view(np.uint16)
+    return qg, k, v, qn, kn, kc, vc
+
+
+@pytest.mark.parametrize("T,H,Hkv,D,n_rot,n_past", [(1, 4, 4, 64, 64, 0), (3, 8, 2, 64, 32, 40), (2, 8, 1, 128, 64, 70)])
+def test_attn_decode_matches_definition(T, H, Hkv, D, n_rot, n_past):
+    n_ctx = n_past + T + 3
+    qg, k, v, qn, kn, kc, vc = attn_inputs(T, H, Hkv, D, n_past, n_ctx, 30 + T)
+    f = lambda b: b.view(np.float16).astype(np.float32)
+    out, kc2, vc2 = orc.attn_decode(qg, k, v, qn, kn, f(kc), f(vc), n_past, n_rot, 1e6, 1e-6)
+    want, wkc, wvc = np_attn_decode(qg, k, v, qn, kn, f(kc), f(vc), n_past, n_rot, 1e6, 1e-6)
+    assert rel_l2(out, want) < 1e-4
+    new = slice(n_past, n_past + T)
+    assert np.array_equal(vc2[new], wvc[new].astype(np.float32))
+    # keys: the same fp16 value unless float32 and float64 round across a half-way point
+    kd = np.abs(kc2[new].astype(np.float16).view(np.uint16).astype(np.int32) -
+                wkc[new].astype(np.float16).view(np.uint16).astype(np.int32))
+    assert kd.max() <= 1 and np.mean(kd) < 0.01
+    assert np.array_equal(kc2[:n_past], f(kc)[:n_past])
+
+
+def test_attn_decode_single_position_returns_gated_value():
+    """At position 0 the softmax has one term: out = fp16(v) * sigmoid(gate) for
+    every query head of the kv head, whatever q and k are."""
+    T, H, Hkv, D = 1, 4, 2, 64
+    qg, k, v, qn, kn, kc, vc = attn_inputs(T, H, Hkv, D, 0, 4, 40)
+    f = lambda b: b.view(np.float16).astype(np.float32)
+    out, _, _ = orc.attn_decode(qg, k, v, qn, kn, f(kc), f(vc), 0, D, 1e4, 1e-6)
+    for h in range(H):
+        g = h // (H // Hkv)
+        want = v[0, g].astype(np.float16).astype(np.float64) / (1 + np.exp(-qg[0, h, D:].astype(np.float64)))
+        assert rel_l2(out[0, h * D:(h + 1) * D], want) < 1e-6
