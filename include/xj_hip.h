@@ -223,6 +223,22 @@ int xjh_attn_decode(int T, int H, int Hkv, int D, int n_rot, float rope_base, fl
                     int n_ctx, const float *qg, const float *k, const float *v, const float *q_norm,
                     const float *k_norm, uint16_t *kc, uint16_t *vc, float *out,
                     char *err, size_t errlen);
+/* T tokens of the DeltaNet recurrence after the conv, through the token
+ * loop's own kernel: per token, q and k of each of the Hk key heads (at
+ * qkv[t*qkv_stride + hk*S] and + k_off) are L2-normalised (double sum,
+ * x / sqrt(sum + eps)), then value head hv (key head hv % Hk, values at
+ * + v_off + hv*S) takes the gated delta rule with b = sigmoid(beta_raw[t][hv]),
+ * decay exp(softplus(alpha_raw[t][hv] + dt[hv]) * A[hv]); out [T][Hv*S] =
+ * (S_j . q) * qscale (before the gated norm). state [Hv][S][S] ([value j][key
+ * i]) is updated; ck [ck_n][Hv][S][S] receives the state after each of the
+ * first ck_n tokens (ck_n <= T). S in {64, 128}; state and ck 16-byte aligned.
+ * Replaces: src/xiaoju-pipe/metal/xj_kernels.metal:552-589 (xj_delta_net,
+ * with the L2 norms of xj_norm mode 1 applied inside); CPU form
+ * xj_cpu.c:183-213, :218. */
+int xjh_delta_step(const float *qkv, int qkv_stride, int k_off, int v_off, const float *beta_raw,
+                   const float *alpha_raw, const float *dt, const float *A, int Hk, int Hv, int S, int T,
+                   float eps, float qscale, float *state, float *out, float *ck, int ck_n,
+                   char *err, size_t errlen);
 /* First index of the maximum of each of T rows of n floats. */
 int xjh_argmax(const float *x, int n, int T, int32_t *out_host, char *err, size_t errlen);
 /* Gated delta rule (standalone, decay and beta given per token and head):

@@ -1271,6 +1271,30 @@ extern "C" int xjh_attn_decode(int T, int H, int Hkv, int D, int n_rot, float ro
     return rc;
 }
 
+extern "C" int xjh_delta_step(const float *qkv, int qkv_stride, int k_off, int v_off, const float *beta_raw,
+                              const float *alpha_raw, const float *dt, const float *A, int Hk, int Hv, int S, int T,
+                              float eps, float qscale, float *state, float *out, float *ck, int ck_n, char *err,
+                              size_t errlen) {
+    if (!ops_stream()) return -1;
+    if ((S != 64 && S != 128) || Hk < 1 || Hv < 1 || T < 1 || ck_n < 0 || ck_n > T || (ck_n && !ck) ||
+        ((uintptr_t)state | (uintptr_t)ck) & 15) {
+        snprintf(err, errlen, "delta_step: bad shape or unaligned state (S=%d (64|128), Hk=%d, Hv=%d, T=%d, ck_n=%d)", S,
+                 Hk, Hv, T, ck_n);
+        return -1;
+    }
+    DeltaArgs d{};
+    d.qkv = qkv; d.qkv_s = qkv_stride; d.k_off = k_off; d.v_off = v_off;
+    d.beta = beta_raw; d.beta_s = Hv; d.alpha = alpha_raw; d.alpha_s = Hv;
+    d.dt = dt; d.A = A; d.state = state; d.ck = ck; d.out = out; d.out_s = Hv * S;
+    d.T = T; d.Hk = Hk; d.Hv = Hv; d.S = S; d.keep_n = ck_n; d.eps = eps; d.qscale = qscale;
+    // the token loop's default form (32 value rows per work-group); XJ_DELTA_SPLIT=0
+    // selects one work-group per value head, read on every call
+    const char *e = getenv("XJ_DELTA_SPLIT");
+    d.split = e == nullptr || atoi(e) != 0;
+    if (delta_launch(d, g_stream)) { snprintf(err, errlen, "delta_step launch failed"); return -1; }
+    return ops_done(err, errlen);
+}
+
 extern "C" int xjh_argmax(const float *x, int n, int T, int32_t *out_host, char *err, size_t errlen) {
     if (!ops_stream()) return -1;
     int32_t *d = nullptr;

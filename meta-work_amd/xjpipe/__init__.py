@@ -164,6 +164,7 @@ def lib():
     _sig(L, "xjh_delta_recurrent", I, I, I, I, P, P, P, P, P, F, P, P, CP, S)
     _sig(L, "xjh_delta_chunked", I, I, I, I, I, P, P, P, P, P, F, P, P, CP, S)
     _sig(L, "xjh_swiglu", I, P, P, I64, CP, S)
+    _sig(L, "xjh_delta_step", I, P, I, I, I, P, P, P, P, I, I, I, I, F, F, P, P, P, I, CP, S)
     _sig(L, "xjh_rope", I, P, I, I, I64, I64, I, I, F, CP, S)
     _sig(L, "xjh_conv_silu", I, P, P, P, I, I, I, P, I, CP, S)
     _sig(L, "xjh_attn_decode", I, I, I, I, I, I, F, F, I, I, P, P, P, P, P, P, P, P, CP, S)
@@ -609,6 +610,22 @@ def attn_decode(qg, k, v, q_norm, k_norm, kc, vc, n_past, n_rot, base, eps):
     _check(lib().xjh_attn_decode(T, H, Hkv, D, n_rot, base, eps, n_past, n_ctx, dq.ptr, dk.ptr, dv.ptr, dqn.ptr,
                                  dkn.ptr, dkc.ptr, dvc.ptr, do.ptr, err, ERR), err, "attn_decode")
     return (do.get(np.float32, (T, H * D)), dkc.get(np.uint16, kc.shape), dvc.get(np.uint16, vc.shape))
+
+
+def delta_step(qkv, k_off, v_off, beta_raw, alpha_raw, dt, A, Hk, Hv, S, eps, qscale, state, ck_n=0):
+    """DeltaNet recurrence on the GPU (the token loop's kernel) for the T rows of
+    qkv [T][stride] (after the conv). Returns (out [T][Hv*S], state, checkpoints)."""
+    qkv = np.ascontiguousarray(qkv, np.float32)
+    T = qkv.shape[0]
+    dq, db, da = Dev(qkv), Dev(np.ascontiguousarray(beta_raw, np.float32)), Dev(np.ascontiguousarray(alpha_raw, np.float32))
+    ddt, dA = Dev(np.ascontiguousarray(dt, np.float32)), Dev(np.ascontiguousarray(A, np.float32))
+    ds, do = Dev(np.ascontiguousarray(state, np.float32)), Dev(nbytes=T * Hv * S * 4)
+    dck = Dev(nbytes=max(1, ck_n * Hv * S * S * 4))
+    err = _err()
+    _check(lib().xjh_delta_step(dq.ptr, qkv.shape[1], k_off, v_off, db.ptr, da.ptr, ddt.ptr, dA.ptr, Hk, Hv, S, T, eps,
+                                qscale, ds.ptr, do.ptr, dck.ptr if ck_n else None, ck_n, err, ERR), err, "delta_step")
+    return (do.get(np.float32, (T, Hv * S)), ds.get(np.float32, (Hv, S, S)),
+            dck.get(np.float32, (ck_n, Hv, S, S)) if ck_n else None)
 
 
 def device_name():

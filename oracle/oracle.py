@@ -58,6 +58,7 @@ def olib():
         _sig(L, "xjo_delta_recurrent", None, I, I, I, P, P, P, P, P, F, P, P)
         _sig(L, "xjo_conv_silu", None, I, I, P, P, P)
         _sig(L, "xjo_swiglu", None, S, P, P)
+        _sig(L, "xjo_delta_step", None, I, I, I, F, F, P, P, P, P, P, P, P, P, P, P)
         _sig(L, "xjo_attn_decode", None, I, I, I, I, I, F, F, I, I, P, P, P, P, P, P, P, P)
         _sig(L, "xjo_abi_offsets", I, C.POINTER(C.c_long), I)
         _o = L
@@ -176,6 +177,25 @@ def attn_decode(qg, k, v, q_norm, k_norm, kc, vc, n_past, n_rot, base, eps, kv_f
                            _ptr(np.ascontiguousarray(v, np.float32)), _ptr(np.ascontiguousarray(q_norm, np.float32)),
                            _ptr(np.ascontiguousarray(k_norm, np.float32)), _ptr(kc), _ptr(vc), _ptr(out))
     return out, kc, vc
+
+
+def delta_step(qkv, k_off, v_off, beta_raw, alpha_raw, dt, A, Hk, Hv, S, eps, qscale, state, ck_n=0):
+    """Tokens of qkv [T][stride] in order through xjo_delta_step; returns (out
+    [T][Hv*S], state, the state after each of the first ck_n tokens)."""
+    qkv = np.array(qkv, np.float32)
+    T = qkv.shape[0]
+    st = np.array(state, np.float32)
+    beta_raw, alpha_raw = np.ascontiguousarray(beta_raw, np.float32), np.ascontiguousarray(alpha_raw, np.float32)
+    dt, A = np.ascontiguousarray(dt, np.float32), np.ascontiguousarray(A, np.float32)
+    out = np.empty((T, Hv * S), np.float32)
+    ck = np.empty((ck_n, Hv, S, S), np.float32)
+    for t in range(T):
+        r = qkv[t]
+        base = r.ctypes.data
+        olib().xjo_delta_step(Hk, Hv, S, eps, qscale, C.c_void_p(base), C.c_void_p(base + 4 * k_off),
+                              C.c_void_p(base + 4 * v_off), _ptr(beta_raw[t]), _ptr(alpha_raw[t]), _ptr(dt), _ptr(A),
+                              _ptr(st), _ptr(out[t]), _ptr(ck[t]) if t < ck_n else None)
+    return out, st, ck
 
 
 def delta_recurrent(q, k, v, decay, beta, state, qscale):

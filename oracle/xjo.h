@@ -58,6 +58,11 @@ int xjo_argmax(const float *x, int n);
 /* One token of the causal depthwise conv + SiLU (xj_cpu.c:172-182), x and
  * state [C][KC-1] updated in place. */
 void xjo_conv_silu(int C, int KC, float *x, const float *w, float *state);
+/* One token of L2 norms + the gated delta rule over all value heads
+ * (xj_cpu.c:183-213); q, k normalised in place, ck may be NULL. */
+void xjo_delta_step(int Hk, int Hv, int S, float eps, float qscale, float *q, float *k, const float *v,
+                    const float *beta_raw, const float *alpha_raw, const float *dt, const float *A, float *state,
+                    float *out, float *ck);
 /* g = silu(g) * u (xj_cpu.c:273). */
 void xjo_swiglu(size_t n, float *g, const float *u);
 /* Gated GQA attention after the projections (xj_cpu.c:106-147); see attn_core. */

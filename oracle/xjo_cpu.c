@@ -8,6 +8,7 @@
  *   xjo_attn_decode   <- xj_cpu.c:106-147  its part after the projections (attn_core)
  *   xjo_conv_silu     <- xj_cpu.c:172-182  one token of the causal conv + SiLU
  *   xjo_swiglu        <- xj_cpu.c:273
+ *   xjo_delta_step    <- xj_cpu.c:183-213  one token of L2 norms + the gated delta rule
  *   attn_linear       <- xj_cpu.c:155-223  conv+SiLU, L2(q,k), gated delta rule, gated RMSNorm
  *   ensure_ck         <- xj_cpu.c:228-242
  *   stage_forward     <- xj_cpu.c:244-280
@@ -232,6 +233,43 @@ void xjo_conv_silu(int C, int KC, float *x, const float *w, float *state) {
     }
 }
 
+/* One token of the gated delta rule over all value heads (xj_cpu.c:183-213,
+ * after the conv): q and k of every key head L2-normalised in place
+ * (xj_cpu.c:185-193), then value head hv (key head hv % Hk) with
+ * b = sigmoid(beta_raw[hv]), eg = exp(softplus(alpha_raw[hv] + dt[hv]) * A[hv]):
+ *   row_j <- row_j * eg; delta_j = (v_j - row_j . k) * b;
+ *   row_j <- row_j + k * delta_j; out_j = (row_j . q) * qscale
+ * over the state [Hv][S (value j)][S (key i)]. ck (may be NULL) receives the
+ * state after the token. */
+void xjo_delta_step(int Hk, int Hv, int S, float eps, float qscale, float *q, float *k, const float *v,
+                    const float *beta_raw, const float *alpha_raw, const float *dt, const float *A, float *state,
+                    float *out, float *ck) {
+    for (int g = 0; g < Hk; g++) {
+        xjo_l2norm(q + g * S, S, eps);
+        xjo_l2norm(k + g * S, S, eps);
+    }
+#pragma omp parallel for schedule(static)
+    for (int hv = 0; hv < Hv; hv++) {
+        const int hk = hv % Hk;
+        const float *qh = q + hk * S, *kh = k + hk * S, *vh = v + hv * S;
+        const float b = sigm(beta_raw[hv]);
+        const float g = softplus(alpha_raw[hv] + dt[hv]) * A[hv];
+        const float eg = expf(g);
+        float *M = state + (size_t)hv * S * S;
+        float *oh = out + hv * S;
+        for (int j = 0; j < S; j++) {
+            float *row = M + (size_t)j * S;
+            float sk = 0;
+            for (int i = 0; i < S; i++) { row[i] *= eg; sk += row[i] * kh[i]; }
+            const float delta = (vh[j] - sk) * b;
+            float acc = 0;
+            for (int i = 0; i < S; i++) { row[i] += kh[i] * delta; acc += row[i] * qh[i]; }
+            oh[j] = acc * qscale;
+        }
+        if (ck) memcpy(ck + (size_t)hv * S * S, M, sizeof(float) * S * S);
+    }
+}
+
 /* g[i] = silu(g[i]) * u[i] (xj_cpu.c:273). */
 void xjo_swiglu(size_t n, float *g, const float *u) {
     for (size_t i = 0; i < n; i++) g[i] = silu(g[i]) * u[i];
@@ -255,35 +293,16 @@ static void attn_linear(xj_stage *s, ostage *o, int il, const float *h, float *o
     for (int t = 0; t < T; t++) {
         float *x = qkv + (size_t)t * CD;
         xjo_conv_silu(CD, KC, x, cw, st->conv);
-        float *q = x, *k = x + hp->key_dim, *v = x + 2 * hp->key_dim;
-        for (int g = 0; g < Hk; g++) {
-            xjo_l2norm(q + g * S, S, hp->eps);
-            xjo_l2norm(k + g * S, S, hp->eps);
-        }
         float *ot = ob + (size_t)t * hp->d_inner;
         const int ck = s->keep && t < T - 1;
+        xjo_delta_step(Hk, Hv, S, hp->eps, qscale, x, x + hp->key_dim, x + 2 * hp->key_dim, beta + (size_t)t * Hv,
+                       alpha + (size_t)t * Hv, dt, A, st->ssm, ot, ck ? st->ck_ssm + (size_t)t * Hv * S * S : NULL);
 #pragma omp parallel for schedule(static)
         for (int hv = 0; hv < Hv; hv++) {
-            const int hk = hv % Hk;
-            const float *qh = q + hk * S, *kh = k + hk * S, *vh = v + hv * S;
-            const float b = sigm(beta[(size_t)t * Hv + hv]);
-            const float g = softplus(alpha[(size_t)t * Hv + hv] + dt[hv]) * A[hv];
-            const float eg = expf(g);
-            float *M = st->ssm + (size_t)hv * S * S;
             float *oh = ot + hv * S;
-            for (int j = 0; j < S; j++) {
-                float *row = M + (size_t)j * S;
-                float sk = 0;
-                for (int i = 0; i < S; i++) { row[i] *= eg; sk += row[i] * kh[i]; }
-                const float delta = (vh[j] - sk) * b;
-                float acc = 0;
-                for (int i = 0; i < S; i++) { row[i] += kh[i] * delta; acc += row[i] * qh[i]; }
-                oh[j] = acc * qscale;
-            }
             const float *zh = z + (size_t)t * hp->d_inner + hv * S;
             xjo_rmsnorm(oh, oh, nw, S, hp->eps);
             for (int j = 0; j < S; j++) oh[j] *= silu(zh[j]);
-            if (ck) memcpy(st->ck_ssm + ((size_t)t * Hv + hv) * S * S, M, sizeof(float) * S * S);
         }
         if (ck) memcpy(st->ck_conv + (size_t)t * CD * (KC - 1), st->conv, sizeof(float) * CD * (KC - 1));
     }

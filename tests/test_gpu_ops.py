@@ -1,8 +1,9 @@
 """Per-op entry points of the gfx950 library against the oracle (same seeded
 inputs): SwiGLU, NeoX RoPE, the causal conv + SiLU (the qkv GEMV's conv
-epilogue run on its own) and gated GQA attention through the token loop's
+epilogue run on its own), gated GQA attention through the token loop's
 attention kernels (fused single-token and kv_store + split paths, more than 64
-splits in the combine).
+splits in the combine) and the DeltaNet step through both forms of the token
+loop's recurrence kernel.
 
 Bars, written per test: elementwise results within a few float32 roundings
 (the device's expf and the compilers' fused multiply-adds differ from glibc's
@@ -141,3 +142,38 @@ def test_per_op_entries_reject_bad_shapes():
     qg, k, v, qn, kn, kc, vc = attn_inputs(1, 6, 2, 64, 0, 8, 1)
     with pytest.raises(xp.XjError):   # H / Hkv = 3
         xp.attn_decode(qg, k, v, qn, kn, kc, vc, 0, 64, 1e4, 1e-6)
+
+
+@pytest.mark.parametrize("split", ["1", "0"])
+@pytest.mark.parametrize("T,Hk,Hv,S,ck_n", [(1, 16, 32, 128, 0), (5, 16, 32, 128, 4), (9, 4, 8, 64, 9), (2, 2, 6, 128, 1)])
+def test_delta_step_matches_oracle(monkeypatch, split, T, Hk, Hv, S, ck_n):
+    """Both forms of the token loop's DeltaNet kernel (32 value rows per
+    work-group, and one work-group per head) against xjo_delta_step: outputs,
+    final state and checkpoints within 1e-5 relative L2 (the 16-lane partial
+    sums are combined in a butterfly instead of one running sum)."""
+    from test_oracle import delta_step_inputs
+    monkeypatch.setenv("XJ_DELTA_SPLIT", split)
+    print(f"delta_step split={split} T={T} Hk={Hk} Hv={Hv} S={S} ck_n={ck_n}", flush=True)
+    qkv, ko, vo, beta, alpha, dt, A, st = delta_step_inputs(T, Hk, Hv, S, 70 + T)
+    qs = 1 / np.sqrt(np.float32(S))
+    got, gst, gck = xp.delta_step(qkv, ko, vo, beta, alpha, dt, A, Hk, Hv, S, 1e-6, qs, st, ck_n)
+    want, wst, wck = orc.delta_step(qkv, ko, vo, beta, alpha, dt, A, Hk, Hv, S, 1e-6, qs, st, ck_n)
+    assert rel_l2(got, want) < 1e-5
+    assert rel_l2(gst, wst) < 1e-5
+    for t in range(ck_n):
+        assert rel_l2(gck[t], wck[t]) < 1e-5
+    if ck_n == T:
+        assert np.array_equal(gck[-1], gst)
+
+
+def test_delta_step_forms_agree_bit_for_bit(monkeypatch):
+    """The per-row arithmetic of the two forms is the same, so their results are
+    identical."""
+    from test_oracle import delta_step_inputs
+    qkv, ko, vo, beta, alpha, dt, A, st = delta_step_inputs(6, 16, 32, 128, 80)
+    res = []
+    for split in ("1", "0"):
+        monkeypatch.setenv("XJ_DELTA_SPLIT", split)
+        res.append(xp.delta_step(qkv, ko, vo, beta, alpha, dt, A, 16, 32, 128, 1e-6, 0.0883883, st, 5))
+    for a, b in zip(res[0], res[1]):
+        assert np.array_equal(a, b)

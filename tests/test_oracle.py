@@ -431,3 +431,60 @@ def test_attn_decode_single_position_returns_gated_value():
         g = h // (H // Hkv)
         want = v[0, g].astype(np.float16).astype(np.float64) / (1 + np.exp(-qg[0, h, D:].astype(np.float64)))
         assert rel_l2(out[0, h * D:(h + 1) * D], want) < 1e-6
+
+
+def delta_step_inputs(T, Hk, Hv, S, seed):
+    """Seeded inputs of the DeltaNet recurrence after the conv: qkv rows
+    [q (Hk*S) | k (Hk*S) | v (Hv*S)], raw gates, dt, A < 0 and a state."""
+    rng = np.random.default_rng(seed)
+    kd = Hk * S
+    qkv = rng.standard_normal((T, 2 * kd + Hv * S)).astype(np.float32)
+    beta = rng.standard_normal((T, Hv)).astype(np.float32)
+    alpha = rng.standard_normal((T, Hv)).astype(np.float32)
+    dt = (0.5 * rng.standard_normal(Hv)).astype(np.float32)
+    A = (-rng.uniform(0.05, 1.0, Hv)).astype(np.float32)
+    st = (0.2 * rng.standard_normal((Hv, S, S))).astype(np.float32)
+    return qkv, kd, 2 * kd, beta, alpha, dt, A, st
+
+
+def test_delta_step_matches_definition():
+    """xjo_delta_step against the float64 definition: L2-normalised q, k of key
+    head hv % Hk; S <- a S; S <- S + b (v - S k) k^T; o = qscale S q, with
+    a = exp(softplus(alpha + dt) A), b = sigmoid(beta); checkpoints hold the
+    state after each token."""
+    T, Hk, Hv, S = 4, 2, 6, 64
+    qkv, ko, vo, beta, alpha, dt, A, st = delta_step_inputs(T, Hk, Hv, S, 60)
+    out, st2, ck = orc.delta_step(qkv, ko, vo, beta, alpha, dt, A, Hk, Hv, S, 1e-6, 0.125, st, ck_n=3)
+    M = st.astype(np.float64)
+    for t in range(T):
+        r = qkv[t].astype(np.float64)
+        for hv in range(Hv):
+            hk = hv % Hk
+            q = r[hk * S:(hk + 1) * S]
+            k = r[ko + hk * S:ko + (hk + 1) * S]
+            q, k = q / np.sqrt(q @ q + 1e-6), k / np.sqrt(k @ k + 1e-6)
+            v = r[vo + hv * S:vo + (hv + 1) * S]
+            a = np.exp(np.log1p(np.exp(alpha[t, hv] + dt[hv])) * A[hv])
+            b = 1 / (1 + np.exp(-float(beta[t, hv])))
+            M[hv] *= a
+            M[hv] += b * np.outer(v - M[hv] @ k, k)
+            assert rel_l2(out[t, hv * S:(hv + 1) * S], 0.125 * M[hv] @ q) < 1e-5
+        if t < 3:
+            assert rel_l2(ck[t], M) < 1e-5
+    assert rel_l2(st2, M) < 1e-5
+
+
+def test_delta_step_equals_recurrent_with_derived_gates():
+    """The layer's step equals the standalone rule fed the same normalised q, k
+    and the gates it derives."""
+    T, Hk, Hv, S = 3, 4, 4, 128
+    qkv, ko, vo, beta, alpha, dt, A, st = delta_step_inputs(T, Hk, Hv, S, 61)
+    out, st2, _ = orc.delta_step(qkv, ko, vo, beta, alpha, dt, A, Hk, Hv, S, 1e-6, 0.0883883, st)
+    nrm = lambda x: (x / np.sqrt((x.astype(np.float64) ** 2).sum(-1, keepdims=True) + 1e-6)).astype(np.float32)
+    q = nrm(qkv[:, :ko].reshape(T, Hk, S))
+    k = nrm(qkv[:, ko:vo].reshape(T, Hk, S))
+    v = qkv[:, vo:].reshape(T, Hv, S)
+    dec = np.exp(np.log1p(np.exp(alpha + dt)) * A).astype(np.float32)
+    b = (1 / (1 + np.exp(-beta))).astype(np.float32)
+    o2, s2 = orc.delta_recurrent(q, k, v, dec, b, st, 0.0883883)
+    assert rel_l2(out, o2.reshape(T, -1)) < 1e-5 and rel_l2(st2, s2) < 1e-5
