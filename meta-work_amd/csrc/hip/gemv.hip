@@ -46,7 +46,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 static int g_lds_max = 64 * 1024;
 constexpr int kCuMaxT = 5;   // tokens of a per-CU launch (speculative verify widths)
 static int g_cus = 256;
-static int g_grid_cap = 256 * 8;
+static int g_grid_cap = 256 * 8;     // work-groups of a looping multi-token launch
+static int g_grid_cap1 = 256 * 8;    // ... of a looping single-token launch
+static bool g_grid_forced = false;   // XJ_GEMV_WG_PER_CU given: one cap for every launch
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
 
@@ -1447,7 +1449,12 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
         if (rc <= 0) return rc;
     }
     const int n_rg = a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg;
-    const int grid = n_rg < g_grid_cap ? n_rg : g_grid_cap;
+    int grid = a.T == 1 ? (n_rg < g_grid_cap1 ? n_rg : g_grid_cap1) : (n_rg < g_grid_cap ? n_rg : g_grid_cap);
+    // a single token with at most two units per lane: one row group per
+    // work-group, whose whole window is requested at once, streams faster than
+    // work-groups that loop with one unit in flight (151936 x 1024 Q4_K:
+    // 30.4 -> 22.1 us with its prep launch)
+    if (a.T == 1 && !g_grid_forced && (a.K / 64 + p.lanes - 1) / p.lanes <= 2 && n_rg <= 64 * g_cus) grid = n_rg;
     hipError_t e;
     switch (p.lanes) {
     case 8: e = launch_ts<8>(a, grid, st); break;
@@ -1501,7 +1508,13 @@ int gemv_init(char *err, size_t errlen) {
     if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) lds = 65536;
     if (cus > 0) {
         g_cus = cus;
-        g_grid_cap = cus * env_or("XJ_GEMV_WG_PER_CU", 8);
+        const int forced = env_or("XJ_GEMV_WG_PER_CU", 0);
+        g_grid_forced = forced > 0;
+        g_grid_cap1 = cus * (forced > 0 ? forced : 8);
+        // several tokens stage T x 3 digit bytes per weight element from LDS:
+        // fewer work-groups per CU contend less (151936 x 1024 Q4_K, T = 2:
+        // 39.2 / 42.2 / 48.7 us at 2 / 4 / 8 per CU)
+        g_grid_cap = cus * (forced > 0 ? forced : env_or("XJ_GEMV_WG_PER_CU_T", 2));
     }
     // keep 4 KB for the static reduction buffers
     int want = lds > 65536 ? lds - 4096 : 65536 - 4096;

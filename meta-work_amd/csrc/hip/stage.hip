@@ -1143,6 +1143,13 @@ static int gemv_enqueue(uint32_t type, const void *dw, int64_t n_rows, int64_t k
     }
     Gemv g(xq);
     g.a.x = x; g.a.xs = (int32_t)k; g.a.pro = PRO_NONE;
+    // quantized rows, one or two tokens: the GEMV's work-groups build the
+    // activations from x (no prep launch); float rows read a prep launch's v,
+    // and from three tokens on one prep launch is cheaper than every
+    // work-group converting all of them (2560 x 9216 Q6_K, T = 3: 17.6 vs 38 us)
+    static const bool inwg = getenv("XJ_GEMV_OP_INWG") == nullptr || atoi(getenv("XJ_GEMV_OP_INWG")) != 0;
+    if (inwg && T <= 2 && type != XJ_F32 && type != XJ_F16 && type != XJ_BF16 && !((uintptr_t)x & 15) && k % 4 == 0)
+        g.a.pro = PRO_X;
     g.seg(w, y, (int32_t)n_rows, add ? EPI_ADD : EPI_STORE);
     return g.run(T, st);
 }
