@@ -20,6 +20,11 @@ Also reported, on the same run:
   gemv_*        stand-alone cold-cache GEMV legs (Q4_K / Q6_K LM-head shapes), and
                 the gate|up and down shapes at T = 1..5 activation rows.
   decode_0_8b   the same measurement on the 0.8B-shape model.
+  speculative_4b  the 4B shape split 0-15 | 16-31 with the 0.8B model drafting
+                4 tokens per step (5-row verify passes): real drafts, drafts
+                from the plain greedy output, and one in four of them
+                perturbed; tok/s and acceptance, each checked token-identical
+                to plain greedy decoding.
 
 usage: python bench.py [--gpus 1] [--steps 512] [--warmup 16] [--no-cpu] [--no-extra]
                        [--copy-calibration MB] [--delta-c3]
@@ -130,6 +135,38 @@ def gemv_tokens(t, rows, k, copies=12, iters=200):
     return {"shape": f"{xp.TYPE_NAMES[t]} {rows}x{k}", "by_T": out}
 
 
+def spec_run(n_prompt=1024, n_gen=128, seed=20261109):
+    """Speculative decode on the 4B shape, split 0-15 | 16-31 on one stream, with the 0.8B model
+    drafting 4 tokens per step and the target verifying them as one 5-row pass: the real draft (random
+    weights: acceptance near 0), drafts taken from the plain greedy output (every draft accepted), and
+    the same with one draft in 4 perturbed. Every run must reproduce the plain greedy tokens."""
+    m, dm = xp.Model(model_path(xp.CONFIG_4B, "synth4b")), xp.Model(model_path(xp.CONFIG_0_8B, "synth08b"))
+    n_ctx = n_prompt + n_gen + 16
+    prompt = np.random.default_rng(seed).integers(0, m.hp.n_vocab, n_prompt).astype(np.int32)
+    a, b = xp.HipStage(m, 0, 16, n_ctx, 8, False), xp.HipStage(m, 16, 32, n_ctx, 8, True)
+    d = xp.HipStage(dm, 0, dm.hp.n_layer, n_ctx, 8, True)
+    tc, dc = xp.Chain([a, b]), xp.Chain([d])
+    plain = np.concatenate([tc.eval(prompt), tc.decode(n_gen - 1)])
+    res = {"prompt": n_prompt, "tokens": n_gen, "k": 4}
+    for mode, orc, miss in (("draft_0_8b", None, 0), ("oracle_drafts", plain, 0), ("oracle_miss_1_in_4", plain, 4)):
+        tc.reset()
+        dc.reset()
+        tc.eval(prompt)
+        dc.eval(prompt)
+        out, st = xp.spec_generate(tc, dc, 4, n_gen, oracle=orc, oracle_miss=miss)
+        if out.tolist() != plain.tolist():
+            raise RuntimeError(f"speculative decode ({mode}) diverged from plain greedy decoding")
+        res[mode] = {"tok_s": round(n_gen / (st.t_total_ms / 1e3), 1), "verify_passes": st.n_steps,
+                     "drafted": st.n_drafted, "accepted": st.n_accepted,
+                     "draft_ms": round(st.t_draft_ms, 1), "total_ms": round(st.t_total_ms, 1)}
+        log(f"spec {mode}: {res[mode]}")
+    for o in (tc, dc):
+        o.free()
+    for s in (a, b, d):
+        s.destroy()
+    return res
+
+
 def delta_c3(reps=3):
     """Gated DeltaNet prefill on the c3 shape (16 heads, d=128, 2048 tokens from a zero state): the chunk-wise
     MFMA kernels (chunk 64) next to the token-by-token kernel. Wall ms per call include the host copies; the
@@ -218,6 +255,7 @@ def main():
         extra["gemv_legs"] = [gemv_leg(xp.Q4_K, 151936, 1024, 8, 64), gemv_leg(xp.Q6_K, 151936, 2560, 3, 24),
                               gemv_leg(xp.Q4_K, 4096, 1024, 256, 512)]
         extra["gemv_tokens"] = [gemv_tokens(xp.Q4_K, 18432, 2560), gemv_tokens(xp.Q6_K, 2560, 9216)]
+        extra["speculative_4b"] = spec_run()
         log(f"extra: {extra}")
 
     cpu = None
