@@ -701,8 +701,9 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
     return s;
 }
 
-extern "C" int xj_hip_stage_snapshot(xj_stage *s, int slot, char *err, size_t errlen) {
-    HStage *S = H(s);
+// The recurrent state of every DeltaNet layer into snapshot slot `slot`,
+// enqueued on `st` (allocated on first use).
+static int snapshot_enqueue(HStage *S, int slot, hipStream_t st, char *err, size_t errlen) {
     if (slot < 0 || slot >= kSnapSlots) { snprintf(err, errlen, "snapshot slot %d out of range", slot); return -1; }
     for (auto &L : S->L) {
         if (!L.rec) continue;
@@ -712,13 +713,17 @@ extern "C" int xj_hip_stage_snapshot(xj_stage *s, int slot, char *err, size_t er
                 return -1;
             }
         }
-        if (hipMemcpyAsync(L.snap_conv[slot], L.conv, S->conv_n * 4, hipMemcpyDeviceToDevice, S->st) != hipSuccess ||
-            hipMemcpyAsync(L.snap_ssm[slot], L.ssm, S->ssm_n * 4, hipMemcpyDeviceToDevice, S->st) != hipSuccess) {
+        if (hipMemcpyAsync(L.snap_conv[slot], L.conv, S->conv_n * 4, hipMemcpyDeviceToDevice, st) != hipSuccess ||
+            hipMemcpyAsync(L.snap_ssm[slot], L.ssm, S->ssm_n * 4, hipMemcpyDeviceToDevice, st) != hipSuccess) {
             snprintf(err, errlen, "snapshot copy failed");
             return -1;
         }
     }
     return 0;
+}
+
+extern "C" int xj_hip_stage_snapshot(xj_stage *s, int slot, char *err, size_t errlen) {
+    return snapshot_enqueue(H(s), slot, H(s)->st, err, errlen);
 }
 
 extern "C" int xj_hip_stage_fill_kv(xj_stage *s, int pos0, uint16_t bits, char *err, size_t errlen) {
@@ -960,9 +965,36 @@ static int draft_step(xjh_chain *d, int t, int *next, char *err, size_t errlen) 
     return 0;
 }
 
-static int snapshot_all(xjh_chain *c, int slot, char *err, size_t errlen) {
-    for (auto *S : c->st)
-        if (xj_hip_stage_snapshot(&S->s, slot, err, errlen)) return -1;
+// kk greedy steps of the draft fed with token t, the state after step j in
+// snapshot slot j: one set-up, the decode graph replayed kk times with the
+// snapshot copies between the replays on the chain's stream, one
+// synchronisation; toks receives the kk argmax tokens.
+static int draft_run(xjh_chain *d, int t, int kk, int32_t *toks, char *err, size_t errlen) {
+    for (auto *S : d->st)
+        if (S->s.n_past + kk > S->s.n_ctx) { snprintf(err, errlen, "context full (%d)", S->s.n_ctx); return -1; }
+    const bool direct = env_int("XJ_DECODE_GRAPH", 1) == 0;
+    if (!direct && !d->exec && build_decode_graph(d, err, errlen)) return -1;
+    d->h_buf[0] = 0;
+    d->h_buf[1] = t;
+    if (hipMemcpyAsync(d->d_step, &d->h_buf[0], 4, hipMemcpyHostToDevice, d->stream) != hipSuccess ||
+        hipMemcpyAsync(d->d_tok, &d->h_buf[1], 4, hipMemcpyHostToDevice, d->stream) != hipSuccess) {
+        snprintf(err, errlen, "draft setup failed"); return -1;
+    }
+    for (auto *S : d->st) if (set_npast(S, d->stream)) { snprintf(err, errlen, "draft setup failed"); return -1; }
+    for (int j = 0; j < kk; j++) {
+        if (direct ? enqueue_decode_step(d) != 0 : hipGraphLaunch(d->exec, d->stream) != hipSuccess) {
+            snprintf(err, errlen, "draft step launch failed"); return -1;
+        }
+        for (auto *S : d->st)
+            if (snapshot_enqueue(S, j, d->stream, err, errlen)) return -1;
+    }
+    if (hipMemcpyAsync(&d->h_buf[2], d->d_hist, 4 * kk, hipMemcpyDeviceToHost, d->stream) != hipSuccess) {
+        snprintf(err, errlen, "draft history copy failed"); return -1;
+    }
+    if (chain_sync(d, err, errlen)) return -1;
+    for (int j = 0; j < kk; j++) toks[j] = d->h_buf[2 + j];
+    for (auto *S : d->st) S->s.n_past += kk;
+    d->last_tok = toks[kk - 1];
     return 0;
 }
 
@@ -1000,13 +1032,7 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
         const double t0 = now_ms();
         int32_t toks[5];
         toks[0] = pending;
-        int cur = pending;
-        for (int j = 0; j < kk; j++) {
-            int nx;
-            if (draft_step(dft, cur, &nx, err, errlen) || snapshot_all(dft, j, err, errlen)) return -1;
-            toks[j + 1] = nx;
-            cur = nx;
-        }
+        if (draft_run(dft, pending, kk, toks + 1, err, errlen)) return -1;
         st.t_draft_ms += now_ms() - t0;
         for (int j = 1; j <= kk && oracle; j++) {
             const long gi = n_gen_tok + j;   // index of the generated token this draft stands for
