@@ -34,7 +34,7 @@ def _short(name):
 
 
 def _gemv1(name):
-    return name.startswith("void xjk::gemv_kernel<1,") or name.startswith("void xjk::gemv_cu_kernel<")
+    return name.startswith("void xjk::gemv_kernel<1,") or name.startswith("void xjk::gemv_cu_kernel<1,")
 
 
 def trace(d):
