@@ -1020,16 +1020,14 @@ __device__ __forceinline__ void tail_swiglu_cu(const GArgs &a, int rg, const GSe
     const XqOff o = xq_off(g.n_rows);
     for (int i = 0; i < ng; i++) {
         if (!last_sh[i]) continue;   // uniform
-        if (tid < 64) {
-            const int k = 32 * (ga + i) + (tid & 31);
-            const bool in = tid < 32;
-#pragma unroll
-            for (int t = 0; t < T; t++) {
-                const float v = in ? xjd::silu(xjd::load_sys(g.y + (int64_t)t * g.ys + k)) *
-                                         xjd::load_sys(u.y + (int64_t)t * u.ys + k)
-                                   : 0.f;
-                xjd::emit_xq(v, k, in, a.post.xq + (int64_t)t * o.stride, o);
-            }
+        // half-wavefront t emits token t: the T tokens' loads are in flight together
+        if (tid < (T * 32 + 63) / 64 * 64) {
+            const int t = tid >> 5, k = 32 * (ga + i) + (tid & 31);
+            const bool in = t < T;
+            const float v = in ? xjd::silu(xjd::load_sys(g.y + (int64_t)t * g.ys + k)) *
+                                     xjd::load_sys(u.y + (int64_t)t * u.ys + k)
+                               : 0.f;
+            xjd::emit_xq(v, k, in, a.post.xq + (int64_t)(in ? t : 0) * o.stride, o);
         }
     }
 }
@@ -1274,7 +1272,9 @@ static int launch_cu_ts(GArgs b, int rpw, int upl, bool q4, bool wf, hipStream_t
         }
     }
     b.rpw = rpw;
-    const int threads = cu_threads(b, teams * TS);
+    int threads = cu_threads(b, teams * TS);
+    // the SwiGLU tail emits token t from half-wavefront t
+    if (b.post.mode == POST_SWIGLU && threads < (b.T * 32 + 63) / 64 * 64) threads = (b.T * 32 + 63) / 64 * 64;
     size_t lds = cu_lds_bytes(b);
     // more than half of a CU's LDS keeps each work-group on a CU of its own
     if (b.pro != PRO_RMSU_X && g_lds_max > 80 * 1024 && lds < 80 * 1024 + 256) lds = 80 * 1024 + 256;
