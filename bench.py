@@ -18,7 +18,8 @@ Also reported, on the same run:
                 of the same workload; the oracle's C restatement if that
                 library is absent.
   gemv_*        stand-alone cold-cache GEMV legs (Q4_K / Q6_K LM-head shapes), and
-                the gate|up and down shapes at T = 1..5 activation rows.
+                at T = 1..5 activation rows the mixed-quant batch (Q6_K 3584x1024,
+                Q8_0 1024x3584, Q4_K 151936x1024) and the 4B gate|up and down shapes.
   decode_0_8b   the same measurement on the 0.8B-shape model.
   speculative_4b  the 4B shape split 0-15 | 16-31 with the 0.8B model drafting
                 4 tokens per step (5-row verify passes): real drafts, drafts
@@ -119,12 +120,14 @@ def gemv_leg(t, rows, k, copies, iters):
             "GBps": round(by / (ms * 1e-3) / 1e9, 1), "frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
 
 
-def gemv_tokens(t, rows, k, copies=12, iters=200):
-    """One weight shape at T = 1..5 activation rows (the speculative-verify widths), cold weights:
-    us per launch and weight GB/s."""
+def gemv_tokens(t, rows, k, iters=200):
+    """One weight shape at T = 1..5 activation rows (the speculative-verify widths), cold weights
+    (rotating copies totalling more than 600 MB): us per launch (the per-op entry, activations built
+    in the GEMV's work-groups for T <= 2, by a prep launch beyond) and weight GB/s."""
+    by = rows * xp.row_bytes(t, k)
+    copies = max(4, -(-600_000_000 // by))
     blob = xp.quantize(t, xp.fill_normal(rows * k, 17, 0.02).reshape(rows, k))
     ws = [xp.DevWeight(t, blob, rows, k) for _ in range(copies)]
-    by = rows * xp.row_bytes(t, k)
     out = []
     for T in range(1, 6):
         xs = np.stack([xp.fill_normal(k, 5 + i, 1.0) for i in range(T)])
@@ -254,7 +257,11 @@ def main():
         r8["st"].destroy()
         extra["gemv_legs"] = [gemv_leg(xp.Q4_K, 151936, 1024, 8, 64), gemv_leg(xp.Q6_K, 151936, 2560, 3, 24),
                               gemv_leg(xp.Q4_K, 4096, 1024, 256, 512)]
-        extra["gemv_tokens"] = [gemv_tokens(xp.Q4_K, 18432, 2560), gemv_tokens(xp.Q6_K, 2560, 9216)]
+        # the mixed-quant batch (T = 1..5: Q6_K 3584x1024, Q8_0 1024x3584, Q4_K 151936x1024) and
+        # the 4B shape's gate|up and down
+        extra["gemv_tokens"] = [gemv_tokens(xp.Q6_K, 3584, 1024), gemv_tokens(xp.Q8_0, 1024, 3584),
+                                gemv_tokens(xp.Q4_K, 151936, 1024), gemv_tokens(xp.Q4_K, 18432, 2560),
+                                gemv_tokens(xp.Q6_K, 2560, 9216)]
         extra["speculative_4b"] = spec_run()
         log(f"extra: {extra}")
 
