@@ -88,6 +88,7 @@ typedef struct {
     uint32_t type_embd, type_out, type_v, type_down;
     float w_std;
     uint64_t seed;
+    int nextn;                          /* 1: one MTP layer (blk.{n_layer}, nextn.*) */
 } xjs_config;
 
 /* Fill out[n] with N(0, std) from the build's generator: splitmix64 feeding

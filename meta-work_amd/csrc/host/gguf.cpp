@@ -8,8 +8,8 @@
 //   hparams, layer pattern,    src/xiaoju-pipe/core/xj_model.c:129-202
 //   tied head, fingerprint
 //   per-layer tensor names     src/xiaoju-pipe/core/xj_model.c:62-101
-// The MTP layer (xj_model.c:104-127) is not loaded: the HIP backend has no MTP
-// stage, so has_mtp stays false.
+//   MTP layer                  src/xiaoju-pipe/core/xj_model.c:104-127 (blk.{block_count-1}
+//                              into layers[n_layer], its nextn.* tensors)
 #include "xj_hip.h"
 
 #include <fcntl.h>
@@ -340,6 +340,33 @@ static bool load_layer(const xj_gguf_file *g, const xj_hparams *hp, int i, xj_la
     return true;
 }
 
+// The MTP layer: blk.{block_count-1} (a full-attention layer) into
+// layers[n_layer], with its nextn.* projection and norms (xj_model.c:104-127).
+static bool load_mtp(const xj_gguf_file *g, xj_model *m, int block_count, char *err, size_t errlen) {
+    const int i = block_count - 1, il = m->hp.n_layer;
+    if (il + 1 > XJ_MAX_LAYERS) { snprintf(err, errlen, "too many layers"); return false; }
+    xj_layer *L = &m->layers[il];
+    memset(L, 0, sizeof(*L));
+    L->recurrent = false;
+    if (!load_layer(g, &m->hp, i, L, err, errlen)) return false;
+    char name[96];
+    const struct { xj_w *w; const char *suffix; } t[] = {{&m->mtp_eh, "eh_proj.weight"}, {&m->mtp_enorm, "enorm.weight"},
+                                                        {&m->mtp_hnorm, "hnorm.weight"},
+                                                        {&m->mtp_head_norm, "shared_head_norm.weight"}};
+    for (const auto &e : t) {
+        snprintf(name, sizeof name, "blk.%d.nextn.%s", i, e.suffix);
+        if (!get_w(g, name, e.w, true, err, errlen)) return false;
+    }
+    if (m->mtp_eh.ne0 != 2 * m->hp.n_embd || m->mtp_eh.ne1 != m->hp.n_embd) {
+        snprintf(err, errlen, "MTP eh_proj shape is wrong"); return false;
+    }
+    if (m->mtp_enorm.type != XJ_F32 || m->mtp_hnorm.type != XJ_F32 || m->mtp_head_norm.type != XJ_F32) {
+        snprintf(err, errlen, "MTP norms must be F32"); return false;
+    }
+    m->has_mtp = true;
+    return true;
+}
+
 extern "C" xj_model *xj_model_load(const char *path, char *err, size_t errlen) {
     xj_gguf_file *g = gguf_open(path, err, errlen);
     if (!g) return nullptr;
@@ -401,6 +428,7 @@ extern "C" xj_model *xj_model_load(const char *path, char *err, size_t errlen) {
     if (!hp->n_vocab) hp->n_vocab = (int)m->tok_embd.ne1;
     for (int i = 0; i < hp->n_layer; i++)
         if (!load_layer(g, hp, i, &m->layers[i], err, errlen)) return fail();
+    if (nextn > 0 && !load_mtp(g, m, block_count, err, errlen)) return fail();
 
     uint64_t h = 1469598103934665603ull;
     h = fnv(h, hp, sizeof(*hp));

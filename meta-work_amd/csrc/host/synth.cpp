@@ -312,6 +312,24 @@ extern "C" int64_t xjs_write_model(const char *path, const xjs_config *c, char *
             vec(p + "attn_k_norm.weight", D, 1);
         }
     }
+    if (c->nextn) {   // the MTP layer: blk.{n_layer}, a full-attention layer + nextn.*
+        std::string p = "blk." + std::to_string(c->n_layer) + ".";
+        vec(p + "attn_norm.weight", E, 1);
+        vec(p + "post_attention_norm.weight", E, 1);
+        mat(p + "ffn_gate.weight", E, FF, c->type_default);
+        mat(p + "ffn_up.weight", E, FF, c->type_default);
+        mat(p + "ffn_down.weight", FF, E, c->type_down);
+        mat(p + "attn_q.weight", E, 2 * H * D, c->type_default);
+        mat(p + "attn_k.weight", E, HKV * D, c->type_default);
+        mat(p + "attn_v.weight", E, HKV * D, c->type_v);
+        mat(p + "attn_output.weight", H * D, E, c->type_default);
+        vec(p + "attn_q_norm.weight", D, 1);
+        vec(p + "attn_k_norm.weight", D, 1);
+        mat(p + "nextn.eh_proj.weight", 2 * E, E, c->type_default);
+        vec(p + "nextn.enorm.weight", E, 1);
+        vec(p + "nextn.hnorm.weight", E, 1);
+        vec(p + "nextn.shared_head_norm.weight", E, 1);
+    }
     const uint64_t ALIGN = 32;
     uint64_t off = 0;
     for (auto &t : ts) {
@@ -323,11 +341,12 @@ extern "C" int64_t xjs_write_model(const char *path, const xjs_config *c, char *
     }
     Writer w;
     w.u32(0x46554747u); w.u32(3); w.u64(ts.size());
-    w.u64(20);  // number of key/values below
+    w.u64(c->nextn ? 21 : 20);  // number of key/values below
     w.kv_str("general.architecture", "qwen35");
     w.kv_str("general.name", "synthetic-qwen35");
     w.kv_u32("general.alignment", (uint32_t)ALIGN);
-    w.kv_u32("qwen35.block_count", c->n_layer);
+    w.kv_u32("qwen35.block_count", c->n_layer + (c->nextn ? 1 : 0));
+    if (c->nextn) w.kv_u32("qwen35.nextn_predict_layers", 1);
     w.kv_u32("qwen35.context_length", 262144);
     w.kv_u32("qwen35.embedding_length", E);
     w.kv_u32("qwen35.feed_forward_length", FF);

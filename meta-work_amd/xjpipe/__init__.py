@@ -16,7 +16,7 @@ import os
 
 import numpy as np
 
-from .configs import CONFIG_0_8B, CONFIG_4B, TINY, TINY_DRAFT, SynthConfig  # noqa: F401
+from .configs import CONFIG_0_8B, CONFIG_0_8B_MTP, CONFIG_4B, TINY, TINY_DRAFT, TINY_MTP, SynthConfig  # noqa: F401
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 # XJ_HIP_LIB selects another build of the same library (e.g. a tuning variant)
@@ -91,7 +91,7 @@ class XjsConfig(C.Structure):
                [("rope_base", C.c_float), ("eps", C.c_float)] + \
                [(n, C.c_int) for n in ("conv_k", "s_k", "h_k", "h_v", "full_attn_interval")] + \
                [(n, C.c_uint32) for n in ("type_default", "type_embd", "type_out", "type_v", "type_down")] + \
-               [("w_std", C.c_float), ("seed", C.c_uint64)]
+               [("w_std", C.c_float), ("seed", C.c_uint64), ("nextn", C.c_int)]
 
 
 # -------------------------------------------------------------- library --

@@ -36,6 +36,7 @@ class SynthConfig:
     type_down: int = Q6_K
     w_std: float = 0.02
     seed: int = BASE_SEED
+    nextn: int = 0        # 1: one MTP layer after the main layers
 
     def with_(self, **kw):
         return replace(self, **kw)
@@ -68,5 +69,10 @@ CONFIG_4B = SynthConfig(n_layer=32, n_embd=2560, n_ff=9216, n_vocab=151936, n_he
 # small models with the same structure for parity tests (value heads a multiple of key heads)
 TINY = SynthConfig(n_layer=8, n_embd=256, n_ff=512, n_vocab=2048, n_head=2, n_head_kv=1, head_dim=128, n_rot=32,
                    rope_base=1e4, s_k=64, h_k=2, h_v=4, w_std=0.05, seed=BASE_SEED + 1)
+# the tiny model with an MTP layer (the main layers' weights are those of TINY)
+TINY_MTP = SynthConfig(n_layer=8, n_embd=256, n_ff=512, n_vocab=2048, n_head=2, n_head_kv=1, head_dim=128, n_rot=32,
+                       rope_base=1e4, s_k=64, h_k=2, h_v=4, w_std=0.05, seed=BASE_SEED + 1, nextn=1)
+# the 0.8B shape with an MTP layer
+CONFIG_0_8B_MTP = CONFIG_0_8B.with_(nextn=1)
 TINY_DRAFT = SynthConfig(n_layer=4, n_embd=256, n_ff=512, n_vocab=2048, n_head=2, n_head_kv=1, head_dim=128,
                          n_rot=32, rope_base=1e4, s_k=64, h_k=4, h_v=4, w_std=0.05, seed=BASE_SEED + 2)

@@ -18,10 +18,11 @@ def w_tuple(w):
 
 
 @pytest.mark.skipif(not orc.ref_available(), reason="reference build (oracle/_ref) not present")
-@pytest.mark.parametrize("cfg", ["TINY", "TINY_DRAFT"])
+@pytest.mark.parametrize("cfg", ["TINY", "TINY_DRAFT", "TINY_MTP"])
 def test_loader_builds_the_reference_model(model_dir, cfg):
     """xj_model_load here and the reference's xj_model_load give the same hparams,
-    tensor table (offsets, sizes, types, shapes), layer pattern and fingerprint."""
+    tensor table (offsets, sizes, types, shapes), layer pattern and fingerprint,
+    and with an MTP layer the same layer n_layer and nextn tensors."""
     from conftest import synth_model
     path = synth_model(model_dir, getattr(xp, cfg), cfg.lower())
     m = xp.Model(path)
@@ -37,6 +38,14 @@ def test_loader_builds_the_reference_model(model_dir, cfg):
         assert rm.layers[i].recurrent == m.m.layers[i].recurrent
         for f in xp._LAYER_W:
             assert w_tuple(getattr(rm.layers[i], f)) == w_tuple(getattr(m.m.layers[i], f)), (i, f)
+    assert rm.has_mtp == m.m.has_mtp == bool(getattr(xp, cfg).nextn)
+    if m.m.has_mtp:
+        i = m.hp.n_layer
+        assert rm.layers[i].recurrent == m.m.layers[i].recurrent == 0
+        for f in xp._LAYER_W:
+            assert w_tuple(getattr(rm.layers[i], f)) == w_tuple(getattr(m.m.layers[i], f)), ("mtp", f)
+        for name in ("mtp_eh", "mtp_enorm", "mtp_hnorm", "mtp_head_norm"):
+            assert w_tuple(getattr(rm, name)) == w_tuple(getattr(m.m, name)), name
     orc.rlib().ref_model_free(r)
 
 
