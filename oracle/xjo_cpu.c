@@ -16,7 +16,8 @@
  *   stage_rollback    <- xj_cpu.c:293-319
  *   stage_reset       <- xj_cpu.c:321-330
  *   xjo_embed         <- xj_cpu.c:369-373
- *   xjo_stage_new     <- xj_cpu.c:375-418  (MTP stages are not restated)
+ *   xjo_stage_new     <- xj_cpu.c:375-418  (the MTP stage included: prologue xj_cpu.c:253-261,
+ *                                           head norm xj_cpu.c:287)
  *
  * Every floating-point expression keeps the reference's shape and order so
  * that, built with the reference's flags (-O3 -fopenmp, GNU C, fp-contract
@@ -335,6 +336,16 @@ static int stage_forward(xj_stage *s, float *x, int T, char *err, size_t errlen)
     if (s->keep && ensure_ck(s, T - 1, err, errlen)) { s->keep = 0; return -1; }
     s->ck_start = s->n_past;
     s->ck_T = s->keep ? T : 0;
+    if (s->mtp) {
+        /* x holds [embedding | hidden] per token: each half RMS-normalised with its
+         * own weights, then eh_proj back to n_embd (xj_cpu.c:253-261) */
+        const xj_model *m = s->m;
+        for (int t = 0; t < T; t++) {
+            xjo_rmsnorm(o->h + (size_t)t * 2 * E, x + (size_t)t * 2 * E, F32(&m->mtp_enorm), E, hp->eps);
+            xjo_rmsnorm(o->h + (size_t)t * 2 * E + E, x + (size_t)t * 2 * E + E, F32(&m->mtp_hnorm), E, hp->eps);
+        }
+        mm(o, &m->mtp_eh, o->h, x, T);
+    }
     for (int il = s->l0; il < s->l1; il++) {
         const xj_layer *L = &s->m->layers[il];
         for (int t = 0; t < T; t++) xjo_rmsnorm(o->h + (size_t)t * E, x + (size_t)t * E, F32(&L->attn_norm), E, hp->eps);
@@ -358,7 +369,8 @@ static int stage_logits(xj_stage *s, const float *x, int T, float *logits, char 
     const int E = s->m->hp.n_embd;
     if (!s->has_head) { snprintf(err, errlen, "this stage has no output head"); return -1; }
     if (T < 1 || T > s->max_batch) { snprintf(err, errlen, "head called with %d tokens", T); return -1; }
-    for (int t = 0; t < T; t++) xjo_rmsnorm(o->h + (size_t)t * E, x + (size_t)t * E, F32(&s->m->output_norm), E, s->m->hp.eps);
+    const xj_w *nw = s->mtp ? &s->m->mtp_head_norm : &s->m->output_norm;   /* xj_cpu.c:287 */
+    for (int t = 0; t < T; t++) xjo_rmsnorm(o->h + (size_t)t * E, x + (size_t)t * E, F32(nw), E, s->m->hp.eps);
     mm(o, &s->m->output, o->h, logits, T);
     return 0;
 }
@@ -437,7 +449,8 @@ void xjo_embed(const xj_model *m, int32_t token, float *out) {
 xj_stage *xjo_stage_new(const xj_model *m, int l0, int l1, int n_ctx, int max_batch, bool has_head,
                         int kv_f16, char *err, size_t errlen) {
     const xj_hparams *hp = &m->hp;
-    if (l0 < 0 || l1 > hp->n_layer || l0 > l1) { snprintf(err, errlen, "bad layer range [%d,%d)", l0, l1); return NULL; }
+    const bool mtp = m->has_mtp && l0 == hp->n_layer && l1 == hp->n_layer + 1;   /* xj_cpu.c:378-379 */
+    if (l0 < 0 || (l1 > hp->n_layer && !mtp) || l0 > l1) { snprintf(err, errlen, "bad layer range [%d,%d)", l0, l1); return NULL; }
     if (hp->head_dim > 1024) { snprintf(err, errlen, "head_dim too large"); return NULL; }
     for (int il = l0; il < l1; il++)
         if (!m->layers[il].ffn_down.data) { snprintf(err, errlen, "layer %d weights are not mapped", il); return NULL; }
@@ -445,7 +458,7 @@ xj_stage *xjo_stage_new(const xj_model *m, int l0, int l1, int n_ctx, int max_ba
     xj_stage *s = calloc(1, sizeof(*s));
     ostage *o = calloc(1, sizeof(*o));
     s->m = m; s->l0 = l0; s->l1 = l1; s->n_ctx = n_ctx; s->max_batch = max_batch; s->has_head = has_head;
-    s->mtp = false;
+    s->mtp = mtp;
     s->backend = kv_f16 ? "cpu-oracle-kvf16" : "cpu-oracle";
     s->forward = stage_forward; s->logits = stage_logits; s->rollback = stage_rollback;
     s->reset = stage_reset; s->destroy = stage_destroy;

@@ -488,3 +488,31 @@ def test_delta_step_equals_recurrent_with_derived_gates():
     b = (1 / (1 + np.exp(-beta))).astype(np.float32)
     o2, s2 = orc.delta_recurrent(q, k, v, dec, b, st, 0.0883883)
     assert rel_l2(out, o2.reshape(T, -1)) < 1e-5 and rel_l2(st2, s2) < 1e-5
+
+
+@needs_ref
+def test_mtp_stage_vs_reference_build(model_dir):
+    """The MTP stage (layer n_layer behind the [embedding | hidden] prologue, head
+    through shared_head_norm) of the oracle and of the reference compiled from
+    source, on one model: hidden states and logits bit for bit over three calls."""
+    from conftest import synth_model
+    path = synth_model(model_dir, xp.TINY_MTP, "tiny_mtp")
+    err = orc.C.create_string_buffer(512)
+    r = orc.rlib().ref_model_load(path.encode(), err, 512)
+    assert r, err.value
+    hp = r.contents.hp
+    n, E = hp.n_layer, hp.n_embd
+    ref = orc.CpuStage(r, n, n + 1, 64, 8, True, ref=True)
+    ora = orc.CpuStage(r, n, n + 1, 64, 8, True)
+    assert ref.s.mtp and ora.s.mtp
+    rng = np.random.default_rng(90)
+    for T in (3, 1, 2):
+        x = rng.standard_normal((T, 2 * E)).astype(np.float32)
+        xr, xo = ref.forward(x.copy()), ora.forward(x.copy())
+        hr, ho = xr.reshape(-1)[:T * E].reshape(T, E), xo.reshape(-1)[:T * E].reshape(T, E)
+        assert np.array_equal(hr.view(np.uint32), ho.view(np.uint32))
+        assert np.array_equal(ref.logits(hr).view(np.uint32), ora.logits(ho).view(np.uint32))
+    assert ref.n_past == ora.n_past == 6
+    for s in (ref, ora):
+        s.destroy()
+    orc.rlib().ref_model_free(r)
