@@ -43,7 +43,14 @@ extern "C" {
  * xj_metal.m:554-663): validates the layer range and weight mapping, copies
  * the weights of [l0,l1) (and the head when has_head) into HBM, allocates the
  * fp16 KV cache of every attention layer ([n_ctx][n_head_kv*head_dim]) and the
- * fp32 conv/recurrent state of every DeltaNet layer. backend = "hip". */
+ * fp32 conv/recurrent state of every DeltaNet layer. backend = "hip".
+ * With a model that has an MTP layer, [n_layer, n_layer + 1) builds the MTP
+ * stage (mtp = true, xj_cpu.c:378-379): forward takes T rows of
+ * [embedding | hidden] (2 n_embd floats each; the result, n_embd per row, is
+ * written to the first T * n_embd floats), each half RMS-normalised with
+ * nextn.enorm / nextn.hnorm and mapped back by nextn.eh_proj before the layer
+ * (xj_cpu.c:253-261); its head normalises with nextn.shared_head_norm
+ * (xj_cpu.c:287). */
 xj_stage   *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_ctx, int max_batch,
                              bool has_head, char *err, size_t errlen);
 const char *xj_hip_device_name(void);

@@ -187,6 +187,9 @@ int argmax_finalize_launch(const unsigned long long *amax, int n_part, int T, in
 // Plain argmax of T rows of n floats (first maximum).
 int argmax_rows_launch(const float *x, int n, int T, int32_t *out, hipStream_t st);
 int norm_launch(int mode, const float *x, const float *w, int n, int rows, float eps, float *out, hipStream_t st);
+// The same over rows r < rows of n elements at x + r * xs, into out + r * os.
+int norm_rows_launch(int mode, const float *x, int64_t xs, const float *w, int n, int rows, float eps, float *out,
+                     int64_t os, hipStream_t st);
 // g = silu(g) * u over n floats.
 int swiglu_launch(float *g, const float *u, int64_t n, hipStream_t st);
 // NeoX RoPE in place of x[t * tok_stride + h * head_stride + i] for T tokens and

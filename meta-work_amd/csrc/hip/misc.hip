@@ -80,15 +80,16 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const float *x, int n,
     if (tid == 0) out[t] = (int32_t)xjd::argmax_key_index(red[0]);
 }
 
-__global__ __launch_bounds__(256) void norm_kernel(int mode, const float *x, const float *w, int n, float eps, float *out) {
+__global__ __launch_bounds__(256) void norm_kernel(int mode, const float *x, int64_t xs, const float *w, int n, float eps,
+                                                   float *out, int64_t os) {
     const int r = blockIdx.x, tid = threadIdx.x;
     __shared__ double red[4];
-    const float *xr = x + (int64_t)r * n;
+    const float *xr = x + (int64_t)r * xs;
     double ss = 0;
     for (int i = tid; i < n; i += 256) ss += (double)xr[i] * xr[i];
     ss = xjd::block_sum_d(ss, red);
     const float sc = mode == 0 ? 1.0f / sqrtf((float)(ss / n) + eps) : 1.0f / sqrtf((float)ss + eps);
-    for (int i = tid; i < n; i += 256) out[(int64_t)r * n + i] = w ? xr[i] * sc * w[i] : xr[i] * sc;
+    for (int i = tid; i < n; i += 256) out[(int64_t)r * os + i] = w ? xr[i] * sc * w[i] : xr[i] * sc;
 }
 
 int embed_launch(const EmbedArgs &a, hipStream_t st) {
@@ -122,7 +123,13 @@ int swiglu_launch(float *g, const float *u, int64_t n, hipStream_t st) {
 }
 
 int norm_launch(int mode, const float *x, const float *w, int n, int rows, float eps, float *out, hipStream_t st) {
-    hipLaunchKernelGGL(norm_kernel, dim3(rows), dim3(256), 0, st, mode, x, w, n, eps, out);
+    return norm_rows_launch(mode, x, n, w, n, rows, eps, out, n, st);
+}
+
+int norm_rows_launch(int mode, const float *x, int64_t xs, const float *w, int n, int rows, float eps, float *out,
+                     int64_t os, hipStream_t st) {
+    if (rows < 1 || n < 1) return rows == 0 ? 0 : -1;
+    hipLaunchKernelGGL(norm_kernel, dim3(rows), dim3(256), 0, st, mode, x, xs, w, n, eps, out, os);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

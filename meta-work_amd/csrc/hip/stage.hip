@@ -57,6 +57,12 @@ struct HStage {
     std::vector<HLayer> L;
     DevW output, tok_embd;
     const float *out_norm = nullptr;
+    // MTP stage: [embedding | hidden] rows in mx, each half normalised into mh,
+    // eh_proj back to n_embd (activations in xq_2e)
+    DevW mtp_eh;
+    const float *mtp_enorm = nullptr, *mtp_hnorm = nullptr;
+    float *mx = nullptr, *mh = nullptr;
+    uint8_t *xq_2e = nullptr;
     float *x = nullptr, *qkv = nullptr, *kb = nullptr, *vb = nullptr, *z = nullptr, *beta = nullptr,
           *alpha = nullptr, *o = nullptr, *g = nullptr, *u = nullptr, *qr = nullptr, *scores = nullptr,
           *logits = nullptr;
@@ -398,13 +404,35 @@ int begin_forward(HStage *S, int T, int *keep_n, char *err, size_t errlen) {
     return 0;
 }
 
+// MTP stage (xj_cpu.c:253-261): x holds T rows of [embedding | hidden] (2 n_embd
+// floats); each half is RMS-normalised with its own weights and eh_proj maps
+// the pair back to n_embd, into S->x.
+int enqueue_mtp_prologue(HStage *S, const float *x, int T) {
+    const xj_hparams &hp = S->s.m->hp;
+    const int E = hp.n_embd;
+    memcpy(S->h_x, x, sizeof(float) * T * 2 * E);
+    if (hipMemcpyAsync(S->mx, S->h_x, sizeof(float) * T * 2 * E, hipMemcpyHostToDevice, S->st) != hipSuccess ||
+        norm_rows_launch(0, S->mx, 2 * E, S->mtp_enorm, E, T, hp.eps, S->mh, 2 * E, S->st) ||
+        norm_rows_launch(0, S->mx + E, 2 * E, S->mtp_hnorm, E, T, hp.eps, S->mh + E, 2 * E, S->st))
+        return -1;
+    Gemv g(S->xq_2e);
+    g.a.x = S->mh; g.a.xs = 2 * E; g.a.pro = PRO_NONE;
+    g.seg(S->mtp_eh, S->x, E, EPI_STORE);
+    return g.run(T, S->st);
+}
+
 int hip_forward(xj_stage *s, float *x, int T, char *err, size_t errlen) {
     HStage *S = H(s);
     const int E = s->m->hp.n_embd;
     int keep_n = 0;
     if (begin_forward(S, T, &keep_n, err, errlen)) return -1;
-    memcpy(S->h_x, x, sizeof(float) * T * E);
-    if (hipMemcpyAsync(S->x, S->h_x, sizeof(float) * T * E, hipMemcpyHostToDevice, S->st) != hipSuccess ||
+    if (s->mtp && enqueue_mtp_prologue(S, x, T)) {
+        snprintf(err, errlen, "kernel launch failed");
+        s->keep = 0;
+        return -1;
+    }
+    if (!s->mtp) memcpy(S->h_x, x, sizeof(float) * T * E);
+    if ((!s->mtp && hipMemcpyAsync(S->x, S->h_x, sizeof(float) * T * E, hipMemcpyHostToDevice, S->st) != hipSuccess) ||
         set_npast(S, S->st) || enqueue_layers(S, S->x, T, keep_n, false, S->st) ||
         hipMemcpyAsync(S->h_x, S->x, sizeof(float) * T * E, hipMemcpyDeviceToHost, S->st) != hipSuccess) {
         snprintf(err, errlen, "kernel launch failed");
@@ -540,11 +568,9 @@ extern "C" uint64_t xj_hip_stage_state_bytes(const xj_model *m, int l0, int l1, 
 extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_ctx, int max_batch, bool has_head,
                                       char *err, size_t errlen) {
     const xj_hparams &hp = m->hp;
-    if (m->has_mtp && l0 == hp.n_layer && l1 == hp.n_layer + 1) {
-        snprintf(err, errlen, "the HIP backend has no MTP stage");
-        return nullptr;
-    }
-    if (l0 < 0 || l1 > hp.n_layer || l0 > l1) { snprintf(err, errlen, "bad layer range [%d,%d)", l0, l1); return nullptr; }
+    // the MTP stage is the range [n_layer, n_layer + 1) of a model with an MTP layer (xj_cpu.c:378-379)
+    const bool mtp = m->has_mtp && l0 == hp.n_layer && l1 == hp.n_layer + 1;
+    if (l0 < 0 || (l1 > hp.n_layer && !mtp) || l0 > l1) { snprintf(err, errlen, "bad layer range [%d,%d)", l0, l1); return nullptr; }
     for (int il = l0; il < l1; il++)
         if (!m->layers[il].ffn_down.data) { snprintf(err, errlen, "layer %d weights are not mapped", il); return nullptr; }
     if (has_head && !m->output.data) { snprintf(err, errlen, "output head is not mapped"); return nullptr; }
@@ -588,6 +614,9 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
             }
         }
         if (has_head && (bad(m->output, E, m->output.ne1, "output", -1) || bad(m->output_norm, E, 1, "output_norm", -1))) return nullptr;
+        if (mtp && (bad(m->mtp_eh, 2 * E, E, "nextn.eh_proj", l0) || bad(m->mtp_enorm, E, 1, "nextn.enorm", l0) ||
+                    bad(m->mtp_hnorm, E, 1, "nextn.hnorm", l0) || bad(m->mtp_head_norm, E, 1, "nextn.shared_head_norm", l0)))
+            return nullptr;
         if (bad(m->tok_embd, E, m->tok_embd.ne1, "token_embd", -1)) return nullptr;
     }
     int ndev = 0;
@@ -599,7 +628,7 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
     xj_stage *s = &S->s;
     memset(s, 0, sizeof(*s));
     s->m = m; s->l0 = l0; s->l1 = l1; s->n_ctx = n_ctx; s->max_batch = max_batch; s->has_head = has_head;
-    s->mtp = false; s->backend = "hip";
+    s->mtp = mtp; s->backend = "hip";
     s->forward = hip_forward; s->logits = hip_logits; s->rollback = hip_rollback; s->reset = hip_reset;
     s->destroy = hip_destroy; s->impl = S;
     auto fail = [&]() -> xj_stage * { hip_destroy(s); return nullptr; };
@@ -641,7 +670,9 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
         if (!ok) return fail();
     }
     if (has_head) {
-        if (!upload(S, m->output, &S->output, err, errlen) || !upload_f32(S, m->output_norm, &S->out_norm, err, errlen))
+        // the MTP stage's head normalises with shared_head_norm (xj_cpu.c:287)
+        if (!upload(S, m->output, &S->output, err, errlen) ||
+            !upload_f32(S, mtp ? m->mtp_head_norm : m->output_norm, &S->out_norm, err, errlen))
             return fail();
         if (S->output.k != hp.n_embd) { snprintf(err, errlen, "output head shape mismatch"); return fail(); }
     }
@@ -690,7 +721,16 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
         rope_table(0, n_ctx, hp.n_rot, hp.rope_base, cs.data());
         XJ_CHECK(hipMemcpy(S->rope, cs.data(), cs.size() * sizeof(float2), hipMemcpyHostToDevice), err, errlen, fail());
     }
-    XJ_CHECK(hipHostMalloc((void **)&S->h_x, sizeof(float) * mb * E, hipHostMallocDefault), err, errlen, fail());
+    if (mtp) {
+        if (!upload(S, m->mtp_eh, &S->mtp_eh, err, errlen) || !upload_f32(S, m->mtp_enorm, &S->mtp_enorm, err, errlen) ||
+            !upload_f32(S, m->mtp_hnorm, &S->mtp_hnorm, err, errlen))
+            return fail();
+        S->mx = dalloc<float>(S, mb * 2 * E, err, errlen);
+        S->mh = dalloc<float>(S, mb * 2 * E, err, errlen);
+        S->xq_2e = dalloc<uint8_t>(S, mb * (size_t)xq_off(2 * (int)E).stride, err, errlen);
+        if (!S->mx || !S->mh || !S->xq_2e) return fail();
+    }
+    XJ_CHECK(hipHostMalloc((void **)&S->h_x, sizeof(float) * mb * E * (mtp ? 2 : 1), hipHostMallocDefault), err, errlen, fail());
     XJ_CHECK(hipHostMalloc((void **)&S->h_i, 64, hipHostMallocDefault), err, errlen, fail());
     hip_reset(s);
     char note[160];
