@@ -81,6 +81,34 @@ int ref_greedy(const xj_model *m, int split, int n_ctx, int max_batch, const int
     return rc ? -1 : 0;
 }
 
+/* The reference's own speculative driver (xj_pipeline over stages a | b, the
+ * MTP stage mtp drafting k tokens per step; mtp = NULL or k = 0: plain
+ * greedy) over whatever stages it is given - the reference's CPU stages, the
+ * oracle's, or the HIP library's through the same vtable. oracle/n_oracle
+ * replace the drafts (the driver's test mode, xj_spec.h:37-38). Greedy tokens
+ * into out; stats = {verify steps, drafted, accepted}. */
+int ref_spec_run(const xj_model *m, xj_stage *a, xj_stage *b, xj_stage *mtp, int k, const int32_t *prompt, int n_prompt,
+                 int n_gen, const int32_t *oracle, int n_oracle, int oracle_miss, int32_t *out, long *stats, char *err,
+                 size_t errlen) {
+    xj_pipeline p;
+    xj_spec sp;
+    int rc = xj_pipeline_init(&p, m, a, NULL, b) || xj_spec_init(&sp, &p, mtp, k);
+    if (rc) { snprintf(err, errlen, "pipeline / spec init failed"); return -1; }
+    sp.oracle = oracle; sp.n_oracle = n_oracle; sp.oracle_miss = oracle_miss;
+    rc = xj_spec_feed(&sp, prompt, n_prompt, err, errlen);
+    int produced = 0;
+    while (!rc && produced < n_gen) {
+        int32_t o[XJ_SPEC_MAXK + 1];
+        const int n = xj_spec_next(&sp, greedy_pick, NULL, o, n_gen - produced, err, errlen);
+        if (n < 1) { rc = -1; break; }
+        for (int i = 0; i < n && produced < n_gen; i++) out[produced++] = o[i];
+    }
+    if (stats) { stats[0] = sp.n_steps; stats[1] = sp.n_drafted; stats[2] = sp.n_accepted; }
+    xj_spec_free(&sp);
+    xj_pipeline_free(&p);
+    return rc ? -1 : 0;
+}
+
 /* offsetof every field of the boundary types, in a fixed order shared with
  * xjo_abi_offsets (oracle/xjo_abi.c, built from include/xj_abi.h) */
 int ref_abi_offsets(long *o, int max) {

@@ -76,3 +76,38 @@ def test_main_stages_of_an_mtp_model_ignore_the_mtp_layer(model_dir):
     assert np.array_equal(ya, yb)
     ga.destroy()
     gb.destroy()
+
+
+def _driver_run(mp, make, L, k, prompt, n_gen, oracle=None):
+    a, b = make(0, L // 2, False), make(L // 2, L, True)
+    mt = make(L, L + 1, True) if k else None
+    out = orc.ref_spec_run(mp, a.ptr, b.ptr, mt.ptr if mt else None, k, prompt, n_gen, oracle)
+    for s in (a, b, mt):
+        if s:
+            s.destroy()
+    return out
+
+
+@pytest.mark.skipif(not orc.ref_available(), reason="reference build (oracle/_ref) not present")
+@pytest.mark.parametrize("shape", ["tiny", "0_8b"])
+def test_reference_mtp_driver_over_hip_stages(model_dir, shape):
+    """The reference's own pipeline and speculative driver (MTP drafting 3 tokens
+    per step) run unchanged over HIP stages through the xj_stage vtable: the
+    tokens equal plain greedy decoding on the same stages and the oracle's
+    (fp16 KV) greedy tokens; with drafts from that output every draft is accepted."""
+    if shape == "tiny":
+        m, n_gen = xp.Model(synth_model(model_dir, xp.TINY_MTP, "tiny_mtp")), 24
+    else:
+        m, n_gen = xp.Model(xp.cached_model(xp.CONFIG_0_8B_MTP, "synth08b_mtp")), 32
+    L = m.hp.n_layer
+    prompt = np.random.default_rng(92).integers(0, m.hp.n_vocab, 20).astype(np.int32)
+    hip = lambda l0, l1, head: xp.HipStage(m, l0, l1, 128, 8, head)
+    cpu = lambda l0, l1, head: orc.CpuStage(m.ptr, l0, l1, 128, 8, head, kv_f16=True)
+    print(f"mtp driver {shape}", flush=True)
+    plain, _ = _driver_run(m.ptr, hip, L, 0, prompt, n_gen)
+    spec, st = _driver_run(m.ptr, hip, L, 3, prompt, n_gen)
+    want, _ = _driver_run(m.ptr, cpu, L, 0, prompt, n_gen)
+    print(f"{shape}: verify steps {st[0]}, drafted {st[1]}, accepted {st[2]}")
+    assert spec.tolist() == plain.tolist() == want.tolist()
+    _, st_all = _driver_run(m.ptr, hip, L, 3, prompt, n_gen, oracle=plain)
+    assert st_all[1] > 0 and st_all[2] == st_all[1]

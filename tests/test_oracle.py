@@ -516,3 +516,40 @@ def test_mtp_stage_vs_reference_build(model_dir):
     for s in (ref, ora):
         s.destroy()
     orc.rlib().ref_model_free(r)
+
+
+@needs_ref
+def test_reference_mtp_driver_over_oracle_stages(model_dir):
+    """The reference's own speculative driver with an MTP stage drafting 3 tokens,
+    run over the reference's CPU stages and over the oracle's (fp32 KV): the same
+    tokens and the same draft statistics, and the tokens of plain greedy decoding
+    (speculation never changes the output); with drafts taken from that output
+    every draft is accepted."""
+    from conftest import synth_model
+    path = synth_model(model_dir, xp.TINY_MTP, "tiny_mtp")
+    m = xp.Model(path)
+    L = m.hp.n_layer
+    err = orc.C.create_string_buffer(512)
+    r = orc.rlib().ref_model_load(path.encode(), err, 512)
+    assert r, err.value
+    prompt = np.random.default_rng(91).integers(0, m.hp.n_vocab, 20).astype(np.int32)
+    n_gen = 24
+
+    def run(mp, ref, k, oracle=None):
+        a = orc.CpuStage(mp, 0, L // 2, 128, 8, False, ref=ref)
+        b = orc.CpuStage(mp, L // 2, L, 128, 8, True, ref=ref)
+        mt = orc.CpuStage(mp, L, L + 1, 128, 8, True, ref=ref) if k else None
+        out = orc.ref_spec_run(mp, a.ptr, b.ptr, mt.ptr if mt else None, k, prompt, n_gen, oracle)
+        for s in (a, b, mt):
+            if s:
+                s.destroy()
+        return out
+
+    plain, _ = run(r, True, 0)
+    spec_ref, st_ref = run(r, True, 3)
+    spec_orc, st_orc = run(m.ptr, False, 3)
+    assert spec_ref.tolist() == plain.tolist() and spec_orc.tolist() == plain.tolist()
+    assert st_ref == st_orc and st_ref[0] > 0
+    _, st_all = run(m.ptr, False, 3, oracle=plain)
+    assert st_all[1] > 0 and st_all[2] == st_all[1]
+    orc.rlib().ref_model_free(r)
