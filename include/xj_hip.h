@@ -163,6 +163,22 @@ int xjh_spec_generate(xjh_chain *target, xjh_chain *draft, int k, int n_gen,
                       const int32_t *oracle, int n_oracle, int oracle_miss,
                       int32_t *out, xjh_spec_stats *stats, char *err, size_t errlen);
 
+/* Speculative decoding with the model's own MTP stage as the drafter, the
+ * reference's algorithm with greedy sampling (xj_spec.c:97-209: the MTP stage
+ * takes every fed position with the token after it, drafts k <= 4 tokens, the
+ * first from the pending positions and each further one from
+ * [embedding(previous draft) | shared_head_norm(previous MTP output)]; the
+ * target verifies [t, d1..dk] in one batch and keeps the agreeing prefix).
+ * Feeds the prompt itself (both models are reset first); out receives n_gen
+ * tokens, which are those of plain greedy decoding. oracle / oracle_miss as
+ * for xjh_spec_generate. mtp: xj_hip_stage_new(m, n_layer, n_layer + 1, ...,
+ * has_head = true) of the target's model.
+ * Replaces: xj_spec_feed / xj_spec_next with an MTP stage
+ * (src/xiaoju-pipe/core/xj_spec.c:117-209) over the device chain. */
+int xjh_spec_generate_mtp(xjh_chain *target, xj_stage *mtp, int k, const int32_t *prompt, int n_prompt,
+                          int n_gen, const int32_t *oracle, int n_oracle, int oracle_miss,
+                          int32_t *out, xjh_spec_stats *stats, char *err, size_t errlen);
+
 /* ----------------------------------------------------- per-op kernels -- */
 
 /* Device memory and stream helpers for tests and benchmarks. All per-op

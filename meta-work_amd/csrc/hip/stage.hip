@@ -1108,6 +1108,189 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
     return 0;
 }
 
+// ------------------------------------------------------------ MTP drafting --
+
+namespace {
+struct MtpRun {
+    HStage *S;                 // the MTP stage
+    xjh_chain *c;              // the target chain (its embedding table)
+    int32_t *d_ids = nullptr;  // token ids of the rows being built
+    int32_t *d_am = nullptr;   // argmax of the MTP head
+    int last_row = 0;          // row of S->x holding the last MTP output
+    std::vector<float> ph;     // pending positions: main-model hidden rows [n][E]
+    std::vector<int32_t> pt;   // and the token after each (-1: not known yet)
+};
+
+// rows [embedding(ids[t]) | hid row t] into S->mx (hid may be null: the
+// caller fills the second half)
+int mtp_rows(MtpRun &R, const int32_t *ids, const float *hid, int T, char *err, size_t errlen) {
+    HStage *S = R.S;
+    const int E = S->s.m->hp.n_embd;
+    EmbedArgs ea{R.d_ids, R.c->st[0]->tok_embd, S->mh, T};
+    if (hipMemcpy(R.d_ids, ids, 4 * T, hipMemcpyHostToDevice) != hipSuccess || embed_launch(ea, S->st) ||
+        hipMemcpy2DAsync(S->mx, 8 * E, S->mh, 4 * E, 4 * E, T, hipMemcpyDeviceToDevice, S->st) != hipSuccess ||
+        (hid && hipMemcpy2DAsync(S->mx + E, 8 * E, hid, 4 * E, 4 * E, T, hipMemcpyHostToDevice, S->st) != hipSuccess) ||
+        sync_check(S, err, errlen)) {
+        if (!err[0]) snprintf(err, errlen, "MTP row setup failed");
+        return -1;
+    }
+    return 0;
+}
+
+// MTP forward over the T rows in S->mx (xj_cpu.c:253-261, then the layer);
+// want: the greedy token after the last row through the shared head
+int mtp_forward(MtpRun &R, int T, bool want, int32_t *tok, char *err, size_t errlen) {
+    HStage *S = R.S;
+    const xj_hparams &hp = S->s.m->hp;
+    const int E = hp.n_embd;
+    int keep_n = 0;
+    if (begin_forward(S, T, &keep_n, err, errlen)) return -1;
+    Gemv g(S->xq_2e);
+    g.a.x = S->mh; g.a.xs = 2 * E; g.a.pro = PRO_NONE;
+    g.seg(S->mtp_eh, S->x, E, EPI_STORE);
+    if (norm_rows_launch(0, S->mx, 2 * E, S->mtp_enorm, E, T, hp.eps, S->mh, 2 * E, S->st) ||
+        norm_rows_launch(0, S->mx + E, 2 * E, S->mtp_hnorm, E, T, hp.eps, S->mh + E, 2 * E, S->st) ||
+        g.run(T, S->st) || set_npast(S, S->st) || enqueue_layers(S, S->x, T, keep_n, false, S->st) ||
+        (want && (enqueue_head(S, S->x + (int64_t)(T - 1) * E, 1, S->logits, S->st) ||
+                  argmax_finalize_launch(S->amax, S->head_nwg, 1, R.d_am, nullptr, nullptr, nullptr, S->st)))) {
+        snprintf(err, errlen, "MTP launch failed");
+        return -1;
+    }
+    if (sync_check(S, err, errlen)) return -1;
+    if (want && hipMemcpy(tok, R.d_am, 4, hipMemcpyDeviceToHost) != hipSuccess) { snprintf(err, errlen, "MTP argmax copy failed"); return -1; }
+    S->s.n_past += T;
+    R.last_row = T - 1;
+    return 0;
+}
+
+// the MTP stage takes the first n pending positions (their next tokens known)
+// in batches; want: the greedy token after the last (xj_spec.c:97-116)
+int mtp_flush(MtpRun &R, int n, bool want, int32_t *tok, char *err, size_t errlen) {
+    const int E = R.S->s.m->hp.n_embd, B = R.S->s.max_batch;
+    for (int i = 0; i < n; i += B) {
+        const int T = n - i < B ? n - i : B;
+        if (mtp_rows(R, R.pt.data() + i, R.ph.data() + (size_t)i * E, T, err, errlen) ||
+            mtp_forward(R, T, want && i + T == n, tok, err, errlen))
+            return -1;
+    }
+    R.ph.erase(R.ph.begin(), R.ph.begin() + (size_t)n * E);
+    R.pt.erase(R.pt.begin(), R.pt.begin() + n);
+    return 0;
+}
+
+// the first `rows` hidden rows of the target's last evaluation become pending
+int push_hidden(MtpRun &R, int rows, char *err, size_t errlen) {
+    const int E = R.S->s.m->hp.n_embd;
+    const size_t n0 = R.ph.size();
+    R.ph.resize(n0 + (size_t)rows * E);
+    if (hipMemcpy(R.ph.data() + n0, R.c->x, sizeof(float) * rows * E, hipMemcpyDeviceToHost) != hipSuccess) {
+        snprintf(err, errlen, "hidden copy failed"); return -1;
+    }
+    return 0;
+}
+}  // namespace
+
+extern "C" int xjh_spec_generate_mtp(xjh_chain *tgt, xj_stage *mtp, int k, const int32_t *prompt, int n_prompt, int n_gen,
+                                     const int32_t *oracle, int n_oracle, int oracle_miss, int32_t *out,
+                                     xjh_spec_stats *stats, char *err, size_t errlen) {
+    err[0] = 0;
+    if (!mtp || !mtp->mtp || strcmp(mtp->backend, "hip") != 0 || mtp->m != tgt->st[0]->s.m || !mtp->has_head) {
+        snprintf(err, errlen, "an MTP stage of the target's model (HIP, with its head) is required"); return -1;
+    }
+    if (n_prompt < 1 || n_gen < 1) { snprintf(err, errlen, "empty prompt or generation"); return -1; }
+    MtpRun R;
+    R.S = H(mtp);
+    R.c = tgt;
+    const int E = R.S->s.m->hp.n_embd, V = (int)tgt->st.back()->output.n_rows, B = tgt->mb;
+    if (k < 1) k = 1;
+    if (k > 4) k = 4;
+    if (k + 1 > B) k = B - 1;
+    if (k > R.S->s.max_batch) k = R.S->s.max_batch;
+    if (hipMalloc(&R.d_ids, 4 * (size_t)R.S->s.max_batch) != hipSuccess || hipMalloc(&R.d_am, 4) != hipSuccess) {
+        snprintf(err, errlen, "hipMalloc failed"); return -1;
+    }
+    auto done = [&](int rc) { (void)hipFree(R.d_ids); (void)hipFree(R.d_am); return rc; };
+    xjh_spec_stats st{};
+    auto now_ms = []() { timespec ts; clock_gettime(CLOCK_MONOTONIC, &ts); return ts.tv_sec * 1e3 + ts.tv_nsec * 1e-6; };
+    xjh_chain_reset(tgt);
+    mtp->reset(mtp);
+    // the prompt (xj_spec.c:117-129): the target in batches, every position
+    // pending for the MTP stage with the token after it, all but the last taken now
+    int32_t t = -1;
+    for (int i = 0; i < n_prompt; i += B) {
+        const int T = n_prompt - i < B ? n_prompt - i : B;
+        int32_t am = -1;
+        if (xjh_chain_eval(tgt, prompt + i, T, i + T == n_prompt ? 1 : 0, 0, nullptr, &am, err, errlen) ||
+            push_hidden(R, T, err, errlen))
+            return done(-1);
+        for (int j = 0; j < T; j++) R.pt.push_back(i + j + 1 < n_prompt ? prompt[i + j + 1] : -1);
+        if (i + T == n_prompt) t = am;
+    }
+    const double t_start = now_ms();
+    if ((int)R.pt.size() > 1 && mtp_flush(R, (int)R.pt.size() - 1, false, nullptr, err, errlen)) return done(-1);
+    int produced = 0;
+    while (produced < n_gen) {
+        out[produced++] = t;   // t: the greedy token after everything fed so far (xj_spec.c:135-140)
+        if (produced == n_gen) break;
+        const int P = tgt->st[0]->s.n_past;
+        R.pt.back() = t;
+        int kk = k;
+        if (kk > n_gen - produced) kk = n_gen - produced;
+        for (auto *S : tgt->st) if (kk > S->s.n_ctx - P - 1) kk = S->s.n_ctx - P - 1;
+        const int mroom = R.S->s.n_ctx - R.S->s.n_past - (int)R.pt.size() - 1;
+        if (kk > mroom) kk = mroom;
+        if (kk <= 0) {   // no room to speculate: feed t alone (xj_spec.c:145-152)
+            int32_t am = -1;
+            if (xjh_chain_eval(tgt, &t, 1, 1, 0, nullptr, &am, err, errlen) || push_hidden(R, 1, err, errlen)) return done(-1);
+            R.pt.push_back(-1);
+            t = am;
+            continue;
+        }
+        // 1) the MTP stage drafts kk tokens (xj_spec.c:154-171): the pending
+        //    positions give draft 1; each further draft comes from the row
+        //    [embedding(previous draft) | shared_head_norm(previous MTP output)]
+        const double t0 = now_ms();
+        int32_t toks[5];
+        toks[0] = t;
+        const int mtp_pos = R.S->s.n_past + (int)R.pt.size();
+        if (mtp_flush(R, (int)R.pt.size(), true, &toks[1], err, errlen)) return done(-1);
+        for (int j = 2; j <= kk; j++) {
+            const int32_t id = toks[j - 1];
+            if (mtp_rows(R, &id, nullptr, 1, err, errlen) ||
+                norm_rows_launch(0, R.S->x + (int64_t)R.last_row * E, E, R.S->out_norm, E, 1, R.S->s.m->hp.eps, R.S->mx + E,
+                                 2 * E, R.S->st) ||
+                mtp_forward(R, 1, true, &toks[j], err, errlen))
+                return done(-1);
+        }
+        if (mtp->rollback(mtp, mtp_pos, err, errlen)) return done(-1);
+        st.t_draft_ms += now_ms() - t0;
+        for (int j = 1; j <= kk && oracle; j++) {   // the driver's test mode (xj_spec.c:173-177)
+            const long gi = produced - 1 + j;
+            if (gi < n_oracle) toks[j] = oracle[gi];
+            if (oracle_miss && (gi * 7 + j) % oracle_miss == 0) toks[j] = (toks[j] + 1) % V;
+        }
+        // 2) verify [t, d1..dk] in one batch with checkpoints; 3) accept the
+        //    agreeing prefix (xj_spec.c:179-201)
+        int32_t am[5];
+        if (xjh_chain_eval(tgt, toks, kk + 1, kk + 1, 1, nullptr, am, err, errlen)) return done(-1);
+        int a = 0;
+        while (a < kk && am[a] == toks[a + 1]) { st.acc_at[a]++; a++; }
+        const int fed = a + 1;
+        for (int i = 1; i < fed && produced < n_gen; i++) out[produced++] = toks[i];
+        st.n_steps++; st.n_drafted += kk; st.n_accepted += a;
+        // 4) the fed positions become pending for the MTP stage (xj_spec.c:204-207)
+        if (push_hidden(R, fed, err, errlen)) return done(-1);
+        for (int i = 1; i < fed; i++) R.pt.push_back(toks[i]);
+        R.pt.push_back(-1);
+        if (fed < kk + 1 && xjh_chain_rollback(tgt, P + fed, err, errlen)) return done(-1);
+        t = am[a];
+    }
+    tgt->last_tok = t;
+    st.t_total_ms = now_ms() - t_start;
+    if (stats) *stats = st;
+    return done(0);
+}
+
 extern "C" int xjh_chain_time_gemv(xjh_chain *c, int iters, double *ms_per_step, double *bytes_per_step,
                                    int *launches_per_step, char *err, size_t errlen) {
     if (iters < 1) iters = 1;

@@ -148,6 +148,7 @@ def lib():
     _sig(L, "xjh_chain_last_decode_ms", D, P)
     _sig(L, "xjh_chain_time_gemv", I, P, I, C.POINTER(D), C.POINTER(D), C.POINTER(I), CP, S)
     _sig(L, "xjh_spec_generate", I, P, P, I, I, P, I, I, P, C.POINTER(XjhSpecStats), CP, S)
+    _sig(L, "xjh_spec_generate_mtp", I, P, PS, I, P, I, I, P, I, I, P, C.POINTER(XjhSpecStats), CP, S)
     _sig(L, "xjh_malloc", P, S)
     _sig(L, "xjh_free", None, P)
     _sig(L, "xjh_h2d", I, P, P, S)
@@ -417,6 +418,20 @@ def spec_generate(target, draft, k, n_gen, oracle=None, oracle_miss=0):
     rc = lib().xjh_spec_generate(target.ptr, draft.ptr, k, n_gen, _ptr(orc) if orc is not None else None,
                                  len(orc) if orc is not None else 0, oracle_miss, _ptr(out), C.byref(st), err, ERR)
     _check(rc, err, "spec generate")
+    return out, st
+
+
+def spec_generate_mtp(target, mtp_stage, k, prompt, n_gen, oracle=None, oracle_miss=0):
+    """Speculative decoding with the model's MTP stage drafting k tokens; feeds the prompt itself."""
+    out = np.empty(n_gen, np.int32)
+    st = XjhSpecStats()
+    err = _err()
+    p = np.ascontiguousarray(prompt, np.int32)
+    orc = np.ascontiguousarray(oracle, np.int32) if oracle is not None else None
+    rc = lib().xjh_spec_generate_mtp(target.ptr, mtp_stage.ptr, k, _ptr(p), len(p), n_gen,
+                                     _ptr(orc) if orc is not None else None, len(orc) if orc is not None else 0,
+                                     oracle_miss, _ptr(out), C.byref(st), err, ERR)
+    _check(rc, err, "MTP speculative generate")
     return out, st
 
 

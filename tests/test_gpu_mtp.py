@@ -111,3 +111,37 @@ def test_reference_mtp_driver_over_hip_stages(model_dir, shape):
     assert spec.tolist() == plain.tolist() == want.tolist()
     _, st_all = _driver_run(m.ptr, hip, L, 3, prompt, n_gen, oracle=plain)
     assert st_all[1] > 0 and st_all[2] == st_all[1]
+
+
+@pytest.mark.parametrize("shape", ["tiny", "0_8b"])
+def test_native_mtp_driver(model_dir, shape):
+    """xjh_spec_generate_mtp over the device chain: the tokens of plain greedy
+    decoding; the same draft statistics as the reference's driver over the same
+    HIP stages (where that build exists); every draft accepted in the driver's
+    test mode, and one in four perturbed drafts rejected."""
+    if shape == "tiny":
+        m, n_gen = xp.Model(synth_model(model_dir, xp.TINY_MTP, "tiny_mtp")), 24
+    else:
+        m, n_gen = xp.Model(xp.cached_model(xp.CONFIG_0_8B_MTP, "synth08b_mtp")), 32
+    L = m.hp.n_layer
+    prompt = np.random.default_rng(93).integers(0, m.hp.n_vocab, 20).astype(np.int32)
+    print(f"native mtp driver {shape}", flush=True)
+    st1 = xp.HipStage(m, 0, L, 128, 8, True)
+    ch = xp.Chain([st1])
+    plain = np.concatenate([ch.eval(prompt), ch.decode(n_gen - 1)])
+    mt = xp.HipStage(m, L, L + 1, 128, 8, True)
+    out, st = xp.spec_generate_mtp(ch, mt, 3, prompt, n_gen)
+    print(f"{shape}: steps {st.n_steps} drafted {st.n_drafted} accepted {st.n_accepted}")
+    assert out.tolist() == plain.tolist()
+    if orc.ref_available():
+        hip = lambda l0, l1, head: xp.HipStage(m, l0, l1, 128, 8, head)
+        ref_out, ref_st = _driver_run(m.ptr, hip, L, 3, prompt, n_gen)
+        assert ref_out.tolist() == plain.tolist()
+        assert (st.n_steps, st.n_drafted, st.n_accepted) == ref_st
+    out, st = xp.spec_generate_mtp(ch, mt, 3, prompt, n_gen, oracle=plain)
+    assert out.tolist() == plain.tolist() and st.n_accepted == st.n_drafted > 0
+    out, st = xp.spec_generate_mtp(ch, mt, 4, prompt, n_gen, oracle=plain, oracle_miss=4)
+    assert out.tolist() == plain.tolist() and 0 < st.n_accepted < st.n_drafted
+    ch.free()
+    st1.destroy()
+    mt.destroy()
