@@ -26,6 +26,8 @@ Also reported, on the same run:
                 from the plain greedy output, and one in four of them
                 perturbed; tok/s and acceptance, each checked token-identical
                 to plain greedy decoding.
+  speculative_4b_mtp  the same with the model's own MTP layer drafting (the
+                4B shape with one MTP layer added).
 
 usage: python bench.py [--gpus 1] [--steps 512] [--warmup 16] [--no-cpu] [--no-extra]
                        [--copy-calibration MB] [--delta-c3]
@@ -170,6 +172,35 @@ def spec_run(n_prompt=1024, n_gen=128, seed=20261109):
     return res
 
 
+def spec_mtp_run(n_prompt=1024, n_gen=128, seed=20261110):
+    """Speculative decoding with the model's own MTP layer as the drafter (k = 4), on the 4B shape with
+    one MTP layer added (its main layers are those of the 4B model): real drafts (random weights:
+    acceptance near 0), drafts from the plain greedy output, one in four of them perturbed. Every run
+    must reproduce the plain greedy tokens."""
+    cfg = xp.CONFIG_4B.with_(nextn=1)
+    m = xp.Model(model_path(cfg, "synth4b_mtp"))
+    L = m.hp.n_layer
+    n_ctx = n_prompt + n_gen + 16
+    prompt = np.random.default_rng(seed).integers(0, m.hp.n_vocab, n_prompt).astype(np.int32)
+    st = xp.HipStage(m, 0, L, n_ctx, 8, True)
+    ch = xp.Chain([st])
+    plain = np.concatenate([ch.eval(prompt), ch.decode(n_gen - 1)])
+    mt = xp.HipStage(m, L, L + 1, n_ctx, 8, True)
+    res = {"prompt": n_prompt, "tokens": n_gen, "k": 4}
+    for mode, orc, miss in (("mtp_drafts", None, 0), ("oracle_drafts", plain, 0), ("oracle_miss_1_in_4", plain, 4)):
+        out, s = xp.spec_generate_mtp(ch, mt, 4, prompt, n_gen, oracle=orc, oracle_miss=miss)
+        if out.tolist() != plain.tolist():
+            raise RuntimeError(f"MTP speculative decode ({mode}) diverged from plain greedy decoding")
+        res[mode] = {"tok_s": round(n_gen / (s.t_total_ms / 1e3), 1), "verify_passes": s.n_steps,
+                     "drafted": s.n_drafted, "accepted": s.n_accepted, "draft_ms": round(s.t_draft_ms, 1),
+                     "total_ms": round(s.t_total_ms, 1)}
+        log(f"spec mtp {mode}: {res[mode]}")
+    ch.free()
+    st.destroy()
+    mt.destroy()
+    return res
+
+
 def delta_c3(reps=3):
     """Gated DeltaNet prefill on the c3 shape (16 heads, d=128, 2048 tokens from a zero state): the chunk-wise
     MFMA kernels (chunk 64) next to the token-by-token kernel. Wall ms per call include the host copies; the
@@ -263,6 +294,7 @@ def main():
                                 gemv_tokens(xp.Q4_K, 151936, 1024), gemv_tokens(xp.Q4_K, 18432, 2560),
                                 gemv_tokens(xp.Q6_K, 2560, 9216)]
         extra["speculative_4b"] = spec_run()
+        extra["speculative_4b_mtp"] = spec_mtp_run()
         log(f"extra: {extra}")
 
     cpu = None
