@@ -263,6 +263,15 @@ int xjh_delta_step(const float *qkv, int qkv_stride, int k_off, int v_off, const
                    const float *alpha_raw, const float *dt, const float *A, int Hk, int Hv, int S, int T,
                    float eps, float qscale, float *state, float *out, float *ck, int ck_n,
                    char *err, size_t errlen);
+/* One token per row of the device logits [T][n]: the app's sampler, top-k 40
+ * then top-p 0.95 at `temperature` (p_i = exp((v_i - v_0) / temperature) in
+ * double over the 40 largest, sorted descending), the pick made with
+ * rand30[t] / 2^30 (host array, each below 2^30) in place of
+ * arc4random_uniform(1 << 30); temperature <= 0: the first maximum.
+ * Replaces: the app's `sample`, src/xiaoju-pipe/ios/App/XJGlue.c:251-282
+ * (ties among the 40 values ordered by index). */
+int xjh_sample(const float *logits, int n, int T, float temperature, const uint32_t *rand30,
+               int32_t *out_host, char *err, size_t errlen);
 /* First index of the maximum of each of T rows of n floats. */
 int xjh_argmax(const float *x, int n, int T, int32_t *out_host, char *err, size_t errlen);
 /* Gated delta rule (standalone, decay and beta given per token and head):

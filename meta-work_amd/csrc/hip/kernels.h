@@ -190,6 +190,9 @@ int norm_launch(int mode, const float *x, const float *w, int n, int rows, float
 // The same over rows r < rows of n elements at x + r * xs, into out + r * os.
 int norm_rows_launch(int mode, const float *x, int64_t xs, const float *w, int n, int rows, float eps, float *out,
                      int64_t os, hipStream_t st);
+// One token per row of lg [T][V]: top-k 40 / top-p 0.95 at temperature temp
+// with rnd[t] / 2^30 as the uniform number (temp <= 0: the first maximum).
+int sample_launch(const float *lg, int V, int T, float temp, const uint32_t *rnd, int32_t *out, hipStream_t st);
 // g = silu(g) * u over n floats.
 int swiglu_launch(float *g, const float *u, int64_t n, hipStream_t st);
 // NeoX RoPE in place of x[t * tok_stride + h * head_stride + i] for T tokens and

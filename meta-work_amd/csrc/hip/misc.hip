@@ -9,6 +9,9 @@
 //                    advances the step counter (one work-group per token row).
 //   argmax_rows      plain first-maximum argmax of T rows (test entry point).
 //   norm_kernel      RMSNorm / L2 rows (xj_cpu.c:56-61, :185-193).
+//   sample_kernel    top-k 40 / top-p 0.95 sampling at a temperature (the
+//                    app's sampler, ios/App/XJGlue.c:251-282, with the random
+//                    number passed in); temperature <= 0: the greedy token.
 //   swiglu_kernel    g = silu(g) * u (xj_cpu.c:273; test entry point: the
 //                    token loop applies SwiGLU inside the gate|up and down GEMVs).
 #include "common.h"
@@ -119,6 +122,129 @@ int swiglu_launch(float *g, const float *u, int64_t n, hipStream_t st) {
     if (n < 0) return -1;
     if (n == 0) return 0;
     hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, n);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// Row t of lg: radix-select the 40th largest value (ordered 32-bit keys, 8 bits
+// per pass, LDS histograms), take every value above it and the lowest indices
+// of those equal to it (the app's selection keeps the first of equal values),
+// then one thread sorts the 40 by value (ties by index), forms
+// p_i = exp((v_i - v_0) / temp) in double, cuts where the running share first
+// reaches 0.95 and picks with r = rnd[t] / 2^30 times the kept mass.
+constexpr int kTopK = 40;
+__device__ __forceinline__ uint32_t okey(float v) {
+    const uint32_t b = __float_as_uint(v);
+    return v != v ? 0u : (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__global__ __launch_bounds__(256) void sample_kernel(const float *lg, int V, float temp, const uint32_t *rnd, int32_t *out) {
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float *x = lg + (int64_t)t * V;
+    __shared__ unsigned long long best_sh[4];
+    if (!(temp > 0.f)) {   // the greedy token: first maximum
+        unsigned long long b = 0ull;
+        for (int i = tid; i < V; i += 256) {
+            const unsigned long long k = xjd::argmax_key(x[i], (uint32_t)i);
+            b = k > b ? k : b;
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            const unsigned long long q = __shfl_xor(b, off, 64);
+            b = q > b ? q : b;
+        }
+        if ((tid & 63) == 0) best_sh[tid >> 6] = b;
+        __syncthreads();
+        if (tid == 0) {
+            unsigned long long m = best_sh[0];
+            for (int w = 1; w < 4; w++) m = best_sh[w] > m ? best_sh[w] : m;
+            out[t] = (int32_t)xjd::argmax_key_index(m);
+        }
+        return;
+    }
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t pre_sh;
+    __shared__ int need_sh, ngt_sh;
+    __shared__ int cnt_eq[256];
+    __shared__ float cv[kTopK];
+    __shared__ int ci[kTopK];
+    const int K = V < kTopK ? V : kTopK;
+    uint32_t pre = 0, mask = 0;
+    int need = K;   // how many of the elements matching the prefix are still to be taken from the top
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        hist[tid] = 0;
+        __syncthreads();
+        for (int i = tid; i < V; i += 256) {
+            const uint32_t k = okey(x[i]);
+            if ((k & mask) == pre) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int cum = 0, b = 255;
+            for (; b > 0; b--) {
+                if (cum + (int)hist[b] >= need) break;
+                cum += hist[b];
+            }
+            pre_sh = pre | ((uint32_t)b << shift);
+            need_sh = need - cum;
+        }
+        __syncthreads();
+        pre = pre_sh;
+        need = need_sh;
+        mask |= 0xFFu << shift;
+        __syncthreads();
+    }
+    // pre = the K-th largest key; take every key above it and the `need` lowest
+    // indices equal to it. Thread tid scans the contiguous chunk [i0, i1).
+    const int chunk = (V + 255) / 256, i0 = tid * chunk, i1 = i0 + chunk < V ? i0 + chunk : V;
+    int my_eq = 0;
+    for (int i = i0; i < i1; i++) my_eq += okey(x[i]) == pre;
+    cnt_eq[tid] = my_eq;
+    if (tid == 0) ngt_sh = 0;
+    __syncthreads();
+    int before = 0;
+    for (int j = 0; j < tid; j++) before += cnt_eq[j];
+    const int n_gt = K - need;
+    for (int i = i0; i < i1; i++) {
+        const uint32_t k = okey(x[i]);
+        if (k > pre) {
+            const int slot = atomicAdd(&ngt_sh, 1);
+            cv[slot] = x[i];
+            ci[slot] = i;
+        } else if (k == pre) {
+            if (before < need) {
+                cv[n_gt + before] = x[i];
+                ci[n_gt + before] = i;
+            }
+            before++;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        // descending by value, ties by index
+        for (int i = 1; i < K; i++) {
+            const float v = cv[i];
+            const int id = ci[i];
+            int j = i - 1;
+            while (j >= 0 && (cv[j] < v || (cv[j] == v && ci[j] > id))) { cv[j + 1] = cv[j]; ci[j + 1] = ci[j]; j--; }
+            cv[j + 1] = v;
+            ci[j + 1] = id;
+        }
+        double p[kTopK], sum = 0;
+        for (int i = 0; i < K; i++) { p[i] = exp((double)((cv[i] - cv[0]) / temp)); sum += p[i]; }
+        double acc = 0;
+        int cut = K;
+        for (int i = 0; i < K; i++) { acc += p[i] / sum; if (acc >= 0.95) { cut = i + 1; break; } }
+        double s2 = 0;
+        for (int i = 0; i < cut; i++) s2 += p[i];
+        double r = (double)rnd[t] / (double)(1u << 30) * s2;
+        int pick = ci[0];
+        for (int i = 0; i < cut; i++) { r -= p[i]; if (r <= 0) { pick = ci[i]; break; } }
+        out[t] = pick;
+    }
+}
+
+int sample_launch(const float *lg, int V, int T, float temp, const uint32_t *rnd, int32_t *out, hipStream_t st) {
+    if (V < 1 || T < 1) return -1;
+    hipLaunchKernelGGL(sample_kernel, dim3(T), dim3(256), 0, st, lg, V, temp, rnd, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -1551,6 +1551,24 @@ extern "C" int xjh_delta_step(const float *qkv, int qkv_stride, int k_off, int v
     return ops_done(err, errlen);
 }
 
+extern "C" int xjh_sample(const float *logits, int n, int T, float temperature, const uint32_t *rand30, int32_t *out_host,
+                          char *err, size_t errlen) {
+    if (!ops_stream()) return -1;
+    if (n < 1 || T < 1) { snprintf(err, errlen, "sample: bad shape (n=%d, T=%d)", n, T); return -1; }
+    for (int t = 0; t < T; t++)
+        if (rand30[t] >= (1u << 30)) { snprintf(err, errlen, "sample: random number %u not below 2^30", rand30[t]); return -1; }
+    uint32_t *d = nullptr;
+    if (hipMalloc(&d, 8 * (size_t)T) != hipSuccess) { snprintf(err, errlen, "hipMalloc failed"); return -1; }
+    int32_t *o = (int32_t *)(d + T);
+    int rc = hipMemcpy(d, rand30, 4 * (size_t)T, hipMemcpyHostToDevice) == hipSuccess ? 0 : -1;
+    if (!rc && sample_launch(logits, n, T, temperature, d, o, g_stream)) rc = -1;
+    if (!rc) rc = ops_done(err, errlen);
+    else snprintf(err, errlen, "sample launch failed");
+    if (!rc && hipMemcpy(out_host, o, 4 * (size_t)T, hipMemcpyDeviceToHost) != hipSuccess) rc = -1;
+    (void)hipFree(d);
+    return rc;
+}
+
 extern "C" int xjh_argmax(const float *x, int n, int T, int32_t *out_host, char *err, size_t errlen) {
     if (!ops_stream()) return -1;
     int32_t *d = nullptr;

@@ -165,6 +165,7 @@ def lib():
     _sig(L, "xjh_delta_recurrent", I, I, I, I, P, P, P, P, P, F, P, P, CP, S)
     _sig(L, "xjh_delta_chunked", I, I, I, I, I, P, P, P, P, P, F, P, P, CP, S)
     _sig(L, "xjh_swiglu", I, P, P, I64, CP, S)
+    _sig(L, "xjh_sample", I, P, I, I, F, P, P, CP, S)
     _sig(L, "xjh_delta_step", I, P, I, I, I, P, P, P, P, I, I, I, I, F, F, P, P, P, I, CP, S)
     _sig(L, "xjh_rope", I, P, I, I, I64, I64, I, I, F, CP, S)
     _sig(L, "xjh_conv_silu", I, P, P, P, I, I, I, P, I, CP, S)
@@ -569,6 +570,20 @@ def delta(q, k, v, decay, beta, state, qscale, chunk=0):
                                        err, ERR)
     _check(rc, err, "delta")
     return do.get(np.float32, (T, H, S)), ds.get(np.float32, (H, S, S))
+
+
+def sample(logits, temperature, rand30):
+    """Top-k 40 / top-p 0.95 sampling on the GPU of each row of logits [T][V] with
+    rand30[t] / 2^30 as the uniform number; temperature <= 0: greedy."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    if lg.ndim == 1:
+        lg = lg[None]
+    r = np.ascontiguousarray(rand30, np.uint32).reshape(-1)
+    d = Dev(lg)
+    out = np.empty(lg.shape[0], np.int32)
+    err = _err()
+    _check(lib().xjh_sample(d.ptr, lg.shape[1], lg.shape[0], temperature, _ptr(r), _ptr(out), err, ERR), err, "sample")
+    return out
 
 
 def swiglu(g, u):

@@ -57,6 +57,7 @@ def olib():
         _sig(L, "xjo_argmax", I, P, I)
         _sig(L, "xjo_delta_recurrent", None, I, I, I, P, P, P, P, P, F, P, P)
         _sig(L, "xjo_conv_silu", None, I, I, P, P, P)
+        _sig(L, "xjo_sample", I, P, I, F, U32)
         _sig(L, "xjo_swiglu", None, S, P, P)
         _sig(L, "xjo_delta_step", None, I, I, I, F, F, P, P, P, P, P, P, P, P, P, P)
         _sig(L, "xjo_attn_decode", None, I, I, I, I, I, F, F, I, I, P, P, P, P, P, P, P, P)
@@ -159,6 +160,11 @@ def rope(v, n_rot, pos, base, ref=False):
     f = rlib().ref_rope if ref else olib().xjo_rope
     f(_ptr(v), n_rot, pos, base)
     return v
+
+
+def sample(lg, temp, rand30):
+    lg = np.ascontiguousarray(lg, np.float32)
+    return olib().xjo_sample(_ptr(lg), lg.size, temp, int(rand30))
 
 
 def swiglu(g, u):

@@ -55,6 +55,9 @@ int xjo_greedy(xj_stage **stages, int n_stages, const int32_t *prompt, int n_pro
 /* First index of the maximum (strict >), xj_spec.c:12-16. */
 int xjo_argmax(const float *x, int n);
 
+/* The app's top-k 40 / top-p 0.95 sampler (ios/App/XJGlue.c:251-282), the
+ * uniform number rand30 / 2^30 passed in. */
+int xjo_sample(const float *lg, int n, float temp, uint32_t rand30);
 /* One token of the causal depthwise conv + SiLU (xj_cpu.c:172-182), x and
  * state [C][KC-1] updated in place. */
 void xjo_conv_silu(int C, int KC, float *x, const float *w, float *state);

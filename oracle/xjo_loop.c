@@ -6,6 +6,8 @@
  *   xjo_greedy          <- eval_once, no-remote branch, src/xiaoju-pipe/core/xj_net.c:532-559
  *                          (chunks of the smallest max_batch, logits of the last row only)
  *                          driven by the greedy loop of src/xiaoju-pipe/tools/xjpipe-host.c:131-144
+ *   xjo_sample          <- the app's sampler, src/xiaoju-pipe/ios/App/XJGlue.c:251-282
+ *                          (the uniform number passed in)
  *   xjo_delta_recurrent <- the per-head update of src/xiaoju-pipe/core/xj_cpu.c:203-213
  *                          (decay and beta are inputs instead of being derived from alpha/dt/A)
  *
@@ -20,6 +22,45 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+
+/* The app's sampler (ios/App/XJGlue.c:251-282) with the uniform number
+ * given as rand30 (< 2^30) in place of arc4random_uniform(1 << 30): greedy at
+ * temp <= 0; otherwise the 40 largest values (the first of equal values kept),
+ * sorted descending, p_i = exp((v_i - v_0) / temp) in double, cut where the
+ * running share first reaches 0.95, pick with r = rand30 / 2^30 * kept mass. */
+int xjo_sample(const float *lg, int n, float temp, uint32_t rand30) {
+    int best = 0;
+    for (int i = 1; i < n; i++) if (lg[i] > lg[best]) best = i;
+    if (temp <= 0) return best;
+    enum { K = 40 };
+    int idx[K], k = 0, mi = 0;
+    float val[K];
+    for (int i = 0; i < n; i++) {
+        const float v = lg[i];
+        if (k < K) {
+            idx[k] = i; val[k] = v;
+            if (v < val[mi]) mi = k;
+            k++;
+        } else if (v > val[mi]) {
+            idx[mi] = i; val[mi] = v;
+            mi = 0;
+            for (int j = 1; j < K; j++) if (val[j] < val[mi]) mi = j;
+        }
+    }
+    for (int i = 0; i < k; i++)
+        for (int j = i + 1; j < k; j++)
+            if (val[j] > val[i]) { float tv = val[i]; val[i] = val[j]; val[j] = tv; int ti = idx[i]; idx[i] = idx[j]; idx[j] = ti; }
+    double p[K], sum = 0;
+    for (int i = 0; i < k; i++) { p[i] = exp((val[i] - val[0]) / temp); sum += p[i]; }
+    double acc = 0;
+    int cut = k;
+    for (int i = 0; i < k; i++) { acc += p[i] / sum; if (acc >= 0.95) { cut = i + 1; break; } }
+    double s2 = 0;
+    for (int i = 0; i < cut; i++) s2 += p[i];
+    double r = (double)rand30 / (double)(1u << 30) * s2;
+    for (int i = 0; i < cut; i++) { r -= p[i]; if (r <= 0) return idx[i]; }
+    return idx[0];
+}
 
 int xjo_argmax(const float *x, int n) {
     int best = 0;

@@ -177,3 +177,17 @@ def test_delta_step_forms_agree_bit_for_bit(monkeypatch):
         res.append(xp.delta_step(qkv, ko, vo, beta, alpha, dt, A, 16, 32, 128, 1e-6, 0.0883883, st, 5))
     for a, b in zip(res[0], res[1]):
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("V", [25, 1000, 151936])
+def test_sample_matches_oracle(V):
+    """The device sampler against the oracle's restatement of the app's sampler,
+    row by row, over temperatures from greedy to nearly uniform."""
+    rng = np.random.default_rng(V + 7)
+    T = 14
+    lg = (rng.standard_normal((T, V)) * 2).astype(np.float32)
+    r30 = rng.integers(0, 1 << 30, T).astype(np.uint32)
+    for temp in (0.0, 0.05, 0.7, 1.3, 50.0):
+        got = xp.sample(lg, temp, r30)
+        want = [orc.sample(lg[t], temp, int(r30[t])) for t in range(T)]
+        assert got.tolist() == want, temp

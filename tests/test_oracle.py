@@ -553,3 +553,47 @@ def test_reference_mtp_driver_over_oracle_stages(model_dir):
     _, st_all = run(m.ptr, False, 3, oracle=plain)
     assert st_all[1] > 0 and st_all[2] == st_all[1]
     orc.rlib().ref_model_free(r)
+
+
+def _np_sample(lg, temp, r30):
+    """The app's sampler from its definition: the 40 largest by value (stable
+    order for equal values), p_i = exp((v_i - v_0) / temp), cut at 0.95 of the
+    mass, r = r30 / 2^30 times the kept mass, first i where the running sum of p
+    reaches r."""
+    if temp <= 0:
+        return int(np.argmax(lg))
+    order = np.argsort(-lg, kind="stable")[:40]
+    v = lg[order]
+    p = np.exp(((v - v[0]).astype(np.float32) / np.float32(temp)).astype(np.float64))
+    tot = 0.0
+    for x in p:
+        tot += x
+    acc, cut = 0.0, len(p)
+    for i, x in enumerate(p):
+        acc += x / tot
+        if acc >= 0.95:
+            cut = i + 1
+            break
+    s2 = 0.0
+    for x in p[:cut]:
+        s2 += x
+    r = r30 / float(1 << 30) * s2
+    for i in range(cut):
+        r -= p[i]
+        if r <= 0:
+            return int(order[i])
+    return int(order[0])
+
+
+@pytest.mark.parametrize("n", [25, 1000, 151936])
+def test_sampler_matches_definition(n):
+    rng = np.random.default_rng(n)
+    for trial in range(12):
+        lg = (rng.standard_normal(n) * rng.uniform(0.5, 4)).astype(np.float32)
+        temp = [0.0, 0.01, 0.3, 0.7, 1.0, 1.5, 100.0][trial % 7]
+        r30 = int(rng.integers(0, 1 << 30))
+        assert orc.sample(lg, temp, r30) == _np_sample(lg, temp, r30), (trial, temp)
+    lg = rng.standard_normal(n).astype(np.float32)
+    top = int(np.argmax(lg))
+    assert orc.sample(lg, 1e-4, (1 << 30) - 1) == top          # a tiny temperature keeps only the maximum
+    assert orc.sample(lg, 1e4, 0) == top                        # r = 0 takes the first kept token
