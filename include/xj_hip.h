@@ -14,6 +14,8 @@
  *  2. Host-side counterparts of the reference loader, needed because the
  *     reference sources do not ship with this library:
  *       xj_model_load / xj_model_free <- src/xiaoju-pipe/core/xj_model.h:125,130
+ *       xj_model_load_layers          <- src/xiaoju-pipe/core/xj_model.h:66
+ *       xj_model_ranges               <- src/xiaoju-pipe/core/xj_model.h:78
  *       xj_row_bytes / xj_type_block  <- src/xiaoju-pipe/core/gguf.h:81-83
  *     plus a writer for synthetic qwen35 GGUF files and the Q4_K / Q6_K /
  *     Q8_0 quantizers it uses (the reference has none for K-quants).
@@ -79,6 +81,20 @@ uint64_t    xj_row_bytes(uint32_t type, int64_t n);
 const char *xj_type_name(uint32_t type);
 xj_model   *xj_model_load(const char *path, char *err, size_t errlen);
 void        xj_model_free(xj_model *m);
+/* Partial load for a stage of layers [l0, l1) (xj_model.h:66, xj_model.c:214-233):
+ * only the GGUF header is read, then one mapping spans the merged byte ranges
+ * of those layers (with_io: also token_embd, output_norm, output). Tensors
+ * outside the mapping keep data = NULL, so a stage over other layers fails
+ * ("weights are not mapped"); the file may be a partial download as long as
+ * it reaches the end of that span. Error for an empty or out-of-range [l0, l1). */
+xj_model   *xj_model_load_layers(const char *path, int l0, int l1, bool with_io, char *err, size_t errlen);
+/* Byte ranges [lo, hi) of the file that layers [l0, l1) (and with include_embd
+ * the embedding, output norm and untied head) occupy, sorted, ranges at most
+ * 4096 bytes apart merged; returns their count, at most max (xj_model.h:78,
+ * xj_model.c:308-328). */
+int         xj_model_ranges(const xj_model *m, int l0, int l1, bool include_embd, uint64_t (*ranges)[2], int max);
+/* Total tensor bytes of layers [l0, l1) (xj_model.h:79, xj_model.c:330-338). */
+uint64_t    xj_model_layer_bytes(const xj_model *m, int l0, int l1);
 
 /* --------------------------------------------------- synthetic models -- */
 

@@ -10,6 +10,9 @@
 //   per-layer tensor names     src/xiaoju-pipe/core/xj_model.c:62-101
 //   MTP layer                  src/xiaoju-pipe/core/xj_model.c:104-127 (blk.{block_count-1}
 //                              into layers[n_layer], its nextn.* tensors)
+//   layer-range load           src/xiaoju-pipe/core/xj_model.c:214-233, 303-328 and
+//                              gguf.c:216-262 (header read with pread, one mapping of
+//                              the merged byte ranges, pointers outside it left NULL)
 #include "xj_hip.h"
 
 #include <fcntl.h>
@@ -19,6 +22,8 @@
 
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
+#include <cstddef>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -88,8 +93,10 @@ bool skip(Reader &r, uint32_t t, KV *kv) {
 
 struct xj_gguf_file {
     int fd = -1;
-    const uint8_t *map = nullptr;
+    const uint8_t *map = nullptr;      // mapping of file bytes [map_off, map_off + map_len)
+    uint64_t map_off = 0, map_len = 0;
     uint64_t size = 0, data_off = 0;
+    std::vector<uint8_t> hdr;          // header bytes when only the header was read
     uint32_t alignment = 32;
     std::vector<KV> kv;
     std::vector<TInfo> tensors;
@@ -141,8 +148,13 @@ struct xj_gguf_file {
         *out = (uint32_t)v;
         return true;
     }
+    // File offset -> pointer into the mapping, NULL when not mapped (gguf.c:257-260).
+    const void *ptr(uint64_t file_off, uint64_t nbytes) const {
+        if (!map || file_off < map_off || file_off + nbytes > map_off + map_len) return nullptr;
+        return map + (file_off - map_off);
+    }
     ~xj_gguf_file() {
-        if (map) munmap((void *)map, size);
+        if (map) munmap((void *)map, map_len);
         if (fd >= 0) close(fd);
     }
 };
@@ -237,6 +249,7 @@ static xj_gguf_file *gguf_open(const char *path, char *err, size_t errlen) {
     xj_gguf_file *f = gguf_parse((const uint8_t *)m, (uint64_t)st.st_size, err, errlen);
     if (!f) { munmap(m, (size_t)st.st_size); close(fd); return nullptr; }
     f->fd = fd; f->map = (const uint8_t *)m; f->size = (uint64_t)st.st_size;
+    f->map_off = 0; f->map_len = f->size;
     for (auto &t : f->tensors)
         if (f->data_off + t.offset + t.nbytes > f->size) {
             snprintf(err, errlen, "tensor %s runs past the end of the file", t.name.c_str());
@@ -244,6 +257,45 @@ static xj_gguf_file *gguf_open(const char *path, char *err, size_t errlen) {
             return nullptr;
         }
     return f;
+}
+
+// Reads only the header (pread into a buffer that doubles from 16 MiB until the
+// parse succeeds); no tensor bytes are mapped and tensors may lie past the end of
+// a partly downloaded file (gguf.c:216-243).
+static xj_gguf_file *gguf_open_header(const char *path, char *err, size_t errlen) {
+    int fd = open(path, O_RDONLY);
+    if (fd < 0) { snprintf(err, errlen, "cannot open %s", path); return nullptr; }
+    struct stat st;
+    if (fstat(fd, &st) != 0 || st.st_size < 16) { close(fd); snprintf(err, errlen, "file too small"); return nullptr; }
+    const uint64_t size = (uint64_t)st.st_size;
+    for (uint64_t want = 16u << 20;; want *= 2) {
+        if (want > size) want = size;
+        std::vector<uint8_t> buf(want);
+        uint64_t got = 0;
+        while (got < want) {
+            ssize_t k = pread(fd, buf.data() + got, want - got, (off_t)got);
+            if (k <= 0) break;
+            got += (uint64_t)k;
+        }
+        xj_gguf_file *f = gguf_parse(buf.data(), got, err, errlen);
+        if (f) {
+            f->hdr = std::move(buf);   // the key/value pointers stay valid: the storage moves with it
+            f->fd = fd; f->size = size;
+            return f;
+        }
+        if (got < want || want >= size) { close(fd); return nullptr; }
+    }
+}
+
+// Maps file bytes [lo, hi) once, from the page below lo (gguf.c:245-255).
+static bool gguf_map_range(xj_gguf_file *f, uint64_t lo, uint64_t hi, char *err, size_t errlen) {
+    if (f->map) { snprintf(err, errlen, "already mapped"); return false; }
+    if (hi > f->size || lo >= hi) { snprintf(err, errlen, "mapping range runs past the end of the file (incomplete download?)"); return false; }
+    const uint64_t page = (uint64_t)getpagesize(), start = lo / page * page;
+    void *m = mmap(nullptr, (size_t)(hi - start), PROT_READ, MAP_SHARED, f->fd, (off_t)start);
+    if (m == MAP_FAILED) { snprintf(err, errlen, "mapping %llu MB failed", (unsigned long long)((hi - start) >> 20)); return false; }
+    f->map = (const uint8_t *)m; f->map_off = start; f->map_len = hi - start;
+    return true;
 }
 
 // ------------------------------------------------------------------ model --
@@ -262,8 +314,8 @@ static bool get_w(const xj_gguf_file *g, const char *name, xj_w *w, bool require
         snprintf(err, errlen, "tensor %s has unsupported type %s", name, xj_type_name(t->type));
         return false;
     }
-    w->data = g->map + g->data_off + t->offset;
     w->file_off = g->data_off + t->offset;
+    w->data = g->ptr(w->file_off, t->nbytes);
     w->nbytes = t->nbytes;
     w->type = t->type;
     w->ne0 = t->ne[0];
@@ -367,9 +419,9 @@ static bool load_mtp(const xj_gguf_file *g, xj_model *m, int block_count, char *
     return true;
 }
 
-extern "C" xj_model *xj_model_load(const char *path, char *err, size_t errlen) {
-    xj_gguf_file *g = gguf_open(path, err, errlen);
-    if (!g) return nullptr;
+// The model table from a parsed file; tensors outside its mapping get data = NULL
+// (xj_model_from_gguf, xj_model.c:129-202). Takes g; deletes it on failure.
+static xj_model *model_from_gguf(xj_gguf_file *g, char *err, size_t errlen) {
     std::string arch;
     if (!g->get_str("general.architecture", &arch) || arch != "qwen35") {
         snprintf(err, errlen, "not a qwen35 model (general.architecture)");
@@ -439,6 +491,86 @@ extern "C" xj_model *xj_model_load(const char *path, char *err, size_t errlen) {
         h = fnv(h, &t.offset, sizeof t.offset);
     }
     m->fingerprint = h;
+    return m;
+}
+
+extern "C" xj_model *xj_model_load(const char *path, char *err, size_t errlen) {
+    xj_gguf_file *g = gguf_open(path, err, errlen);
+    return g ? model_from_gguf(g, err, errlen) : nullptr;
+}
+
+// The xj_w fields of a layer, attn_norm to the end (the reference walks them the same way).
+static int layer_ws(xj_layer *L, xj_w **ws) {
+    *ws = &L->attn_norm;
+    return (int)((sizeof(xj_layer) - offsetof(xj_layer, attn_norm)) / sizeof(xj_w));
+}
+
+static int add_range(const xj_w *w, uint64_t (*r)[2], int n, int max) {
+    if (!w->nbytes || n >= max) return n;
+    r[n][0] = w->file_off;
+    r[n][1] = w->file_off + w->nbytes;
+    return n + 1;
+}
+
+extern "C" int xj_model_ranges(const xj_model *m, int l0, int l1, bool include_embd, uint64_t (*r)[2], int max) {
+    int n = 0;
+    if (include_embd) {
+        n = add_range(&m->tok_embd, r, n, max);
+        n = add_range(&m->output_norm, r, n, max);
+        if (m->output.file_off != m->tok_embd.file_off) n = add_range(&m->output, r, n, max);
+    }
+    for (int i = l0; i < l1; i++) {
+        xj_w *ws;
+        const int count = layer_ws(const_cast<xj_layer *>(&m->layers[i]), &ws);
+        for (int k = 0; k < count; k++) n = add_range(&ws[k], r, n, max);
+    }
+    std::vector<std::pair<uint64_t, uint64_t>> v(n);
+    for (int i = 0; i < n; i++) v[i] = {r[i][0], r[i][1]};
+    std::stable_sort(v.begin(), v.end(), [](const auto &a, const auto &b) { return a.first < b.first; });
+    for (int i = 0; i < n; i++) { r[i][0] = v[i].first; r[i][1] = v[i].second; }
+    // ranges at most one page apart become one, so a stage maps one span per run of tensors
+    int k = 0;
+    for (int i = 0; i < n; i++) {
+        if (k && r[i][0] <= r[k - 1][1] + 4096) { if (r[i][1] > r[k - 1][1]) r[k - 1][1] = r[i][1]; }
+        else { r[k][0] = r[i][0]; r[k][1] = r[i][1]; k++; }
+    }
+    return k;
+}
+
+extern "C" uint64_t xj_model_layer_bytes(const xj_model *m, int l0, int l1) {
+    uint64_t s = 0;
+    for (int i = l0; i < l1; i++) {
+        xj_w *ws;
+        const int count = layer_ws(const_cast<xj_layer *>(&m->layers[i]), &ws);
+        for (int k = 0; k < count; k++) s += ws[k].nbytes;
+    }
+    return s;
+}
+
+extern "C" xj_model *xj_model_load_layers(const char *path, int l0, int l1, bool with_io, char *err, size_t errlen) {
+    xj_gguf_file *g = gguf_open_header(path, err, errlen);
+    if (!g) return nullptr;
+    xj_model *m = model_from_gguf(g, err, errlen);
+    if (!m) return nullptr;
+    if (l0 < 0 || l1 > m->hp.n_layer || l0 >= l1) {
+        snprintf(err, errlen, "bad layer range [%d,%d)", l0, l1);
+        xj_model_free(m);
+        return nullptr;
+    }
+    uint64_t r[512][2];
+    const int n = xj_model_ranges(m, l0, l1, with_io, r, 512);
+    if (n <= 0 || !gguf_map_range(g, r[0][0], r[n - 1][1], err, errlen)) {
+        if (n <= 0) snprintf(err, errlen, "these layers hold no weights");
+        xj_model_free(m);
+        return nullptr;
+    }
+    auto fix = [&](xj_w *w) { if (w->nbytes) w->data = g->ptr(w->file_off, w->nbytes); };
+    fix(&m->tok_embd); fix(&m->output_norm); fix(&m->output);
+    for (int i = 0; i < m->hp.n_layer; i++) {
+        xj_w *ws;
+        const int count = layer_ws(&m->layers[i], &ws);
+        for (int k = 0; k < count; k++) fix(&ws[k]);
+    }
     return m;
 }
 

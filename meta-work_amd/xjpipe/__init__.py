@@ -133,6 +133,9 @@ def lib():
     _sig(L, "xj_type_name", CP, U32)
     _sig(L, "xj_model_load", C.POINTER(XjModel), CP, CP, S)
     _sig(L, "xj_model_free", None, C.POINTER(XjModel))
+    _sig(L, "xj_model_load_layers", C.POINTER(XjModel), CP, C.c_int, C.c_int, C.c_bool, CP, S)
+    _sig(L, "xj_model_ranges", C.c_int, C.POINTER(XjModel), C.c_int, C.c_int, C.c_bool, C.POINTER(C.c_uint64), C.c_int)
+    _sig(L, "xj_model_layer_bytes", C.c_uint64, C.POINTER(XjModel), C.c_int, C.c_int)
     _sig(L, "xjs_fill_normal", None, P, I64, U64, F)
     _sig(L, "xjs_tensor_seed", U64, U64, CP)
     _sig(L, "xjs_quantize", I, U32, P, I64, I64, P, CP, S)
@@ -244,11 +247,16 @@ def quantize(t, x):
 
 
 class Model:
-    """xj_model_load: the GGUF is mmapped; weights stay on the host until a stage uploads them."""
+    """xj_model_load: the GGUF is mmapped; weights stay on the host until a stage uploads them.
+    With layers=(l0, l1): xj_model_load_layers, only the header is read and one mapping
+    covers those layers (with_io: the embedding and head as well); other weights are NULL."""
 
-    def __init__(self, path):
+    def __init__(self, path, layers=None, with_io=False):
         err = _err()
-        self.ptr = lib().xj_model_load(path.encode(), err, ERR)
+        if layers is None:
+            self.ptr = lib().xj_model_load(path.encode(), err, ERR)
+        else:
+            self.ptr = lib().xj_model_load_layers(path.encode(), int(layers[0]), int(layers[1]), bool(with_io), err, ERR)
         if not self.ptr:
             raise XjError(err.value.decode())
         self.path = path
@@ -271,6 +279,12 @@ class Model:
             self.close()
         except Exception:
             pass
+
+    def ranges(self, l0, l1, include_embd=False, max_ranges=512):
+        """xj_model_ranges: merged file byte ranges [(lo, hi), ...] of layers [l0, l1)."""
+        r = (C.c_uint64 * (2 * max_ranges))()
+        n = lib().xj_model_ranges(self.ptr, l0, l1, include_embd, r, max_ranges)
+        return [(r[2 * i], r[2 * i + 1]) for i in range(n)]
 
     def tensor_bytes(self, w):
         """Raw GGUF bytes of an XjW as a numpy uint8 view (no copy)."""

@@ -38,6 +38,10 @@ void ref_rope(float *v, int n_rot, int pos, float base) { rope(v, n_rot, pos, ba
 
 xj_model *ref_model_load(const char *path, char *err, size_t errlen) { return xj_model_load(path, err, errlen); }
 void ref_model_free(xj_model *m) { xj_model_free(m); }
+xj_model *ref_model_load_layers(const char *path, int l0, int l1, bool with_io, char *err, size_t errlen) {
+    return xj_model_load_layers(path, l0, l1, with_io, err, errlen);
+}
+int ref_model_ranges(const xj_model *m, int l0, int l1, bool io, uint64_t (*r)[2], int max) { return xj_model_ranges(m, l0, l1, io, r, max); }
 xj_stage *ref_stage_new(const xj_model *m, int l0, int l1, int n_ctx, int max_batch, bool has_head, char *err, size_t errlen) {
     return xj_cpu_stage_new(m, l0, l1, n_ctx, max_batch, has_head, err, errlen);
 }

@@ -227,3 +227,33 @@ def test_spec_decode_equals_greedy(tiny, tiny_draft_path, mode):
         o.free()
     t.destroy()
     d.destroy()
+
+
+def test_stage_over_a_layer_range_load(tiny, tiny_path, tmp_path):
+    """A stage built from xj_model_load_layers on a file cut after its layers
+    (a partial download, xj_model.c:214-233) computes bit for bit what the stage
+    built from the whole file computes; a stage over layers outside the mapping
+    is refused."""
+    m, L = tiny, tiny.hp.n_layer
+    part0 = xp.Model(tiny_path, layers=(0, L // 2))
+    hi = part0.ranges(0, L // 2)[-1][1]
+    part0.close()
+    cut = str(tmp_path / "front.gguf")
+    with open(tiny_path, "rb") as f, open(cut, "wb") as g:
+        g.write(f.read(hi))
+    part = xp.Model(cut, layers=(0, L // 2))
+    toks = prompt_ids(m, 9, 5)
+    x = embed(m, toks)
+    a = xp.HipStage(part, 0, L // 2, 64, 16, False)
+    b = xp.HipStage(m, 0, L // 2, 64, 16, False)
+    xa, xb = a.forward(x[:8].copy()), b.forward(x[:8].copy())
+    assert np.array_equal(xa, xb)
+    xa, xb = a.forward(x[8:].copy()), b.forward(x[8:].copy())
+    assert np.array_equal(xa, xb)
+    a.destroy()
+    b.destroy()
+    with pytest.raises(xp.XjError, match="not mapped"):
+        xp.HipStage(part, L // 2, L, 64, 16, False)
+    with pytest.raises(xp.XjError, match="not mapped"):
+        xp.HipStage(part, 0, L // 2, 64, 16, True)
+    part.close()

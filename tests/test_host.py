@@ -113,3 +113,72 @@ def test_quantizer_edge_rows():
         assert np.array_equal(y[0], x[0])
         assert np.isfinite(y).all()
         assert rel_l2(y[3], x[3]) < 0.1
+
+
+def _truncated_copy(src, dst, nbytes):
+    with open(src, "rb") as f, open(dst, "wb") as g:
+        g.write(f.read(nbytes))
+    return dst
+
+
+@pytest.mark.skipif(not orc.ref_available(), reason="reference build (oracle/_ref) not present")
+@pytest.mark.parametrize("l0,l1,io", [(0, 4, False), (4, 8, False), (2, 3, False), (0, 2, True), (6, 8, True), (0, 8, True)])
+def test_layer_range_loader_matches_the_reference(tiny_path, tmp_path, l0, l1, io):
+    """xj_model_load_layers and xj_model_ranges against the reference's own
+    (xj_model.c:214-233, 308-328): the same byte ranges, the same tensor table,
+    the same tensors left unmapped (data NULL), and the mapped bytes equal to
+    the file's. A file cut right after the last range still loads in both,
+    while the full loader rejects it; bad ranges fail in both."""
+    full = xp.Model(tiny_path)
+    L = full.hp.n_layer
+    part = xp.Model(tiny_path, layers=(l0, l1), with_io=io)
+    err = orc.C.create_string_buffer(512)
+    r = orc.rlib().ref_model_load_layers(tiny_path.encode(), l0, l1, io, err, 512)
+    assert r, err.value
+    rm = r.contents
+    assert bytes(rm.hp) == bytes(part.m.hp) and rm.fingerprint == part.m.fingerprint == full.m.fingerprint
+
+    rr = (orc.C.c_uint64 * 1024)()
+    n = orc.rlib().ref_model_ranges(r, l0, l1, io, rr, 512)
+    ranges = part.ranges(l0, l1, io)
+    assert ranges == [(rr[2 * i], rr[2 * i + 1]) for i in range(n)]
+    assert ranges == full.ranges(l0, l1, io)
+    lo, hi = ranges[0][0], ranges[-1][1]
+    map_lo = lo // os.sysconf("SC_PAGE_SIZE") * os.sysconf("SC_PAGE_SIZE")  # the mapping starts on a page
+    assert sum(b - a for a, b in ranges) >= xp.lib().xj_model_layer_bytes(part.ptr, l0, l1)
+
+    def check(mine, ref, whole):
+        assert w_tuple(mine) == w_tuple(ref)
+        assert (mine.data is None) == (ref.data is None)
+        mapped = bool(mine.nbytes) and map_lo <= mine.file_off and mine.file_off + mine.nbytes <= hi
+        assert (mine.data is not None) == mapped
+        if mapped:
+            assert np.array_equal(part.tensor_bytes(mine), full.tensor_bytes(whole))
+
+    for name in ("tok_embd", "output_norm", "output"):
+        check(getattr(part.m, name), getattr(rm, name), getattr(full.m, name))
+    for i in range(L):
+        for f in xp._LAYER_W:
+            check(getattr(part.m.layers[i], f), getattr(rm.layers[i], f), getattr(full.m.layers[i], f))
+    for i in range(l0, l1):
+        assert part.m.layers[i].ffn_down.data is not None
+    orc.rlib().ref_model_free(r)
+    part.close()
+
+    cut = _truncated_copy(tiny_path, str(tmp_path / "cut.gguf"), hi)
+    if hi < os.path.getsize(tiny_path):
+        with pytest.raises(xp.XjError):
+            xp.Model(cut)
+    p2 = xp.Model(cut, layers=(l0, l1), with_io=io)
+    r2 = orc.rlib().ref_model_load_layers(cut.encode(), l0, l1, io, err, 512)
+    assert r2, err.value
+    for i in range(l0, l1):
+        assert np.array_equal(p2.tensor_bytes(p2.m.layers[i].wo if not p2.m.layers[i].recurrent else p2.m.layers[i].ssm_out),
+                              full.tensor_bytes(full.m.layers[i].wo if not full.m.layers[i].recurrent else full.m.layers[i].ssm_out))
+    orc.rlib().ref_model_free(r2)
+    p2.close()
+
+    for a, b in ((l1, l0), (0, L + 1), (-1, 2)):
+        with pytest.raises(xp.XjError):
+            xp.Model(tiny_path, layers=(a, b))
+        assert not orc.rlib().ref_model_load_layers(tiny_path.encode(), a, b, io, err, 512)
