@@ -222,6 +222,16 @@ int xjh_dequant(uint32_t type, const void *dw, int64_t n_rows, int64_t k, int64_
 /* y[t][r] = W[r] . x[t] (add != 0: y += ...), T in 1..max, fp32 accumulate. */
 int xjh_gemv(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T,
              float *y, int add, char *err, size_t errlen);
+/* The same product for a prefill chunk on the matrix cores: Q4_K or Q6_K
+ * rows, k % 256 == 0, T in 1..64. Integer sub-block sums are those of
+ * xjh_gemv (v_mfma_i32_16x16x32_i8 in place of dot4), so the two agree to
+ * fp32 rounding. Counterpart of the Metal batched kernel mvb
+ * (src/xiaoju-pipe/metal/xj_kernels.metal:84-388) for long batches. */
+int xjh_gemm(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T,
+             float *y, int add, char *err, size_t errlen);
+/* Mean ms of xjh_gemm (prep launch included) over rotating copies, like xjh_gemv_time. */
+double xjh_gemm_time(uint32_t type, void *const *dws, int n_copies, int64_t n_rows, int64_t k,
+                     const float *x, int T, float *y, int iters, char *err, size_t errlen);
 /* Time `iters` back-to-back launches of xjh_gemv over n_copies weights
  * (rotating, to defeat the caches), with HIP events on the library stream.
  * Returns the mean ms per launch, or -1. */

@@ -116,6 +116,21 @@ int gemv_init(char *err, size_t errlen);       // raise the dynamic-LDS limit on
 int gemv_max_tile(int K);                       // largest T tile whose activations fit in LDS
 size_t gemv_xq_bytes(int K);                    // xq bytes for the largest tile of this K
 
+// Multi-token GEMM on the matrix cores (gemm.hip): y[t][r] (+)= W[r] . v[t] for
+// T in 1..gemm_max_tokens() tokens of prepared activations (xq, stride xs per
+// token), Q4_K or Q6_K rows. With `part` (capacity part_floats) short weights
+// split K over work-groups and a reduce launch adds the splits in order.
+struct GemmArgs {
+    const uint8_t *w; uint32_t type; int32_t N, K, T;
+    const uint8_t *xq; int64_t xs;
+    float *part;
+    float *y; int32_t ys; int32_t add;
+    int32_t nsplit;   // set by gemm_launch
+};
+int gemm_max_tokens();
+int gemm_splits(int N, int K, int T, int64_t part_floats);
+int gemm_launch(const GemmArgs &a, int64_t part_floats, hipStream_t st);
+
 // Repack a GGUF tensor into the device layout. dst must hold `bytes` =
 // n_rows * row_bytes(type, k); src is host memory in GGUF layout.
 int upload_repack(uint32_t type, const void *src, int64_t n_rows, int64_t k, uint8_t *dst,

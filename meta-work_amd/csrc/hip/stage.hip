@@ -1414,6 +1414,69 @@ extern "C" int xjh_gemv(uint32_t type, const void *dw, int64_t n_rows, int64_t k
     return ops_done(err, errlen);
 }
 
+// Prepared activations of T tokens (prep launch) and the matrix-core GEMM.
+static int gemm_enqueue(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T, float *y, int add,
+                        hipStream_t st) {
+    static uint8_t *xq = nullptr;   // grown on demand; the per-op entries are synchronous on one stream
+    static float *part = nullptr;
+    static size_t xq_cap = 0, part_cap = 0;
+    const int64_t xs = xq_off((int)k).stride;
+    const size_t need = (size_t)T * xs, pneed = (size_t)gemm_splits((int)n_rows, (int)k, T, INT64_MAX) * T * n_rows;
+    if (need > xq_cap) {
+        if (xq) (void)hipFree(xq);
+        xq = nullptr, xq_cap = 0;
+        if (hipMalloc(&xq, need) != hipSuccess) return -1;
+        xq_cap = need;
+    }
+    if (pneed > part_cap) {
+        if (part) (void)hipFree(part);
+        part = nullptr, part_cap = 0;
+        if (hipMalloc(&part, pneed * 4) != hipSuccess) return -1;
+        part_cap = pneed;
+    }
+    GArgs p{};
+    p.x = x; p.xs = (int32_t)k; p.pro = PRO_NONE; p.xq = xq; p.K = (int32_t)k; p.T = T;
+    if (prep_launch(p, st)) return -1;
+    GemmArgs g{};
+    g.w = (const uint8_t *)dw; g.type = type; g.N = (int32_t)n_rows; g.K = (int32_t)k; g.T = T;
+    g.xq = xq; g.xs = xs; g.part = part; g.y = y; g.ys = (int32_t)n_rows; g.add = add;
+    return gemm_launch(g, (int64_t)part_cap, st);
+}
+
+extern "C" int xjh_gemm(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T, float *y, int add,
+                        char *err, size_t errlen) {
+    if (!ops_stream()) return -1;
+    if ((type != XJ_Q4_K && type != XJ_Q6_K) || T < 1 || T > gemm_max_tokens() || n_rows < 1 || n_rows > INT32_MAX ||
+        k < 256 || k % 256) {
+        snprintf(err, errlen, "unsupported GEMM shape/type (Q4_K or Q6_K, K %% 256 == 0, 1 <= T <= %d)", gemm_max_tokens());
+        return -1;
+    }
+    if (gemm_enqueue(type, dw, n_rows, k, x, T, y, add, g_stream)) { snprintf(err, errlen, "GEMM launch failed"); return -1; }
+    return ops_done(err, errlen);
+}
+
+extern "C" double xjh_gemm_time(uint32_t type, void *const *dws, int n_copies, int64_t n_rows, int64_t k, const float *x,
+                                int T, float *y, int iters, char *err, size_t errlen) {
+    if (!ops_stream()) return -1;
+    if ((type != XJ_Q4_K && type != XJ_Q6_K) || T < 1 || T > gemm_max_tokens() || k < 256 || k % 256) {
+        snprintf(err, errlen, "unsupported GEMM shape/type"); return -1;
+    }
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) { snprintf(err, errlen, "event creation failed"); return -1; }
+    for (int i = 0; i < n_copies; i++)
+        if (gemm_enqueue(type, dws[i], n_rows, k, x, T, y, 0, g_stream)) { snprintf(err, errlen, "GEMM launch failed"); return -1; }
+    (void)hipEventRecord(e0, g_stream);
+    for (int i = 0; i < iters; i++)
+        if (gemm_enqueue(type, dws[i % n_copies], n_rows, k, x, T, y, 0, g_stream)) { snprintf(err, errlen, "GEMM launch failed"); return -1; }
+    (void)hipEventRecord(e1, g_stream);
+    if (ops_done(err, errlen)) return -1;
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return (double)ms / iters;
+}
+
 extern "C" double xjh_gemv_time(uint32_t type, void *const *dws, int n_copies, int64_t n_rows, int64_t k, const float *x,
                                 int T, float *y, int iters, char *err, size_t errlen) {
     if (!ops_stream()) return -1;

@@ -162,7 +162,9 @@ def lib():
     _sig(L, "xjh_upload_weight", P, U32, P, I64, I64, CP, S)
     _sig(L, "xjh_dequant", I, U32, P, I64, I64, I64, I64, P, CP, S)
     _sig(L, "xjh_gemv", I, U32, P, I64, I64, P, I, P, I, CP, S)
+    _sig(L, "xjh_gemm", I, U32, P, I64, I64, P, I, P, I, CP, S)
     _sig(L, "xjh_gemv_time", D, U32, C.POINTER(P), I, I64, I64, P, I, P, I, CP, S)
+    _sig(L, "xjh_gemm_time", D, U32, C.POINTER(P), I, I64, I64, P, I, P, I, CP, S)
     _sig(L, "xjh_norm", I, I, P, P, I, I, F, P, CP, S)
     _sig(L, "xjh_argmax", I, P, I, I, P, CP, S)
     _sig(L, "xjh_delta_recurrent", I, I, I, I, P, P, P, P, P, F, P, P, CP, S)
@@ -531,6 +533,31 @@ def gemv(w, x, add_to=None):
     err = _err()
     _check(lib().xjh_gemv(w.t, w.ptr, w.rows, w.k, dx.ptr, T, dy.ptr, int(add_to is not None), err, ERR), err, "gemv")
     return dy.get(np.float32, (T, w.rows))
+
+
+def gemm(w, x, add_to=None):
+    """y[t] = W x[t] on the matrix cores (xjh_gemm); x float32 [T][k], T <= 64."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, w.k)
+    T = x.shape[0]
+    dx = Dev(x)
+    dy = Dev(add_to.astype(np.float32)) if add_to is not None else Dev(nbytes=T * w.rows * 4)
+    err = _err()
+    _check(lib().xjh_gemm(w.t, w.ptr, w.rows, w.k, dx.ptr, T, dy.ptr, int(add_to is not None), err, ERR), err, "gemm")
+    return dy.get(np.float32, (T, w.rows))
+
+
+def gemm_time(weights, x, iters):
+    """Mean ms per xjh_gemm call over rotating copies (HIP events on the library stream)."""
+    w0 = weights[0]
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, w0.k)
+    T = x.shape[0]
+    dx, dy = Dev(x), Dev(nbytes=T * w0.rows * 4)
+    arr = (C.c_void_p * len(weights))(*[w.ptr for w in weights])
+    err = _err()
+    ms = lib().xjh_gemm_time(w0.t, arr, len(weights), w0.rows, w0.k, dx.ptr, T, dy.ptr, iters, err, ERR)
+    if ms < 0:
+        raise XjError(err.value.decode())
+    return ms
 
 
 def gemv_time(weights, x, iters):
