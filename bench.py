@@ -30,9 +30,11 @@ Also reported, on the same run:
                 4B shape with one MTP layer added).
 
 usage: python bench.py [--gpus 1] [--steps 512] [--warmup 16] [--no-cpu] [--no-extra]
-                       [--copy-calibration MB] [--delta-c3]
+                       [--copy-calibration MB] [--delta-c3] [--gemm-tokens]
 --copy-calibration MB first copies MB megabytes device-to-device (one runtime
 copy kernel of known size, to calibrate the HBM byte counters of a profiler run).
+--gemm-tokens runs only the prefill-chunk GEMM legs (matrix-core GEMM vs
+GEMV tiles at T = 16/32/64).
 --delta-c3 runs only the Gated DeltaNet prefill comparison (16 heads, d=128,
 2048 tokens: chunk-wise MFMA kernels vs the token-by-token kernel) and prints
 its JSON line.
@@ -140,6 +142,26 @@ def gemv_tokens(t, rows, k, iters=200):
     return {"shape": f"{xp.TYPE_NAMES[t]} {rows}x{k}", "by_T": out}
 
 
+def gemm_tokens(t, rows, k, iters=50):
+    """Prefill chunks of T = 16 / 32 / 64 tokens on one weight shape, cold weights: the matrix-core
+    GEMM (xjh_gemm, its prep launch included) against the dot-product GEMV in tiles of 5 tokens
+    (xjh_gemv at T = 5, scaled by T / 5), us per chunk and GFLOP/s (2 rows k T)."""
+    by = rows * xp.row_bytes(t, k)
+    copies = max(4, -(-600_000_000 // by))
+    blob = xp.quantize(t, xp.fill_normal(rows * k, 17, 0.02).reshape(rows, k))
+    ws = [xp.DevWeight(t, blob, rows, k) for _ in range(copies)]
+    out = []
+    for T in (16, 32, 64):
+        xs = xp.fill_normal(T * k, 23 + T, 1.0).reshape(T, k)
+        ms = xp.gemm_time(ws, xs, iters)
+        mv = xp.gemv_time(ws, xs[:5], iters) * T / 5
+        out.append({"T": T, "gemm_us": round(ms * 1e3, 1), "gemv_tiles_us": round(mv * 1e3, 1),
+                    "gemm_GFLOPs": round(2.0 * rows * k * T / (ms * 1e-3) / 1e9, 1)})
+    for w in ws:
+        w.free()
+    return {"shape": f"{xp.TYPE_NAMES[t]} {rows}x{k}", "by_T": out}
+
+
 def spec_run(n_prompt=1024, n_gen=128, seed=20261109):
     """Speculative decode on the 4B shape, split 0-15 | 16-31 on one stream, with the 0.8B model
     drafting 4 tokens per step and the target verifying them as one 5-row pass: the real draft (random
@@ -240,6 +262,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the 0.8B run and the GEMV legs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB")
     ap.add_argument("--delta-c3", action="store_true", help="only the chunked vs token-by-token DeltaNet prefill")
+    ap.add_argument("--gemm-tokens", action="store_true", help="only the prefill-chunk GEMM vs GEMV-tile legs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the token loop on a single MI355X and has no "
@@ -247,6 +270,10 @@ def main():
         sys.exit(2)
 
     log(f"device: {xp.device_name()}")
+    if args.gemm_tokens:
+        print(json.dumps([gemm_tokens(xp.Q4_K, 18432, 2560), gemm_tokens(xp.Q6_K, 2560, 9216),
+                          gemm_tokens(xp.Q4_K, 2560, 4096)]), flush=True)
+        return
     if args.delta_c3:
         print(json.dumps(delta_c3()), flush=True)
         return
@@ -293,6 +320,8 @@ def main():
         extra["gemv_tokens"] = [gemv_tokens(xp.Q6_K, 3584, 1024), gemv_tokens(xp.Q8_0, 1024, 3584),
                                 gemv_tokens(xp.Q4_K, 151936, 1024), gemv_tokens(xp.Q4_K, 18432, 2560),
                                 gemv_tokens(xp.Q6_K, 2560, 9216)]
+        extra["gemm_tokens"] = [gemm_tokens(xp.Q4_K, 18432, 2560), gemm_tokens(xp.Q6_K, 2560, 9216),
+                                gemm_tokens(xp.Q4_K, 2560, 4096)]
         extra["speculative_4b"] = spec_run()
         extra["speculative_4b_mtp"] = spec_mtp_run()
         log(f"extra: {extra}")
