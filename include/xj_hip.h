@@ -12,11 +12,20 @@
  *       xj_hip_tune_note    <- xj_metal_tune_note  src/xiaoju-pipe/core/xj_stage.h:50
  *
  *  2. Host-side counterparts of the reference loader, needed because the
- *     reference sources do not ship with this library:
- *       xj_model_load / xj_model_free <- src/xiaoju-pipe/core/xj_model.h:125,130
- *       xj_model_load_layers          <- src/xiaoju-pipe/core/xj_model.h:66
- *       xj_model_ranges               <- src/xiaoju-pipe/core/xj_model.h:78
- *       xj_row_bytes / xj_type_block  <- src/xiaoju-pipe/core/gguf.h:81-83
+ *     reference sources do not ship with this library. They carry the xjh_
+ *     prefix so that a program linking the reference's own core objects next to
+ *     this library sees no duplicate symbols; a model built by either loader
+ *     can be passed to xj_hip_stage_new (the struct layout is the same):
+ *       xjh_model_load / xjh_model_free <- xj_model_load / xj_model_free
+ *                                          src/xiaoju-pipe/core/xj_model.h:64,69
+ *       xjh_model_load_layers           <- xj_model_load_layers  xj_model.h:66
+ *       xjh_model_attach_mtp            <- xj_model_attach_mtp   xj_model.h:72
+ *       xjh_model_mtp_range             <- xj_model_mtp_range    xj_model.h:74
+ *                                          (takes a path instead of a gguf_file)
+ *       xjh_model_ranges                <- xj_model_ranges       xj_model.h:78
+ *       xjh_model_layer_bytes           <- xj_model_layer_bytes  xj_model.h:80
+ *       xjh_row_bytes / xjh_type_block  <- xj_row_bytes / xj_type_block
+ *       / xjh_type_name                    / xj_type_name  src/xiaoju-pipe/core/gguf.h:81-83
  *     plus a writer for synthetic qwen35 GGUF files and the Q4_K / Q6_K /
  *     Q8_0 quantizers it uses (the reference has none for K-quants).
  *
@@ -76,25 +85,35 @@ int xj_hip_stage_fill_kv(xj_stage *s, int pos0, uint16_t bits, char *err, size_t
 
 /* -------------------------------------------------------- host loader -- */
 
-int         xj_type_block(uint32_t type, int *block_bytes);
-uint64_t    xj_row_bytes(uint32_t type, int64_t n);
-const char *xj_type_name(uint32_t type);
-xj_model   *xj_model_load(const char *path, char *err, size_t errlen);
-void        xj_model_free(xj_model *m);
-/* Partial load for a stage of layers [l0, l1) (xj_model.h:66, xj_model.c:214-233):
+int         xjh_type_block(uint32_t type, int *block_bytes);
+uint64_t    xjh_row_bytes(uint32_t type, int64_t n);
+const char *xjh_type_name(uint32_t type);
+/* The whole file mapped; the model table as xj_model_load builds it
+ * (xj_model.c:129-209): hparams, layer pattern, tensors, tied head, eos/eot,
+ * fingerprint, and the MTP layer in layers[n_layer] when the file has one. */
+xj_model   *xjh_model_load(const char *path, char *err, size_t errlen);
+void        xjh_model_free(xj_model *m);
+/* Partial load for a stage of layers [l0, l1) (xj_model.c:214-233):
  * only the GGUF header is read, then one mapping spans the merged byte ranges
  * of those layers (with_io: also token_embd, output_norm, output). Tensors
  * outside the mapping keep data = NULL, so a stage over other layers fails
  * ("weights are not mapped"); the file may be a partial download as long as
  * it reaches the end of that span. Error for an empty or out-of-range [l0, l1). */
-xj_model   *xj_model_load_layers(const char *path, int l0, int l1, bool with_io, char *err, size_t errlen);
+xj_model   *xjh_model_load_layers(const char *path, int l0, int l1, bool with_io, char *err, size_t errlen);
+/* Attach the MTP layer of another GGUF of the same model (xj_model.c:275-300):
+ * only its header and the MTP layer's byte span need to be present in that
+ * file. No-op when m already has one; error when the shapes differ or the
+ * file has no MTP layer. The mapping is released by xjh_model_free(m). */
+int         xjh_model_attach_mtp(xj_model *m, const char *path, char *err, size_t errlen);
+/* Byte span [lo, hi) of the MTP layer (layer tensors and nextn.*) of the
+ * GGUF at path, from its header alone (xj_model.c:262-273). */
+int         xjh_model_mtp_range(const char *path, uint64_t *lo, uint64_t *hi, char *err, size_t errlen);
 /* Byte ranges [lo, hi) of the file that layers [l0, l1) (and with include_embd
  * the embedding, output norm and untied head) occupy, sorted, ranges at most
- * 4096 bytes apart merged; returns their count, at most max (xj_model.h:78,
- * xj_model.c:308-328). */
-int         xj_model_ranges(const xj_model *m, int l0, int l1, bool include_embd, uint64_t (*ranges)[2], int max);
-/* Total tensor bytes of layers [l0, l1) (xj_model.h:79, xj_model.c:330-338). */
-uint64_t    xj_model_layer_bytes(const xj_model *m, int l0, int l1);
+ * 4096 bytes apart merged; returns their count, at most max (xj_model.c:315-328). */
+int         xjh_model_ranges(const xj_model *m, int l0, int l1, bool include_embd, uint64_t (*ranges)[2], int max);
+/* Total tensor bytes of layers [l0, l1) (xj_model.c:330-338). */
+uint64_t    xjh_model_layer_bytes(const xj_model *m, int l0, int l1);
 
 /* --------------------------------------------------- synthetic models -- */
 

@@ -1530,7 +1530,7 @@ int gemv_init(char *err, size_t errlen) {
 int upload_repack(uint32_t type, const void *src, int64_t n_rows, int64_t k, uint8_t *dst, hipStream_t st,
                   char *err, size_t errlen) {
     const uint8_t *s = (const uint8_t *)src;
-    const uint64_t bytes = xj_row_bytes(type, k) * (uint64_t)n_rows;
+    const uint64_t bytes = xjh_row_bytes(type, k) * (uint64_t)n_rows;
     if (type == XJ_F32 || type == XJ_F16 || type == XJ_BF16 || type == XJ_Q4_K || type == XJ_Q5_K) {
         XJ_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st), err, errlen, -1);
         XJ_CHECK(hipStreamSynchronize(st), err, errlen, -1);
@@ -1555,7 +1555,7 @@ int upload_repack(uint32_t type, const void *src, int64_t n_rows, int64_t k, uin
             memcpy(qs + g * 32, s + g * 34 + 2, 32);
         }
     } else {
-        snprintf(err, errlen, "no device layout for %s tensors", xj_type_name(type));
+        snprintf(err, errlen, "no device layout for %s tensors", xjh_type_name(type));
         return -1;
     }
     XJ_CHECK(hipMemcpyAsync(dst, tmp.data(), bytes, hipMemcpyHostToDevice, st), err, errlen, -1);

@@ -115,7 +115,7 @@ bool upload(HStage *S, const xj_w &w, DevW *out, char *err, size_t errlen) {
     auto it = S->wcache.find(w.data);
     if (it != S->wcache.end()) { *out = it->second; return true; }
     if (!gemv_type_ok(w.type)) {
-        snprintf(err, errlen, "tensor type %s is not supported by the HIP backend", xj_type_name(w.type));
+        snprintf(err, errlen, "tensor type %s is not supported by the HIP backend", xjh_type_name(w.type));
         return false;
     }
     uint8_t *p = dalloc<uint8_t>(S, w.nbytes + kWeightPad, err, errlen);
@@ -145,7 +145,7 @@ double gemv_algo_bytes(const GArgs &a, int T) {
     double b = (double)T * xq_off(a.K).v_off;
     for (int i = 0; i < a.nseg; i++) {
         const GSeg &s = a.seg[i];
-        b += (double)s.n_rows * xj_row_bytes(s.type, a.K) + (double)T * s.n_rows * 4 * (s.epi == EPI_ADD ? 2 : 1);
+        b += (double)s.n_rows * xjh_row_bytes(s.type, a.K) + (double)T * s.n_rows * 4 * (s.epi == EPI_ADD ? 2 : 1);
     }
     return b;
 }
@@ -1358,8 +1358,8 @@ extern "C" const char *xjh_last_error(void) { return g_lasterr; }
 
 extern "C" void *xjh_upload_weight(uint32_t type, const void *host, int64_t n_rows, int64_t k, char *err, size_t errlen) {
     if (!ops_stream()) { snprintf(err, errlen, "no HIP stream"); return nullptr; }
-    if (!gemv_type_ok(type)) { snprintf(err, errlen, "type %s has no device layout", xj_type_name(type)); return nullptr; }
-    const uint64_t bytes = xj_row_bytes(type, k) * (uint64_t)n_rows;
+    if (!gemv_type_ok(type)) { snprintf(err, errlen, "type %s has no device layout", xjh_type_name(type)); return nullptr; }
+    const uint64_t bytes = xjh_row_bytes(type, k) * (uint64_t)n_rows;
     void *p = nullptr;
     if (hipMalloc(&p, bytes + kWeightPad) != hipSuccess) { snprintf(err, errlen, "hipMalloc failed"); return nullptr; }
     if (upload_repack(type, host, n_rows, k, (uint8_t *)p, g_stream, err, errlen)) { (void)hipFree(p); return nullptr; }

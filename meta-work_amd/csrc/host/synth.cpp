@@ -257,12 +257,12 @@ extern "C" uint64_t xjs_tensor_seed(uint64_t seed, const char *name) {
 
 extern "C" int xjs_quantize(uint32_t type, const float *x, int64_t n_rows, int64_t k, void *out,
                             char *err, size_t errlen) {
-    int bb = 0, bn = xj_type_block(type, &bb);
-    if (!bn || k % bn) { snprintf(err, errlen, "cannot quantize %lld columns to %s", (long long)k, xj_type_name(type)); return -1; }
+    int bb = 0, bn = xjh_type_block(type, &bb);
+    if (!bn || k % bn) { snprintf(err, errlen, "cannot quantize %lld columns to %s", (long long)k, xjh_type_name(type)); return -1; }
     if (type != XJ_F32 && type != XJ_Q8_0 && type != XJ_Q4_K && type != XJ_Q6_K) {
-        snprintf(err, errlen, "no quantizer for %s", xj_type_name(type)); return -1;
+        snprintf(err, errlen, "no quantizer for %s", xjh_type_name(type)); return -1;
     }
-    const uint64_t rb = xj_row_bytes(type, k);
+    const uint64_t rb = xjh_row_bytes(type, k);
     parallel_rows(n_rows, [&](int64_t r) {
         const float *src = x + r * k;
         uint8_t *dst = (uint8_t *)out + r * rb;
@@ -333,10 +333,10 @@ extern "C" int64_t xjs_write_model(const char *path, const xjs_config *c, char *
     const uint64_t ALIGN = 32;
     uint64_t off = 0;
     for (auto &t : ts) {
-        int bn = xj_type_block(t.type, nullptr);
-        if (!bn || t.ne0 % bn) { snprintf(err, errlen, "tensor %s: %lld columns do not fit %s", t.name.c_str(), (long long)t.ne0, xj_type_name(t.type)); return -1; }
+        int bn = xjh_type_block(t.type, nullptr);
+        if (!bn || t.ne0 % bn) { snprintf(err, errlen, "tensor %s: %lld columns do not fit %s", t.name.c_str(), (long long)t.ne0, xjh_type_name(t.type)); return -1; }
         t.offset = off;
-        t.nbytes = xj_row_bytes(t.type, t.ne0) * (uint64_t)(t.ne1 ? t.ne1 : 1);
+        t.nbytes = xjh_row_bytes(t.type, t.ne0) * (uint64_t)(t.ne1 ? t.ne1 : 1);
         off = (off + t.nbytes + ALIGN - 1) / ALIGN * ALIGN;
     }
     Writer w;

@@ -6,7 +6,7 @@ library. Importing this module never falls back to anything else: if the
 library is missing it raises.
 
     import xjpipe as xp
-    m = xp.Model(path)                       # xj_model_load
+    m = xp.Model(path)                       # xjh_model_load
     a = xp.HipStage(m, 0, m.hp.n_layer, n_ctx=1024, max_batch=8, has_head=True)
     x = m.embed_host(token)  ...             # or a device chain:
     c = xp.Chain([a]); c.eval(prompt); toks = c.decode(256)
@@ -128,14 +128,16 @@ def lib():
     _sig(L, "xj_hip_stage_snapshot", I, PS, I, CP, S)
     _sig(L, "xj_hip_stage_restore", I, PS, I, I, CP, S)
     _sig(L, "xj_hip_stage_fill_kv", I, PS, I, C.c_uint16, CP, S)
-    _sig(L, "xj_type_block", I, U32, C.POINTER(I))
-    _sig(L, "xj_row_bytes", U64, U32, I64)
-    _sig(L, "xj_type_name", CP, U32)
-    _sig(L, "xj_model_load", C.POINTER(XjModel), CP, CP, S)
-    _sig(L, "xj_model_free", None, C.POINTER(XjModel))
-    _sig(L, "xj_model_load_layers", C.POINTER(XjModel), CP, C.c_int, C.c_int, C.c_bool, CP, S)
-    _sig(L, "xj_model_ranges", C.c_int, C.POINTER(XjModel), C.c_int, C.c_int, C.c_bool, C.POINTER(C.c_uint64), C.c_int)
-    _sig(L, "xj_model_layer_bytes", C.c_uint64, C.POINTER(XjModel), C.c_int, C.c_int)
+    _sig(L, "xjh_type_block", I, U32, C.POINTER(I))
+    _sig(L, "xjh_row_bytes", U64, U32, I64)
+    _sig(L, "xjh_type_name", CP, U32)
+    _sig(L, "xjh_model_load", C.POINTER(XjModel), CP, CP, S)
+    _sig(L, "xjh_model_free", None, C.POINTER(XjModel))
+    _sig(L, "xjh_model_load_layers", C.POINTER(XjModel), CP, C.c_int, C.c_int, C.c_bool, CP, S)
+    _sig(L, "xjh_model_ranges", C.c_int, C.POINTER(XjModel), C.c_int, C.c_int, C.c_bool, C.POINTER(C.c_uint64), C.c_int)
+    _sig(L, "xjh_model_layer_bytes", C.c_uint64, C.POINTER(XjModel), C.c_int, C.c_int)
+    _sig(L, "xjh_model_attach_mtp", I, C.POINTER(XjModel), CP, CP, S)
+    _sig(L, "xjh_model_mtp_range", I, CP, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), CP, S)
     _sig(L, "xjs_fill_normal", None, P, I64, U64, F)
     _sig(L, "xjs_tensor_seed", U64, U64, CP)
     _sig(L, "xjs_quantize", I, U32, P, I64, I64, P, CP, S)
@@ -249,16 +251,16 @@ def quantize(t, x):
 
 
 class Model:
-    """xj_model_load: the GGUF is mmapped; weights stay on the host until a stage uploads them.
-    With layers=(l0, l1): xj_model_load_layers, only the header is read and one mapping
+    """xjh_model_load: the GGUF is mmapped; weights stay on the host until a stage uploads them.
+    With layers=(l0, l1): xjh_model_load_layers, only the header is read and one mapping
     covers those layers (with_io: the embedding and head as well); other weights are NULL."""
 
     def __init__(self, path, layers=None, with_io=False):
         err = _err()
         if layers is None:
-            self.ptr = lib().xj_model_load(path.encode(), err, ERR)
+            self.ptr = lib().xjh_model_load(path.encode(), err, ERR)
         else:
-            self.ptr = lib().xj_model_load_layers(path.encode(), int(layers[0]), int(layers[1]), bool(with_io), err, ERR)
+            self.ptr = lib().xjh_model_load_layers(path.encode(), int(layers[0]), int(layers[1]), bool(with_io), err, ERR)
         if not self.ptr:
             raise XjError(err.value.decode())
         self.path = path
@@ -273,7 +275,7 @@ class Model:
 
     def close(self):
         if self.ptr:
-            lib().xj_model_free(self.ptr)
+            lib().xjh_model_free(self.ptr)
             self.ptr = None
 
     def __del__(self):
@@ -283,10 +285,15 @@ class Model:
             pass
 
     def ranges(self, l0, l1, include_embd=False, max_ranges=512):
-        """xj_model_ranges: merged file byte ranges [(lo, hi), ...] of layers [l0, l1)."""
+        """xjh_model_ranges: merged file byte ranges [(lo, hi), ...] of layers [l0, l1)."""
         r = (C.c_uint64 * (2 * max_ranges))()
-        n = lib().xj_model_ranges(self.ptr, l0, l1, include_embd, r, max_ranges)
+        n = lib().xjh_model_ranges(self.ptr, l0, l1, include_embd, r, max_ranges)
         return [(r[2 * i], r[2 * i + 1]) for i in range(n)]
+
+    def attach_mtp(self, path):
+        """xjh_model_attach_mtp: take the MTP layer from another GGUF of the same model."""
+        err = _err()
+        _check(lib().xjh_model_attach_mtp(self.ptr, path.encode(), err, ERR), err, "attach_mtp")
 
     def tensor_bytes(self, w):
         """Raw GGUF bytes of an XjW as a numpy uint8 view (no copy)."""

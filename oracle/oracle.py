@@ -91,6 +91,8 @@ def rlib(native=False):
         _sig(L, "ref_model_free", None, PM)
         _sig(L, "ref_model_load_layers", PM, CP, I, I, C.c_bool, CP, S)
         _sig(L, "ref_model_ranges", I, PM, I, I, C.c_bool, C.POINTER(C.c_uint64), I)
+        _sig(L, "ref_model_attach_mtp", I, PM, CP, CP, S)
+        _sig(L, "ref_model_mtp_range", I, CP, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), CP, S)
         _sig(L, "ref_stage_new", PS, PM, I, I, I, I, C.c_bool, CP, S)
         _sig(L, "ref_embed", None, PM, C.c_int32, P)
         _sig(L, "ref_greedy", I, PM, I, I, I, P, I, I, P, P, CP, S)

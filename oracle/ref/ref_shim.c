@@ -42,6 +42,14 @@ xj_model *ref_model_load_layers(const char *path, int l0, int l1, bool with_io, 
     return xj_model_load_layers(path, l0, l1, with_io, err, errlen);
 }
 int ref_model_ranges(const xj_model *m, int l0, int l1, bool io, uint64_t (*r)[2], int max) { return xj_model_ranges(m, l0, l1, io, r, max); }
+int ref_model_attach_mtp(xj_model *m, const char *path, char *err, size_t errlen) { return xj_model_attach_mtp(m, path, err, errlen); }
+int ref_model_mtp_range(const char *path, uint64_t *lo, uint64_t *hi, char *err, size_t errlen) {
+    gguf_file *g = gguf_open_header(path, err, errlen);
+    if (!g) return -1;
+    const int rc = xj_model_mtp_range(g, lo, hi, err, errlen);
+    gguf_close(g);
+    return rc;
+}
 xj_stage *ref_stage_new(const xj_model *m, int l0, int l1, int n_ctx, int max_batch, bool has_head, char *err, size_t errlen) {
     return xj_cpu_stage_new(m, l0, l1, n_ctx, max_batch, has_head, err, errlen);
 }

@@ -20,7 +20,7 @@ def w_tuple(w):
 @pytest.mark.skipif(not orc.ref_available(), reason="reference build (oracle/_ref) not present")
 @pytest.mark.parametrize("cfg", ["TINY", "TINY_DRAFT", "TINY_MTP"])
 def test_loader_builds_the_reference_model(model_dir, cfg):
-    """xj_model_load here and the reference's xj_model_load give the same hparams,
+    """xjh_model_load here and the reference's xj_model_load give the same hparams,
     tensor table (offsets, sizes, types, shapes), layer pattern and fingerprint,
     and with an MTP layer the same layer n_layer and nextn tensors."""
     from conftest import synth_model
@@ -124,7 +124,8 @@ def _truncated_copy(src, dst, nbytes):
 @pytest.mark.skipif(not orc.ref_available(), reason="reference build (oracle/_ref) not present")
 @pytest.mark.parametrize("l0,l1,io", [(0, 4, False), (4, 8, False), (2, 3, False), (0, 2, True), (6, 8, True), (0, 8, True)])
 def test_layer_range_loader_matches_the_reference(tiny_path, tmp_path, l0, l1, io):
-    """xj_model_load_layers and xj_model_ranges against the reference's own
+    """xjh_model_load_layers and xjh_model_ranges against the reference's own
+    xj_model_load_layers and xj_model_ranges
     (xj_model.c:214-233, 308-328): the same byte ranges, the same tensor table,
     the same tensors left unmapped (data NULL), and the mapped bytes equal to
     the file's. A file cut right after the last range still loads in both,
@@ -145,7 +146,7 @@ def test_layer_range_loader_matches_the_reference(tiny_path, tmp_path, l0, l1, i
     assert ranges == full.ranges(l0, l1, io)
     lo, hi = ranges[0][0], ranges[-1][1]
     map_lo = lo // os.sysconf("SC_PAGE_SIZE") * os.sysconf("SC_PAGE_SIZE")  # the mapping starts on a page
-    assert sum(b - a for a, b in ranges) >= xp.lib().xj_model_layer_bytes(part.ptr, l0, l1)
+    assert sum(b - a for a, b in ranges) >= xp.lib().xjh_model_layer_bytes(part.ptr, l0, l1)
 
     def check(mine, ref, whole):
         assert w_tuple(mine) == w_tuple(ref)
@@ -182,3 +183,67 @@ def test_layer_range_loader_matches_the_reference(tiny_path, tmp_path, l0, l1, i
         with pytest.raises(xp.XjError):
             xp.Model(tiny_path, layers=(a, b))
         assert not orc.rlib().ref_model_load_layers(tiny_path.encode(), a, b, io, err, 512)
+
+
+@pytest.mark.skipif(not orc.ref_available(), reason="reference build (oracle/_ref) not present")
+def test_attach_mtp_matches_the_reference(model_dir, tiny_path, tmp_path):
+    """xjh_model_attach_mtp against the reference's xj_model_attach_mtp
+    (xj_model.c:275-300): the MTP layer and nextn tensors of a second file of
+    the same model land in layers[n_layer] with the same table entries, mapped
+    from that file, bytes equal to the file's own; only the header and the MTP
+    span need to be present (the rest zeroed here); a file without an MTP layer
+    or of another shape is refused by both."""
+    from conftest import synth_model
+    mtp_path = synth_model(model_dir, xp.TINY_MTP, "tiny_mtp")
+    whole = xp.Model(mtp_path)
+    lo, hi = orc.C.c_uint64(), orc.C.c_uint64()
+    rlo, rhi = orc.C.c_uint64(), orc.C.c_uint64()
+    err = orc.C.create_string_buffer(512)
+    assert xp.lib().xjh_model_mtp_range(mtp_path.encode(), orc.C.byref(lo), orc.C.byref(hi), err, 512) == 0, err.value
+    assert orc.rlib().ref_model_mtp_range(mtp_path.encode(), orc.C.byref(rlo), orc.C.byref(rhi), err, 512) == 0
+    assert (lo.value, hi.value) == (rlo.value, rhi.value) and lo.value < hi.value
+
+    # a copy holding only the header and the MTP span
+    raw = bytearray(open(mtp_path, "rb").read())
+    first = min(t.file_off for t in (whole.m.tok_embd, whole.m.output_norm))
+    holes = bytearray(len(raw))
+    holes[:first] = raw[:first]
+    holes[lo.value:hi.value] = raw[lo.value:hi.value]
+    sparse = tmp_path / "mtp_only.gguf"
+    sparse.write_bytes(bytes(holes))
+
+    for src in (mtp_path, str(sparse)):
+        m = xp.Model(tiny_path)
+        assert not m.m.has_mtp
+        m.attach_mtp(src)
+        r = orc.rlib().ref_model_load(tiny_path.encode(), err, 512)
+        assert r, err.value
+        assert orc.rlib().ref_model_attach_mtp(r, src.encode(), err, 512) == 0, err.value
+        rm = r.contents
+        assert m.m.has_mtp and rm.has_mtp
+        i = m.hp.n_layer
+        assert bytes(rm.hp) == bytes(m.m.hp) and rm.fingerprint == m.m.fingerprint
+        for f in xp._LAYER_W:
+            mine, ref = getattr(m.m.layers[i], f), getattr(rm.layers[i], f)
+            assert w_tuple(mine) == w_tuple(ref), f
+            assert (mine.data is None) == (ref.data is None) == (mine.nbytes == 0), f
+            if mine.nbytes:
+                assert np.array_equal(m.tensor_bytes(mine), whole.tensor_bytes(getattr(whole.m.layers[i], f))), f
+        for name in ("mtp_eh", "mtp_enorm", "mtp_hnorm", "mtp_head_norm"):
+            mine = getattr(m.m, name)
+            assert w_tuple(mine) == w_tuple(getattr(rm, name)) == w_tuple(getattr(whole.m, name)), name
+            assert np.array_equal(m.tensor_bytes(mine), whole.tensor_bytes(getattr(whole.m, name))), name
+        m.attach_mtp(src)                      # already attached: a no-op in both
+        assert orc.rlib().ref_model_attach_mtp(r, src.encode(), err, 512) == 0
+        orc.rlib().ref_model_free(r)
+        m.close()
+
+    draft = synth_model(model_dir, xp.TINY_DRAFT, "tiny_draft")
+    for bad in (tiny_path, draft):             # no MTP layer / another model's shape
+        m = xp.Model(tiny_path)
+        with pytest.raises(xp.XjError):
+            m.attach_mtp(bad)
+        r = orc.rlib().ref_model_load(tiny_path.encode(), err, 512)
+        assert orc.rlib().ref_model_attach_mtp(r, bad.encode(), err, 512) != 0
+        orc.rlib().ref_model_free(r)
+        m.close()
