@@ -131,6 +131,8 @@ typedef struct {
     float w_std;
     uint64_t seed;
     int nextn;                          /* 1: one MTP layer (blk.{n_layer}, nextn.*) */
+    int32_t eos_id;                     /* >= 0: tokenizer.ggml.eos_token_id */
+    int32_t eot_id;                     /* >= 0: a token list with "<|im_end|>" at this id */
 } xjs_config;
 
 /* Fill out[n] with N(0, std) from the build's generator: splitmix64 feeding
@@ -160,10 +162,13 @@ void       xjh_chain_free(xjh_chain *c);
  * all n tokens in one chunk, recurrent checkpoints kept for rollback. */
 int  xjh_chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int keep,
                     float *logits, int32_t *argmax, char *err, size_t errlen);
-/* n_steps greedy steps entirely on the device. The first input token is the
- * argmax left by the previous eval/decode; out[i] receives the token chosen
+/* Up to n_steps greedy steps entirely on the device. The first input token is
+ * the argmax left by the previous eval/decode; out[i] receives the token chosen
  * after step i (so out[0] is the argmax of the first step's logits). One step
- * is one HIP graph launch. */
+ * is one HIP graph launch. Generation stops at the model's end token
+ * (hp.eos / hp.eot, xj_spec.c:29,139): it is the last token written and it is
+ * not fed, so the state is that of the tokens before it. Returns the number of
+ * tokens written (0 when the previous token already was an end token), or -1. */
 int  xjh_chain_decode(xjh_chain *c, int n_steps, int32_t *out, char *err, size_t errlen);
 /* Greedy token that the next decode step would feed (the last argmax). */
 int  xjh_chain_last_token(xjh_chain *c);
@@ -194,6 +199,10 @@ typedef struct {
     long acc_at[4];
     double t_total_ms, t_draft_ms;
 } xjh_spec_stats;
+/* Returns the number of tokens written to out (at most n_gen): generation
+ * stops after an end token (hp.eos / hp.eot), which is written but not fed,
+ * and an accepted end token cuts the accepted drafts there (xj_spec.c:139,
+ * :193-194). -1 on error. */
 int xjh_spec_generate(xjh_chain *target, xjh_chain *draft, int k, int n_gen,
                       const int32_t *oracle, int n_oracle, int oracle_miss,
                       int32_t *out, xjh_spec_stats *stats, char *err, size_t errlen);
@@ -204,15 +213,22 @@ int xjh_spec_generate(xjh_chain *target, xjh_chain *draft, int k, int n_gen,
  * first from the pending positions and each further one from
  * [embedding(previous draft) | shared_head_norm(previous MTP output)]; the
  * target verifies [t, d1..dk] in one batch and keeps the agreeing prefix).
- * Feeds the prompt itself (both models are reset first); out receives n_gen
- * tokens, which are those of plain greedy decoding. oracle / oracle_miss as
- * for xjh_spec_generate. mtp: xj_hip_stage_new(m, n_layer, n_layer + 1, ...,
- * has_head = true) of the target's model.
+ * The target's hidden rows pass its output_norm before the MTP stage takes
+ * them, and an MTP output passes shared_head_norm before it is fed back, both
+ * as x * (sc * w) (the driver's defaults, XJ_MTP_MAIN_POST / XJ_MTP_CHAIN_POST
+ * = 0 turn them off as in the reference).
+ * Feeds the prompt itself (both models are reset first); out receives the
+ * tokens of plain greedy decoding, end tokens handled as in xjh_spec_generate;
+ * returns their count or -1. draft_log (optional) receives the first
+ * draft_cap drafted tokens in order, before any oracle replacement. oracle /
+ * oracle_miss as for xjh_spec_generate. mtp: xj_hip_stage_new(m, n_layer,
+ * n_layer + 1, ..., has_head = true) of the target's model.
  * Replaces: xj_spec_feed / xj_spec_next with an MTP stage
  * (src/xiaoju-pipe/core/xj_spec.c:117-209) over the device chain. */
 int xjh_spec_generate_mtp(xjh_chain *target, xj_stage *mtp, int k, const int32_t *prompt, int n_prompt,
                           int n_gen, const int32_t *oracle, int n_oracle, int oracle_miss,
-                          int32_t *out, xjh_spec_stats *stats, char *err, size_t errlen);
+                          int32_t *out, xjh_spec_stats *stats, int32_t *draft_log, int draft_cap,
+                          char *err, size_t errlen);
 
 /* ----------------------------------------------------- per-op kernels -- */
 
@@ -256,7 +272,9 @@ double xjh_gemm_time(uint32_t type, void *const *dws, int n_copies, int64_t n_ro
  * Returns the mean ms per launch, or -1. */
 double xjh_gemv_time(uint32_t type, void *const *dws, int n_copies, int64_t n_rows, int64_t k,
                      const float *x, int T, float *y, int iters, char *err, size_t errlen);
-/* out[t] = rmsnorm(x[t]) * w  (mode 0) or x[t]/sqrt(sum x^2 + eps) (mode 1). */
+/* out[t] = rmsnorm(x[t]) * w  (mode 0: x * sc * w, xj_cpu.c:56-61), x[t]/sqrt(sum x^2 + eps)
+ * (mode 1, xj_cpu.c:185-193) or x * (sc * w) (mode 2, the speculative driver's norm_inplace,
+ * xj_spec.c:19-25); sc = 1/sqrt(sum x^2 / n + eps) with the sum in double. */
 int xjh_norm(int mode, const float *x, const float *w, int n, int rows, float eps, float *out,
              char *err, size_t errlen);
 /* g[i] = silu(g[i]) * u[i] over n floats, in place.

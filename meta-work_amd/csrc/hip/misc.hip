@@ -8,7 +8,8 @@
 //                    xj_spec.c:12-16; also records the token in the history and
 //                    advances the step counter (one work-group per token row).
 //   argmax_rows      plain first-maximum argmax of T rows (test entry point).
-//   norm_kernel      RMSNorm / L2 rows (xj_cpu.c:56-61, :185-193).
+//   norm_kernel      RMSNorm / L2 rows (xj_cpu.c:56-61, :185-193); mode 2 is the
+//                    RMSNorm with the product order of xj_spec.c:19-25.
 //   sample_kernel    top-k 40 / top-p 0.95 sampling at a temperature (the
 //                    app's sampler, ios/App/XJGlue.c:251-282, with the random
 //                    number passed in); temperature <= 0: the greedy token.
@@ -91,8 +92,11 @@ __global__ __launch_bounds__(256) void norm_kernel(int mode, const float *x, int
     double ss = 0;
     for (int i = tid; i < n; i += 256) ss += (double)xr[i] * xr[i];
     ss = xjd::block_sum_d(ss, red);
-    const float sc = mode == 0 ? 1.0f / sqrtf((float)(ss / n) + eps) : 1.0f / sqrtf((float)ss + eps);
-    for (int i = tid; i < n; i += 256) out[(int64_t)r * os + i] = w ? xr[i] * sc * w[i] : xr[i] * sc;
+    const float sc = mode != 1 ? 1.0f / sqrtf((float)(ss / n) + eps) : 1.0f / sqrtf((float)ss + eps);
+    if (mode == 2)   // x * (sc * w): the speculative driver's in-place norm (xj_spec.c:19-25)
+        for (int i = tid; i < n; i += 256) out[(int64_t)r * os + i] = xr[i] * (sc * w[i]);
+    else
+        for (int i = tid; i < n; i += 256) out[(int64_t)r * os + i] = w ? xr[i] * sc * w[i] : xr[i] * sc;
 }
 
 int embed_launch(const EmbedArgs &a, hipStream_t st) {

@@ -33,7 +33,8 @@ using namespace xjk;
 
 namespace {
 
-constexpr int kSnapSlots = 8;
+constexpr int kSnapSlots = 9;       // 0..7 for callers, kDecodeSlot for xjh_chain_decode
+constexpr int kDecodeSlot = kSnapSlots - 1;
 
 struct HLayer {
     bool rec = false;
@@ -112,6 +113,8 @@ bool gemv_type_ok(uint32_t t) {
 bool upload(HStage *S, const xj_w &w, DevW *out, char *err, size_t errlen) {
     *out = DevW();
     if (!w.nbytes) return true;
+    // a layer-range load leaves tensors outside its mapping with data == NULL
+    if (!w.data) { snprintf(err, errlen, "tensor not mapped (%lld x %lld)", (long long)w.ne1, (long long)w.ne0); return false; }
     auto it = S->wcache.find(w.data);
     if (it != S->wcache.end()) { *out = it->second; return true; }
     if (!gemv_type_ok(w.type)) {
@@ -763,6 +766,7 @@ static int snapshot_enqueue(HStage *S, int slot, hipStream_t st, char *err, size
 }
 
 extern "C" int xj_hip_stage_snapshot(xj_stage *s, int slot, char *err, size_t errlen) {
+    if (slot < 0 || slot >= kDecodeSlot) { snprintf(err, errlen, "snapshot slot %d out of range", slot); return -1; }
     return snapshot_enqueue(H(s), slot, H(s)->st, err, errlen);
 }
 
@@ -782,9 +786,27 @@ extern "C" int xj_hip_stage_fill_kv(xj_stage *s, int pos0, uint16_t bits, char *
     return sync_check(S, err, errlen);
 }
 
+// Restores slot `slot` on `st` (enqueued only) and sets n_past.
+static int restore_enqueue(HStage *S, int slot, int n_past, hipStream_t st, char *err, size_t errlen) {
+    xj_stage *s = &S->s;
+    if (n_past < 0 || n_past > s->n_ctx) { snprintf(err, errlen, "bad n_past %d", n_past); return -1; }
+    for (auto &L : S->L) {
+        if (!L.rec) continue;
+        if (!L.snap_conv[slot]) { snprintf(err, errlen, "snapshot slot %d is empty", slot); return -1; }
+        if (hipMemcpyAsync(L.conv, L.snap_conv[slot], S->conv_n * 4, hipMemcpyDeviceToDevice, st) != hipSuccess ||
+            hipMemcpyAsync(L.ssm, L.snap_ssm[slot], S->ssm_n * 4, hipMemcpyDeviceToDevice, st) != hipSuccess) {
+            snprintf(err, errlen, "restore copy failed");
+            return -1;
+        }
+    }
+    s->n_past = n_past;
+    s->ck_T = 0;
+    return 0;
+}
+
 extern "C" int xj_hip_stage_restore(xj_stage *s, int slot, int n_past, char *err, size_t errlen) {
     HStage *S = H(s);
-    if (slot < 0 || slot >= kSnapSlots) { snprintf(err, errlen, "snapshot slot %d out of range", slot); return -1; }
+    if (slot < 0 || slot >= kDecodeSlot) { snprintf(err, errlen, "snapshot slot %d out of range", slot); return -1; }
     if (n_past < 0 || n_past > s->n_ctx) { snprintf(err, errlen, "bad n_past %d", n_past); return -1; }
     for (auto &L : S->L) {
         if (!L.rec) continue;
@@ -942,43 +964,78 @@ static int build_decode_graph(xjh_chain *c, char *err, size_t errlen) {
     return 0;
 }
 
+// End tokens of the model (xj_spec.c:29): greedy generation stops at either.
+static bool is_end(const xj_hparams &hp, int32_t t) { return (uint32_t)t == hp.eot || (uint32_t)t == hp.eos; }
+static bool has_end(const xj_hparams &hp) { return hp.eos != UINT32_MAX || hp.eot != UINT32_MAX; }
+
+// n replays of the decode step from token `tok` at the stages' current n_past
+// (enqueued, not synchronised); the tokens land in d_hist[0, n).
+static int decode_enqueue(xjh_chain *c, int tok, int n, bool direct, char *err, size_t errlen) {
+    c->h_buf[0] = 0;
+    c->h_buf[1] = tok;
+    if (hipMemcpyAsync(c->d_step, &c->h_buf[0], 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+        hipMemcpyAsync(c->d_tok, &c->h_buf[1], 4, hipMemcpyHostToDevice, c->stream) != hipSuccess) {
+        snprintf(err, errlen, "decode setup failed"); return -1;
+    }
+    for (auto *S : c->st) if (set_npast(S, c->stream)) { snprintf(err, errlen, "decode setup failed"); return -1; }
+    if (chain_sync(c, err, errlen)) return -1;   // the pinned set-up words are reused below
+    (void)hipEventRecord(c->ev0, c->stream);
+    for (int i = 0; i < n; i++)
+        if (direct ? enqueue_decode_step(c) != 0 : hipGraphLaunch(c->exec, c->stream) != hipSuccess) {
+            snprintf(err, errlen, "decode step launch failed"); return -1;
+        }
+    (void)hipEventRecord(c->ev1, c->stream);
+    return 0;
+}
+
 extern "C" int xjh_chain_decode(xjh_chain *c, int n_steps, int32_t *out, char *err, size_t errlen) {
     if (n_steps <= 0) return 0;
     if (c->last_tok < 0) { snprintf(err, errlen, "decode needs a previous eval with logits"); return -1; }
+    const xj_hparams &hp = c->st[0]->s.m->hp;
+    if (is_end(hp, c->last_tok)) return 0;   // an end token is never fed (xj_spec.c:139)
     for (auto *S : c->st)
         if (S->s.n_past + n_steps > S->s.n_ctx) { snprintf(err, errlen, "context full (%d)", S->s.n_ctx); return -1; }
     // XJ_DECODE_GRAPH=0 enqueues the same kernels step by step instead of
     // replaying the captured graph (for tracing tools that do not follow graphs)
     const bool direct = env_int("XJ_DECODE_GRAPH", 1) == 0;
     if (!direct && !c->exec && build_decode_graph(c, err, errlen)) return -1;
+    // With end tokens the steps run in windows, the recurrent state saved at
+    // the start of each: when step j of a window yields an end token, the
+    // window is replayed from the saved state for j + 1 steps only, so the
+    // state is that of feeding exactly the tokens before the end token.
+    const int window = has_end(hp) ? 32 : c->hist_cap;
     double total_ms = 0;
-    for (int done = 0; done < n_steps;) {
-        const int n = n_steps - done < c->hist_cap ? n_steps - done : c->hist_cap;
-        c->h_buf[0] = 0;
-        c->h_buf[1] = c->last_tok;
-        if (hipMemcpyAsync(c->d_step, &c->h_buf[0], 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
-            hipMemcpyAsync(c->d_tok, &c->h_buf[1], 4, hipMemcpyHostToDevice, c->stream) != hipSuccess) {
-            snprintf(err, errlen, "decode setup failed"); return -1;
-        }
-        for (auto *S : c->st) if (set_npast(S, c->stream)) { snprintf(err, errlen, "decode setup failed"); return -1; }
-        if (chain_sync(c, err, errlen)) return -1;
-        (void)hipEventRecord(c->ev0, c->stream);
-        for (int i = 0; i < n; i++)
-            if (direct ? enqueue_decode_step(c) != 0 : hipGraphLaunch(c->exec, c->stream) != hipSuccess) {
-                snprintf(err, errlen, "decode step launch failed"); return -1;
+    int done = 0;
+    while (done < n_steps) {
+        const int n = n_steps - done < window ? n_steps - done : window;
+        std::vector<int> past0;
+        if (has_end(hp))
+            for (auto *S : c->st) {
+                past0.push_back(S->s.n_past);
+                if (snapshot_enqueue(S, kDecodeSlot, c->stream, err, errlen)) return -1;
             }
-        (void)hipEventRecord(c->ev1, c->stream);
-        if (chain_sync(c, err, errlen)) return -1;
+        const int tok0 = c->last_tok;
+        if (decode_enqueue(c, tok0, n, direct, err, errlen) || chain_sync(c, err, errlen)) return -1;
         float ms = 0;
         (void)hipEventElapsedTime(&ms, c->ev0, c->ev1);
         total_ms += ms;
         if (hipMemcpy(out + done, c->d_hist, 4 * n, hipMemcpyDeviceToHost) != hipSuccess) { snprintf(err, errlen, "history copy failed"); return -1; }
-        for (auto *S : c->st) S->s.n_past += n;
-        c->last_tok = out[done + n - 1];
-        done += n;
+        int ran = n;
+        if (has_end(hp))
+            for (int j = 0; j < n; j++)
+                if (is_end(hp, out[done + j])) { ran = j + 1; break; }
+        if (ran < n) {
+            for (size_t i = 0; i < c->st.size(); i++)
+                if (restore_enqueue(c->st[i], kDecodeSlot, past0[i], c->stream, err, errlen)) return -1;
+            if (decode_enqueue(c, tok0, ran, direct, err, errlen) || chain_sync(c, err, errlen)) return -1;
+        }
+        for (auto *S : c->st) S->s.n_past += ran;
+        c->last_tok = out[done + ran - 1];
+        done += ran;
+        if (ran < n) break;
     }
-    c->last_ms = total_ms / n_steps;
-    return 0;
+    c->last_ms = total_ms / done;
+    return done;
 }
 
 extern "C" int xjh_chain_last_token(xjh_chain *c) { return c->last_tok; }
@@ -998,10 +1055,16 @@ extern "C" void xjh_chain_reset(xjh_chain *c) {
 
 // one greedy step of the draft fed with token t; returns its argmax
 static int draft_step(xjh_chain *d, int t, int *next, char *err, size_t errlen) {
-    d->last_tok = t;
-    int32_t o;
-    if (xjh_chain_decode(d, 1, &o, err, errlen)) return -1;
-    *next = o;
+    for (auto *S : d->st)
+        if (S->s.n_past + 1 > S->s.n_ctx) { snprintf(err, errlen, "context full (%d)", S->s.n_ctx); return -1; }
+    const bool direct = env_int("XJ_DECODE_GRAPH", 1) == 0;
+    if (!direct && !d->exec && build_decode_graph(d, err, errlen)) return -1;
+    if (decode_enqueue(d, t, 1, direct, err, errlen) ||
+        hipMemcpyAsync(&d->h_buf[2], d->d_hist, 4, hipMemcpyDeviceToHost, d->stream) != hipSuccess ||
+        chain_sync(d, err, errlen))
+        return -1;
+    for (auto *S : d->st) S->s.n_past += 1;
+    *next = d->last_tok = d->h_buf[2];
     return 0;
 }
 
@@ -1041,6 +1104,7 @@ static int draft_run(xjh_chain *d, int t, int kk, int32_t *toks, char *err, size
 extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_gen, const int32_t *oracle, int n_oracle,
                                  int oracle_miss, int32_t *out, xjh_spec_stats *stats, char *err, size_t errlen) {
     xjh_spec_stats st{};
+    const xj_hparams &hp = tgt->st[0]->s.m->hp;
     const int V = (int)tgt->st.back()->output.n_rows;
     if (k < 1) k = 1;
     if (k > 4) k = 4;
@@ -1055,6 +1119,7 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
     long n_gen_tok = 0;
     int pending = tgt->last_tok;
     while (produced < n_gen) {
+        if (is_end(hp, pending)) { out[produced++] = pending; break; }   // returned, never fed (xj_spec.c:139)
         const int P = tgt->st[0]->s.n_past;
         int kk = k;
         if (kk > n_gen - produced - 1) kk = n_gen - produced - 1;
@@ -1082,22 +1147,27 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
         // 2) verify [t, d1..dk] on the target in one batch with checkpoints
         int32_t am[5];
         if (xjh_chain_eval(tgt, toks, kk + 1, kk + 1, 1, nullptr, am, err, errlen)) return -1;
-        // 3) accept the longest agreeing prefix (xj_spec.c:184-191)
+        // 3) accept the longest agreeing prefix (xj_spec.c:184-191); an accepted
+        //    end token is returned but neither it nor what follows is fed (:193-194)
         int a = 0;
         while (a < kk && am[a] == toks[a + 1]) { st.acc_at[a]++; a++; }
-        const int fed = a + 1;
-        for (int i = 0; i < fed && produced < n_gen; i++) out[produced++] = toks[i];
+        int fed = a + 1, n_out = a + 1;
+        for (int i = 1; i <= a; i++)
+            if (is_end(hp, toks[i])) { fed = i; n_out = i + 1; break; }
+        for (int i = 0; i < n_out && produced < n_gen; i++) out[produced++] = toks[i];
         n_gen_tok += fed;
-        st.n_steps++; st.n_drafted += kk; st.n_accepted += a;
+        st.n_steps++; st.n_drafted += kk; st.n_accepted += fed - 1 < a ? fed - 1 : a;
         if (fed < kk + 1 && xjh_chain_rollback(tgt, P + fed, err, errlen)) return -1;
-        // 4) bring the draft to the same prefix [.., t, d1..da]
-        if (a < kk) {
+        // 4) bring the draft to the same prefix [.., t, d1..d(fed-1)]: slot j holds
+        //    its state after feeding toks[0..j]
+        if (fed < kk + 1) {
             for (auto *S : dft->st)
-                if (xj_hip_stage_restore(&S->s, a, P + fed, err, errlen)) return -1;
+                if (xj_hip_stage_restore(&S->s, fed - 1, P + fed, err, errlen)) return -1;
         } else {
             int nx;
             if (draft_step(dft, toks[kk], &nx, err, errlen)) return -1;
         }
+        if (n_out > fed) { pending = toks[fed]; break; }   // stopped at an accepted end token
         pending = am[a];
         tgt->last_tok = pending;
     }
@@ -1105,7 +1175,7 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
     st.t_total_ms = now_ms() - t_start;
     if (stats) *stats = st;
     tgt->last_tok = pending;
-    return 0;
+    return produced;
 }
 
 // ------------------------------------------------------------ MTP drafting --
@@ -1116,6 +1186,9 @@ struct MtpRun {
     xjh_chain *c;              // the target chain (its embedding table)
     int32_t *d_ids = nullptr;  // token ids of the rows being built
     int32_t *d_am = nullptr;   // argmax of the MTP head
+    float *d_hn = nullptr;     // output_norm of the target's hidden rows [mb][E]
+    bool main_post = true;     // hidden rows pass the target's output_norm (XJ_MTP_MAIN_POST)
+    bool chain_post = true;    // an MTP output passes shared_head_norm before it is fed back (XJ_MTP_CHAIN_POST)
     int last_row = 0;          // row of S->x holding the last MTP output
     std::vector<float> ph;     // pending positions: main-model hidden rows [n][E]
     std::vector<int32_t> pt;   // and the token after each (-1: not known yet)
@@ -1178,13 +1251,26 @@ int mtp_flush(MtpRun &R, int n, bool want, int32_t *tok, char *err, size_t errle
     return 0;
 }
 
-// the first `rows` hidden rows of the target's last evaluation become pending
+// the first `rows` hidden rows of the target's last evaluation become
+// pending, normalised with the target's output_norm as the reference driver
+// does by default (push_ph, xj_spec.c:50-58)
 int push_hidden(MtpRun &R, int rows, char *err, size_t errlen) {
-    const int E = R.S->s.m->hp.n_embd;
+    const xj_hparams &hp = R.S->s.m->hp;
+    const int E = hp.n_embd;
     const size_t n0 = R.ph.size();
     R.ph.resize(n0 + (size_t)rows * E);
-    if (hipMemcpy(R.ph.data() + n0, R.c->x, sizeof(float) * rows * E, hipMemcpyDeviceToHost) != hipSuccess) {
-        snprintf(err, errlen, "hidden copy failed"); return -1;
+    hipStream_t st = R.c->stream;
+    const float *src = R.c->x;
+    if (R.main_post) {
+        if (norm_rows_launch(2, R.c->x, E, R.c->st.back()->out_norm, E, rows, hp.eps, R.d_hn, E, st)) {
+            snprintf(err, errlen, "hidden norm launch failed"); return -1;
+        }
+        src = R.d_hn;
+    }
+    if (hipMemcpyAsync(R.ph.data() + n0, src, sizeof(float) * rows * E, hipMemcpyDeviceToHost, st) != hipSuccess ||
+        chain_sync(R.c, err, errlen)) {
+        if (!err[0]) snprintf(err, errlen, "hidden copy failed");
+        return -1;
     }
     return 0;
 }
@@ -1192,7 +1278,7 @@ int push_hidden(MtpRun &R, int rows, char *err, size_t errlen) {
 
 extern "C" int xjh_spec_generate_mtp(xjh_chain *tgt, xj_stage *mtp, int k, const int32_t *prompt, int n_prompt, int n_gen,
                                      const int32_t *oracle, int n_oracle, int oracle_miss, int32_t *out,
-                                     xjh_spec_stats *stats, char *err, size_t errlen) {
+                                     xjh_spec_stats *stats, int32_t *draft_log, int draft_cap, char *err, size_t errlen) {
     err[0] = 0;
     if (!mtp || !mtp->mtp || strcmp(mtp->backend, "hip") != 0 || mtp->m != tgt->st[0]->s.m || !mtp->has_head) {
         snprintf(err, errlen, "an MTP stage of the target's model (HIP, with its head) is required"); return -1;
@@ -1201,15 +1287,23 @@ extern "C" int xjh_spec_generate_mtp(xjh_chain *tgt, xj_stage *mtp, int k, const
     MtpRun R;
     R.S = H(mtp);
     R.c = tgt;
-    const int E = R.S->s.m->hp.n_embd, V = (int)tgt->st.back()->output.n_rows, B = tgt->mb;
+    const xj_hparams &hp = R.S->s.m->hp;
+    const int E = hp.n_embd, V = (int)tgt->st.back()->output.n_rows, B = tgt->mb;
+    R.main_post = env_int("XJ_MTP_MAIN_POST", 1) != 0;
+    R.chain_post = env_int("XJ_MTP_CHAIN_POST", 1) != 0;
     if (k < 1) k = 1;
     if (k > 4) k = 4;
     if (k + 1 > B) k = B - 1;
     if (k > R.S->s.max_batch) k = R.S->s.max_batch;
-    if (hipMalloc(&R.d_ids, 4 * (size_t)R.S->s.max_batch) != hipSuccess || hipMalloc(&R.d_am, 4) != hipSuccess) {
-        snprintf(err, errlen, "hipMalloc failed"); return -1;
+    if (hipMalloc(&R.d_ids, 4 * (size_t)R.S->s.max_batch) != hipSuccess || hipMalloc(&R.d_am, 4) != hipSuccess ||
+        hipMalloc(&R.d_hn, sizeof(float) * (size_t)B * E) != hipSuccess) {
+        snprintf(err, errlen, "hipMalloc failed");
+        (void)hipFree(R.d_ids); (void)hipFree(R.d_am);
+        return -1;
     }
-    auto done = [&](int rc) { (void)hipFree(R.d_ids); (void)hipFree(R.d_am); return rc; };
+    auto done = [&](int rc) { (void)hipFree(R.d_ids); (void)hipFree(R.d_am); (void)hipFree(R.d_hn); return rc; };
+    int n_log = 0;
+    auto log_draft = [&](int32_t d) { if (draft_log && n_log < draft_cap) draft_log[n_log++] = d; };
     xjh_spec_stats st{};
     auto now_ms = []() { timespec ts; clock_gettime(CLOCK_MONOTONIC, &ts); return ts.tv_sec * 1e3 + ts.tv_nsec * 1e-6; };
     xjh_chain_reset(tgt);
@@ -1231,7 +1325,7 @@ extern "C" int xjh_spec_generate_mtp(xjh_chain *tgt, xj_stage *mtp, int k, const
     int produced = 0;
     while (produced < n_gen) {
         out[produced++] = t;   // t: the greedy token after everything fed so far (xj_spec.c:135-140)
-        if (produced == n_gen) break;
+        if (produced == n_gen || is_end(hp, t)) break;   // an end token is returned, never fed
         const int P = tgt->st[0]->s.n_past;
         R.pt.back() = t;
         int kk = k;
@@ -1254,13 +1348,16 @@ extern "C" int xjh_spec_generate_mtp(xjh_chain *tgt, xj_stage *mtp, int k, const
         toks[0] = t;
         const int mtp_pos = R.S->s.n_past + (int)R.pt.size();
         if (mtp_flush(R, (int)R.pt.size(), true, &toks[1], err, errlen)) return done(-1);
+        log_draft(toks[1]);
         for (int j = 2; j <= kk; j++) {
             const int32_t id = toks[j - 1];
+            const float *prev = R.S->x + (int64_t)R.last_row * E;
             if (mtp_rows(R, &id, nullptr, 1, err, errlen) ||
-                norm_rows_launch(0, R.S->x + (int64_t)R.last_row * E, E, R.S->out_norm, E, 1, R.S->s.m->hp.eps, R.S->mx + E,
-                                 2 * E, R.S->st) ||
+                (R.chain_post ? norm_rows_launch(2, prev, E, R.S->out_norm, E, 1, hp.eps, R.S->mx + E, 2 * E, R.S->st)
+                              : hipMemcpyAsync(R.S->mx + E, prev, 4 * E, hipMemcpyDeviceToDevice, R.S->st) != hipSuccess) ||
                 mtp_forward(R, 1, true, &toks[j], err, errlen))
                 return done(-1);
+            log_draft(toks[j]);
         }
         if (mtp->rollback(mtp, mtp_pos, err, errlen)) return done(-1);
         st.t_draft_ms += now_ms() - t0;
@@ -1270,25 +1367,29 @@ extern "C" int xjh_spec_generate_mtp(xjh_chain *tgt, xj_stage *mtp, int k, const
             if (oracle_miss && (gi * 7 + j) % oracle_miss == 0) toks[j] = (toks[j] + 1) % V;
         }
         // 2) verify [t, d1..dk] in one batch with checkpoints; 3) accept the
-        //    agreeing prefix (xj_spec.c:179-201)
+        //    agreeing prefix; an accepted end token is returned, and neither it
+        //    nor what follows is fed (xj_spec.c:179-201)
         int32_t am[5];
         if (xjh_chain_eval(tgt, toks, kk + 1, kk + 1, 1, nullptr, am, err, errlen)) return done(-1);
         int a = 0;
         while (a < kk && am[a] == toks[a + 1]) { st.acc_at[a]++; a++; }
-        const int fed = a + 1;
-        for (int i = 1; i < fed && produced < n_gen; i++) out[produced++] = toks[i];
-        st.n_steps++; st.n_drafted += kk; st.n_accepted += a;
+        int fed = a + 1, n_out = a + 1;
+        for (int i = 1; i <= a; i++)
+            if (is_end(hp, toks[i])) { fed = i; n_out = i + 1; break; }
+        for (int i = 1; i < n_out && produced < n_gen; i++) out[produced++] = toks[i];
+        st.n_steps++; st.n_drafted += kk; st.n_accepted += fed - 1 < a ? fed - 1 : a;
         // 4) the fed positions become pending for the MTP stage (xj_spec.c:204-207)
         if (push_hidden(R, fed, err, errlen)) return done(-1);
         for (int i = 1; i < fed; i++) R.pt.push_back(toks[i]);
         R.pt.push_back(-1);
         if (fed < kk + 1 && xjh_chain_rollback(tgt, P + fed, err, errlen)) return done(-1);
+        if (n_out > fed) { t = toks[fed]; break; }   // stopped at an accepted end token
         t = am[a];
     }
     tgt->last_tok = t;
     st.t_total_ms = now_ms() - t_start;
     if (stats) *stats = st;
-    return done(0);
+    return done(produced);
 }
 
 extern "C" int xjh_chain_time_gemv(xjh_chain *c, int iters, double *ms_per_step, double *bytes_per_step,

@@ -228,6 +228,10 @@ struct Writer {
     void kv_u32(const char *k, uint32_t v) { str(k); u32(4 /*U32*/); u32(v); }
     void kv_f32(const char *k, float v) { str(k); u32(6 /*F32*/); uint32_t b; memcpy(&b, &v, 4); u32(b); }
     void kv_str(const char *k, const char *v) { str(k); u32(8 /*STR*/); str(v); }
+    void kv_strs(const char *k, const std::vector<std::string> &v) {
+        str(k); u32(9 /*ARR*/); u32(8 /*STR*/); u64(v.size());
+        for (const auto &e : v) str(e);
+    }
 };
 
 struct TensorSpec {
@@ -339,9 +343,10 @@ extern "C" int64_t xjs_write_model(const char *path, const xjs_config *c, char *
         t.nbytes = xjh_row_bytes(t.type, t.ne0) * (uint64_t)(t.ne1 ? t.ne1 : 1);
         off = (off + t.nbytes + ALIGN - 1) / ALIGN * ALIGN;
     }
+    if (c->eos_id >= V || c->eot_id >= V) { snprintf(err, errlen, "end token id outside the vocabulary"); return -1; }
     Writer w;
     w.u32(0x46554747u); w.u32(3); w.u64(ts.size());
-    w.u64(c->nextn ? 21 : 20);  // number of key/values below
+    w.u64(20 + (c->nextn ? 1 : 0) + (c->eos_id >= 0) + (c->eot_id >= 0));  // number of key/values below
     w.kv_str("general.architecture", "qwen35");
     w.kv_str("general.name", "synthetic-qwen35");
     w.kv_u32("general.alignment", (uint32_t)ALIGN);
@@ -363,6 +368,13 @@ extern "C" int64_t xjs_write_model(const char *path, const xjs_config *c, char *
     w.kv_u32("qwen35.ssm.group_count", HK);
     w.kv_u32("qwen35.ssm.time_step_rank", HV);
     w.kv_u32("qwen35.full_attention_interval", c->full_attn_interval);
+    if (c->eos_id >= 0) w.kv_u32("tokenizer.ggml.eos_token_id", (uint32_t)c->eos_id);
+    if (c->eot_id >= 0) {   // a vocabulary of placeholder pieces with <|im_end|> at eot_id
+        std::vector<std::string> toks((size_t)V);
+        for (int i = 0; i < V; i++) toks[i] = "<t" + std::to_string(i) + ">";
+        toks[(size_t)c->eot_id] = "<|im_end|>";
+        w.kv_strs("tokenizer.ggml.tokens", toks);
+    }
     for (auto &t : ts) {
         w.str(t.name);
         w.u32(t.ne1 ? 2 : 1);

@@ -91,7 +91,8 @@ class XjsConfig(C.Structure):
                [("rope_base", C.c_float), ("eps", C.c_float)] + \
                [(n, C.c_int) for n in ("conv_k", "s_k", "h_k", "h_v", "full_attn_interval")] + \
                [(n, C.c_uint32) for n in ("type_default", "type_embd", "type_out", "type_v", "type_down")] + \
-               [("w_std", C.c_float), ("seed", C.c_uint64), ("nextn", C.c_int)]
+               [("w_std", C.c_float), ("seed", C.c_uint64), ("nextn", C.c_int), ("eos_id", C.c_int32),
+                ("eot_id", C.c_int32)]
 
 
 # -------------------------------------------------------------- library --
@@ -153,7 +154,7 @@ def lib():
     _sig(L, "xjh_chain_last_decode_ms", D, P)
     _sig(L, "xjh_chain_time_gemv", I, P, I, C.POINTER(D), C.POINTER(D), C.POINTER(I), CP, S)
     _sig(L, "xjh_spec_generate", I, P, P, I, I, P, I, I, P, C.POINTER(XjhSpecStats), CP, S)
-    _sig(L, "xjh_spec_generate_mtp", I, P, PS, I, P, I, I, P, I, I, P, C.POINTER(XjhSpecStats), CP, S)
+    _sig(L, "xjh_spec_generate_mtp", I, P, PS, I, P, I, I, P, I, I, P, C.POINTER(XjhSpecStats), P, I, CP, S)
     _sig(L, "xjh_malloc", P, S)
     _sig(L, "xjh_free", None, P)
     _sig(L, "xjh_h2d", I, P, P, S)
@@ -396,10 +397,12 @@ class Chain:
         return (am[:nl], lg[:nl]) if want_logits else am[:nl]
 
     def decode(self, n):
-        out = np.empty(n, np.int32)
+        """Up to n greedy tokens; fewer when an end token came (it is the last one returned)."""
+        out = np.empty(max(n, 1), np.int32)
         err = _err()
-        _check(lib().xjh_chain_decode(self.ptr, n, _ptr(out), err, ERR), err, "chain decode")
-        return out
+        rc = lib().xjh_chain_decode(self.ptr, n, _ptr(out), err, ERR)
+        _check(rc < 0, err, "chain decode")
+        return out[:rc]
 
     @property
     def last_token(self):
@@ -441,22 +444,28 @@ def spec_generate(target, draft, k, n_gen, oracle=None, oracle_miss=0):
     orc = np.ascontiguousarray(oracle, np.int32) if oracle is not None else None
     rc = lib().xjh_spec_generate(target.ptr, draft.ptr, k, n_gen, _ptr(orc) if orc is not None else None,
                                  len(orc) if orc is not None else 0, oracle_miss, _ptr(out), C.byref(st), err, ERR)
-    _check(rc, err, "spec generate")
-    return out, st
+    _check(rc < 0, err, "spec generate")
+    return out[:rc], st
 
 
-def spec_generate_mtp(target, mtp_stage, k, prompt, n_gen, oracle=None, oracle_miss=0):
-    """Speculative decoding with the model's MTP stage drafting k tokens; feeds the prompt itself."""
+def spec_generate_mtp(target, mtp_stage, k, prompt, n_gen, oracle=None, oracle_miss=0, draft_log=False):
+    """Speculative decoding with the model's MTP stage drafting k tokens; feeds the prompt itself.
+    Returns (tokens, stats) or, with draft_log, (tokens, stats, drafted tokens in order)."""
     out = np.empty(n_gen, np.int32)
     st = XjhSpecStats()
     err = _err()
     p = np.ascontiguousarray(prompt, np.int32)
     orc = np.ascontiguousarray(oracle, np.int32) if oracle is not None else None
+    cap = 4 * n_gen + 4
+    log = np.full(cap, -1, np.int32)
     rc = lib().xjh_spec_generate_mtp(target.ptr, mtp_stage.ptr, k, _ptr(p), len(p), n_gen,
                                      _ptr(orc) if orc is not None else None, len(orc) if orc is not None else 0,
-                                     oracle_miss, _ptr(out), C.byref(st), err, ERR)
-    _check(rc, err, "MTP speculative generate")
-    return out, st
+                                     oracle_miss, _ptr(out), C.byref(st), _ptr(log) if draft_log else None,
+                                     cap if draft_log else 0, err, ERR)
+    _check(rc < 0, err, "MTP speculative generate")
+    if draft_log:
+        return out[:rc], st, log[:min(st.n_drafted, cap)]
+    return out[:rc], st
 
 
 # --------------------------------------------------------- device memory --

@@ -37,6 +37,8 @@ class SynthConfig:
     w_std: float = 0.02
     seed: int = BASE_SEED
     nextn: int = 0        # 1: one MTP layer after the main layers
+    eos_id: int = -1      # >= 0: tokenizer.ggml.eos_token_id
+    eot_id: int = -1      # >= 0: a token list with "<|im_end|>" at this id
 
     def with_(self, **kw):
         return replace(self, **kw)

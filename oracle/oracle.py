@@ -97,28 +97,35 @@ def rlib(native=False):
         _sig(L, "ref_embed", None, PM, C.c_int32, P)
         _sig(L, "ref_greedy", I, PM, I, I, I, P, I, I, P, P, CP, S)
         _sig(L, "ref_abi_offsets", I, C.POINTER(C.c_long), I)
-        _sig(L, "ref_spec_run", I, PM, PS, PS, PS, I, P, I, I, P, I, I, P, C.POINTER(C.c_long), CP, S)
+        _sig(L, "ref_spec_run", I, PM, PS, PS, PS, I, P, I, I, P, I, I, P, C.POINTER(C.c_long), P, I,
+             C.POINTER(C.c_int), CP, S)
         _r[key] = L
     return _r[key]
 
 
-def ref_spec_run(model_ptr, a, b, mtp, k, prompt, n_gen, oracle=None, oracle_miss=0):
+def ref_spec_run(model_ptr, a, b, mtp, k, prompt, n_gen, oracle=None, oracle_miss=0, drafts=False):
     """The reference's own pipeline + speculative driver (greedy) over the given
     stage pointers (any backend behind the xj_stage vtable; b and mtp may be None).
-    Returns (tokens, (verify steps, drafted, accepted))."""
+    Stops after an end token, as xjpipe-host does (the token is kept).
+    Returns (tokens, (verify steps, drafted, accepted)) and, with drafts, the
+    MTP stage's proposals in order as a third item."""
     PS = C.POINTER(xp.XjStage)
     p = np.ascontiguousarray(prompt, np.int32)
     o = np.ascontiguousarray(oracle, np.int32) if oracle is not None else None
     out = np.empty(n_gen, np.int32)
     st = (C.c_long * 3)()
+    cap = 4 * n_gen + 4
+    log = np.full(cap, -1, np.int32)
+    nd = C.c_int(0)
     err = C.create_string_buffer(ERR)
     rc = rlib().ref_spec_run(C.cast(model_ptr, C.POINTER(xp.XjModel)), C.cast(a, PS), C.cast(b, PS) if b else None,
                              C.cast(mtp, PS) if mtp else None, k, _ptr(p), len(p), n_gen,
                              _ptr(o) if o is not None else None, len(o) if o is not None else 0, oracle_miss,
-                             _ptr(out), st, err, ERR)
-    if rc:
+                             _ptr(out), st, _ptr(log), cap, C.byref(nd), err, ERR)
+    if rc < 0:
         raise RuntimeError(err.value.decode())
-    return out, (st[0], st[1], st[2])
+    res = (out[:rc], (st[0], st[1], st[2]))
+    return res + (log[:nd.value],) if drafts else res
 
 
 # ---------------------------------------------------------------- oracle --

@@ -93,32 +93,86 @@ int ref_greedy(const xj_model *m, int split, int n_ctx, int max_batch, const int
     return rc ? -1 : 0;
 }
 
+/* A stage that forwards every call to `inner` and records the greedy token
+ * of every logits row it returns: wrapped around the MTP stage, that is the
+ * sequence of drafts the driver proposes (one logits call per draft,
+ * xj_spec.c:157,170). */
+typedef struct {
+    struct xj_stage s;
+    xj_stage *inner;
+    int32_t *log;
+    int cap, n;
+} rec_stage;
+
+static int rec_forward(xj_stage *s, float *x, int T, char *err, size_t errlen) {
+    rec_stage *r = (rec_stage *)s;
+    r->inner->keep = s->keep;
+    const int rc = r->inner->forward(r->inner, x, T, err, errlen);
+    s->n_past = r->inner->n_past; s->keep = r->inner->keep; s->ck_start = r->inner->ck_start; s->ck_T = r->inner->ck_T;
+    return rc;
+}
+static int rec_logits(xj_stage *s, const float *x, int T, float *logits, char *err, size_t errlen) {
+    rec_stage *r = (rec_stage *)s;
+    const int rc = r->inner->logits(r->inner, x, T, logits, err, errlen);
+    const int V = s->m->hp.n_vocab;
+    for (int t = 0; !rc && t < T; t++)
+        if (r->n < r->cap) r->log[r->n++] = greedy_pick(NULL, logits + (size_t)t * V, V);
+    return rc;
+}
+static int rec_rollback(xj_stage *s, int n_past, char *err, size_t errlen) {
+    rec_stage *r = (rec_stage *)s;
+    const int rc = r->inner->rollback(r->inner, n_past, err, errlen);
+    s->n_past = r->inner->n_past; s->ck_T = r->inner->ck_T;
+    return rc;
+}
+static void rec_reset(xj_stage *s) {
+    rec_stage *r = (rec_stage *)s;
+    r->inner->reset(r->inner);
+    s->n_past = r->inner->n_past;
+}
+
+static int is_end_tok(const xj_model *m, int32_t t) { return (uint32_t)t == m->hp.eot || (uint32_t)t == m->hp.eos; }
+
 /* The reference's own speculative driver (xj_pipeline over stages a | b, the
  * MTP stage mtp drafting k tokens per step; mtp = NULL or k = 0: plain
  * greedy) over whatever stages it is given - the reference's CPU stages, the
  * oracle's, or the HIP library's through the same vtable. oracle/n_oracle
- * replace the drafts (the driver's test mode, xj_spec.h:37-38). Greedy tokens
- * into out; stats = {verify steps, drafted, accepted}. */
+ * replace the drafts (the driver's test mode, xj_spec.h:37-38). Tokens into
+ * out, ending after an end token as xjpipe-host's loop does
+ * (tools/xjpipe-host.c:129-136; the end token is kept here); returns their
+ * count. stats = {verify steps, drafted, accepted}; drafts (optional) gets the
+ * MTP stage's proposals in order. */
 int ref_spec_run(const xj_model *m, xj_stage *a, xj_stage *b, xj_stage *mtp, int k, const int32_t *prompt, int n_prompt,
-                 int n_gen, const int32_t *oracle, int n_oracle, int oracle_miss, int32_t *out, long *stats, char *err,
-                 size_t errlen) {
+                 int n_gen, const int32_t *oracle, int n_oracle, int oracle_miss, int32_t *out, long *stats,
+                 int32_t *drafts, int draft_cap, int *n_drafts, char *err, size_t errlen) {
     xj_pipeline p;
     xj_spec sp;
-    int rc = xj_pipeline_init(&p, m, a, NULL, b) || xj_spec_init(&sp, &p, mtp, k);
+    rec_stage rec;
+    memset(&rec, 0, sizeof rec);
+    if (mtp) {
+        rec.s = *mtp;
+        rec.s.forward = rec_forward; rec.s.logits = rec_logits; rec.s.rollback = rec_rollback; rec.s.reset = rec_reset;
+        rec.inner = mtp; rec.log = drafts; rec.cap = drafts ? draft_cap : 0;
+    }
+    int rc = xj_pipeline_init(&p, m, a, NULL, b) || xj_spec_init(&sp, &p, mtp ? &rec.s : NULL, k);
     if (rc) { snprintf(err, errlen, "pipeline / spec init failed"); return -1; }
     sp.oracle = oracle; sp.n_oracle = n_oracle; sp.oracle_miss = oracle_miss;
     rc = xj_spec_feed(&sp, prompt, n_prompt, err, errlen);
-    int produced = 0;
-    while (!rc && produced < n_gen) {
+    int produced = 0, ended = 0;
+    while (!rc && produced < n_gen && !ended) {
         int32_t o[XJ_SPEC_MAXK + 1];
         const int n = xj_spec_next(&sp, greedy_pick, NULL, o, n_gen - produced, err, errlen);
         if (n < 1) { rc = -1; break; }
-        for (int i = 0; i < n && produced < n_gen; i++) out[produced++] = o[i];
+        for (int i = 0; i < n && produced < n_gen && !ended; i++) {
+            out[produced++] = o[i];
+            ended = is_end_tok(m, o[i]);
+        }
     }
     if (stats) { stats[0] = sp.n_steps; stats[1] = sp.n_drafted; stats[2] = sp.n_accepted; }
+    if (n_drafts) *n_drafts = rec.n;
     xj_spec_free(&sp);
     xj_pipeline_free(&p);
-    return rc ? -1 : 0;
+    return rc ? -1 : produced;
 }
 
 /* offsetof every field of the boundary types, in a fixed order shared with

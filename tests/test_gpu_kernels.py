@@ -127,11 +127,12 @@ def test_gemv_residual_add():
 
 
 def test_gemv_lm_head_shape():
-    """Q4_K 151936 x 1024 (the LM-head shape of the mixed batch) at T = 1 and 5."""
+    """Q4_K 151936 x 1024 (the LM-head shape of the mixed batch) at every
+    speculative-verify width T = 1..5."""
     rows, k = 151936, 1024
     blob = _weights(xp.Q4_K, rows, k, 31)
     w = xp.DevWeight(xp.Q4_K, blob, rows, k)
-    for T in (1, 5):
+    for T in (1, 2, 3, 4, 5):
         xs = xp.fill_normal(T * k, 40 + T, 1.0).reshape(T, k)
         got = xp.gemv(w, xs)
         want = orc.matmul(xp.Q4_K, blob, k, rows, xs)

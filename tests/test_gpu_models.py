@@ -73,27 +73,32 @@ def test_4b_two_stage_greedy_512_steps():
     b.destroy()
 
 
-@pytest.mark.parametrize("mode", ["draft_0_8b", "oracle_drafts"])
+@pytest.mark.parametrize("mode", ["draft_0_8b", "oracle_drafts", "oracle_miss"])
 def test_4b_speculative_with_0_8b_draft(mode):
+    """Config 5 in full: the 4B shape split 0-15 | 16-31 on one GPU, the 0.8B
+    model drafting 4 tokens per step, 1024-token prompt, 512 tokens; the
+    output equals the committed greedy tokens of the 4B shape (the oracle's
+    fp16-KV run, itself equal to the reference's) with the draft's own
+    proposals, with proposals taken from that output, and with one in four of
+    those perturbed."""
+    rec = fixture("greedy_4b.json")
     path = xp.cached_model(xp.CONFIG_4B, "synth4b")
+    check_model(path, rec)
     dpath = xp.cached_model(xp.CONFIG_0_8B, "synth08b")
     m, dm = xp.Model(path), xp.Model(dpath)
-    prompt = np.random.default_rng(11).integers(0, m.hp.n_vocab, 256).astype(np.int32)
-    n_gen = 96
-    st = xp.HipStage(m, 0, 32, 512, 8, True)
-    ch = xp.Chain([st])
-    plain = np.concatenate([ch.eval(prompt), ch.decode(n_gen - 1)])
-    ch.free()
-    st.destroy()
-    a, b = xp.HipStage(m, 0, 16, 512, 8, False), xp.HipStage(m, 16, 32, 512, 8, True)
-    d = xp.HipStage(dm, 0, dm.hp.n_layer, 512, 8, True)
+    prompt = np.random.default_rng(rec["prompt_seed"]).integers(0, m.hp.n_vocab, rec["n_prompt"]).astype(np.int32)
+    n_gen, want = rec["n_gen"], rec["oracle_kvf16"]["tokens"]
+    a = xp.HipStage(m, 0, 16, rec["n_ctx"], rec["max_batch"], False)
+    b = xp.HipStage(m, 16, 32, rec["n_ctx"], rec["max_batch"], True)
+    d = xp.HipStage(dm, 0, dm.hp.n_layer, rec["n_ctx"], rec["max_batch"], True)
     tc, dc = xp.Chain([a, b]), xp.Chain([d])
     tc.eval(prompt)
     dc.eval(prompt)
-    out, stats = xp.spec_generate(tc, dc, 4, n_gen, oracle=plain if mode == "oracle_drafts" else None)
+    oracle = None if mode == "draft_0_8b" else np.array(want, np.int32)
+    out, stats = xp.spec_generate(tc, dc, 4, n_gen, oracle=oracle, oracle_miss=4 if mode == "oracle_miss" else 0)
     print(f"{mode}: steps {stats.n_steps}, drafted {stats.n_drafted}, accepted {stats.n_accepted}, "
           f"{n_gen / (stats.t_total_ms / 1e3):.1f} tok/s")
-    assert out.tolist() == plain.tolist()
+    assert out.tolist() == want, f"diverges at {first_divergence(out.tolist(), want)}"
     if mode == "oracle_drafts":
         assert stats.n_accepted == stats.n_drafted
     for o in (tc, dc):

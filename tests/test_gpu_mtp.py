@@ -130,14 +130,22 @@ def test_native_mtp_driver(model_dir, shape):
     ch = xp.Chain([st1])
     plain = np.concatenate([ch.eval(prompt), ch.decode(n_gen - 1)])
     mt = xp.HipStage(m, L, L + 1, 128, 8, True)
-    out, st = xp.spec_generate_mtp(ch, mt, 3, prompt, n_gen)
+    out, st, log = xp.spec_generate_mtp(ch, mt, 3, prompt, n_gen, draft_log=True)
     print(f"{shape}: steps {st.n_steps} drafted {st.n_drafted} accepted {st.n_accepted}")
     assert out.tolist() == plain.tolist()
+    assert len(log) == st.n_drafted
     if orc.ref_available():
+        # the reference driver over the same HIP stages proposes the same drafts
+        # (hidden rows through output_norm, MTP outputs through shared_head_norm,
+        # both as x * (sc * w)), so its statistics are the native driver's
         hip = lambda l0, l1, head: xp.HipStage(m, l0, l1, 128, 8, head)
-        ref_out, ref_st = _driver_run(m.ptr, hip, L, 3, prompt, n_gen)
+        a, b, m2 = hip(0, L // 2, False), hip(L // 2, L, True), hip(L, L + 1, True)
+        ref_out, ref_st, ref_log = orc.ref_spec_run(m.ptr, a.ptr, b.ptr, m2.ptr, 3, prompt, n_gen, drafts=True)
+        for s in (a, b, m2):
+            s.destroy()
         assert ref_out.tolist() == plain.tolist()
         assert (st.n_steps, st.n_drafted, st.n_accepted) == ref_st
+        assert log.tolist() == ref_log.tolist()
     out, st = xp.spec_generate_mtp(ch, mt, 3, prompt, n_gen, oracle=plain)
     assert out.tolist() == plain.tolist() and st.n_accepted == st.n_drafted > 0
     out, st = xp.spec_generate_mtp(ch, mt, 4, prompt, n_gen, oracle=plain, oracle_miss=4)

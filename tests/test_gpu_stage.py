@@ -257,3 +257,60 @@ def test_stage_over_a_layer_range_load(tiny, tiny_path, tmp_path):
     with pytest.raises(xp.XjError, match="not mapped"):
         xp.HipStage(part, 0, L // 2, 64, 16, True)
     part.close()
+
+
+class RefLoaded:
+    """A model table built by the reference's own loader (xj_model_load,
+    core/xj_model.c:204), seen through the boundary struct."""
+
+    def __init__(self, path, mtp_from=None):
+        err = orc.C.create_string_buffer(512)
+        r = orc.rlib().ref_model_load(path.encode(), err, 512)
+        assert r, err.value
+        if mtp_from:
+            assert orc.rlib().ref_model_attach_mtp(r, mtp_from.encode(), err, 512) == 0, err.value
+        self.r = r
+        self.ptr = orc.C.cast(r, orc.C.POINTER(xp.XjModel))
+
+    @property
+    def hp(self):
+        return self.ptr.contents.hp
+
+    def free(self):
+        orc.rlib().ref_model_free(self.r)
+
+
+@pytest.mark.skipif(not orc.ref_available(), reason="reference build (oracle/_ref) not present")
+def test_hip_stages_over_the_reference_loader(model_dir, tiny_path):
+    """The literal drop-in (core/xj_stage.h:46): xj_hip_stage_new over a model
+    that the reference's own loader built, driven by the reference's own
+    pipeline and greedy driver (split 0-3 | 3-8, as xjpipe-host runs it):
+    the oracle's fp16-KV greedy tokens, and bit for bit the tokens of HIP
+    stages over this library's loader. The MTP layer attached by the
+    reference's xj_model_attach_mtp (core/xj_model.c:275-300) from a second
+    file serves a HIP MTP stage whose drafts leave the output unchanged."""
+    from conftest import synth_model
+    rec_prompt = prompt_ids(xp.Model(tiny_path), 24, 41)
+    mine = xp.Model(tiny_path)
+    L = mine.hp.n_layer
+    ref = RefLoaded(tiny_path, mtp_from=synth_model(model_dir, xp.TINY_MTP, "tiny_mtp"))
+    n_gen = 32
+
+    def drive(model, k):
+        a, b = xp.HipStage(model, 0, 3, 256, 8, False), xp.HipStage(model, 3, L, 256, 8, True)
+        mt = xp.HipStage(model, L, L + 1, 256, 8, True) if k else None
+        out, st = orc.ref_spec_run(model.ptr, a.ptr, b.ptr, mt.ptr if mt else None, k, rec_prompt, n_gen)
+        for s in (a, b, mt):
+            if s:
+                s.destroy()
+        return out, st
+
+    c = orc.CpuStage(mine.ptr, 0, L, 256, 8, True, kv_f16=True)
+    want, _ = orc.greedy([c], rec_prompt, n_gen)
+    c.destroy()
+    got_ref, _ = drive(ref, 0)
+    got_mine, _ = drive(mine, 0)
+    assert got_ref.tolist() == got_mine.tolist() == want.tolist()
+    spec, st = drive(ref, 3)
+    assert spec.tolist() == want.tolist() and st[1] > 0
+    ref.free()

@@ -539,19 +539,77 @@ def test_reference_mtp_driver_over_oracle_stages(model_dir):
         a = orc.CpuStage(mp, 0, L // 2, 128, 8, False, ref=ref)
         b = orc.CpuStage(mp, L // 2, L, 128, 8, True, ref=ref)
         mt = orc.CpuStage(mp, L, L + 1, 128, 8, True, ref=ref) if k else None
-        out = orc.ref_spec_run(mp, a.ptr, b.ptr, mt.ptr if mt else None, k, prompt, n_gen, oracle)
+        out = orc.ref_spec_run(mp, a.ptr, b.ptr, mt.ptr if mt else None, k, prompt, n_gen, oracle, drafts=True)
         for s in (a, b, mt):
             if s:
                 s.destroy()
         return out
 
-    plain, _ = run(r, True, 0)
-    spec_ref, st_ref = run(r, True, 3)
-    spec_orc, st_orc = run(m.ptr, False, 3)
+    plain, _, _ = run(r, True, 0)
+    spec_ref, st_ref, d_ref = run(r, True, 3)
+    spec_orc, st_orc, d_orc = run(m.ptr, False, 3)
     assert spec_ref.tolist() == plain.tolist() and spec_orc.tolist() == plain.tolist()
     assert st_ref == st_orc and st_ref[0] > 0
-    _, st_all = run(m.ptr, False, 3, oracle=plain)
+    # the drafted tokens themselves, one per call of the MTP head, in order
+    assert len(d_ref) == st_ref[1] and d_ref.tolist() == d_orc.tolist()
+    _, st_all, _ = run(m.ptr, False, 3, oracle=plain)
     assert st_all[1] > 0 and st_all[2] == st_all[1]
+    orc.rlib().ref_model_free(r)
+
+
+def end_token_model(model_dir, cfg, name, prompt, n, min_pos=6, kind="eos"):
+    """(path, greedy tokens, i): cfg's model rewritten with an end token that
+    first appears at index i >= min_pos of its greedy output after `prompt`
+    (the oracle's fp32-KV greedy loop on the same weights), as
+    tokenizer.ggml.eos_token_id (kind "eos") or as the "<|im_end|>" entry of a
+    token list (kind "eot")."""
+    from conftest import synth_model
+    base = xp.Model(synth_model(model_dir, cfg, name))
+    L = base.hp.n_layer
+    st = orc.CpuStage(base.ptr, 0, L, 256, 8, True)
+    toks, _ = orc.greedy([st], prompt, n)
+    st.destroy()
+    base.close()
+    i = next(j for j in range(min_pos, n) if toks[j] not in toks[:j])
+    end = int(toks[i])
+    ecfg = cfg.with_(eos_id=end) if kind == "eos" else cfg.with_(eot_id=end)
+    return synth_model(model_dir, ecfg, f"{name}_{kind}{end}"), toks, i
+
+
+@needs_ref
+@pytest.mark.parametrize("kind", ["eos", "eot"])
+def test_end_tokens_in_the_reference_driver(model_dir, kind):
+    """A model whose end token (eos id key or "<|im_end|>" in its token list) is
+    the greedy output's token at index i: the loader reads it as the reference
+    does, and the reference driver over the oracle's stages and over its own
+    stops there with the tokens of plain greedy decoding up to and including it,
+    with and without MTP speculation (oracle drafts carry the end token into a
+    verify batch)."""
+    prompt = np.random.default_rng(95).integers(0, xp.TINY_MTP.n_vocab, 14).astype(np.int32)
+    path, plain, i = end_token_model(model_dir, xp.TINY_MTP, "tiny_mtp", prompt, 40, kind=kind)
+    m = xp.Model(path)
+    err = orc.C.create_string_buffer(512)
+    r = orc.rlib().ref_model_load(path.encode(), err, 512)
+    assert r, err.value
+    assert bytes(r.contents.hp) == bytes(m.m.hp)
+    end = int(plain[i])
+    assert (m.hp.eos if kind == "eos" else m.hp.eot) == end
+    L = m.hp.n_layer
+
+    def run(mp, ref, k, oracle=None):
+        a = orc.CpuStage(mp, 0, L // 2, 128, 8, False, ref=ref)
+        b = orc.CpuStage(mp, L // 2, L, 128, 8, True, ref=ref)
+        mt = orc.CpuStage(mp, L, L + 1, 128, 8, True, ref=ref) if k else None
+        out = orc.ref_spec_run(mp, a.ptr, b.ptr, mt.ptr if mt else None, k, prompt, 40, oracle)
+        for s in (a, b, mt):
+            if s:
+                s.destroy()
+        return out
+
+    for mp, ref in ((r, True), (m.ptr, False)):
+        for k, oracle in ((0, None), (3, None), (3, plain), (4, plain)):
+            out, _ = run(mp, ref, k, oracle)
+            assert out.tolist() == plain[:i + 1].tolist(), (ref, k, oracle is not None)
     orc.rlib().ref_model_free(r)
 
 
