@@ -257,6 +257,18 @@ int xjh_dequant(uint32_t type, const void *dw, int64_t n_rows, int64_t k, int64_
 /* y[t][r] = W[r] . x[t] (add != 0: y += ...), T in 1..max, fp32 accumulate. */
 int xjh_gemv(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T,
              float *y, int add, char *err, size_t errlen);
+/* xjh_gemv without any allocation: no counterpart in the reference. For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The same kernels and
+ * results as xjh_gemv, bit for bit; the prepared activations go to a static
+ * 1 MiB scratch array that each GPU holds from the library's load to the end
+ * of the process, so T * (7.625 * k rounded up to 256 bytes) must fit in
+ * 1 MiB (k = 9216: T <= 14), or the call fails with a message. Nothing in the
+ * scratch needs to start at zero; every call on a GPU reuses that GPU's copy,
+ * so calls that overlap on one GPU (other threads) race. The first call in a
+ * process creates the library's stream, as every per-op entry does. */
+int xjh_gemv_noalloc(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T,
+                     float *y, int add, char *err, size_t errlen);
 /* The same product for a prefill chunk on the matrix cores: Q4_K or Q6_K
  * rows, k % 256 == 0, T in 1..64. Integer sub-block sums are those of
  * xjh_gemv (v_mfma_i32_16x16x32_i8 in place of dot4), so the two agree to

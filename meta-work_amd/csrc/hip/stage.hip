@@ -26,6 +26,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -1477,19 +1478,26 @@ extern "C" int xjh_dequant(uint32_t type, const void *dw, int64_t n_rows, int64_
     return ops_done(err, errlen);
 }
 
+// The per-op GEMV on `st`. Its prepared activations (T tokens of
+// xq_off(k).stride bytes) go to xq_given when it is not null, otherwise to a
+// library buffer grown on demand (the per-op entries are synchronous on one stream).
 static int gemv_enqueue(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T, float *y, int add,
-                        hipStream_t st) {
+                        hipStream_t st, uint8_t *xq_given = nullptr) {
     DevW w;
     w.p = (const uint8_t *)dw; w.type = type; w.n_rows = n_rows; w.k = k;
-    static uint8_t *xq = nullptr;   // grown on demand; the per-op entries are synchronous on one stream
+    static uint8_t *xq_own = nullptr;
     static size_t xq_cap = 0;
-    const size_t need = (size_t)T * xq_off((int)k).stride;
-    if (need > xq_cap) {
-        if (xq) (void)hipFree(xq);
-        xq = nullptr;
-        xq_cap = 0;
-        if (hipMalloc(&xq, need) != hipSuccess) return -1;
-        xq_cap = need;
+    uint8_t *xq = xq_given;
+    if (!xq) {
+        const size_t need = (size_t)T * xq_off((int)k).stride;
+        if (need > xq_cap) {
+            if (xq_own) (void)hipFree(xq_own);
+            xq_own = nullptr;
+            xq_cap = 0;
+            if (hipMalloc(&xq_own, need) != hipSuccess) return -1;
+            xq_cap = need;
+        }
+        xq = xq_own;
     }
     Gemv g(xq);
     g.a.x = x; g.a.xs = (int32_t)k; g.a.pro = PRO_NONE;
@@ -1504,14 +1512,65 @@ static int gemv_enqueue(uint32_t type, const void *dw, int64_t n_rows, int64_t k
     return g.run(T, st);
 }
 
+static bool gemv_shape_ok(uint32_t type, int64_t n_rows, int64_t k, int T) {
+    return gemv_type_ok(type) && T >= 1 && n_rows >= 1 && k >= 32 && k % 32 == 0 && k <= INT32_MAX / 8 &&
+           !((type == XJ_Q4_K || type == XJ_Q6_K || type == XJ_Q5_K) && k % 256);
+}
+
 extern "C" int xjh_gemv(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T, float *y, int add,
                         char *err, size_t errlen) {
     if (!ops_stream()) return -1;
-    if (!gemv_type_ok(type) || T < 1 || n_rows < 1 || k % 32 ||
-        ((type == XJ_Q4_K || type == XJ_Q6_K || type == XJ_Q5_K) && k % 256)) {
-        snprintf(err, errlen, "unsupported GEMV shape/type"); return -1;
-    }
+    if (!gemv_shape_ok(type, n_rows, k, T)) { snprintf(err, errlen, "unsupported GEMV shape/type"); return -1; }
     if (gemv_enqueue(type, dw, n_rows, k, x, T, y, add, g_stream)) { snprintf(err, errlen, "GEMV launch failed"); return -1; }
+    return ops_done(err, errlen);
+}
+
+// Scratch of xjh_gemv_noalloc: the prepared activations of one call. Each GPU
+// holds its own copy of this array from the library's load to the process's
+// end; host code reaches it only through the per-device address taken with
+// hipGetSymbolAddress (the array's name is not a device address on the host).
+constexpr size_t kNoAllocScratchBytes = size_t(1) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+uint8_t *g_scratch_dev[kMaxDevices];   // device address of `scratch` on each device, set once
+std::mutex g_scratch_mu;
+
+// The current device's address of `scratch`, looked up on the first call on that device.
+uint8_t *scratch_address(char *err, size_t errlen) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        snprintf(err, errlen, "no usable HIP device (%d)", dev);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            snprintf(err, errlen, "scratch address lookup failed: %s", hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_dev[dev] = (uint8_t *)p;
+    }
+    return g_scratch_dev[dev];
+}
+}  // namespace
+
+extern "C" int xjh_gemv_noalloc(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T, float *y,
+                                int add, char *err, size_t errlen) {
+    if (!gemv_shape_ok(type, n_rows, k, T)) { snprintf(err, errlen, "unsupported GEMV shape/type"); return -1; }
+    const size_t need = (size_t)T * (size_t)xq_off((int)k).stride;
+    if (need > kNoAllocScratchBytes) {
+        snprintf(err, errlen, "xjh_gemv_noalloc: %d tokens of %lld inputs need %zu scratch bytes, above its %zu-byte maximum",
+                 T, (long long)k, need, kNoAllocScratchBytes);
+        return -1;
+    }
+    if (!ops_stream()) { snprintf(err, errlen, "no HIP stream"); return -1; }
+    uint8_t *xq = scratch_address(err, errlen);
+    if (!xq) return -1;
+    if (gemv_enqueue(type, dw, n_rows, k, x, T, y, add, g_stream, xq)) { snprintf(err, errlen, "GEMV launch failed"); return -1; }
     return ops_done(err, errlen);
 }
 

@@ -165,6 +165,7 @@ def lib():
     _sig(L, "xjh_upload_weight", P, U32, P, I64, I64, CP, S)
     _sig(L, "xjh_dequant", I, U32, P, I64, I64, I64, I64, P, CP, S)
     _sig(L, "xjh_gemv", I, U32, P, I64, I64, P, I, P, I, CP, S)
+    _sig(L, "xjh_gemv_noalloc", I, U32, P, I64, I64, P, I, P, I, CP, S)
     _sig(L, "xjh_gemm", I, U32, P, I64, I64, P, I, P, I, CP, S)
     _sig(L, "xjh_gemv_time", D, U32, C.POINTER(P), I, I64, I64, P, I, P, I, CP, S)
     _sig(L, "xjh_gemm_time", D, U32, C.POINTER(P), I, I64, I64, P, I, P, I, CP, S)
