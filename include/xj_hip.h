@@ -347,6 +347,21 @@ int xjh_delta_step(const float *qkv, int qkv_stride, int k_off, int v_off, const
  * (ties among the 40 values ordered by index). */
 int xjh_sample(const float *logits, int n, int T, float temperature, const uint32_t *rand30,
                int32_t *out_host, char *err, size_t errlen);
+/* UTF-8 piece streaming (host only): pieces of generated text go to cb only
+ * as whole UTF-8 characters. xjh_utf8_emit appends piece (its first 256
+ * bytes) to the bytes held back from earlier pieces, passes everything up to
+ * an incomplete trailing character (judged from the last 4 bytes) to cb,
+ * holds that character back and returns cb's result (0 when nothing is
+ * passed). Replaces: the app's `emit`, src/xiaoju-pipe/ios/App/XJGlue.c:285-305,
+ * with the state the app keeps in host_box (XJGlue.c:161) as its own struct;
+ * xjh_piece_fn is xjg_piece_fn (XJGlue.h:12). */
+typedef int (*xjh_piece_fn)(void *ctx, const char *utf8, int len);
+typedef struct {
+    char pending[8];
+    int32_t npending;
+} xjh_utf8_state;
+void xjh_utf8_reset(xjh_utf8_state *st);
+int xjh_utf8_emit(xjh_utf8_state *st, const char *piece, int n, xjh_piece_fn cb, void *ctx);
 /* First index of the maximum of each of T rows of n floats. */
 int xjh_argmax(const float *x, int n, int T, int32_t *out_host, char *err, size_t errlen);
 /* Gated delta rule (standalone, decay and beta given per token and head):

@@ -131,8 +131,11 @@ int swiglu_launch(float *g, const float *u, int64_t n, hipStream_t st) {
 
 // Row t of lg: radix-select the 40th largest value (ordered 32-bit keys, 8 bits
 // per pass, LDS histograms), take every value above it and the lowest indices
-// of those equal to it (the app's selection keeps the first of equal values),
-// then one thread sorts the 40 by value (ties by index), forms
+// of those equal to it, then one thread sorts the 40 by value (equal values in
+// index order) - the app's result whenever the kept values are distinct (its
+// replace-the-minimum loop and exchange sort keep and order equal values by
+// slot, not index; a value tied at the 40th place is never drawn, the 0.95 cut
+// always ending before the last kept value) - forms
 // p_i = exp((v_i - v_0) / temp) in double, cuts where the running share first
 // reaches 0.95 and picks with r = rnd[t] / 2^30 times the kept mass.
 constexpr int kTopK = 40;

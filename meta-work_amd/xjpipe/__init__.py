@@ -175,6 +175,8 @@ def lib():
     _sig(L, "xjh_delta_chunked", I, I, I, I, I, P, P, P, P, P, F, P, P, CP, S)
     _sig(L, "xjh_swiglu", I, P, P, I64, CP, S)
     _sig(L, "xjh_sample", I, P, I, I, F, P, P, CP, S)
+    _sig(L, "xjh_utf8_reset", None, P)
+    _sig(L, "xjh_utf8_emit", I, P, P, I, P, P)
     _sig(L, "xjh_delta_step", I, P, I, I, I, P, P, P, P, I, I, I, I, F, F, P, P, P, I, CP, S)
     _sig(L, "xjh_rope", I, P, I, I, I64, I64, I, I, F, CP, S)
     _sig(L, "xjh_conv_silu", I, P, P, P, I, I, I, P, I, CP, S)
@@ -628,6 +630,39 @@ def delta(q, k, v, decay, beta, state, qscale, chunk=0):
                                        err, ERR)
     _check(rc, err, "delta")
     return do.get(np.float32, (T, H, S)), ds.get(np.float32, (H, S, S))
+
+
+_PIECE_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_char), C.c_int)
+
+
+class Utf8Stream:
+    """Streams generated text pieces as whole UTF-8 characters (xjh_utf8_emit):
+    emit(piece) returns the bytes passed to the callback for that piece (b""
+    when the piece ends inside a character and nothing is complete yet);
+    stop_after makes the callback ask to stop (return 1) once that many
+    chunks were passed."""
+
+    def __init__(self, stop_after=None):
+        self._st = C.create_string_buffer(12)   # xjh_utf8_state: char[8] + int32
+        lib().xjh_utf8_reset(self._st)
+        self.chunks, self.stop_after = [], stop_after
+
+        def cb(ctx, p, n):
+            self.chunks.append(C.string_at(p, n))
+            return 1 if self.stop_after is not None and len(self.chunks) >= self.stop_after else 0
+
+        self._cb = _PIECE_FN(cb)
+
+    def emit(self, piece):
+        piece = bytes(piece)
+        before = len(self.chunks)
+        stop = lib().xjh_utf8_emit(self._st, piece, len(piece), self._cb, None)
+        return (self.chunks[before] if len(self.chunks) > before else b""), stop
+
+    @property
+    def pending(self):
+        n = int.from_bytes(self._st.raw[8:12], "little", signed=True)
+        return self._st.raw[:n]
 
 
 def sample(logits, temperature, rand30):

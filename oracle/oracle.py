@@ -58,6 +58,7 @@ def olib():
         _sig(L, "xjo_delta_recurrent", None, I, I, I, P, P, P, P, P, F, P, P)
         _sig(L, "xjo_conv_silu", None, I, I, P, P, P)
         _sig(L, "xjo_sample", I, P, I, F, U32)
+        _sig(L, "xjo_utf8_emit", I, P, P, I, P)
         _sig(L, "xjo_swiglu", None, S, P, P)
         _sig(L, "xjo_delta_step", None, I, I, I, F, F, P, P, P, P, P, P, P, P, P, P)
         _sig(L, "xjo_attn_decode", None, I, I, I, I, I, F, F, I, I, P, P, P, P, P, P, P, P)
@@ -176,6 +177,20 @@ def rope(v, n_rot, pos, base, ref=False):
 def sample(lg, temp, rand30):
     lg = np.ascontiguousarray(lg, np.float32)
     return olib().xjo_sample(_ptr(lg), lg.size, temp, int(rand30))
+
+
+class Utf8Emit:
+    """The app's UTF-8 streaming (xjo_utf8_emit): emit(piece) returns the bytes
+    the app would pass to its callback for that piece (b"" when none)."""
+
+    def __init__(self):
+        self._st = C.create_string_buffer(12)   # xjo_utf8: char[8] + int
+
+    def emit(self, piece):
+        piece = bytes(piece)
+        out = C.create_string_buffer(8 + 256)
+        n = olib().xjo_utf8_emit(self._st, piece, len(piece), out)
+        return out.raw[:n]
 
 
 def swiglu(g, u):

@@ -58,6 +58,11 @@ int xjo_argmax(const float *x, int n);
 /* The app's top-k 40 / top-p 0.95 sampler (ios/App/XJGlue.c:251-282), the
  * uniform number rand30 / 2^30 passed in. */
 int xjo_sample(const float *lg, int n, float temp, uint32_t rand30);
+/* The app's UTF-8 piece streaming (ios/App/XJGlue.c:285-305): piece (its first
+ * 256 bytes) after the held-back bytes; the bytes up to an incomplete trailing
+ * character go to *out (returned count), that character is held back. */
+typedef struct { char pending[8]; int npending; } xjo_utf8;
+int xjo_utf8_emit(xjo_utf8 *h, const char *s, int n, char *out);
 /* One token of the causal depthwise conv + SiLU (xj_cpu.c:172-182), x and
  * state [C][KC-1] updated in place. */
 void xjo_conv_silu(int C, int KC, float *x, const float *w, float *state);

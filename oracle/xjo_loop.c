@@ -8,6 +8,8 @@
  *                          driven by the greedy loop of src/xiaoju-pipe/tools/xjpipe-host.c:131-144
  *   xjo_sample          <- the app's sampler, src/xiaoju-pipe/ios/App/XJGlue.c:251-282
  *                          (the uniform number passed in)
+ *   xjo_utf8_emit       <- the app's emit, src/xiaoju-pipe/ios/App/XJGlue.c:285-305
+ *                          (the callback replaced by an output buffer)
  *   xjo_delta_recurrent <- the per-head update of src/xiaoju-pipe/core/xj_cpu.c:203-213
  *                          (decay and beta are inputs instead of being derived from alpha/dt/A)
  *
@@ -60,6 +62,30 @@ int xjo_sample(const float *lg, int n, float temp, uint32_t rand30) {
     double r = (double)rand30 / (double)(1u << 30) * s2;
     for (int i = 0; i < cut; i++) { r -= p[i]; if (r <= 0) return idx[i]; }
     return idx[0];
+}
+
+/* The app's emit (ios/App/XJGlue.c:285-305): the held-back bytes, then at most
+ * 256 bytes of the piece; from the end, skip up to 4 bytes of continuation
+ * (10xxxxxx) to the last lead byte, whose sequence length (4 from 0xF0, 3 from
+ * 0xE0, 2 from 0xC0, else 1) says whether its character is complete; an
+ * incomplete one is held back for the next piece. */
+int xjo_utf8_emit(xjo_utf8 *h, const char *s, int n, char *out) {
+    int o = h->npending;
+    memcpy(out, h->pending, (size_t)o);
+    if (n > 256) n = 256;
+    memcpy(out + o, s, (size_t)n);
+    o += n;
+    int ok = o;
+    for (int back = 1; back <= 4 && back <= o; back++) {
+        const unsigned char c = (unsigned char)out[o - back];
+        if ((c & 0xC0) == 0x80) continue;
+        const int need = c >= 0xF0 ? 4 : c >= 0xE0 ? 3 : c >= 0xC0 ? 2 : 1;
+        if (need > back) ok = o - back;
+        break;
+    }
+    h->npending = o - ok;
+    memcpy(h->pending, out + ok, (size_t)h->npending);
+    return ok;
 }
 
 int xjo_argmax(const float *x, int n) {

@@ -28,3 +28,36 @@ def random_blocks(t, rows, k, seed):
     elif t == xp.Q8_0:
         blocks[:, 0:2] = hb[:, :2]
     return blob
+
+
+def np_sample(lg, temp, r30):
+    """The sampler from its definition: the 40 largest by value (equal values
+    in index order), p_i = exp((v_i - v_0) / temp), cut at 0.95 of the mass,
+    r = r30 / 2^30 times the kept mass, first i where the running sum of p
+    reaches r. This is the app's sampler (ios/App/XJGlue.c:251-282) whenever
+    the kept values are distinct; the app orders equal kept values differently
+    (test_oracle.py::test_sampler_equal_values_keep_the_apps_order) and the
+    device sampler follows this rule."""
+    if temp <= 0:
+        return int(np.argmax(lg))
+    order = np.argsort(-lg, kind="stable")[:40]
+    v = lg[order]
+    p = np.exp(((v - v[0]).astype(np.float32) / np.float32(temp)).astype(np.float64))
+    tot = 0.0
+    for x in p:
+        tot += x
+    acc, cut = 0.0, len(p)
+    for i, x in enumerate(p):
+        acc += x / tot
+        if acc >= 0.95:
+            cut = i + 1
+            break
+    s2 = 0.0
+    for x in p[:cut]:
+        s2 += x
+    r = r30 / float(1 << 30) * s2
+    for i in range(cut):
+        r -= p[i]
+        if r <= 0:
+            return int(order[i])
+    return int(order[0])

@@ -15,6 +15,7 @@ import pytest
 
 import oracle as orc
 import xjpipe as xp
+from helpers import np_sample
 from conftest import rel_l2
 from test_oracle import attn_inputs
 
@@ -177,6 +178,25 @@ def test_delta_step_forms_agree_bit_for_bit(monkeypatch):
         res.append(xp.delta_step(qkv, ko, vo, beta, alpha, dt, A, 16, 32, 128, 1e-6, 0.0883883, st, 5))
     for a, b in zip(res[0], res[1]):
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("V", [40, 1000, 151936])
+def test_sample_equal_values_by_index(V):
+    """Logits with many exact ties (multiples of 1/4, so the kept set holds
+    equal values and values equal to the 40th straddle the cut): the device
+    sampler follows its stated rule, equal values in index order (np_sample),
+    row by row. The app's exchange sort orders equal kept values differently
+    (test_oracle.py::test_sampler_equal_values_keep_the_apps_order)."""
+    rng = np.random.default_rng(V + 11)
+    T = 12
+    lg = (np.round(rng.standard_normal((T, V)) * 8) / 4).astype(np.float32)
+    r30 = rng.integers(0, 1 << 30, T).astype(np.uint32)
+    for temp in (0.0, 0.3, 1.0, 10.0):
+        got = xp.sample(lg, temp, r30)
+        want = [np_sample(lg[t], temp, int(r30[t])) for t in range(T)]
+        assert got.tolist() == want, temp
+    lg = np.array([[3.0, 3.0, 5.0]], np.float32)
+    assert xp.sample(lg, 10.0, np.array([1 << 29], np.uint32)).tolist() == [0]
 
 
 @pytest.mark.parametrize("V", [25, 1000, 151936])

@@ -247,3 +247,74 @@ def test_attach_mtp_matches_the_reference(model_dir, tiny_path, tmp_path):
         assert orc.rlib().ref_model_attach_mtp(r, bad.encode(), err, 512) != 0
         orc.rlib().ref_model_free(r)
         m.close()
+
+
+def _utf8_text(rng, n_chars):
+    """Random text of 1- to 4-byte UTF-8 characters."""
+    cps = []
+    for _ in range(n_chars):
+        w = rng.integers(0, 4)
+        cps.append(chr(int(rng.integers(0x20, 0x7F) if w == 0 else rng.integers(0xA0, 0x800) if w == 1 else
+                           rng.integers(0x4E00, 0x9FFF) if w == 2 else rng.integers(0x1F300, 0x1FAFF))))
+    return "".join(cps).encode("utf-8")
+
+
+def _pieces(rng, data, max_len):
+    out, i = [], 0
+    while i < len(data):
+        n = int(rng.integers(0, max_len + 1))
+        out.append(data[i:i + n])
+        i += n
+    return out
+
+
+def test_utf8_stream_known_splits():
+    """Characters split across pieces reach the callback whole
+    (ios/App/XJGlue.c:285-305): the 3-byte CJK characters and a 4-byte emoji
+    held back until their last byte arrives."""
+    s = xp.Utf8Stream()
+    seq = [(b"\xe4", b""), (b"\xbd\xa0\xe5", b"\xe4\xbd\xa0"), (b"\xa5\xbd", b"\xe5\xa5\xbd"), (b"", b""),
+           (b"ab", b"ab"), (b"\xf0\x9f", b""), (b"\x98", b""), (b"\x80!", b"\xf0\x9f\x98\x80!")]
+    for piece, want in seq:
+        assert s.emit(piece) == (want, 0), piece
+    assert s.pending == b""
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_utf8_stream_matches_the_app(seed):
+    """Chunk by chunk equal to the oracle's restatement of the app's emit on
+    random text split at random byte positions, pieces of up to 300 bytes
+    (the app keeps the first 256 of a piece), and on random bytes that are
+    not UTF-8 (stray continuation bytes, cut sequences)."""
+    rng = np.random.default_rng(seed)
+    streams = [_utf8_text(rng, 400), bytes(rng.integers(0, 256, 900, dtype=np.uint8)),
+               bytes(rng.choice(np.array([0x41, 0x80, 0xBF, 0xC3, 0xE4, 0xF0], np.uint8), 600))]
+    for data in streams:
+        s, o = xp.Utf8Stream(), orc.Utf8Emit()
+        for piece in _pieces(rng, data, 300):
+            got, stop = s.emit(piece)
+            assert stop == 0
+            assert got == o.emit(piece)
+
+
+def test_utf8_stream_round_trip():
+    """With pieces of at most 256 bytes nothing is dropped: the chunks and the
+    held-back bytes concatenate to the input, and every chunk is whole UTF-8."""
+    rng = np.random.default_rng(9)
+    data = _utf8_text(rng, 2000)
+    s = xp.Utf8Stream()
+    got = b""
+    for piece in _pieces(rng, data, 256):
+        chunk, _ = s.emit(piece)
+        chunk.decode("utf-8")          # raises on a split character
+        got += chunk
+    assert got + s.pending == data
+    assert s.pending == b""            # the text ends with a whole character
+
+
+def test_utf8_stream_stop():
+    """The callback's nonzero return is xjh_utf8_emit's (the app stops its token loop on it)."""
+    s = xp.Utf8Stream(stop_after=2)
+    assert s.emit(b"a") == (b"a", 0)
+    assert s.emit(b"\xe4\xbd") == (b"", 0)     # nothing complete: the callback is not called
+    assert s.emit(b"\xa0b") == (b"\xe4\xbd\xa0b", 1)

@@ -23,7 +23,7 @@ import pytest
 import oracle as orc
 import xjpipe as xp
 from conftest import GOLDEN, rel_l2
-from helpers import random_blocks
+from helpers import np_sample, random_blocks
 
 needs_ref = pytest.mark.skipif(not orc.ref_available(), reason="reference build (oracle/_ref) not present")
 
@@ -613,36 +613,6 @@ def test_end_tokens_in_the_reference_driver(model_dir, kind):
     orc.rlib().ref_model_free(r)
 
 
-def _np_sample(lg, temp, r30):
-    """The app's sampler from its definition: the 40 largest by value (stable
-    order for equal values), p_i = exp((v_i - v_0) / temp), cut at 0.95 of the
-    mass, r = r30 / 2^30 times the kept mass, first i where the running sum of p
-    reaches r."""
-    if temp <= 0:
-        return int(np.argmax(lg))
-    order = np.argsort(-lg, kind="stable")[:40]
-    v = lg[order]
-    p = np.exp(((v - v[0]).astype(np.float32) / np.float32(temp)).astype(np.float64))
-    tot = 0.0
-    for x in p:
-        tot += x
-    acc, cut = 0.0, len(p)
-    for i, x in enumerate(p):
-        acc += x / tot
-        if acc >= 0.95:
-            cut = i + 1
-            break
-    s2 = 0.0
-    for x in p[:cut]:
-        s2 += x
-    r = r30 / float(1 << 30) * s2
-    for i in range(cut):
-        r -= p[i]
-        if r <= 0:
-            return int(order[i])
-    return int(order[0])
-
-
 @pytest.mark.parametrize("n", [25, 1000, 151936])
 def test_sampler_matches_definition(n):
     rng = np.random.default_rng(n)
@@ -650,8 +620,25 @@ def test_sampler_matches_definition(n):
         lg = (rng.standard_normal(n) * rng.uniform(0.5, 4)).astype(np.float32)
         temp = [0.0, 0.01, 0.3, 0.7, 1.0, 1.5, 100.0][trial % 7]
         r30 = int(rng.integers(0, 1 << 30))
-        assert orc.sample(lg, temp, r30) == _np_sample(lg, temp, r30), (trial, temp)
+        assert orc.sample(lg, temp, r30) == np_sample(lg, temp, r30), (trial, temp)
     lg = rng.standard_normal(n).astype(np.float32)
     top = int(np.argmax(lg))
     assert orc.sample(lg, 1e-4, (1 << 30) - 1) == top          # a tiny temperature keeps only the maximum
     assert orc.sample(lg, 1e4, 0) == top                        # r = 0 takes the first kept token
+
+
+def test_sampler_equal_values_keep_the_apps_order():
+    """Equal values inside the kept set: the app's exchange sort (ios/App/XJGlue.c:270)
+    is not stable, so for logits [3, 3, 5] it ranks index 1 before index 0, and a
+    draw landing on the second kept value returns 1. The device sampler ranks
+    equal values by index (np_sample's rule) and returns 0 there; this test pins
+    the oracle to the app's order, test_gpu_ops.py pins the device to its rule.
+    (A value tied at the 40th place is never drawn: the last kept value holds at
+    most 1/40 of the kept mass, and the 0.95 cut always ends before it.)"""
+    lg = np.array([3.0, 3.0, 5.0], np.float32)
+    r30 = 1 << 29                       # r = 0.5 of the mass: past p_0 = 1, within p_1
+    assert orc.sample(lg, 10.0, r30) == 1
+    assert np_sample(lg, 10.0, r30) == 0
+    # without equal values the two orders agree
+    lg = np.array([3.0, 3.5, 5.0], np.float32)
+    assert orc.sample(lg, 10.0, r30) == np_sample(lg, 10.0, r30) == 1
