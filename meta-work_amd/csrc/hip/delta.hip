@@ -193,6 +193,35 @@ __global__ __launch_bounds__(512) void delta_part_kernel(const DeltaArgs a) {
     store_row<S>(a.state + ((int64_t)hv * S + j) * S + i0, m);
 }
 
+// Work-group (t, hv), S threads (element i): the inputs of the chunked rule
+// with the recurrent kernels' expressions (head_sum_d over the same S
+// threads, x * (1 / sqrt(sum + eps)), expf(softplus(alpha + dt) * A), sigm).
+template <int S>
+__global__ __launch_bounds__(S) void delta_prefill_prep_kernel(const DeltaPrepArgs a) {
+    const int t = blockIdx.x, hv = blockIdx.y, i = threadIdx.x, hk = hv % a.Hk;
+    __shared__ double red[8];
+    const float *row = a.qkv + (int64_t)t * a.qkv_s;
+    const float qv = row[hk * S + i], kv = row[a.k_off + hk * S + i];
+    const double sq = xjd::head_sum_d<S / 64>((double)qv * qv, red);
+    const double sk2 = xjd::head_sum_d<S / 64>((double)kv * kv, red + 4);
+    const int64_t o = ((int64_t)t * a.Hv + hv) * S + i;
+    a.q[o] = qv * (1.0f / sqrtf((float)sq + a.eps));
+    a.k[o] = kv * (1.0f / sqrtf((float)sk2 + a.eps));
+    a.v[o] = row[a.v_off + hv * S + i];
+    if (i == 0) {
+        a.decay[(int64_t)t * a.Hv + hv] = expf(xjd::softplus(a.alpha[(int64_t)t * a.alpha_s + hv] + a.dt[hv]) * a.A[hv]);
+        a.bt[(int64_t)t * a.Hv + hv] = xjd::sigm(a.beta[(int64_t)t * a.beta_s + hv]);
+    }
+}
+
+int delta_prefill_prep_launch(const DeltaPrepArgs &a, hipStream_t st) {
+    if (a.T < 1 || a.Hk < 1 || a.Hv < 1) return -1;
+    if (a.S == 128) hipLaunchKernelGGL(delta_prefill_prep_kernel<128>, dim3(a.T, a.Hv), dim3(128), 0, st, a);
+    else if (a.S == 64) hipLaunchKernelGGL(delta_prefill_prep_kernel<64>, dim3(a.T, a.Hv), dim3(64), 0, st, a);
+    else return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 template <int S>
 __global__ __launch_bounds__(256) void delta_rec_kernel(int H, int T, const float *q, const float *k, const float *v,
                                                         const float *decay, const float *beta, float qscale,

@@ -225,7 +225,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const GemmArgs a) {
                 a.part[((int64_t)sp * a.T + t) * a.N + r] = acc[tg][i];
             } else {
                 float *yp = a.y + (int64_t)t * a.ys + r;
-                *yp = a.add ? *yp + acc[tg][i] : acc[tg][i];
+                const float v = a.tsc ? acc[tg][i] * a.tsc[t] : acc[tg][i];
+                *yp = a.add ? *yp + v : v;
             }
         }
     }
@@ -238,9 +239,24 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const GemmArgs a) {
     const int t = (int)(idx / a.N), r = (int)(idx % a.N);
     float s = 0.f;
     for (int k = 0; k < a.nsplit; k++) s += a.part[((int64_t)k * a.T + t) * a.N + r];
+    if (a.tsc) s *= a.tsc[t];
     float *yp = a.y + (int64_t)t * a.ys + r;
     *yp = a.add ? *yp + s : s;
 }
+
+// PRO_RMSU scale per token (one wavefront per token): the groups' sums of
+// x^2 in double, lane-strided then the wavefront sum, as rmsu_scale.
+__global__ __launch_bounds__(64) void rms_scale_kernel(const uint8_t *xq, int64_t xs, int K, float eps, float *tsc) {
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const XqOff o = xq_off(K);
+    const double *ss = (const double *)(xq + (int64_t)t * xs + o.ss_off);
+    double s = 0;
+    for (int g = lane; g < o.G; g += 64) s += ss[g];
+    s = xjd::wave_sum_d(s);
+    if (lane == 0) tsc[t] = 1.0f / sqrtf((float)(s / K) + eps);
+}
+
+__global__ void inc_kernel(int32_t *p, int32_t by) { *p += by; }
 
 template <bool Q6, int NTG>
 void launch_g(const GemmArgs &a, dim3 grid, size_t lds, hipStream_t st) {
@@ -292,7 +308,22 @@ int gemm_launch(const GemmArgs &in, int64_t part_floats, hipStream_t st) {
         hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
         if (hipGetLastError() != hipSuccess) return -1;
     }
+    if (a.inc_ptr) {
+        hipLaunchKernelGGL(inc_kernel, dim3(1), dim3(1), 0, st, a.inc_ptr, a.inc_by);
+        if (hipGetLastError() != hipSuccess) return -1;
+    }
     return 0;
+}
+
+int inc_launch(int32_t *p, int32_t by, hipStream_t st) {
+    hipLaunchKernelGGL(inc_kernel, dim3(1), dim3(1), 0, st, p, by);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int rms_scale_launch(const uint8_t *xq, int64_t xs, int K, int T, float eps, float *tsc, hipStream_t st) {
+    if (T < 1 || K < 32 || K % 32 || !xq || !tsc) return -1;
+    hipLaunchKernelGGL(rms_scale_kernel, dim3(T), dim3(64), 0, st, xq, xs, K, eps, tsc);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 }  // namespace xjk

@@ -126,7 +126,17 @@ struct GemmArgs {
     float *part;
     float *y; int32_t ys; int32_t add;
     int32_t nsplit;   // set by gemm_launch
+    // optional: y[t][r] = (sum) * tsc[t] before the add (an RMSNorm input's
+    // per-token scale, applied after the dot product as the GEMV applies it)
+    const float *tsc;
+    int32_t *inc_ptr; int32_t inc_by;   // optional: *inc_ptr += inc_by once
 };
+// Per-token RMSNorm scale of T tokens of PRO_RMSU activations (xq, token
+// stride xs): tsc[t] = 1 / sqrt(sum of the groups' ss / K + eps), the
+// GEMV's rmsu_scale.
+int rms_scale_launch(const uint8_t *xq, int64_t xs, int K, int T, float eps, float *tsc, hipStream_t st);
+// *p += by on the device, in stream order (one thread).
+int inc_launch(int32_t *p, int32_t by, hipStream_t st);
 int gemm_max_tokens();
 int gemm_splits(int N, int K, int T, int64_t part_floats);
 int gemm_launch(const GemmArgs &a, int64_t part_floats, hipStream_t st);
@@ -177,6 +187,20 @@ struct DeltaArgs {
     int32_t split;
 };
 int delta_launch(const DeltaArgs &a, hipStream_t st);
+// Prefill inputs of the chunked rule from a layer's projections, per token t
+// and value head hv (key head hv % Hk): q and k L2-normalised as the
+// recurrent kernel normalises them, v gathered, decay = exp(softplus(alpha +
+// dt) * A) and sigmoid(beta); q, k, v [T][Hv][S], decay and beta [T][Hv].
+struct DeltaPrepArgs {
+    const float *qkv; int32_t qkv_s, k_off, v_off;
+    const float *beta; int32_t beta_s;
+    const float *alpha; int32_t alpha_s;
+    const float *dt, *A;
+    float *q, *k, *v, *decay, *bt;
+    int32_t T, Hk, Hv, S;
+    float eps;
+};
+int delta_prefill_prep_launch(const DeltaPrepArgs &a, hipStream_t st);
 
 // Standalone gated delta rule (decay/beta given), recurrent and chunked.
 int delta_recurrent_launch(int H, int S, int T, const float *q, const float *k, const float *v,

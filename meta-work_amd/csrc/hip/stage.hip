@@ -77,6 +77,10 @@ struct HStage {
     uint8_t *xq_e = nullptr, *xq_di = nullptr, *xq_att = nullptr, *xq_ff = nullptr;
     // arrival counters of the producer tails (zero between launches)
     int32_t *cnt_grp = nullptr;
+    // prefill on the matrix cores: per-token RMSNorm scales, the GEMM's K-split
+    // partials and the chunked delta rule's work area
+    float *tsc = nullptr, *gpart = nullptr, *dwork = nullptr;
+    int64_t gpart_floats = 0;
     float2 *rope = nullptr;
     float *h_x = nullptr;            // pinned staging [max_batch][n_embd]
     int32_t *h_i = nullptr;          // pinned scalar
@@ -175,6 +179,10 @@ struct Gemv {
     Profile *prof = nullptr;
     bool prepared = false;
     explicit Gemv(uint8_t *xq, Profile *p = nullptr) : prof(p) { a.xq = xq; }
+    Gemv(uint8_t *xq, Profile *p, float *tsc_, float *part_, int64_t part_floats_)
+        : prof(p), tsc(tsc_), part(part_), part_floats(part_floats_) {
+        a.xq = xq;
+    }
     Gemv &seg(const DevW &w, float *y, int ys, int epi) {
         GSeg &s = a.seg[a.nseg];
         s = GSeg{};
@@ -216,8 +224,86 @@ struct Gemv {
             a.seg[i].nwg = (int32_t)((a.seg[i].n_rows + rows - 1) / rows);
         }
     }
+    // Prefill buffers of the stage (set by the stage for its GEMVs; without
+    // them every launch takes the GEMV form).
+    float *tsc = nullptr, *part = nullptr;
+    int64_t part_floats = 0;
+    // Chunks of at least kGemmMinT tokens take the matrix-core GEMM
+    // (gemm.hip): the prep launch builds the T tokens' activations once, the
+    // RMSNorm scale is applied per token after the dot products (as the GEMV
+    // applies it), the conv + SiLU runs as its own launch and the SwiGLU tail
+    // as the down projection's prep. Segments the GEMM does not take (float
+    // rows) and every other case keep the GEMV.
+    static constexpr int kGemmMinT = 16;
+    bool gemm_ok(int T) const {
+        static const bool on = env_int("XJ_PREFILL_GEMM", 1) != 0;
+        if (!on || T < kGemmMinT || prof || !tsc || !part || !a.xq) return false;
+        if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_SWIGLU && a.pro != PRO_GATED_RMS) return false;
+        if (a.post.mode != POST_NONE && a.post.mode != POST_SWIGLU) return false;
+        if (a.K % 256) return false;
+        bool any = false;
+        for (int i = 0; i < a.nseg; i++) any = any || a.seg[i].type == XJ_Q4_K || a.seg[i].type == XJ_Q6_K;
+        return any;
+    }
+    int run_gemm(int T, hipStream_t st) {
+        const int64_t xs = xq_off(a.K).stride;
+        if (!prepared) {   // the T tokens' activations, once
+            GArgs b = a;
+            b.T = T;
+            if (prep_launch(b, st)) return -1;
+        }
+        const bool rms = a.pro == PRO_RMSU;
+        if (rms && rms_scale_launch(a.xq, xs, a.K, T, a.eps, tsc, st)) return -1;
+        const int mt = gemm_max_tokens(), tile = gemv_max_tile(a.K);
+        for (int i = 0; i < a.nseg; i++) {
+            const GSeg &s = a.seg[i];
+            if (s.type == XJ_Q4_K || s.type == XJ_Q6_K) {
+                for (int t0 = 0; t0 < T; t0 += mt) {
+                    GemmArgs g{};
+                    g.w = s.w; g.type = s.type; g.N = s.n_rows; g.K = a.K; g.T = T - t0 < mt ? T - t0 : mt;
+                    g.xq = a.xq + t0 * xs; g.xs = xs; g.part = part;
+                    g.y = s.y + (int64_t)t0 * s.ys; g.ys = s.ys; g.add = s.epi == EPI_ADD;
+                    g.tsc = rms ? tsc + t0 : nullptr;
+                    if (gemm_launch(g, part_floats, st)) return -1;
+                }
+            } else {   // this segment alone on the GEMV, reading the prepared activations
+                if (tile < 1) return -1;
+                GArgs one = a;
+                one.nseg = 1;
+                one.seg[0] = s;
+                one.seg[0].epi = s.epi == EPI_CONV ? EPI_STORE : s.epi;
+                one.post = PostPrep{};
+                one.inc_ptr = nullptr;
+                one.pro = rms ? PRO_RMSU : PRO_NONE;
+                one.seg[0].wg0 = 0;
+                one.seg[0].nwg = (int32_t)((s.n_rows + gemv_plan(a.K, s.n_rows).rows_per_group - 1) /
+                                           gemv_plan(a.K, s.n_rows).rows_per_group);
+                for (int t0 = 0; t0 < T; t0 += tile) {
+                    GArgs b = one;
+                    b.T = T - t0 < tile ? T - t0 : tile;
+                    b.xq = a.xq + t0 * xs;
+                    b.x = nullptr; b.x2 = nullptr;
+                    b.seg[0].y = s.y + (int64_t)t0 * s.ys;
+                    if (gemv_launch(b, st)) return -1;
+                }
+            }
+            // depthwise causal conv + SiLU over the T tokens, with its state and checkpoints
+            if (s.epi == EPI_CONV &&
+                conv_silu_launch(s.y, s.conv_state, s.conv_w, s.n_rows, s.conv_k, T, s.conv_ck, a.keep_n, st))
+                return -1;
+        }
+        if (a.post.mode == POST_SWIGLU) {   // silu(gate) * up as the next GEMV's activations
+            GArgs b{};
+            b.x = a.seg[0].y; b.xs = a.seg[0].ys; b.x2 = a.seg[1].y; b.x2s = a.seg[1].ys;
+            b.pro = PRO_SWIGLU; b.K = a.seg[0].n_rows; b.T = T; b.xq = a.post.xq;
+            if (prep_launch(b, st)) return -1;
+        }
+        if (a.inc_ptr && inc_launch(a.inc_ptr, a.inc_by, st)) return -1;
+        return 0;
+    }
     // Run over T tokens in tiles that fit LDS; row results do not depend on the tiling.
     int run(int T, hipStream_t st) {
+        if (gemm_ok(T)) return run_gemm(T, st);
         const int tile = gemv_max_tile(a.K);
         if (tile < 1 || !a.xq) return -1;
         place();
@@ -270,12 +356,14 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
     const xj_hparams &hp = S->s.m->hp;
     HLayer &L = S->L[il - S->s.l0];
     const int E = hp.n_embd, FF = hp.n_ff;
+    // every GEMV of the layer with the stage's prefill buffers
+    auto gemv = [&](uint8_t *xq) { return Gemv(xq, pf, S->tsc, S->gpart, S->gpart_floats); };
     auto rms_in = [&](Gemv &g, const float *w) {
         g.a.x = x; g.a.xs = E; g.a.pro = PRO_RMSU; g.a.pro_w = w; g.a.eps = hp.eps;
     };
     if (L.rec) {
         const int CD = hp.conv_dim, DI = hp.d_inner, Hv = hp.h_v;
-        Gemv p(S->xq_e, pf);
+        Gemv p = gemv(S->xq_e);
         rms_in(p, L.attn_norm);
         p.a.keep_n = keep_n;
         p.seg(L.ssm_qkv, S->qkv, CD, EPI_CONV).seg(L.ssm_gate, S->z, DI, EPI_STORE)
@@ -283,6 +371,29 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
         GSeg &cs = p.a.seg[0];
         cs.conv_state = L.conv; cs.conv_w = L.conv_w; cs.conv_ck = L.ck_conv; cs.conv_k = hp.conv_k;
         if (p.run(T, st)) return -1;
+        // a prefill chunk without checkpoints: the chunked rule on the matrix
+        // cores (delta_chunk.hip) over inputs prepared from the projections,
+        // then the gated RMSNorm (xj_cpu.c:215-217) as ssm_out's prep launch
+        static const bool chunked_on = env_int("XJ_PREFILL_CHUNKED", 1) != 0;
+        const int Sd = hp.s_k;
+        if (chunked_on && !pf && keep_n == 0 && T >= Gemv::kGemmMinT && S->dwork && (Sd == 64 || Sd == 128) &&
+            hp.s_v == Sd && T <= S->s.max_batch) {
+            DeltaPrepArgs dp{};
+            dp.qkv = S->qkv; dp.qkv_s = CD; dp.k_off = hp.key_dim; dp.v_off = 2 * hp.key_dim;
+            dp.beta = S->beta; dp.beta_s = Hv; dp.alpha = S->alpha; dp.alpha_s = Hv; dp.dt = L.dt; dp.A = L.A;
+            // kb / vb / u / g are free until the FFN: q, k, v [T][Hv][S], decay and beta [T][Hv]
+            dp.q = S->kb; dp.k = S->vb; dp.v = S->u; dp.decay = S->g; dp.bt = S->g + (size_t)T * Hv;
+            dp.T = T; dp.Hk = hp.h_k; dp.Hv = Hv; dp.S = Sd; dp.eps = hp.eps;
+            if (delta_prefill_prep_launch(dp, st) ||
+                delta_chunked_launch(Hv, Sd, T, 64, dp.q, dp.k, dp.v, dp.decay, dp.bt, 1.0f / sqrtf((float)Sd), L.ssm,
+                                     S->o, S->dwork, st))
+                return -1;
+            Gemv q = gemv(S->xq_di);
+            q.a.x = S->o; q.a.xs = DI; q.a.x2 = S->z; q.a.x2s = DI;
+            q.a.pro = PRO_GATED_RMS; q.a.pro_w = L.ssm_norm; q.a.group = Sd; q.a.eps = hp.eps;
+            q.seg(L.ssm_out, x, E, EPI_ADD);
+            if (q.run(T, st)) return -1;
+        } else {
         DeltaArgs d{};
         d.qkv = S->qkv; d.qkv_s = CD; d.k_off = hp.key_dim; d.v_off = 2 * hp.key_dim;
         d.beta = S->beta; d.beta_s = Hv; d.alpha = S->alpha; d.alpha_s = Hv; d.dt = L.dt; d.A = L.A;
@@ -296,16 +407,17 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
         static const bool split_on = env_int("XJ_DELTA_SPLIT", 1) != 0;
         d.split = split_on && ot != XJ_F32 && ot != XJ_F16 && ot != XJ_BF16 && hp.s_k % 32 == 0;
         if (!pf && delta_launch(d, st)) return -1;
-        Gemv q(S->xq_di, pf);
+        Gemv q = gemv(S->xq_di);
         q.prepared = true;
         if (d.split) {
             q.a.pro = PRO_HEADRMS; q.a.group = hp.s_k; q.a.eps = hp.eps;
         }
         q.seg(L.ssm_out, x, E, EPI_ADD);
         if (q.run(T, st)) return -1;
+        }
     } else {
         const int D = hp.head_dim, Hq = hp.n_head, Hkv = hp.n_head_kv, nq = 2 * Hq * D, nk = Hkv * D;
-        Gemv p(S->xq_e, pf);
+        Gemv p = gemv(S->xq_e);
         rms_in(p, L.attn_norm);
         AttnArgs at{};
         if (L.wqkv.p) {
@@ -325,12 +437,12 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
         at.eps = hp.eps; at.scale = 1.0f / sqrtf((float)D);
         at.xq = S->xq_att;
         if (!pf && attn_launch(at, st)) return -1;
-        Gemv q(S->xq_att, pf);
+        Gemv q = gemv(S->xq_att);
         q.prepared = true;
         q.seg(L.wo, x, E, EPI_ADD);
         if (q.run(T, st)) return -1;
     }
-    Gemv f(S->xq_e, pf);
+    Gemv f = gemv(S->xq_e);
     rms_in(f, L.post_norm);
     f.seg(L.ffn_gate, S->g, FF, EPI_STORE).seg(L.ffn_up, S->u, FF, EPI_STORE);
     // one token: every work-group of gate|up leaves silu(gate) * up of its
@@ -340,7 +452,7 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
     const bool h = T == 1 && dt != XJ_F32 && dt != XJ_F16 && dt != XJ_BF16 && f.swiglu_h(S->g);
     if (!h) f.post(POST_SWIGLU, S->xq_ff, S->cnt_grp);
     if (f.run(T, st)) return -1;
-    Gemv dn(S->xq_ff, pf);
+    Gemv dn = gemv(S->xq_ff);
     if (h) {
         dn.a.x = S->g; dn.a.xs = FF; dn.a.pro = PRO_X;
     } else {
@@ -566,6 +678,11 @@ extern "C" uint64_t xj_hip_stage_state_bytes(const xj_model *m, int l0, int l1, 
     }
     b += 10ull * 4 * max_batch * scratch_floats(hp) +
          4ull * max_batch * hp.n_head * ((n_ctx + 63) / 64) * (hp.head_dim + 2);
+    // prefill on the matrix cores: RMSNorm scales, K-split partials, chunked-rule work
+    b += 4ull * max_batch + 16ull * max_batch * scratch_floats(hp);
+    bool rec = false;
+    for (int il = l0; il < l1 && il < (int)hp.n_layer; il++) rec = rec || m->layers[il].recurrent;
+    if (rec) b += delta_chunked_work_bytes(hp.h_v, hp.s_k, max_batch, 64);
     return b;
 }
 
@@ -695,6 +812,20 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
     S->qr = dalloc<float>(S, mb * hp.n_head * (size_t)hp.head_dim, err, errlen);
     S->scores = dalloc<float>(S, mb * hp.n_head * (size_t)attn_splits(n_ctx) * (hp.head_dim + 2), err, errlen);
     S->npast = dalloc<int32_t>(S, 1, err, errlen);
+    // prefill on the matrix cores (chunks of at least 16 tokens)
+    S->tsc = dalloc<float>(S, mb, err, errlen);
+    S->gpart_floats = 4 * (int64_t)mb * (int64_t)sf;
+    S->gpart = dalloc<float>(S, (size_t)S->gpart_floats, err, errlen);
+    if (!S->tsc || !S->gpart) return fail();
+    {
+        bool rec = false;
+        for (int il = l0; il < l1 && il < hp.n_layer; il++) rec = rec || m->layers[il].recurrent;
+        const size_t wb = rec ? delta_chunked_work_bytes(hp.h_v, hp.s_k, (int)mb, 64) : 0;
+        if (wb) {
+            S->dwork = (float *)dalloc<uint8_t>(S, wb, err, errlen);
+            if (!S->dwork) return fail();
+        }
+    }
     {
         auto xqb = [&](int K) { return K >= 32 ? mb * (size_t)xq_off(K).stride : 256; };
         S->xq_e = dalloc<uint8_t>(S, xqb(hp.n_embd), err, errlen);

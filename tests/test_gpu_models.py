@@ -35,13 +35,17 @@ def first_divergence(a, b):
     return next((i for i, (x, y) in enumerate(zip(a, b)) if x != y), None)
 
 
-def test_0_8b_greedy_256_steps():
+@pytest.mark.parametrize("max_batch", [8, 64])
+def test_0_8b_greedy_256_steps(max_batch):
+    """max_batch 8 (the recorded runs' chunking: prefill on the GEMV) and 64
+    (prefill chunks on the matrix-core GEMM and the chunked delta rule); the
+    reference's tokens do not depend on the chunking."""
     rec = fixture("greedy_0_8b.json")
     path = xp.cached_model(xp.CONFIG_0_8B, "synth08b")
     check_model(path, rec)
     m = xp.Model(path)
     prompt = np.random.default_rng(rec["prompt_seed"]).integers(0, m.hp.n_vocab, rec["n_prompt"]).astype(np.int32)
-    st = xp.HipStage(m, 0, m.hp.n_layer, rec["n_ctx"], rec["max_batch"], True)
+    st = xp.HipStage(m, 0, m.hp.n_layer, rec["n_ctx"], max_batch, True)
     ch = xp.Chain([st])
     toks = np.concatenate([ch.eval(prompt), ch.decode(rec["n_gen"] - 1)]).tolist()
     want = rec["oracle_kvf16"]["tokens"]
@@ -53,14 +57,17 @@ def test_0_8b_greedy_256_steps():
     st.destroy()
 
 
-def test_4b_two_stage_greedy_512_steps():
+@pytest.mark.parametrize("max_batch", [8, 64])
+def test_4b_two_stage_greedy_512_steps(max_batch):
+    """As the 0.8B test: prefill chunks of 8 (GEMV) and of 64 (matrix-core GEMM,
+    chunked delta rule)."""
     rec = fixture("greedy_4b.json")
     path = xp.cached_model(xp.CONFIG_4B, "synth4b")
     check_model(path, rec)
     m = xp.Model(path)
     prompt = np.random.default_rng(rec["prompt_seed"]).integers(0, m.hp.n_vocab, rec["n_prompt"]).astype(np.int32)
-    a = xp.HipStage(m, 0, 16, rec["n_ctx"], rec["max_batch"], False)
-    b = xp.HipStage(m, 16, 32, rec["n_ctx"], rec["max_batch"], True)
+    a = xp.HipStage(m, 0, 16, rec["n_ctx"], max_batch, False)
+    b = xp.HipStage(m, 16, 32, rec["n_ctx"], max_batch, True)
     ch = xp.Chain([a, b])
     toks = np.concatenate([ch.eval(prompt), ch.decode(rec["n_gen"] - 1)]).tolist()
     want = rec["oracle_kvf16"]["tokens"]

@@ -314,3 +314,54 @@ def test_hip_stages_over_the_reference_loader(model_dir, tiny_path):
     spec, st = drive(ref, 3)
     assert spec.tolist() == want.tolist() and st[1] > 0
     ref.free()
+
+
+@pytest.mark.parametrize("T", [16, 40, 64])
+def test_prefill_chunk_matches_oracle(tiny, T):
+    """A prefill chunk of at least 16 tokens takes the matrix-core path: GEMM
+    projections (RMSNorm scale per token after the dot products), the conv +
+    SiLU launch, the chunked delta rule over prepared q/k/v/decay/beta (GQA
+    heads: key head hv % Hk), the gated RMSNorm as ssm_out's prep. Hidden states
+    against the oracle, then decode steps continue from the chunk's recurrent
+    and KV state."""
+    m, L = tiny, tiny.hp.n_layer
+    toks = prompt_ids(m, T + 3, 21 + T)
+    g = xp.HipStage(m, 0, L, 128, 64, True)
+    c = orc.CpuStage(m.ptr, 0, L, 128, 64, True, kv_f16=True)
+    x = embed(m, toks[:T])
+    xg, xc = g.forward(x.copy()), c.forward(x.copy())
+    assert rel_l2(xg, xc) < 1e-3
+    for t in range(T, T + 3):
+        x1 = embed(m, toks[t:t + 1])
+        yg, yc = g.forward(x1.copy()), c.forward(x1.copy())
+        assert rel_l2(yg, yc) < 1e-3, t
+    lg, lc = g.logits(yg), c.logits(yc)
+    assert rel_l2(lg, lc) < 1e-3
+    assert int(np.argmax(lg)) == int(np.argmax(lc))
+    g.destroy()
+    c.destroy()
+
+
+def test_prefill_chunk_with_checkpoints_rolls_back(tiny):
+    """A 20-token chunk with keep: GEMM projections, the conv launch writing
+    its checkpoints, the recurrent rule writing the state checkpoints; rolled
+    back into the chunk it continues as a fresh stage fed the kept prefix
+    (which itself takes the chunked rule, 18 tokens without keep)."""
+    m, L = tiny, tiny.hp.n_layer
+    toks = prompt_ids(m, 40, 22)
+    g = xp.HipStage(m, 0, L, 128, 64, True)
+    g.forward(embed(m, toks[:8]))
+    g.set_keep(20)
+    g.forward(embed(m, toks[8:28]))
+    g.rollback(14)
+    assert g.n_past == 14
+    x_after = g.forward(embed(m, toks[30:34]))
+    ref = xp.HipStage(m, 0, L, 128, 64, True)
+    xr = ref.forward(embed(m, np.concatenate([toks[:14], toks[30:34]])))
+    assert rel_l2(x_after, xr[14:]) < 1e-4
+    c = orc.CpuStage(m.ptr, 0, L, 128, 64, True, kv_f16=True)
+    xc = c.forward(embed(m, np.concatenate([toks[:14], toks[30:34]])))
+    assert rel_l2(x_after, xc[14:]) < 1e-3
+    for s_ in (g, ref, c):
+        s_.destroy()
+
