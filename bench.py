@@ -80,6 +80,7 @@ def decode_run(cfg, name, n_prompt, steps, warmup, seed):
     first = ch.eval(prompt)
     prefill_s = time.perf_counter() - t
     log(f"{name}: prefill {n_prompt} tokens in {prefill_s:.3f} s, first token {int(first[0])}")
+    assert n_prompt >= 64
     if warmup:
         ch.decode(warmup)
     t0 = time.perf_counter()
@@ -90,19 +91,41 @@ def decode_run(cfg, name, n_prompt, steps, warmup, seed):
                 prefill_s=prefill_s)
 
 
-def cpu_baseline(cfg, name, n_prompt_cpu, n_steps_cpu, seed):
-    """Reference CPU path (oracle/_ref) or the oracle restatement on the host cores."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def oracle_mod():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
+    return orc
+
+
+def cpu_baseline(cfg, name, n_prompt_cpu, n_steps_cpu, seed, at_pos=None):
+    """Reference CPU path (oracle/_ref) or the oracle restatement on the host cores. With at_pos, the
+    decode steps run at positions at_pos.. (the GPU run's context): after the n_prompt_cpu-token
+    prompt the stage's n_past is set to at_pos, so each step attends over at_pos + 1 positions whose
+    cache entries past the prompt stay as allocated - a timing sample, not a token-parity run (a
+    real 1024-token CPU prefill would take about a minute)."""
+    orc = oracle_mod()
     kind = "reference" if orc.ref_available() else "port"
     m = xp.Model(model_path(cfg, name))
     hp = m.hp
-    stage = orc.CpuStage(m.ptr, 0, hp.n_layer, n_prompt_cpu + n_steps_cpu + 8, n_prompt_cpu, True,
-                         ref=(kind == "reference"))
+    n_ctx = (at_pos or n_prompt_cpu) + n_steps_cpu + 8
+    stage = orc.CpuStage(m.ptr, 0, hp.n_layer, n_ctx, n_prompt_cpu, True, ref=(kind == "reference"))
     prompt = np.random.default_rng(seed).integers(0, hp.n_vocab, n_prompt_cpu).astype(np.int32)
     x = np.stack([orc.embed(m.ptr, int(t)) for t in prompt])
     stage.forward(x)
     tok = int(np.argmax(stage.logits(x[-1:])[0]))
+    if at_pos:
+        stage.ptr.contents.n_past = at_pos
     t0 = time.perf_counter()
     for _ in range(n_steps_cpu):
         x = orc.embed(m.ptr, tok)[None].copy()
@@ -111,9 +134,86 @@ def cpu_baseline(cfg, name, n_prompt_cpu, n_steps_cpu, seed):
     dt = time.perf_counter() - t0
     stage.destroy()
     cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(n_steps_cpu / dt, 3), "unit": "tok/s", "cores": cores, "kind": kind,
-            "sample": f"{name} model, {n_prompt_cpu}-token random prompt, {n_steps_cpu} timed greedy decode steps "
+    where = (f"positions {at_pos}..{at_pos + n_steps_cpu - 1} (n_past set to {at_pos} after a {n_prompt_cpu}-token "
+             f"prompt, as the GPU run's context)" if at_pos else f"after a {n_prompt_cpu}-token prompt")
+    return {"value": round(n_steps_cpu / dt, 3), "unit": "tok/s", "cores": cores, "kind": kind, "cpu": cpu_model(),
+            "sample": f"{name} model, {n_steps_cpu} timed greedy decode steps at {where} "
                       f"(fp32 KV, OpenMP over {cores} threads, {dt:.1f} s)"}
+
+
+def cpu_configs(seed=20261107):
+    """CPU figures of the smaller configs on the host cores (the reference's own C core when
+    oracle/_ref is built, else the oracle restatement): the Q4_K GEMV 4096x1024 (config 1) and the
+    mixed-quant batch at T = 1 and 5 (config 2) as us and effective GB/s, the standalone DeltaNet
+    layer recurrence over 2048 + 256 tokens (config 3, the oracle's restatement: the reference runs
+    it inside its layer), the 0.8B decode at its GPU context (config 4)."""
+    orc = oracle_mod()
+    ref = orc.ref_available()
+
+    def matmul_leg(t, rows, k, T, reps):
+        blob = xp.quantize(t, xp.fill_normal(rows * k, 17, 0.02).reshape(rows, k))
+        x = xp.fill_normal(T * k, 5, 1.0).reshape(T, k)
+        orc.matmul(t, blob, k, rows, x, ref=ref)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            orc.matmul(t, blob, k, rows, x, ref=ref)
+        dt = (time.perf_counter() - t0) / reps
+        by = rows * xp.row_bytes(t, k) + T * k * 4 + T * rows * 4
+        return {"shape": f"{xp.TYPE_NAMES[t]} {rows}x{k}", "T": T, "us": round(dt * 1e6, 1),
+                "GBps": round(by / dt / 1e9, 2)}
+
+    out = {"kind": "reference" if ref else "port", "cpu": cpu_model(),
+           "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))}
+    out["config1"] = matmul_leg(xp.Q4_K, 4096, 1024, 1, 200)
+    out["config2"] = [matmul_leg(t, r, k, T, 40 if r < 10000 else 5)
+                      for (t, r, k) in ((xp.Q6_K, 3584, 1024), (xp.Q8_0, 1024, 3584), (xp.Q4_K, 151936, 1024))
+                      for T in (1, 5)]
+    T, H, S = 2048 + 256, 16, 128
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((T, H, S)).astype(np.float32)
+    k = rng.standard_normal((T, H, S)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rng.standard_normal((T, H, S)).astype(np.float32)
+    dec = (1 / (1 + np.exp(-rng.standard_normal((T, H))))).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((T, H))))).astype(np.float32)
+    t0 = time.perf_counter()
+    orc.delta_recurrent(q, k, v, dec, beta, np.zeros((H, S, S), np.float32), 1 / np.sqrt(S))
+    dt = time.perf_counter() - t0
+    out["config3"] = {"shape": "H=16 d=128, 2048-token prefill + 256 steps (token by token, oracle)",
+                      "ms": round(dt * 1e3, 1), "us_per_token": round(dt * 1e6 / T, 2),
+                      "state_GBps": round(T * 2 * H * S * S * 4 / dt / 1e9, 2)}
+    out["config4"] = cpu_baseline(xp.CONFIG_0_8B, "synth08b", 16, 24, seed=20261108, at_pos=512)
+    return out
+
+
+def dropin_run(n_prompt=1024, n_gen=64, seed=20261107):
+    """The drop-in path: the reference's own driver (greedy loop, xjpipe-host.c:131-144, compiled
+    from source in oracle/_ref) over HIP stages behind the xj_stage vtable - logits copied to the
+    host every token, the argmax on the host - on the 4B shape, one stage, 1024-token prompt."""
+    orc = oracle_mod()
+    if not orc.ref_available():
+        return None
+    m = xp.Model(model_path(xp.CONFIG_4B, "synth4b"))
+    hp = m.hp
+    n_ctx = n_prompt + 2 * n_gen + 16
+    a, b = xp.HipStage(m, 0, 16, n_ctx, 64, False), xp.HipStage(m, 16, hp.n_layer, n_ctx, 64, True)
+    prompt = np.random.default_rng(seed).integers(0, hp.n_vocab, n_prompt).astype(np.int32)
+    runs = {}
+    for n in (1, n_gen):   # the prefill alone (one token generated), then the prefill and n_gen tokens
+        for s_ in (a, b):
+            s_.reset()
+        t0 = time.perf_counter()
+        toks, _ = orc.ref_spec_run(m.ptr, a.ptr, b.ptr, None, 0, prompt, n)
+        runs[n] = (time.perf_counter() - t0, toks)
+    for s_ in (a, b):
+        s_.destroy()
+    dec_s = runs[n_gen][0] - runs[1][0]
+    return {"tok_s": round((n_gen - 1) / dec_s, 1), "prefill_s": round(runs[1][0], 3), "tokens": n_gen,
+            "prompt": n_prompt, "first_token": int(runs[n_gen][1][0]),
+            "note": ("the reference's own pipeline and greedy driver (compiled from source) over two HIP "
+                     "stages (layers 0-15 | 16-31) behind the xj_stage vtable: the logits of every token "
+                     "copied to the host, the argmax on the host; tok_s = decode steps after the first token")}
 
 
 def gemv_leg(t, rows, k, copies, iters):
@@ -316,6 +416,7 @@ def main():
         r8 = decode_run(xp.CONFIG_0_8B, "synth08b", 512, 256, 8, seed=20261108)
         extra["decode_0_8b"] = {"tok_s": round(256 / r8["wall"], 1), "gpu_ms_per_step": round(r8["gpu_ms"], 4),
                                 "prompt": 512, "steps": 256}
+        extra["decode_0_8b"]["prefill_s"] = round(r8["prefill_s"], 4)
         r8["ch"].free()
         r8["st"].destroy()
         extra["gemv_legs"] = [gemv_leg(xp.Q4_K, 151936, 1024, 8, 64), gemv_leg(xp.Q6_K, 151936, 2560, 3, 24),
@@ -329,22 +430,33 @@ def main():
                                 gemm_tokens(xp.Q4_K, 2560, 4096)]
         extra["speculative_4b"] = spec_run()
         extra["speculative_4b_mtp"] = spec_mtp_run()
+        d = dropin_run()
+        if d:
+            extra["dropin_vtable_4b"] = d
         log(f"extra: {extra}")
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(xp.CONFIG_4B, "synth4b", 16, 48, seed=20261107)
+        cpu = cpu_baseline(xp.CONFIG_4B, "synth4b", 16, 48, seed=20261107, at_pos=1024)
         log(f"cpu baseline: {cpu}")
+        if not args.no_extra:
+            extra["cpu_configs"] = cpu_configs()
+            log(f"cpu configs: {extra['cpu_configs']}")
 
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32", "data": "synthetic (random-init weights, uniform random prompt ids)",
+        "vs_baseline": None, "dtype": "f32",
+        "dtype_note": ("fp32 arithmetic; the GEMV/GEMM inputs enter as 21-bit fixed point per 32-element group "
+                       "(three int8 digit planes, exact int32 sub-block sums, <= 2^-21 of the group maximum per "
+                       "element), KV cache fp16"),
+        "data": "synthetic (random-init weights, uniform random prompt ids)",
         "config": {"workload": "greedy decode, synthetic hybrid 4B shape: hidden 2560, 32 layers (24 Gated-DeltaNet "
                                "32x128 + 8 gated GQA 16q/4kv d256), FFN 9216, vocab 151936, Q4_K_M-style "
                                "(Q4_K + Q6_K v/down/head), fp16 KV cache, 1024-token prompt, batch 1",
                    "global_batch": 1, "prompt": 1024, "parallelism": "single GPU"},
         "gpu_ms_per_step": round(r["gpu_ms"], 4),
+        "prefill_1024_s": round(r["prefill_s"], 4),
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
