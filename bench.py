@@ -91,6 +91,25 @@ def decode_run(cfg, name, n_prompt, steps, warmup, seed):
                 prefill_s=prefill_s)
 
 
+def prefill_only(n_prompt=1024, reps=3, seed=20261107):
+    """The 4B shape's 1024-token prefill (chunks of 64: the matrix-core GEMM and the chunked delta
+    rule), reps times from a reset stage, for a kernel trace of the prefill alone."""
+    m = xp.Model(model_path(xp.CONFIG_4B, "synth4b"))
+    hp = m.hp
+    st = xp.HipStage(m, 0, hp.n_layer, n_prompt + 8, 64, True)
+    ch = xp.Chain([st])
+    prompt = np.random.default_rng(seed).integers(0, hp.n_vocab, n_prompt).astype(np.int32)
+    times, first = [], None
+    for _ in range(reps):
+        ch.reset()
+        t0 = time.perf_counter()
+        first = int(ch.eval(prompt)[0])
+        times.append(time.perf_counter() - t0)
+    ch.free()
+    st.destroy()
+    return {"prefill_tokens": n_prompt, "prefill_s": [round(t, 4) for t in times], "first_token": first}
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -368,6 +387,7 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB")
     ap.add_argument("--delta-c3", action="store_true", help="only the chunked vs token-by-token DeltaNet prefill")
     ap.add_argument("--gemm-tokens", action="store_true", help="only the prefill-chunk GEMM vs GEMV-tile legs")
+    ap.add_argument("--prefill-only", action="store_true", help="only the 4B 1024-token prefill, three times")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the token loop on a single MI355X and has no "
@@ -381,6 +401,9 @@ def main():
         return
     if args.delta_c3:
         print(json.dumps(delta_c3()), flush=True)
+        return
+    if args.prefill_only:
+        print(json.dumps(prefill_only()), flush=True)
         return
     if args.copy_calibration:
         n = args.copy_calibration << 20

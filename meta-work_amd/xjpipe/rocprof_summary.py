@@ -8,7 +8,8 @@ trace    per-kernel statistics, and the decode step broken down by kernel
 traffic  HBM bytes per single-token GEMV launch from FETCH_SIZE / WRITE_SIZE
          (KiB per dispatch), each scaled by the factor that makes the same
          counter read the known size of the calibration copy (the largest
-         runtime copy-kernel dispatch of the run)
+         runtime copy-kernel dispatch of the run); the same per dispatch for
+         the attention, DeltaNet and prefill kernels (KERNELS_OF_INTEREST)
 
 Single-token GEMV launches are the gemv_kernel<1, ...> and gemv_cu_kernel
 dispatches (the two launch forms of the same fused dequant-GEMV).
@@ -29,12 +30,17 @@ def _one(d, suffix):
     return f[0]
 
 
+def _norm(name):
+    return name.replace("void ", "").replace("(anonymous namespace)::", "")
+
+
 def _short(name):
-    return name.split("(")[0].replace("void ", "")
+    return _norm(name).split("(")[0]
 
 
 def _gemv1(name):
-    return name.startswith("void xjk::gemv_kernel<1,") or name.startswith("void xjk::gemv_cu_kernel<1,")
+    n = _norm(name)
+    return n.startswith("xjk::gemv_kernel<1,") or n.startswith("xjk::gemv_cu_kernel<1,")
 
 
 def trace(d):
@@ -76,6 +82,13 @@ def trace(d):
     return "\n".join(out)
 
 
+# kernels whose traffic the summary also lists: decode attention, the DeltaNet
+# step, and the prefill's GEMM and chunked-rule kernels
+KERNELS_OF_INTEREST = ("attn_part_kernel", "attn_combine_kernel", "kv_store_kernel", "delta_part_kernel",
+                       "delta_head_kernel", "gemm_mfma_kernel", "gemm_reduce_kernel", "rms_scale_kernel", "dc_prep",
+                       "dc_scan", "delta_prefill_prep_kernel", "conv_silu_kernel", "prep_kernel")
+
+
 def _counter(d, name):
     rows = list(csv.DictReader(open(_one(d, "_counter_collection.csv"))))
     return [(r["Kernel_Name"], float(r["Counter_Value"])) for r in rows if r["Counter_Name"] == name]
@@ -91,9 +104,20 @@ def traffic(dfetch, dwrite, copy_bytes, out_json=None):
         res[name] = {"factor": factor, "launches": len(g1), "kib_per_launch_raw": sum(g1) / len(g1),
                      "bytes_per_launch": sum(g1) / len(g1) * 1024.0 * factor}
     total = res["FETCH_SIZE"]["bytes_per_launch"] + res["WRITE_SIZE"]["bytes_per_launch"]
+    # the other kernels of the run (by full template name): HBM bytes per dispatch
+    others = {}
+    for name, d in (("FETCH_SIZE", dfetch), ("WRITE_SIZE", dwrite)):
+        factor = res[name]["factor"]
+        per = collections.defaultdict(list)
+        for k, v in _counter(d, name):
+            if any(_norm(k).startswith("xjk::" + f) for f in KERNELS_OF_INTEREST):
+                per[_short(k)].append(v)
+        for k, v in per.items():
+            others.setdefault(k, {"dispatches": len(v)})[name.split("_")[0].lower() + "_bytes"] = round(
+                sum(v) / len(v) * 1024.0 * factor)
     doc = {"kernel": "gemv_kernel<1,...> / gemv_cu_kernel (single-token GEMV launches of the decode step)",
            "bytes_per_launch": round(total), "fetch": res["FETCH_SIZE"], "write": res["WRITE_SIZE"],
-           "calibration_copy_bytes": copy_bytes}
+           "calibration_copy_bytes": copy_bytes, "other_kernels": others}
     if out_json:
         with open(out_json, "w") as f:
             json.dump(doc, f, indent=1)
