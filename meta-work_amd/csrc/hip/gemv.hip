@@ -1574,36 +1574,60 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *__restrict_
     xjd::dequant_chunk(W, type, K, nblk, r0 + rr, c, y + rr * K + c * 32);
 }
 
-// Depthwise causal conv + SiLU of T tokens in place, one thread per channel,
-// tokens in order: the EPI_CONV epilogue's own code (epi_load / epi_row) with
-// the token's input as the row's dot product. Checkpoint t (t < keep_n) holds
-// the state after token t.
-__global__ __launch_bounds__(256) void conv_silu_kernel(const GArgs a, float *x, int T) {
-    const GSeg &sg0 = a.seg[0];
-    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (r >= sg0.n_rows) return;
-    for (int t = 0; t < T; t++) {
-        GSeg sg = sg0;
-        sg.y = x + (int64_t)t * sg0.n_rows;
-        GArgs b = a;
-        b.t0 = t;
-        EpiIn<1> e;
-        epi_load<1>(sg, r, e);
-        const float acc[1] = {sg.y[r]};
-        epi_row<1>(b, sg, r, acc, e);
+// Depthwise causal conv + SiLU of T tokens in place (xj_cpu.c:164-181), one
+// thread per channel walking the tokens with the window in registers: the
+// EPI_CONV epilogue's expressions (s = sum over k of st[k] * wc[k] in k
+// order, then fma(x, wc[KC-1], s); the window shifted, the input appended),
+// so results equal the epilogue's bit for bit. The inputs of 16 tokens are
+// requested at once (the stores of earlier tokens go to other addresses).
+// Checkpoint t (t < ck_n) holds the state after token t.
+template <int KC>
+__global__ __launch_bounds__(64) void conv_silu_kernel(float *x, float *state, const float *w, int C, int T, float *ck,
+                                                       int ck_n) {
+    const int64_t r = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (r >= C) return;
+    float st[KC - 1], wc[KC];
+#pragma unroll
+    for (int k = 0; k < KC - 1; k++) st[k] = state[r * (KC - 1) + k];
+#pragma unroll
+    for (int k = 0; k < KC; k++) wc[k] = w[r * KC + k];
+    for (int t0 = 0; t0 < T; t0 += 16) {
+        float xv[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) xv[i] = x[(int64_t)(t0 + i < T ? t0 + i : T - 1) * C + r];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int t = t0 + i;
+            if (t >= T) break;
+            float s = 0.f;
+#pragma unroll
+            for (int k = 0; k < KC - 1; k++) s = fmaf(st[k], wc[k], s);
+            s = fmaf(xv[i], wc[KC - 1], s);
+#pragma unroll
+            for (int k = 0; k + 1 < KC - 1; k++) st[k] = st[k + 1];
+            st[KC - 2] = xv[i];
+            x[(int64_t)t * C + r] = xjd::silu(s);
+            if (t < ck_n)
+#pragma unroll
+                for (int k = 0; k < KC - 1; k++) ck[((int64_t)t * C + r) * (KC - 1) + k] = st[k];
+        }
     }
+#pragma unroll
+    for (int k = 0; k < KC - 1; k++) state[r * (KC - 1) + k] = st[k];
 }
 
 int conv_silu_launch(float *x, float *state, const float *w, int C, int K, int T, float *ck, int ck_n, hipStream_t st) {
     if (C < 1 || T < 1 || K < 2 || K > 8 || ck_n < 0 || ck_n > T || (ck_n && !ck)) return -1;
-    GArgs a{};
-    a.keep_n = ck_n;
-    a.post.mode = POST_NONE;
-    a.nseg = 1;
-    GSeg &sg = a.seg[0];
-    sg.n_rows = C; sg.ys = C; sg.epi = EPI_CONV;
-    sg.conv_state = state; sg.conv_w = w; sg.conv_ck = ck; sg.conv_k = K;
-    hipLaunchKernelGGL(conv_silu_kernel, dim3((C + 255) / 256), dim3(256), 0, st, a, x, T);
+    const dim3 g((C + 63) / 64), b(64);
+    switch (K) {
+    case 2: hipLaunchKernelGGL(conv_silu_kernel<2>, g, b, 0, st, x, state, w, C, T, ck, ck_n); break;
+    case 3: hipLaunchKernelGGL(conv_silu_kernel<3>, g, b, 0, st, x, state, w, C, T, ck, ck_n); break;
+    case 4: hipLaunchKernelGGL(conv_silu_kernel<4>, g, b, 0, st, x, state, w, C, T, ck, ck_n); break;
+    case 5: hipLaunchKernelGGL(conv_silu_kernel<5>, g, b, 0, st, x, state, w, C, T, ck, ck_n); break;
+    case 6: hipLaunchKernelGGL(conv_silu_kernel<6>, g, b, 0, st, x, state, w, C, T, ck, ck_n); break;
+    case 7: hipLaunchKernelGGL(conv_silu_kernel<7>, g, b, 0, st, x, state, w, C, T, ck, ck_n); break;
+    default: hipLaunchKernelGGL(conv_silu_kernel<8>, g, b, 0, st, x, state, w, C, T, ck, ck_n); break;
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
