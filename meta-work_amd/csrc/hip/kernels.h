@@ -116,21 +116,39 @@ int gemv_init(char *err, size_t errlen);       // raise the dynamic-LDS limit on
 int gemv_max_tile(int K);                       // largest T tile whose activations fit in LDS
 size_t gemv_xq_bytes(int K);                    // xq bytes for the largest tile of this K
 
-// Multi-token GEMM on the matrix cores (gemm.hip): y[t][r] (+)= W[r] . v[t] for
-// T in 1..gemm_max_tokens() tokens of prepared activations (xq, stride xs per
-// token), Q4_K or Q6_K rows. With `part` (capacity part_floats) short weights
-// split K over work-groups and a reduce launch adds the splits in order.
+// Multi-token GEMM on the matrix cores (gemm.hip): for each segment i,
+// y_i[t][r] (+)= (W_i[r] . v[t]) (* tsc[t]) for T in 1..gemm_max_tokens()
+// tokens of prepared activations (xq, stride xs per token); every segment of
+// one launch has the same type (Q4_K or Q6_K) and inner size K. One
+// persistent work-group per CU takes an equal, contiguous share of the
+// (row group of 128 rows, 256-element block) units of all segments; a row
+// group whose blocks are shared by several work-groups leaves their partial
+// sums in `part`, which the last of them to arrive adds in work-group order,
+// so results do not depend on timing.
+constexpr int kGemmMaxSeg = 4;
+struct GemmSeg {
+    const uint8_t *w; int32_t N;
+    float *y; int32_t ys; int32_t add;   // add: y += instead of y =
+};
 struct GemmArgs {
-    const uint8_t *w; uint32_t type; int32_t N, K, T;
+    uint32_t type; int32_t K, T;
     const uint8_t *xq; int64_t xs;
-    float *part;
-    float *y; int32_t ys; int32_t add;
-    int32_t nsplit;   // set by gemm_launch
+    int32_t nseg;
+    GemmSeg seg[kGemmMaxSeg];
     // optional: y[t][r] = (sum) * tsc[t] before the add (an RMSNorm input's
     // per-token scale, applied after the dot product as the GEMV applies it)
     const float *tsc;
+    float *part;     // partial sums: gemm_part_floats(rows, T) floats
+    int32_t *cnt;    // arrival counters: gemm_counters(rows) ints, zero before the first launch
     int32_t *inc_ptr; int32_t inc_by;   // optional: *inc_ptr += inc_by once
+    // set by gemm_launch
+    int32_t rg0[kGemmMaxSeg + 1];       // first row group of each segment (prefix)
+    int32_t nb, G;                      // blocks per row, work-groups
+    int64_t P;                          // units
 };
+// Capacities for a launch over `rows` rows in all (at most kGemmMaxSeg) segments.
+int64_t gemm_part_floats(int64_t rows, int T);
+int gemm_counters(int64_t rows);
 // Per-token RMSNorm scale of T tokens of PRO_RMSU activations (xq, token
 // stride xs): tsc[t] = 1 / sqrt(sum of the groups' ss / K + eps), the
 // GEMV's rmsu_scale.
@@ -138,8 +156,7 @@ int rms_scale_launch(const uint8_t *xq, int64_t xs, int K, int T, float eps, flo
 // *p += by on the device, in stream order (one thread).
 int inc_launch(int32_t *p, int32_t by, hipStream_t st);
 int gemm_max_tokens();
-int gemm_splits(int N, int K, int T, int64_t part_floats);
-int gemm_launch(const GemmArgs &a, int64_t part_floats, hipStream_t st);
+int gemm_launch(const GemmArgs &a, int64_t part_floats, int n_cnt, hipStream_t st);
 
 // Repack a GGUF tensor into the device layout. dst must hold `bytes` =
 // n_rows * row_bytes(type, k); src is host memory in GGUF layout.

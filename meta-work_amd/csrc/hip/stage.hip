@@ -81,6 +81,8 @@ struct HStage {
     // partials and the chunked delta rule's work area
     float *tsc = nullptr, *gpart = nullptr, *dwork = nullptr;
     int64_t gpart_floats = 0;
+    int32_t *gcnt = nullptr;   // the GEMM's arrival counters (zero between launches)
+    int32_t n_gcnt = 0;
     float2 *rope = nullptr;
     float *h_x = nullptr;            // pinned staging [max_batch][n_embd]
     int32_t *h_i = nullptr;          // pinned scalar
@@ -179,8 +181,8 @@ struct Gemv {
     Profile *prof = nullptr;
     bool prepared = false;
     explicit Gemv(uint8_t *xq, Profile *p = nullptr) : prof(p) { a.xq = xq; }
-    Gemv(uint8_t *xq, Profile *p, float *tsc_, float *part_, int64_t part_floats_)
-        : prof(p), tsc(tsc_), part(part_), part_floats(part_floats_) {
+    Gemv(uint8_t *xq, Profile *p, float *tsc_, float *part_, int64_t part_floats_, int32_t *cnt_, int32_t n_cnt_)
+        : prof(p), tsc(tsc_), part(part_), part_floats(part_floats_), cnt(cnt_), n_cnt(n_cnt_) {
         a.xq = xq;
     }
     Gemv &seg(const DevW &w, float *y, int ys, int epi) {
@@ -228,6 +230,8 @@ struct Gemv {
     // them every launch takes the GEMV form).
     float *tsc = nullptr, *part = nullptr;
     int64_t part_floats = 0;
+    int32_t *cnt = nullptr;
+    int32_t n_cnt = 0;
     // Chunks of at least kGemmMinT tokens take the matrix-core GEMM
     // (gemm.hip): the prep launch builds the T tokens' activations once, the
     // RMSNorm scale is applied per token after the dot products (as the GEMV
@@ -237,7 +241,7 @@ struct Gemv {
     static constexpr int kGemmMinT = 16;
     bool gemm_ok(int T) const {
         static const bool on = env_int("XJ_PREFILL_GEMM", 1) != 0;
-        if (!on || T < kGemmMinT || prof || !tsc || !part || !a.xq) return false;
+        if (!on || T < kGemmMinT || prof || !tsc || !part || !cnt || !a.xq) return false;
         if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_SWIGLU && a.pro != PRO_GATED_RMS) return false;
         if (a.post.mode != POST_NONE && a.post.mode != POST_SWIGLU) return false;
         if (a.K % 256) return false;
@@ -255,18 +259,28 @@ struct Gemv {
         const bool rms = a.pro == PRO_RMSU;
         if (rms && rms_scale_launch(a.xq, xs, a.K, T, a.eps, tsc, st)) return -1;
         const int mt = gemm_max_tokens(), tile = gemv_max_tile(a.K);
+        // the segments of each type in one launch, sharing the activations
+        for (uint32_t ty : {(uint32_t)XJ_Q4_K, (uint32_t)XJ_Q6_K}) {
+            GemmArgs g{};
+            g.type = ty; g.K = a.K; g.xs = xs; g.part = part; g.cnt = cnt;
+            for (int i = 0; i < a.nseg; i++) {
+                const GSeg &s = a.seg[i];
+                if (s.type != ty) continue;
+                g.seg[g.nseg++] = GemmSeg{s.w, s.n_rows, s.y, s.ys, s.epi == EPI_ADD};
+            }
+            if (!g.nseg) continue;
+            for (int t0 = 0; t0 < T; t0 += mt) {
+                GemmArgs b = g;
+                b.T = T - t0 < mt ? T - t0 : mt;
+                b.xq = a.xq + t0 * xs;
+                for (int i = 0; i < b.nseg; i++) b.seg[i].y = g.seg[i].y + (int64_t)t0 * g.seg[i].ys;
+                b.tsc = rms ? tsc + t0 : nullptr;
+                if (gemm_launch(b, part_floats, n_cnt, st)) return -1;
+            }
+        }
         for (int i = 0; i < a.nseg; i++) {
             const GSeg &s = a.seg[i];
-            if (s.type == XJ_Q4_K || s.type == XJ_Q6_K) {
-                for (int t0 = 0; t0 < T; t0 += mt) {
-                    GemmArgs g{};
-                    g.w = s.w; g.type = s.type; g.N = s.n_rows; g.K = a.K; g.T = T - t0 < mt ? T - t0 : mt;
-                    g.xq = a.xq + t0 * xs; g.xs = xs; g.part = part;
-                    g.y = s.y + (int64_t)t0 * s.ys; g.ys = s.ys; g.add = s.epi == EPI_ADD;
-                    g.tsc = rms ? tsc + t0 : nullptr;
-                    if (gemm_launch(g, part_floats, st)) return -1;
-                }
-            } else {   // this segment alone on the GEMV, reading the prepared activations
+            if (s.type != XJ_Q4_K && s.type != XJ_Q6_K) {   // this segment alone on the GEMV, reading the prepared activations
                 if (tile < 1) return -1;
                 GArgs one = a;
                 one.nseg = 1;
@@ -357,7 +371,7 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
     HLayer &L = S->L[il - S->s.l0];
     const int E = hp.n_embd, FF = hp.n_ff;
     // every GEMV of the layer with the stage's prefill buffers
-    auto gemv = [&](uint8_t *xq) { return Gemv(xq, pf, S->tsc, S->gpart, S->gpart_floats); };
+    auto gemv = [&](uint8_t *xq) { return Gemv(xq, pf, S->tsc, S->gpart, S->gpart_floats, S->gcnt, S->n_gcnt); };
     auto rms_in = [&](Gemv &g, const float *w) {
         g.a.x = x; g.a.xs = E; g.a.pro = PRO_RMSU; g.a.pro_w = w; g.a.eps = hp.eps;
     };
@@ -678,8 +692,10 @@ extern "C" uint64_t xj_hip_stage_state_bytes(const xj_model *m, int l0, int l1, 
     }
     b += 10ull * 4 * max_batch * scratch_floats(hp) +
          4ull * max_batch * hp.n_head * ((n_ctx + 63) / 64) * (hp.head_dim + 2);
-    // prefill on the matrix cores: RMSNorm scales, K-split partials, chunked-rule work
-    b += 4ull * max_batch + 16ull * max_batch * scratch_floats(hp);
+    // prefill on the matrix cores: RMSNorm scales, K-split partials and counters, chunked-rule work
+    const int64_t grows = 2 * (int64_t)scratch_floats(hp) + 2 * (int64_t)hp.h_v;
+    b += 4ull * max_batch + 4ull * gemm_part_floats(grows, max_batch < gemm_max_tokens() ? max_batch : gemm_max_tokens()) +
+         4ull * gemm_counters(grows);
     bool rec = false;
     for (int il = l0; il < l1 && il < (int)hp.n_layer; il++) rec = rec || m->layers[il].recurrent;
     if (rec) b += delta_chunked_work_bytes(hp.h_v, hp.s_k, max_batch, 64);
@@ -814,9 +830,14 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
     S->npast = dalloc<int32_t>(S, 1, err, errlen);
     // prefill on the matrix cores (chunks of at least 16 tokens)
     S->tsc = dalloc<float>(S, mb, err, errlen);
-    S->gpart_floats = 4 * (int64_t)mb * (int64_t)sf;
+    // every GEMM launch covers at most 2 sf + 2 h_v rows (gate|up, the DeltaNet in-projection)
+    const int64_t grows = 2 * (int64_t)sf + 2 * (int64_t)hp.h_v;
+    S->gpart_floats = gemm_part_floats(grows, (int)(mb < gemm_max_tokens() ? mb : gemm_max_tokens()));
     S->gpart = dalloc<float>(S, (size_t)S->gpart_floats, err, errlen);
-    if (!S->tsc || !S->gpart) return fail();
+    S->n_gcnt = gemm_counters(grows);
+    S->gcnt = dalloc<int32_t>(S, (size_t)S->n_gcnt, err, errlen);
+    if (!S->tsc || !S->gpart || !S->gcnt) return fail();
+    XJ_CHECK(hipMemset(S->gcnt, 0, (size_t)S->n_gcnt * 4), err, errlen, fail());
     {
         bool rec = false;
         for (int il = l0; il < l1 && il < hp.n_layer; il++) rec = rec || m->layers[il].recurrent;
@@ -1710,9 +1731,10 @@ static int gemm_enqueue(uint32_t type, const void *dw, int64_t n_rows, int64_t k
                         hipStream_t st) {
     static uint8_t *xq = nullptr;   // grown on demand; the per-op entries are synchronous on one stream
     static float *part = nullptr;
-    static size_t xq_cap = 0, part_cap = 0;
+    static int32_t *cnt = nullptr;
+    static size_t xq_cap = 0, part_cap = 0, cnt_cap = 0;
     const int64_t xs = xq_off((int)k).stride;
-    const size_t need = (size_t)T * xs, pneed = (size_t)gemm_splits((int)n_rows, (int)k, T, INT64_MAX) * T * n_rows;
+    const size_t need = (size_t)T * xs, pneed = (size_t)gemm_part_floats(n_rows, T), cneed = (size_t)gemm_counters(n_rows);
     if (need > xq_cap) {
         if (xq) (void)hipFree(xq);
         xq = nullptr, xq_cap = 0;
@@ -1725,13 +1747,20 @@ static int gemm_enqueue(uint32_t type, const void *dw, int64_t n_rows, int64_t k
         if (hipMalloc(&part, pneed * 4) != hipSuccess) return -1;
         part_cap = pneed;
     }
+    if (cneed > cnt_cap) {   // zero once; the kernel leaves them zero
+        if (cnt) (void)hipFree(cnt);
+        cnt = nullptr, cnt_cap = 0;
+        if (hipMalloc(&cnt, cneed * 4) != hipSuccess || hipMemsetAsync(cnt, 0, cneed * 4, st) != hipSuccess) return -1;
+        cnt_cap = cneed;
+    }
     GArgs p{};
     p.x = x; p.xs = (int32_t)k; p.pro = PRO_NONE; p.xq = xq; p.K = (int32_t)k; p.T = T;
     if (prep_launch(p, st)) return -1;
     GemmArgs g{};
-    g.w = (const uint8_t *)dw; g.type = type; g.N = (int32_t)n_rows; g.K = (int32_t)k; g.T = T;
-    g.xq = xq; g.xs = xs; g.part = part; g.y = y; g.ys = (int32_t)n_rows; g.add = add;
-    return gemm_launch(g, (int64_t)part_cap, st);
+    g.type = type; g.K = (int32_t)k; g.T = T; g.xq = xq; g.xs = xs; g.part = part; g.cnt = cnt;
+    g.nseg = 1;
+    g.seg[0] = GemmSeg{(const uint8_t *)dw, (int32_t)n_rows, y, (int32_t)n_rows, add};
+    return gemm_launch(g, (int64_t)part_cap, (int)cnt_cap, st);
 }
 
 extern "C" int xjh_gemm(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T, float *y, int add,
