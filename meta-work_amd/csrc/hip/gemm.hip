@@ -20,9 +20,9 @@
 // column groups), eight wavefronts = a row group of 128 rows. The units, a
 // (row group, 256-element block) pair each over every segment of the launch,
 // are dealt out in equal contiguous ranges to one persistent work-group per
-// CU. A work-group stages a unit's activations of all tokens in LDS with one
-// round of copies (864 bytes per token) and requests its weights, then
-// computes the previous unit from the other LDS buffer while they arrive.
+// CU. A work-group requests a unit's weights and stages its activations of
+// all tokens in LDS (864 bytes per token), half of the copies before and half
+// in the middle of computing the previous unit from the other LDS buffer.
 // A row group covered by one work-group is stored directly; one shared by
 // several leaves a partial sum per work-group, and the last to arrive adds
 // them in work-group order (the hand-off of the GEMV's SwiGLU tail:
@@ -75,10 +75,11 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) {
 
 // The T tokens' activations of block blk into buf: slot c = 55 t + q (chunk
 // q < 54 of token t; q = 54 is padding) at buf + 16 c, slot c by thread c
-// mod blockDim.
-__device__ __forceinline__ void stage_blk(const GemmArgs &a, const XqOff &o, int blk, uint8_t *buf) {
+// mod blockDim; `part` 0 / 1 issues the first / second half of the rounds.
+__device__ __forceinline__ void stage_blk(const GemmArgs &a, const XqOff &o, int blk, uint8_t *buf, int part) {
     const int nslots = a.T * kTokChunks, wv = threadIdx.x >> 6;
-    for (int j0 = 0; j0 < nslots; j0 += kThreads) {
+    const int rounds = (nslots + kThreads - 1) / kThreads, r0 = part ? rounds / 2 : 0, r1 = part ? rounds : rounds / 2;
+    for (int j0 = r0 * kThreads; j0 < r1 * kThreads; j0 += kThreads) {
         const int c = j0 + (int)threadIdx.x;
         const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(buf + 16 * (j0 + 64 * wv)));
         const int t = c / kTokChunks, q = c - t * kTokChunks;
@@ -183,14 +184,15 @@ __device__ __forceinline__ void q6k_scales(const WReg &r, int li, int kq, float4
                                         d * (float)(int8_t)((w >> 16) & 0xFFu), d * (float)(int8_t)(w >> 24)};
 }
 
-// One block of one wavefront: acc[tg][i] += the block's terms of row rb + 4 kq + i
-// and token tok[tg] (= 16 tg + li).
-template <bool Q6, int NTG>
+// Half HALF (32-element groups 4 HALF .. 4 HALF + 3) of one block of one
+// wavefront: acc[tg][i] += the terms of row rb + 4 kq + i and token tok[tg]
+// (= 16 tg + li).
+template <bool Q6, int NTG, int HALF>
 __device__ __forceinline__ void compute_blk(const WReg &r, const uint8_t *buf, const float4 *scl, const int (&tok)[NTG],
                                             int kq, float (&acc)[NTG][4]) {
     if constexpr (!Q6) {
 #pragma unroll
-        for (int p = 0; p < 4; p++) {
+        for (int p = 2 * HALF; p < 2 * HALF + 2; p++) {
             const long A[2] = {(long)(r.qa[p] & 0x0F0F0F0F0F0F0F0Full), (long)((r.qa[p] >> 4) & 0x0F0F0F0F0F0F0F0Full)};
             // ds, dm of sub-blocks 2p, 2p+1 for the four output rows (q4k_scales)
             float4 sd[4];
@@ -221,8 +223,8 @@ __device__ __forceinline__ void compute_blk(const WReg &r, const uint8_t *buf, c
         }
     } else {
         const uint64_t hbs[2] = {(uint64_t)r.hc[0].x | ((uint64_t)r.hc[0].y << 32), (uint64_t)r.hc[0].z | ((uint64_t)r.hc[0].w << 32)};
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
+        {
+            constexpr int h = HALF;
             const uint64_t l0 = r.qa[2 * h], l1 = r.qa[2 * h + 1], hb = hbs[h];
 #pragma unroll
             for (int G = 0; G < 4; G++) {
@@ -266,27 +268,25 @@ __device__ __forceinline__ void compute_blk(const WReg &r, const uint8_t *buf, c
 }
 
 // Work-group holding unit u: the w whose range [w P / G, (w + 1) P / G) holds u.
-__device__ __forceinline__ int wg_of(int64_t u, int64_t P, int G) { return (int)(((u + 1) * G - 1) / P); }
+__device__ __forceinline__ int wg_of(int u, int P, int G) { return ((u + 1) * G - 1) / P; }
 
 template <bool Q6, int NTG>
 __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(const GemmArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ int last_sh;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, kq = lane >> 4;
-    const int nb = a.nb, G = a.G, w = blockIdx.x;
-    const int64_t P = a.P, u0 = (int64_t)w * P / G, u1 = (int64_t)(w + 1) * P / G;
+    const int nb = a.nb, G = a.G, w = blockIdx.x, P = (int)a.P;
+    const int u0 = w * P / G, u1 = (w + 1) * P / G;
     const XqOff o = xq_off(a.K);
     uint8_t *const buf0 = lds, *const buf1 = lds + a.T * kTokStride;
     float4 *const scl = (float4 *)(lds + 2 * a.T * kTokStride) + wv * 64;   // this wavefront's scale table
     int tok[NTG];
 #pragma unroll
     for (int tg = 0; tg < NTG; tg++) tok[tg] = min(16 * tg + li, a.T - 1);
-    // unit -> segment s, row group g (global) and block; this wavefront's rows
-    // (clamped so that every load stays inside the weights; rows past N
-    // compute values that are never stored)
-    auto locate = [&](int64_t u, int &s, int &g, int &blk, int &rb, int &rowA, int (&rowC)[4]) {
-        g = (int)(u / nb);
-        blk = (int)(u - (int64_t)g * nb);
+    // row group g (global) -> segment s; this wavefront's rows (clamped so that
+    // every load stays inside the weights; rows past N compute values that
+    // are never stored)
+    auto rows_of = [&](int g, int &s, int &rb, int &rowA, int (&rowC)[4]) {
         s = 0;
 #pragma unroll
         for (int i = 1; i < kGemmMaxSeg; i++) s += i < a.nseg && g >= a.rg0[i];
@@ -296,36 +296,44 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(const GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) rowC[i] = min(rb + 4 * kq + i, N - 1);
     };
-    int s, g, blk, rb, rowA, rowC[4];
-    locate(u0, s, g, blk, rb, rowA, rowC);
+    int g = u0 / nb, blk = u0 - g * nb, s, rb, rowA, rowC[4];
+    rows_of(g, s, rb, rowA, rowC);
     WReg cur, nxt;
-    stage_blk(a, o, blk, buf0);
     load_w<Q6>(a.seg[s].w, (int64_t)a.seg[s].N * nb, nb, rowA, rowC, blk, kq, cur);
+    stage_blk(a, o, blk, buf0, 0);
+    stage_blk(a, o, blk, buf0, 1);
     float acc[NTG][4];
 #pragma unroll
     for (int tg = 0; tg < NTG; tg++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[tg][i] = 0.f;
-    for (int64_t u = u0; u < u1; u++) {
+    for (int u = u0; u < u1; u++) {
         uint8_t *const bc = ((u - u0) & 1) ? buf1 : buf0, *const bn = ((u - u0) & 1) ? buf0 : buf1;
         __builtin_amdgcn_s_waitcnt(0);   // unit u's weights and staged activations have landed
         __syncthreads();                 // ... for every wavefront; unit u - 1's reads of bn are done
-        // unit u + 1's requests are in flight while unit u computes
-        int s2 = s, g2 = g, blk2 = blk, rb2 = rb, rowA2 = rowA, rowC2[4] = {rowC[0], rowC[1], rowC[2], rowC[3]};
-        if (u + 1 < u1) {
-            locate(u + 1, s2, g2, blk2, rb2, rowA2, rowC2);
-            stage_blk(a, o, blk2, bn);
+        // unit u + 1's requests are in flight while unit u computes: its
+        // weights, then half of its activation copies before each half of
+        // the computation
+        const bool more = u + 1 < u1;
+        int g2 = blk + 1 == nb ? g + 1 : g, blk2 = blk + 1 == nb ? 0 : blk + 1, s2 = s, rb2 = rb, rowA2 = rowA;
+        int rowC2[4] = {rowC[0], rowC[1], rowC[2], rowC[3]};
+        if (more) {
+            if (g2 != g) rows_of(g2, s2, rb2, rowA2, rowC2);
             load_w<Q6>(a.seg[s2].w, (int64_t)a.seg[s2].N * nb, nb, rowA2, rowC2, blk2, kq, nxt);
+            stage_blk(a, o, blk2, bn, 0);
         }
         const GemmSeg &sg = a.seg[s];
-        if (rb < sg.N) {
+        const bool act = rb < sg.N;
+        if (act) {
             if constexpr (Q6) q6k_scales(cur, li, kq, scl);
             else q4k_scales(cur, li, kq, scl);
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the table, written by other lanes of the wavefront
-            compute_blk<Q6, NTG>(cur, bc, scl, tok, kq, acc);
+            compute_blk<Q6, NTG, 0>(cur, bc, scl, tok, kq, acc);
         }
+        if (more) stage_blk(a, o, blk2, bn, 1);
+        if (act) compute_blk<Q6, NTG, 1>(cur, bc, scl, tok, kq, acc);
         if (u + 1 == u1 || blk == nb - 1) {   // the last of this row group's blocks here (uniform)
-            const int64_t first = (int64_t)g * nb;
+            const int first = g * nb;
             const int wf = wg_of(first, P, G), wl = wg_of(first + nb - 1, P, G);
             const int r0 = (g - a.rg0[s]) * kRG;
             if (wf == wl) {
@@ -464,6 +472,7 @@ int gemm_launch(const GemmArgs &in, int64_t part_floats, int n_cnt, hipStream_t 
     a.nb = a.K / 256;
     a.P = (int64_t)a.rg0[a.nseg] * a.nb;
     a.G = (int)(a.P < cu_count() ? a.P : cu_count());
+    if (a.P >= (1 << 23)) return -1;   // unit indices times G stay in 32 bits
     if (a.rg0[a.nseg] > n_cnt || (int64_t)(a.G + a.rg0[a.nseg]) * a.T * kRG > part_floats) return -1;
     const size_t lds = 2 * (size_t)a.T * kTokStride + kScaleBytes;
     const bool q6 = a.type == XJ_Q6_K;
