@@ -16,7 +16,8 @@
 // Every chunk-level dense product runs on the matrix cores in fp32
 // (v_mfma_f32_16x16x4f32: fp32 products, fp32 sums). Phase 1 (all chunks and
 // heads in parallel) forms K K^T and Q K^T, solves for X (one wavefront, row
-// by row, while the others finish P), then W = X diag(e^lg) K and U = X V.
+// by row with its column of X in registers, while the others finish P from
+// the chunk's q, k and v staged in LDS), then W = X diag(e^lg) K and U = X V.
 // Phase 2 walks the chunks in order, one work-group per (head, 16 value rows)
 // since the value rows of the state are independent: delta = U - W M0^T, O,
 // M_C.
@@ -44,7 +45,7 @@ struct WorkLayout {
 };
 
 template <int S>
-constexpr size_t prep_lds_bytes() { return (size_t)(2 * kC * (S + 4) + kC * (kC + 4)) * 4; }
+constexpr size_t prep_lds_bytes() { return (size_t)(3 * kC * (S + 4) + kC * (kC + 4)) * 4; }
 template <int S>
 constexpr size_t scan_lds_bytes() { return (size_t)((16 + kC) * (S + 4) + kC * 20) * 4; }
 
@@ -57,7 +58,8 @@ __global__ __launch_bounds__(256) void dc_prep(int H, int T, const float *__rest
     extern __shared__ __align__(16) float sm[];
     float *Ks = sm;                // [kC][KS] the chunk's k rows (zero past T)
     float *Vs = Ks + kC * KS;      // [kC][KS] v rows
-    float *AX = Vs + kC * KS;      // [kC][XS] A, then X in place
+    float *Qs = Vs + kC * KS;      // [kC][KS] q rows
+    float *AX = Qs + kC * KS;      // [kC][XS] A, then X
     __shared__ float lg[kC], bb[kC];
     __shared__ __align__(16) float gam[kC];
     const int n = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
@@ -65,13 +67,15 @@ __global__ __launch_bounds__(256) void dc_prep(int H, int T, const float *__rest
     float *wk = work + ((int64_t)n * H + h) * WL::SIZE;
     for (int idx = tid; idx < kC * S / 4; idx += 256) {
         const int t = idx / (S / 4), c = 4 * (idx % (S / 4)), tok = n * kC + t;
-        v4f kv = {0.f, 0.f, 0.f, 0.f}, vv = kv;
+        v4f kv = {0.f, 0.f, 0.f, 0.f}, vv = kv, qv = kv;
         if (tok < T) {
             kv = ld4(k + ((int64_t)tok * H + h) * S + c);
             vv = ld4(v + ((int64_t)tok * H + h) * S + c);
+            qv = ld4(q + ((int64_t)tok * H + h) * S + c);
         }
         *(v4f *)(Ks + t * KS + c) = kv;
         *(v4f *)(Vs + t * KS + c) = vv;
+        *(v4f *)(Qs + t * KS + c) = qv;
     }
     if (tid < kC) {
         const int tok = n * kC + tid;
@@ -105,25 +109,37 @@ __global__ __launch_bounds__(256) void dc_prep(int H, int T, const float *__rest
     }
     __syncthreads();
     if (w == 0) {
-        // X = (I + A)^-1 diag(beta), row by row in place; lane l owns column l.
-        // One wavefront: its LDS reads of row s precede its writes of row s.
+        // X = (I + A)^-1 diag(beta) by forward substitution, row by row: lane l
+        // owns column l, held in registers (X[s][l] = beta_s [l == s] - sum over
+        // m < s of A[s][m] X[m][l]; X is lower triangular), A's rows read as
+        // broadcasts, four partial sums per row; then X replaces A in LDS.
+        // (row s + 1 of A is requested while row s is computed; the two row
+        // buffers alternate with the parity of s, eight partial sums per row)
+        float xc[kC];
+        v4f arow[2][kC / 4];
+#pragma unroll
         for (int s = 0; s < kC; s++) {
-            float x = 0.f;
-            for (int m = 0; m < s; m++) x = fmaf(-AX[s * XS + m], AX[m * XS + l], x);
-            AX[s * XS + l] = l < s ? x : l == s ? bb[s] : 0.f;
+            if (s + 1 < kC) {
+#pragma unroll
+                for (int j = 0; 4 * j < s + 1; j++) arow[(s + 1) & 1][j] = ld4(AX + (s + 1) * XS + 4 * j);
+            }
+            float pp[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int m = 0; m < s; m++) pp[m & 7] = fmaf(-arow[s & 1][m / 4][m & 3], xc[m], pp[m & 7]);
+            const float x = ((pp[0] + pp[1]) + (pp[2] + pp[3])) + ((pp[4] + pp[5]) + (pp[6] + pp[7]));
+            xc[s] = l < s ? x : l == s ? bb[s] : 0.f;
         }
-    } else {
+#pragma unroll
+        for (int s = 0; s < kC; s++) AX[s * XS + l] = xc[s];    } else {
         // P[t][r] = e^(lg_t - lg_r) q_t.k_r for r <= t (zero elsewhere and past T):
         // the 10 tiles on and below the diagonal over wavefronts 1..3
         for (int tile = w - 1; tile < 16; tile += 3) {
             const int I = tile / 4, J = tile % 4;
             v4f qk = {0.f, 0.f, 0.f, 0.f};
-            const int tokA = n * kC + 16 * I + lr;
             if (J <= I) {
-                const float *qa = q + ((int64_t)tokA * H + h) * S;
                 for (int b = 0; b < S / 16; b++) {
                     const int c = 16 * b + 4 * lq;
-                    const v4f a4 = tokA < T ? ld4(qa + c) : v4f{0.f, 0.f, 0.f, 0.f};
+                    const v4f a4 = ld4(Qs + (16 * I + lr) * KS + c);   // zero past T
                     const v4f kb = ld4(Ks + (16 * J + lr) * KS + c);
 #pragma unroll
                     for (int s = 0; s < 4; s++) qk = mma(qk, a4[s], kb[s]);
