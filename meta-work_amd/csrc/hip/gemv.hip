@@ -47,7 +47,7 @@ static int g_lds_max = 64 * 1024;
 constexpr int kCuMaxT = 5;   // tokens of a per-CU launch (speculative verify widths)
 static int g_cus = 256;
 static int g_grid_cap = 256 * 8;     // work-groups of a looping multi-token launch
-static int g_grid_cap1 = 256 * 8;    // ... of a looping single-token launch
+static int g_grid_cap1 = 256 * 3;    // ... of a looping single-token launch
 static bool g_grid_forced = false;   // XJ_GEMV_WG_PER_CU given: one cap for every launch
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
@@ -1510,7 +1510,11 @@ int gemv_init(char *err, size_t errlen) {
         g_cus = cus;
         const int forced = env_or("XJ_GEMV_WG_PER_CU", 0);
         g_grid_forced = forced > 0;
-        g_grid_cap1 = cus * (forced > 0 ? forced : 8);
+        // a looping single-token launch (the LM head): three work-groups per
+        // CU, one resident round that pays the activation prologue once per
+        // work-group (151936 x 2560 Q6_K: 65.2 / 60.4 / 74.4 / 62.9 us at
+        // 8 / 3 / 4 / 6 per CU)
+        g_grid_cap1 = cus * (forced > 0 ? forced : env_or("XJ_GEMV_WG_PER_CU_1", 3));
         // several tokens stage T x 3 digit bytes per weight element from LDS:
         // fewer work-groups per CU contend less (151936 x 1024 Q4_K, T = 2:
         // 39.2 / 42.2 / 48.7 us at 2 / 4 / 8 per CU)
