@@ -989,6 +989,12 @@ struct xjh_chain {
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     double last_ms = 0;
     int last_tok = -1;
+    // prefill: the whole prompt's ids on the device, and per stage the events
+    // of the chunk hand-off (this stage's layers done; its copy of the
+    // upstream stage's output done)
+    int32_t *d_prompt = nullptr;
+    int prompt_cap = 0;
+    std::vector<hipEvent_t> ev_done, ev_taken;
 };
 
 extern "C" void xjh_chain_free(xjh_chain *c) {
@@ -996,8 +1002,12 @@ extern "C" void xjh_chain_free(xjh_chain *c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     if (c->exec) (void)hipGraphExecDestroy(c->exec);
     if (c->graph) (void)hipGraphDestroy(c->graph);
+    for (auto *S : c->st) if (S->st) (void)hipStreamSynchronize(S->st);
     if (c->ev0) (void)hipEventDestroy(c->ev0);
     if (c->ev1) (void)hipEventDestroy(c->ev1);
+    for (hipEvent_t e : c->ev_done) if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : c->ev_taken) if (e) (void)hipEventDestroy(e);
+    if (c->d_prompt) (void)hipFree(c->d_prompt);
     for (int32_t *p : {c->d_tokens, c->d_argmax, c->d_tok, c->d_hist, c->d_step}) if (p) (void)hipFree(p);
     if (c->h_buf) (void)hipHostFree(c->h_buf);
     delete c;
@@ -1033,6 +1043,15 @@ extern "C" xjh_chain *xjh_chain_new(xj_stage **stages, int n, char *err, size_t 
         xjh_chain_free(c);
         return nullptr;
     }
+    c->ev_done.assign(c->st.size(), nullptr);
+    c->ev_taken.assign(c->st.size(), nullptr);
+    for (size_t i = 0; i < c->st.size(); i++)
+        if (hipEventCreateWithFlags(&c->ev_done[i], hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&c->ev_taken[i], hipEventDisableTiming) != hipSuccess) {
+            snprintf(err, errlen, "chain allocation failed");
+            xjh_chain_free(c);
+            return nullptr;
+        }
     return c;
 }
 
@@ -1043,49 +1062,109 @@ static int chain_sync(xjh_chain *c, char *err, size_t errlen) {
     return 0;
 }
 
+// The prompt in chunks of max_batch, the stages pipelined (pipe/core/xj_net.c:561-604
+// pipelines a remote worker's half against the host's): each stage runs on its
+// own stream from its own hidden-state buffer, so stage i works on chunk k + 1
+// while stage i + 1 works on chunk k. Stage i + 1 takes chunk k by a device
+// copy once stage i has finished it (event done[i]); stage i overwrites its
+// buffer with chunk k + 1 only after that copy (event taken[i + 1]). Every
+// stage's n_past advances on the device at the end of each chunk, so no host
+// round trip separates the chunks; XJ_CHAIN_OVERLAP=0 runs all stages on one
+// stream.
 extern "C" int xjh_chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int keep, float *logits,
                               int32_t *argmax, char *err, size_t errlen) {
-    const int B = c->mb, E = c->st[0]->s.m->hp.n_embd;
+    const int B = c->mb, E = c->st[0]->s.m->hp.n_embd, ns = (int)c->st.size();
     if (n <= 0) { snprintf(err, errlen, "no tokens"); return -1; }
     if (keep && n > B) { snprintf(err, errlen, "verify batch %d exceeds max_batch %d", n, B); return -1; }
+    static const bool overlap = env_int("XJ_CHAIN_OVERLAP", 1) != 0;
     HStage *head = c->st.back();
-    for (int i = 0; i < n; i += B) {
-        const int T = n - i < B ? n - i : B;
-        memcpy(c->h_buf, tokens + i, 4 * T);
-        if (hipMemcpyAsync(c->d_tokens, c->h_buf, 4 * T, hipMemcpyHostToDevice, c->stream) != hipSuccess) {
-            snprintf(err, errlen, "token upload failed"); return -1;
+    auto stream_of = [&](int i) { return overlap ? c->st[i]->st : c->stream; };
+    auto fail_sync = [&]() {
+        for (int i = 0; i < ns; i++) (void)hipStreamSynchronize(c->st[i]->st);
+        for (auto *S : c->st) S->s.keep = 0;
+        return -1;
+    };
+    for (auto *S : c->st)
+        if (S->s.n_past + n > S->s.n_ctx) { snprintf(err, errlen, "context full (%d)", S->s.n_ctx); return -1; }
+    if (n > c->prompt_cap) {
+        if (c->d_prompt) (void)hipFree(c->d_prompt);
+        c->d_prompt = nullptr, c->prompt_cap = 0;
+        if (hipMalloc(&c->d_prompt, 4 * (size_t)n) != hipSuccess) { snprintf(err, errlen, "prompt allocation failed"); return -1; }
+        c->prompt_cap = n;
+    }
+    // the ids (synchronous copy from the caller's memory) and every stage's
+    // starting position
+    if (hipMemcpy(c->d_prompt, tokens, 4 * (size_t)n, hipMemcpyHostToDevice) != hipSuccess) {
+        snprintf(err, errlen, "token upload failed"); return -1;
+    }
+    for (int i = 0; i < ns; i++) {
+        HStage *S = c->st[i];
+        *S->h_i = S->s.n_past;
+        if (hipMemcpyAsync(S->npast, S->h_i, 4, hipMemcpyHostToDevice, stream_of(i)) != hipSuccess ||
+            hipStreamSynchronize(stream_of(i)) != hipSuccess) {   // h_i is reused by later calls
+            snprintf(err, errlen, "position upload failed"); return -1;
         }
-        EmbedArgs ea{c->d_tokens, c->st[0]->tok_embd, c->x, T};
-        if (embed_launch(ea, c->stream)) { snprintf(err, errlen, "embed launch failed"); return -1; }
-        const bool last = i + T == n;
-        for (auto *S : c->st) {
+    }
+    for (int k0 = 0; k0 < n; k0 += B) {
+        const int T = n - k0 < B ? n - k0 : B;
+        for (int i = 0; i < ns; i++) {
+            HStage *S = c->st[i];
+            hipStream_t st = stream_of(i);
+            if (i == 0) {
+                // chunk k0 into stage 0's buffer, once stage 1 has taken the previous chunk
+                if (ns > 1 && k0 > 0 && hipStreamWaitEvent(st, c->ev_taken[1], 0) != hipSuccess) return fail_sync();
+                EmbedArgs ea{c->d_prompt + k0, S->tok_embd, S->x, T};
+                if (embed_launch(ea, st)) { snprintf(err, errlen, "embed launch failed"); return fail_sync(); }
+            } else {
+                // this stage's previous chunk is done with its buffer (same stream); the
+                // upstream stage's output of this chunk is final
+                if (i + 1 < ns && k0 > 0 && hipStreamWaitEvent(st, c->ev_taken[i + 1], 0) != hipSuccess) return fail_sync();
+                if (hipStreamWaitEvent(st, c->ev_done[i - 1], 0) != hipSuccess ||
+                    hipMemcpyAsync(S->x, c->st[i - 1]->x, sizeof(float) * (size_t)T * E, hipMemcpyDeviceToDevice, st) != hipSuccess ||
+                    hipEventRecord(c->ev_taken[i], st) != hipSuccess) {
+                    snprintf(err, errlen, "chunk hand-off failed"); return fail_sync();
+                }
+            }
             if (keep) S->s.keep = T;
             int keep_n = 0;
-            if (begin_forward(S, T, &keep_n, err, errlen)) return -1;
-            *S->h_i = S->s.n_past;
-            if (hipMemcpyAsync(S->npast, S->h_i, 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
-                enqueue_layers(S, c->x, T, keep_n, false, c->stream)) {
-                snprintf(err, errlen, "layer launch failed"); S->s.keep = 0; return -1;
+            if (begin_forward(S, T, &keep_n, err, errlen)) return fail_sync();
+            if (enqueue_layers(S, S->x, T, keep_n, true, st) || hipEventRecord(c->ev_done[i], st) != hipSuccess) {
+                snprintf(err, errlen, "layer launch failed"); return fail_sync();
             }
+            S->s.n_past += T;
+            if (k0 + T < n) S->s.keep = 0;
         }
-        if (last && nlog > 0) {
-            const int nl = nlog < T ? nlog : T;
-            if (enqueue_head(head, c->x + (int64_t)(T - nl) * E, nl, head->logits, c->stream) ||
-                argmax_finalize_launch(head->amax, head->head_nwg, nl, c->d_argmax, c->d_tok, nullptr, nullptr, c->stream)) {
-                snprintf(err, errlen, "head launch failed"); return -1;
-            }
-            if (chain_sync(c, err, errlen)) return -1;
-            if (logits && hipMemcpy(logits, head->logits, sizeof(float) * nl * head->output.n_rows, hipMemcpyDeviceToHost) != hipSuccess) {
-                snprintf(err, errlen, "logits copy failed"); return -1;
-            }
-            if (hipMemcpy(c->h_buf, c->d_argmax, 4 * nl, hipMemcpyDeviceToHost) != hipSuccess) { snprintf(err, errlen, "argmax copy failed"); return -1; }
-            if (argmax) memcpy(argmax, c->h_buf, 4 * nl);
-            c->last_tok = c->h_buf[nl - 1];
-        } else if (chain_sync(c, err, errlen)) {
-            return -1;
-        }
-        for (auto *S : c->st) { S->s.n_past += T; S->s.keep = 0; }
     }
+    const int T = n - (n - 1) / B * B;   // tokens of the last chunk
+    hipStream_t hs = stream_of(ns - 1);
+    if (nlog > 0) {
+        const int nl = nlog < T ? nlog : T;
+        if (enqueue_head(head, head->x + (int64_t)(T - nl) * E, nl, head->logits, hs) ||
+            argmax_finalize_launch(head->amax, head->head_nwg, nl, c->d_argmax, c->d_tok, nullptr, nullptr, hs)) {
+            snprintf(err, errlen, "head launch failed"); return fail_sync();
+        }
+    }
+    // the last chunk's hidden rows where the decode step and the drivers read
+    // them (the chain's buffer, stage 0's); the head stream is ordered after
+    // every stage's last chunk through the hand-off events
+    if (ns > 1 && hipMemcpyAsync(c->x, head->x, sizeof(float) * (size_t)T * E, hipMemcpyDeviceToDevice, hs) != hipSuccess) {
+        snprintf(err, errlen, "hidden copy failed"); return fail_sync();
+    }
+    for (int i = 0; i < ns; i++) {
+        hipError_t e = hipStreamSynchronize(stream_of(i));
+        if (e == hipSuccess) e = hipGetLastError();
+        if (e != hipSuccess) { snprintf(err, errlen, "GPU error: %s", hipGetErrorString(e)); return fail_sync(); }
+    }
+    if (nlog > 0) {
+        const int nl = nlog < T ? nlog : T;
+        if (logits && hipMemcpy(logits, head->logits, sizeof(float) * nl * head->output.n_rows, hipMemcpyDeviceToHost) != hipSuccess) {
+            snprintf(err, errlen, "logits copy failed"); return -1;
+        }
+        if (hipMemcpy(c->h_buf, c->d_argmax, 4 * nl, hipMemcpyDeviceToHost) != hipSuccess) { snprintf(err, errlen, "argmax copy failed"); return -1; }
+        if (argmax) memcpy(argmax, c->h_buf, 4 * nl);
+        c->last_tok = c->h_buf[nl - 1];
+    }
+    for (auto *S : c->st) S->s.keep = 0;
     return 0;
 }
 
