@@ -21,6 +21,8 @@ Also reported, on the same run:
                 at T = 1..5 activation rows the mixed-quant batch (Q6_K 3584x1024,
                 Q8_0 1024x3584, Q4_K 151936x1024) and the 4B gate|up and down shapes.
   decode_0_8b   the same measurement on the 0.8B-shape model.
+  prefill_1024_two_stages  the 1024-token prefill with the 4B shape split 0-15 | 16-31, the two
+                stages' chunks pipelined on two streams.
   speculative_4b  the 4B shape split 0-15 | 16-31 with the 0.8B model drafting
                 4 tokens per step (5-row verify passes): real drafts, drafts
                 from the plain greedy output, and one in four of them
@@ -91,13 +93,16 @@ def decode_run(cfg, name, n_prompt, steps, warmup, seed):
                 prefill_s=prefill_s)
 
 
-def prefill_only(n_prompt=1024, reps=3, seed=20261107):
+def prefill_only(n_prompt=1024, reps=3, seed=20261107, split=None):
     """The 4B shape's 1024-token prefill (chunks of 64: the matrix-core GEMM and the chunked delta
-    rule), reps times from a reset stage, for a kernel trace of the prefill alone."""
+    rule), reps times from a reset state, for a kernel trace of the prefill alone. split = l: two
+    stages [0, l) | [l, n_layer) whose chunks are pipelined on two streams (the reference's 4B
+    setup splits at 16)."""
     m = xp.Model(model_path(xp.CONFIG_4B, "synth4b"))
     hp = m.hp
-    st = xp.HipStage(m, 0, hp.n_layer, n_prompt + 8, 64, True)
-    ch = xp.Chain([st])
+    cuts = [0, hp.n_layer] if split is None else [0, split, hp.n_layer]
+    sts = [xp.HipStage(m, cuts[i], cuts[i + 1], n_prompt + 8, 64, i + 2 == len(cuts)) for i in range(len(cuts) - 1)]
+    ch = xp.Chain(sts)
     prompt = np.random.default_rng(seed).integers(0, hp.n_vocab, n_prompt).astype(np.int32)
     times, first = [], None
     for _ in range(reps):
@@ -106,8 +111,9 @@ def prefill_only(n_prompt=1024, reps=3, seed=20261107):
         first = int(ch.eval(prompt)[0])
         times.append(time.perf_counter() - t0)
     ch.free()
-    st.destroy()
-    return {"prefill_tokens": n_prompt, "prefill_s": [round(t, 4) for t in times], "first_token": first}
+    for st in sts:
+        st.destroy()
+    return {"prefill_tokens": n_prompt, "stages": len(sts), "prefill_s": [round(t, 4) for t in times], "first_token": first}
 
 
 def cpu_model():
@@ -404,6 +410,7 @@ def main():
         return
     if args.prefill_only:
         print(json.dumps(prefill_only()), flush=True)
+        print(json.dumps(prefill_only(split=16)), flush=True)
         return
     if args.copy_calibration:
         n = args.copy_calibration << 20
@@ -451,6 +458,9 @@ def main():
                                 gemv_tokens(xp.Q6_K, 2560, 9216)]
         extra["gemm_tokens"] = [gemm_tokens(xp.Q4_K, 18432, 2560), gemm_tokens(xp.Q6_K, 2560, 9216),
                                 gemm_tokens(xp.Q4_K, 2560, 4096)]
+        p2 = prefill_only(split=16)
+        extra["prefill_1024_two_stages"] = {"split": "0-15 | 16-31, chunks pipelined on two streams",
+                                            "prefill_s": min(p2["prefill_s"]), "first_token": p2["first_token"]}
         extra["speculative_4b"] = spec_run()
         extra["speculative_4b_mtp"] = spec_mtp_run()
         d = dropin_run()

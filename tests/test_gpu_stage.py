@@ -179,6 +179,38 @@ def test_chain_split_and_vtable_agree(tiny):
     g.destroy()
 
 
+@pytest.mark.parametrize("cuts", [(0, 4, 8), (0, 2, 5, 8)])
+def test_pipelined_chain_prefill_equals_one_stage(tiny, cuts):
+    """A prompt of many chunks through a chain whose stages run on their own
+    streams, chunk k + 1 in stage i while chunk k is in stage i + 1
+    (xj_net.c:561-604): the logits of the last rows, the hidden rows left for
+    the drivers and the tokens decoded after it equal those of one stage
+    computing the same chunks in order, bit for bit."""
+    m, L = tiny, tiny.hp.n_layer
+    assert cuts[-1] == L
+    prompt = prompt_ids(m, 70, 29)            # max_batch 16: chunks 16 x 4 + 6
+    one = xp.HipStage(m, 0, L, 128, 16, True)
+    c1 = xp.Chain([one])
+    am1, lg1 = c1.eval(prompt, nlog=3, want_logits=True)
+    t1 = c1.decode(12)
+    sts = [xp.HipStage(m, cuts[i], cuts[i + 1], 128, 16, i + 2 == len(cuts)) for i in range(len(cuts) - 1)]
+    c2 = xp.Chain(sts)
+    am2, lg2 = c2.eval(prompt, nlog=3, want_logits=True)
+    assert np.array_equal(lg1.view(np.uint32), lg2.view(np.uint32))
+    assert am1.tolist() == am2.tolist()
+    assert c2.decode(12).tolist() == t1.tolist()
+    # again from a reset state: the device positions restart with the host's
+    c2.reset()
+    c1.reset()
+    a1 = c1.eval(prompt[:37])
+    a2 = c2.eval(prompt[:37])
+    assert a1.tolist() == a2.tolist()
+    for c in (c1, c2):
+        c.free()
+    for st in [one] + sts:
+        st.destroy()
+
+
 def test_chain_verify_and_rollback(tiny):
     m, L = tiny, tiny.hp.n_layer
     prompt = prompt_ids(m, 16, 8)
