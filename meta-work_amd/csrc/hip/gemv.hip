@@ -224,6 +224,95 @@ __device__ __forceinline__ void q6k_unit(const RawU &w, int hl, int gb, const ui
     }
 }
 
+// The same units of two rows (same lane position, so the same x-groups):
+// each activation read from LDS serves both rows. Every row's arithmetic is
+// q4k_unit's / q6k_unit's, statement for statement, so a row's result does
+// not depend on whether it was computed alone or in a pair.
+template <int T>
+__device__ __forceinline__ void q4k_unit2(const RawU &w0, const RawU &w1, int p, int g0, const uint8_t *xl, int ldsT,
+                                          const XqOff &o, float (&acc0)[T], float (&acc1)[T]) {
+    const int jm = (2 * p) & 3;
+    const bool hi4 = p >= 2;
+    float ds[2][2], dm[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const RawU &w = i ? w1 : w0;
+        const float d = xjd::f16_to_f32(w.a.x & 0xFFFFu), dmin = xjd::f16_to_f32(w.a.x >> 16);
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const uint32_t A = byte_of(w.a.y, jm + s), B = byte_of(w.a.z, jm + s), C = byte_of(w.a.w, jm + s);
+            const uint32_t sc = hi4 ? ((C & 0xF) | ((A >> 6) << 4)) : (A & 63);
+            const uint32_t mn = hi4 ? ((C >> 4) | ((B >> 6) << 4)) : (B & 63);
+            ds[i][s] = d * (float)sc;
+            dm[i][s] = dmin * (float)mn;
+        }
+    }
+    const uint32_t q0[8] = {w0.b.x, w0.b.y, w0.b.z, w0.b.w, w0.c.x, w0.c.y, w0.c.z, w0.c.w};
+    const uint32_t q1[8] = {w1.b.x, w1.b.y, w1.b.z, w1.b.w, w1.c.x, w1.c.y, w1.c.z, w1.c.w};
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        uint32_t n0[8], n1[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            n0[j] = s ? (q0[j] >> 4) & 0x0F0F0F0Fu : q0[j] & 0x0F0F0F0Fu;
+            n1[j] = s ? (q1[j] >> 4) & 0x0F0F0F0Fu : q1[j] & 0x0F0F0F0Fu;
+        }
+        const int g = g0 + s;
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const uint8_t *xt = xl + t * ldsT;
+            u32x4 pa[2], pb[2], pc[2];
+            planes<8>(xt + g * kDigStride, pa, pb, pc);
+            const float f = ((const float *)(xt + o.f_off))[g];
+            const int2 sxp = ((const int2 *)(xt + o.sx_off))[g];
+            const float SX = (float)(sxp.x + sxp.y);
+            const int S0 = qdot<8>(n0, pa, pb, pc), S1 = qdot<8>(n1, pa, pb, pc);
+            const float part0 = (float)S0 * ds[0][s] - SX * dm[0][s];
+            const float part1 = (float)S1 * ds[1][s] - SX * dm[1][s];
+            acc0[t] = fmaf(part0, f, acc0[t]);
+            acc1[t] = fmaf(part1, f, acc1[t]);
+        }
+    }
+}
+
+template <int T>
+__device__ __forceinline__ void q6k_unit2(const RawU &w0, const RawU &w1, int hl, int gb, const uint8_t *xl, int ldsT,
+                                          const XqOff &o, float (&acc0)[T], float (&acc1)[T]) {
+    const float d0 = xjd::f16_to_f32(w0.f), d1 = xjd::f16_to_f32(w1.f);
+#pragma unroll
+    for (int G = 0; G < 4; G++) {
+        uint32_t q6[2][4];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const RawU &w = i ? w1 : w0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t a0 = w.a[j], a1 = w.b[j], hb = w.c[j];
+                q6[i][j] = G == 0 ? (a0 & 0x0F0F0F0Fu) | ((hb << 4) & 0x30303030u)
+                         : G == 1 ? (a1 & 0x0F0F0F0Fu) | ((hb << 2) & 0x30303030u)
+                         : G == 2 ? ((a0 >> 4) & 0x0F0F0F0Fu) | (hb & 0x30303030u)
+                                  : ((a1 >> 4) & 0x0F0F0F0Fu) | ((hb >> 2) & 0x30303030u);
+            }
+        }
+        const uint32_t sw0 = G < 2 ? w0.e.x : w0.e.y, sw1 = G < 2 ? w1.e.x : w1.e.y;
+        const float dsc0 = d0 * (float)(int8_t)byte_of(sw0, 2 * (G & 1) + hl);
+        const float dsc1 = d1 * (float)(int8_t)byte_of(sw1, 2 * (G & 1) + hl);
+        const int g = gb + G;
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const uint8_t *xt = xl + t * ldsT;
+            u32x4 pa[1], pb[1], pc[1];
+            planes<4>(xt + g * kDigStride + 16 * hl, pa, pb, pc);
+            const float f = ((const float *)(xt + o.f_off))[g];
+            const int sxh = ((const int *)(xt + o.sx_off))[2 * g + hl];
+            const int S0 = qdot<4>(q6[0], pa, pb, pc) - 32 * sxh;
+            const int S1 = qdot<4>(q6[1], pa, pb, pc) - 32 * sxh;
+            acc0[t] = fmaf((float)S0 * dsc0, f, acc0[t]);
+            acc1[t] = fmaf((float)S1 * dsc1, f, acc1[t]);
+        }
+    }
+}
+
 // Q8_0 unit u = block u (32 elements). |q| <= 128 can reach 2^32 over 32
 // elements, so the c plane is added in fp32: ((sum q*a) * 128 + sum q*b) * 128 + sum q*c.
 template <int T, int RPT>
@@ -396,6 +485,53 @@ __device__ __forceinline__ void rows_q6k(const uint8_t *__restrict__ W, int64_t 
             gb += 8 * DB;
             cur = nxt;
         }
+    }
+}
+
+// Two rows of a team in the rolled loop (several tokens): rows rb0 and rb1 at
+// the same lane positions, the next unit of both in flight; `w0`, `w1` hold
+// unit `lane` of each on entry.
+template <int T, int TS>
+__device__ __forceinline__ void rows2_q4k(const uint8_t *__restrict__ W, int64_t rb0, int64_t rb1, int nu, int lane,
+                                          const RawU &w0, const RawU &w1, const uint8_t *xl, int ldsT, const XqOff &o,
+                                          float (&acc0)[T], float (&acc1)[T]) {
+    constexpr int DB = TS / 4;
+    const int p = lane & 3;
+    const uint8_t *b0 = W + (rb0 + (lane >> 2)) * 144, *b1 = W + (rb1 + (lane >> 2)) * 144;
+    RawU c0 = w0, c1 = w1;
+    int g = 8 * (lane >> 2) + 2 * p;
+    for (int u = lane; u < nu; u += TS) {
+        b0 += DB * 144;
+        b1 += DB * 144;
+        const RawU n0 = ld_q4k(b0, p), n1 = ld_q4k(b1, p);
+        q4k_unit2<T>(c0, c1, p, g, xl, ldsT, o, acc0, acc1);
+        g += 8 * DB;
+        c0 = n0;
+        c1 = n1;
+    }
+}
+
+template <int T, int TS>
+__device__ __forceinline__ void rows2_q6k(const uint8_t *__restrict__ W, int64_t nblk, int64_t rb0, int64_t rb1, int nu,
+                                          int lane, const RawU &w0, const RawU &w1, const uint8_t *xl, int ldsT,
+                                          const XqOff &o, float (&acc0)[T], float (&acc1)[T]) {
+    constexpr int DB = TS / 4;
+    const int h = (lane >> 1) & 1, hl = lane & 1;
+    const int64_t b0 = rb0 + (lane >> 2), b1 = rb1 + (lane >> 2);
+    Q6Ptr q0{W + b0 * 128 + 64 * h + 16 * hl, W + nblk * 128 + b0 * 64 + 32 * h + 16 * hl,
+             W + nblk * 192 + b0 * 16 + 8 * h, W + nblk * 208 + b0 * 2};
+    Q6Ptr q1{W + b1 * 128 + 64 * h + 16 * hl, W + nblk * 128 + b1 * 64 + 32 * h + 16 * hl,
+             W + nblk * 192 + b1 * 16 + 8 * h, W + nblk * 208 + b1 * 2};
+    int gb = 8 * (lane >> 2) + 4 * h;
+    RawU c0 = w0, c1 = w1;
+    for (int u = lane; u < nu; u += TS) {
+        q0.ql += DB * 128; q0.qh += DB * 64; q0.sc += DB * 16; q0.dd += DB * 2;
+        q1.ql += DB * 128; q1.qh += DB * 64; q1.sc += DB * 16; q1.dd += DB * 2;
+        const RawU n0 = ld_q6k(q0, 0), n1 = ld_q6k(q1, 0);
+        q6k_unit2<T>(c0, c1, hl, gb, xl, ldsT, o, acc0, acc1);
+        gb += 8 * DB;
+        c0 = n0;
+        c1 = n1;
     }
 }
 
@@ -1047,7 +1183,10 @@ __device__ __forceinline__ void swiglu_h_cu(const GArgs &a, int rg, int ho, int 
 // Single-token launch with one work-group per CU (per-segment ranges of
 // work-groups): work-group g of segment i (g in [wg0, wg0 + nwg)) takes rows
 // (g - wg0) * rpw + team, one per team of TS lanes (blockDim.x / TS >= rpw
-// teams; the others repeat a valid row and store nothing). POST_SWIGLU_H:
+// teams; the others repeat a valid row and store nothing); with T >= 4
+// tokens and TS >= 16, rows (g - wg0) * rpw + 2 team + i, i = 0, 1 (rpw / 2
+// teams, rounded up), each row's lanes and arithmetic as for one token.
+// POST_SWIGLU_H:
 // work-group g takes rows g * rpw + team of the gate (segment 0) in teams
 // [0, rpw) and the same rows of the up (segment 1) in teams [ho, ho + rpw),
 // ho = rpw rounded up to whole wavefronts. The activations (prepared, or
@@ -1060,8 +1199,17 @@ __device__ __forceinline__ void swiglu_h_cu(const GArgs &a, int rg, int ho, int 
 // SwiGLU tail (or its work-group-local form, POST_SWIGLU_H); no argmax
 // partials.
 template <int T, int TS, int MU, bool Q4, bool WF>
-__global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
+__global__ __launch_bounds__(T >= 4 && TS >= 16 ? 512 : 1024, 1) void gemv_cu_kernel(const GArgs a) {
     extern __shared__ u32x4 lds_v[];
+    // rows per team: with four or five tokens and teams of 16+ lanes (few
+    // rows per work-group), each activation digit read from LDS serves two
+    // rows (Q6_K 2560 x 9216, T = 4: 22.8 -> 20.7 us; T = 2, 3 lose with half
+    // the wavefronts: 14.0 -> 15.6, 17.7 -> 18.0 us). 8-lane teams (many rows)
+    // keep one row each: pairing their rows halves their wavefronts (18432 x
+    // 2560 Q4_K, T = 5: 23.7 -> 24.6 us), and pairing them in two groups of
+    // teams that split the tokens keeps the wavefronts but loads every weight
+    // twice (24.8 us)
+    constexpr int R = T >= 4 && TS >= 16 ? 2 : 1;
     // WF: one unit requested right behind the activation copies, the rest
     // from the unit loop one ahead (more in flight before the conversion
     // delays it, more ahead in the loop congests: both measured slower);
@@ -1069,7 +1217,11 @@ __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
     // tokens): a rolled unit loop with the next unit in flight.
     constexpr int NW = WF || MU == 0 ? 1 : MU, PD = NW - 1;
     const int K = a.K, nu = K / 64;
-    const XqOff o = xq_off(K);
+    // prepared inputs need no group sums of x^2 in LDS: each token is staged
+    // without them (v_off here is the LDS bytes per token), so that five
+    // tokens of K = 9216 fit
+    XqOff o = xq_off(K);
+    if (a.pro == PRO_NONE) o.v_off = o.ss_off;
     const int tid = threadIdx.x, team = tid / TS, lane = tid % TS;
     const int rg = blockIdx.x;
     const bool H = a.post.mode == POST_SWIGLU_H;
@@ -1079,23 +1231,30 @@ __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
     const int si = H ? __builtin_amdgcn_readfirstlane((int)(team >= ho)) : seg_of(a, rg);
     const GSeg &sg = a.seg[si];
     const int tr = H && si ? team - ho : team;
-    const int64_t r0 = (int64_t)(rg - sg.wg0) * a.rpw + tr;
-    const bool mine = tr < a.rpw && r0 < sg.n_rows;
-    const int64_t row = mine ? r0 : (int64_t)sg.n_rows - 1;
-    const int64_t rb = row * (K / 256);
+    bool mine[R];
+    int64_t row[R], rb[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const int64_t r0 = (int64_t)(rg - sg.wg0) * a.rpw + tr * R + i;
+        mine[i] = tr * R + i < a.rpw && r0 < sg.n_rows;
+        row[i] = mine[i] ? r0 : (int64_t)sg.n_rows - 1;
+        rb[i] = row[i] * (K / 256);
+    }
     uint8_t *lds = (uint8_t *)lds_v;
     const bool inwg = pro_inwg(a.pro);
     if (inwg) rmsx1_issue<T>(a, o, lds);
     else dma_xq<T>(a, o, lds);
     if (!WF) wait_vm<0>();   // the activations complete before any weight request
     barrier_raw();
-    RawU win[NW];
+    RawU win[R][NW];
     const int u0 = lane < nu ? lane : nu - 1;
 #pragma unroll
-    for (int m = 0; m < NW; m++) win[m] = load_unit<Q4>(sg.type, sg.w, sg.nblk, rb, u0 + m * TS);
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int m = 0; m < NW; m++) win[i][m] = load_unit<Q4>(sg.type, sg.w, sg.nblk, rb[i], u0 + m * TS);
     if (WF) {   // the copies complete, the window's loads stay in flight
         __builtin_amdgcn_sched_barrier(0);
-        wait_vm<(Q4 ? 3 : 5) * NW>();
+        wait_vm<(Q4 ? 3 : 5) * NW * R>();
         barrier_raw();
     }
     if (inwg) {
@@ -1110,22 +1269,33 @@ __global__ __launch_bounds__(1024, 1) void gemv_cu_kernel(const GArgs a) {
     float sc[T];
 #pragma unroll
     for (int t = 0; t < T; t++) sc[t] = a.pro == PRO_RMSU || a.pro == PRO_RMSU_X ? rmsu_scale(a, o, lds, t) : 1.f;
-    EpiIn<T> ein;
-    epi_load<T>(sg, row, ein);
-    float acc[T];
+    EpiIn<T> ein[R];
 #pragma unroll
-    for (int t = 0; t < T; t++) acc[t] = 0.f;
+    for (int i = 0; i < R; i++) epi_load<T>(sg, row[i], ein[i]);
+    float acc[R][T];
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int t = 0; t < T; t++) acc[i][t] = 0.f;
     if (Q4 || sg.type == XJ_Q4_K) {
-        rows_q4k<T, TS, MU, PD>(sg.w, rb, nu, lane, win, lds, o.v_off, o, acc);
+        if constexpr (R == 2) rows2_q4k<T, TS>(sg.w, rb[0], rb[1], nu, lane, win[0][0], win[1][0], lds, o.v_off, o, acc[0], acc[1]);
+        else rows_q4k<T, TS, MU, PD>(sg.w, rb[0], nu, lane, win[0], lds, o.v_off, o, acc[0]);
     } else if constexpr (!Q4) {
-        rows_q6k<T, TS, MU, PD>(sg.w, sg.nblk, rb, nu, lane, win, lds, o.v_off, o, acc);
+        if constexpr (R == 2)
+            rows2_q6k<T, TS>(sg.w, sg.nblk, rb[0], rb[1], nu, lane, win[0][0], win[1][0], lds, o.v_off, o, acc[0], acc[1]);
+        else rows_q6k<T, TS, MU, PD>(sg.w, sg.nblk, rb[0], nu, lane, win[0], lds, o.v_off, o, acc[0]);
     }
 #pragma unroll
-    for (int t = 0; t < T; t++) acc[t] = team_sum<TS>(acc[t]) * sc[t];
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int t = 0; t < T; t++) acc[i][t] = team_sum<TS>(acc[i][t]) * sc[t];
     if (T == 1 && H) {
-        swiglu_h_cu(a, rg, ho, team, lane, acc[0]);
+        swiglu_h_cu(a, rg, ho, team, lane, acc[0][0]);
     } else {
-        if (mine && lane == 0) epi_row<T>(a, sg, row, acc, ein);
+        // lane i of the team stores row i
+#pragma unroll
+        for (int i = 0; i < R; i++)
+            if (mine[i] && lane == i) epi_row<T>(a, sg, row[i], acc[i], ein[i]);
         if (a.post.mode == POST_SWIGLU) tail_swiglu_cu<T>(a, rg, sg);
     }
     if (a.inc_ptr && blockIdx.x == 0 && tid == 0) *a.inc_ptr += a.inc_by;
@@ -1159,7 +1329,8 @@ GemvPlan gemv_plan(int K, int64_t rows) {
 
 int gemv_max_tile(int K) {
     static const int cap = env_or("XJ_GEMV_TILE", kCuMaxT);
-    const int per_t = xq_off(K).v_off;
+    // the per-CU launches of prepared inputs stage ss_off bytes per token
+    const int per_t = xq_off(K).ss_off;
     int t = (int)(g_lds_max / per_t);
     const int c = cap < 1 ? 1 : cap > kTileT ? kTileT : cap;
     return t < 1 ? 0 : t > c ? c : t;
@@ -1242,7 +1413,8 @@ static int cu_threads(const GArgs &a, int need) {
 // Dynamic LDS of a per-CU launch: the T tokens' activations, and for an
 // input built in the work-group the copies of x (one per token) and of w.
 static size_t cu_lds_bytes(const GArgs &a) {
-    const size_t b = (size_t)a.T * xq_off(a.K).v_off;
+    const XqOff o = xq_off(a.K);
+    const size_t b = (size_t)a.T * (a.pro == PRO_NONE ? o.ss_off : o.v_off);   // prepared: staged without ss
     return a.pro == PRO_RMSU_X ? b + (size_t)(a.T + 1) * 4 * a.K : a.pro == PRO_X ? b + (size_t)a.T * 4 * a.K : b;
 }
 
@@ -1259,7 +1431,8 @@ static int cu_teams(int rpw, int ts, bool h) {
 // (POST_SWIGLU_H: shared by both segments), at most one per CU in total.
 template <int TS>
 static int launch_cu_ts(GArgs b, int rpw, int upl, bool q4, bool wf, hipStream_t st) {
-    int wg = 0, teams = rpw;
+    // four or five tokens and teams of 16+ lanes: two rows per team
+    int wg = 0, teams = b.T >= 4 && TS >= 16 ? (rpw + 1) / 2 : rpw;
     if (b.post.mode == POST_SWIGLU_H) {   // gate and up rows of the same indices in each work-group
         wg = (b.seg[0].n_rows + rpw - 1) / rpw;
         for (int i = 0; i < 2; i++) b.seg[i].wg0 = 0, b.seg[i].nwg = wg;
@@ -1391,7 +1564,8 @@ bool gemv_swiglu_h_ok(const GArgs &a) {
 
 int gemv_launch(const GArgs &a, hipStream_t st) {
     if (a.T < 1 || a.T > kTileT || a.nseg < 1 || a.nseg > kMaxSeg || a.K < 32 || a.K % 32 || !a.xq) return -1;
-    if (gemv_lds_bytes(a) > (size_t)g_lds_max) return -1;
+    // (the per-CU launch stages prepared tokens in fewer bytes)
+    if (gemv_lds_bytes(a) > (size_t)g_lds_max && cu_lds_bytes(a) > (size_t)g_lds_max) return -1;
     int64_t total = 0;
     for (int i = 0; i < a.nseg; i++) total += a.seg[i].n_rows;
     const GemvPlan p = gemv_plan(a.K, total);
@@ -1448,6 +1622,7 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
         const int rc = gemv_launch_cu(a, st);
         if (rc <= 0) return rc;
     }
+    if (gemv_lds_bytes(a) > (size_t)g_lds_max) return -1;
     const int n_rg = a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg;
     int grid = a.T == 1 ? (n_rg < g_grid_cap1 ? n_rg : g_grid_cap1) : (n_rg < g_grid_cap ? n_rg : g_grid_cap);
     // a single token with at most two units per lane: one row group per

@@ -103,16 +103,25 @@ def test_gemv_secondary_types(t, rows, k, T):
     assert np.array_equal(xp.dequant(w).view(np.uint32), orc.dequant_rows(t, blob, rows, k).view(np.uint32))
 
 
-@pytest.mark.parametrize("t", [xp.Q4_K, xp.Q6_K, xp.Q8_0])
-def test_gemv_rows_do_not_depend_on_T(t):
-    rows, k = 777, 2560 if t != xp.Q8_0 else 3584
+@pytest.mark.parametrize("t,rows,k,tmax", [
+    (xp.Q4_K, 777, 2560, 5), (xp.Q6_K, 777, 2560, 5), (xp.Q8_0, 777, 3584, 5),
+    (xp.Q4_K, 763, 2560, 5), (xp.Q6_K, 763, 2560, 5),    # 3 rows per work-group: a team with one row
+    (xp.Q4_K, 18432, 2560, 5),                            # gate | up of the 4B shape
+    (xp.Q6_K, 18000, 2560, 5),                            # 8-lane teams of Q6_K rows
+    (xp.Q4_K, 2560, 4096, 5),                             # ssm_out / wo
+    (xp.Q6_K, 2560, 9216, 4),                             # down (its tile: four tokens in LDS)
+    (xp.Q6_K, 3584, 1024, 5),                             # 14 rows per work-group, 64 lanes per row
+])
+def test_gemv_rows_do_not_depend_on_T(t, rows, k, tmax):
+    """Row r of a T-token launch equals the single-token launch bit for bit
+    (speculative verification reproduces greedy decoding), for every T."""
     blob = _weights(t, rows, k, 5)
     xs = xp.fill_normal(5 * k, 6, 1.0).reshape(5, k)
     w = xp.DevWeight(t, blob, rows, k)
-    y5 = xp.gemv(w, xs)
-    for i in range(5):
-        y1 = xp.gemv(w, xs[i:i + 1])
-        assert np.array_equal(y1[0].view(np.uint32), y5[i].view(np.uint32))
+    y1 = np.stack([xp.gemv(w, xs[i:i + 1])[0] for i in range(tmax)])
+    for T in range(2, tmax + 1):
+        yT = xp.gemv(w, xs[:T])
+        assert np.array_equal(yT.view(np.uint32), y1[:T].view(np.uint32)), T
 
 
 def test_gemv_residual_add():

@@ -112,3 +112,27 @@ def test_4b_speculative_with_0_8b_draft(mode):
         o.free()
     for s in (a, b, d):
         s.destroy()
+
+
+def test_4b_verify_pass_equals_single_steps():
+    """At the 4B shape a 4- and a 5-token verification pass (the widths whose
+    GEMVs pair the rows of a team) give, bit for bit, the logits of feeding
+    the same tokens one at a time."""
+    path = xp.cached_model(xp.CONFIG_4B, "synth4b")
+    m = xp.Model(path)
+    L = m.hp.n_layer
+    rng = np.random.default_rng(77)
+    prompt = rng.integers(0, m.hp.n_vocab, 96).astype(np.int32)
+    cand = rng.integers(0, m.hp.n_vocab, 5).astype(np.int32)
+    stages = [xp.HipStage(m, 0, L, 128, 8, True) for _ in range(3)]
+    chains = [xp.Chain([s]) for s in stages]
+    for c in chains:
+        c.eval(prompt)
+    lg1 = np.stack([chains[0].eval(cand[i:i + 1], nlog=1, want_logits=True)[1][0] for i in range(5)])
+    for c, T in ((chains[1], 4), (chains[2], 5)):
+        _, lgT = c.eval(cand[:T], nlog=T, keep=True, want_logits=True)
+        assert np.array_equal(lgT.view(np.uint32), lg1[:T].view(np.uint32)), T
+    for c in chains:
+        c.free()
+    for s in stages:
+        s.destroy()

@@ -233,6 +233,24 @@ def test_chain_verify_and_rollback(tiny):
     g2.destroy()
 
 
+def test_verify_pass_logits_equal_single_steps(tiny):
+    """A 5-token verification pass gives, bit for bit, the logits of feeding
+    the same tokens one at a time (the decode step's kernels)."""
+    m, L = tiny, tiny.hp.n_layer
+    prompt, cand = prompt_ids(m, 16, 8), prompt_ids(m, 5, 9)
+    g1, g2 = xp.HipStage(m, 0, L, 128, 8, True), xp.HipStage(m, 0, L, 128, 8, True)
+    c1, c2 = xp.Chain([g1]), xp.Chain([g2])
+    c1.eval(prompt)
+    c2.eval(prompt)
+    _, lg5 = c1.eval(cand, nlog=5, keep=True, want_logits=True)
+    lg1 = np.stack([c2.eval(cand[i:i + 1], nlog=1, want_logits=True)[1][0] for i in range(5)])
+    assert np.array_equal(lg5.view(np.uint32), lg1.view(np.uint32))
+    for o in (c1, c2):
+        o.free()
+    g1.destroy()
+    g2.destroy()
+
+
 @pytest.mark.parametrize("mode", ["draft", "oracle_all", "oracle_miss"])
 def test_spec_decode_equals_greedy(tiny, tiny_draft_path, mode):
     m, L = tiny, tiny.hp.n_layer
