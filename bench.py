@@ -23,6 +23,8 @@ Also reported, on the same run:
   decode_0_8b   the same measurement on the 0.8B-shape model.
   prefill_1024_two_stages  the 1024-token prefill with the 4B shape split 0-15 | 16-31, the two
                 stages' chunks pipelined on two streams.
+  verify_4b     one pass of T = 1..5 tokens with checkpoints on the 4B shape (the
+                speculative verification widths), ms per pass beside the decode step.
   speculative_4b  the 4B shape split 0-15 | 16-31 with the 0.8B model drafting
                 4 tokens per step (5-row verify passes): real drafts, drafts
                 from the plain greedy output, and one in four of them
@@ -353,6 +355,37 @@ def spec_mtp_run(n_prompt=1024, n_gen=128, seed=20261110):
     return res
 
 
+def verify_widths(widths=(1, 2, 3, 4, 5), n_prompt=1024, reps=30, seed=20261112, pause_s=0.0):
+    """Speculative-verification passes on the 4B shape (one stage): after a 1024-token prompt, T = 1..5
+    tokens fed as one pass with checkpoints, then rolled back to the first of them (the next pass starts
+    one position later); ms per pass, median of `reps`, host round trip included. pause_s: an idle gap
+    before the timed passes (marks them in a kernel trace)."""
+    m = xp.Model(model_path(xp.CONFIG_4B, "synth4b"))
+    st = xp.HipStage(m, 0, m.hp.n_layer, n_prompt + (len(widths) + 1) * reps + 16, 64, True)
+    ch = xp.Chain([st])
+    rng = np.random.default_rng(seed)
+    ch.eval(rng.integers(0, m.hp.n_vocab, n_prompt).astype(np.int32))
+    toks = rng.integers(0, m.hp.n_vocab, 5).astype(np.int32)
+
+    def run(T, n):
+        ts = []
+        for _ in range(n):
+            p0 = ch.n_past
+            t0 = time.perf_counter()
+            ch.eval(toks[:T], nlog=T, keep=True)
+            ts.append(time.perf_counter() - t0)
+            ch.rollback(p0 + 1)
+        return float(np.median(ts)) * 1e3
+
+    run(max(widths), 3)
+    if pause_s:
+        time.sleep(pause_s)
+    out = [{"T": T, "ms": round(run(T, reps), 3)} for T in widths]
+    ch.free()
+    st.destroy()
+    return out
+
+
 def delta_c3(reps=3):
     """Gated DeltaNet prefill on the c3 shape (16 heads, d=128, 2048 tokens from a zero state): the chunk-wise
     MFMA kernels (chunk 64) next to the token-by-token kernel. Wall ms per call include the host copies; the
@@ -394,6 +427,8 @@ def main():
     ap.add_argument("--delta-c3", action="store_true", help="only the chunked vs token-by-token DeltaNet prefill")
     ap.add_argument("--gemm-tokens", action="store_true", help="only the prefill-chunk GEMM vs GEMV-tile legs")
     ap.add_argument("--prefill-only", action="store_true", help="only the 4B 1024-token prefill, three times")
+    ap.add_argument("--verify-only", nargs="?", const="1,2,3,4,5", default=None, metavar="WIDTHS",
+                    help="only the 4B verification passes of the given widths (after a 0.2 s pause)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the token loop on a single MI355X and has no "
@@ -407,6 +442,9 @@ def main():
         return
     if args.delta_c3:
         print(json.dumps(delta_c3()), flush=True)
+        return
+    if args.verify_only:
+        print(json.dumps(verify_widths([int(w) for w in args.verify_only.split(",")], pause_s=0.2)), flush=True)
         return
     if args.prefill_only:
         print(json.dumps(prefill_only()), flush=True)
@@ -461,6 +499,8 @@ def main():
         p2 = prefill_only(split=16)
         extra["prefill_1024_two_stages"] = {"split": "0-15 | 16-31, chunks pipelined on two streams",
                                             "prefill_s": min(p2["prefill_s"]), "first_token": p2["first_token"]}
+        extra["verify_4b"] = {"ms_per_pass": verify_widths(), "decode_ms_per_step": round(ms_step, 4),
+                              "note": "T tokens fed as one pass with checkpoints at position ~1024, then rolled back"}
         extra["speculative_4b"] = spec_run()
         extra["speculative_4b_mtp"] = spec_mtp_run()
         d = dropin_run()

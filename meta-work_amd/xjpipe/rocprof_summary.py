@@ -2,6 +2,7 @@
 
     python -m xjpipe.rocprof_summary trace <dir with *_kernel_stats.csv and *_kernel_trace.csv>
     python -m xjpipe.rocprof_summary traffic <FETCH_SIZE dir> <WRITE_SIZE dir> <copy bytes> [out.json]
+    python -m xjpipe.rocprof_summary passes <dir with *_kernel_trace.csv> <number of passes>
 
 trace    per-kernel statistics, and the decode step broken down by kernel
          (steps delimited by the single-token embedding launch)
@@ -10,6 +11,8 @@ traffic  HBM bytes per single-token GEMV launch from FETCH_SIZE / WRITE_SIZE
          counter read the known size of the calibration copy (the largest
          runtime copy-kernel dispatch of the run); the same per dispatch for
          the attention, DeltaNet and prefill kernels (KERNELS_OF_INTEREST)
+passes   the dispatches after the run's longest idle gap (a pause the
+         program makes before its timed passes), per pass and kernel
 
 Single-token GEMV launches are the gemv_kernel<1, ...> and gemv_cu_kernel
 dispatches (the two launch forms of the same fused dequant-GEMV).
@@ -124,9 +127,29 @@ def traffic(dfetch, dwrite, copy_bytes, out_json=None):
     return doc
 
 
+def passes(d, n):
+    ev = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"])
+                for r in csv.DictReader(open(_one(d, "_kernel_trace.csv"))))
+    gap, i0 = max((ev[i + 1][0] - ev[i][1], i) for i in range(len(ev) - 1))
+    tail = ev[i0 + 1:]
+    acc = collections.defaultdict(lambda: [0, 0])
+    for s, e, k in tail:
+        acc[_short(k)][0] += 1
+        acc[_short(k)][1] += e - s
+    busy = sum(v[1] for v in acc.values())
+    out = [f"Dispatches after the {gap / 1e6:.1f} ms gap: {len(tail)}; per pass: kernel time {busy / n / 1e3:.1f} us, "
+           f"first start to last end {(tail[-1][1] - tail[0][0]) / n / 1e3:.1f} us.", "",
+           "| kernel | launches/pass | us/pass | us/launch |", "|---|---:|---:|---:|"]
+    for k, (c, t) in sorted(acc.items(), key=lambda x: -x[1][1]):
+        out.append(f"| `{k}` | {c / n:.1f} | {t / n / 1e3:.1f} | {t / c / 1e3:.2f} |")
+    return "\n".join(out)
+
+
 if __name__ == "__main__":
     if len(sys.argv) >= 3 and sys.argv[1] == "trace":
         print(trace(sys.argv[2]))
+    elif len(sys.argv) >= 4 and sys.argv[1] == "passes":
+        print(passes(sys.argv[2], int(sys.argv[3])))
     elif len(sys.argv) >= 5 and sys.argv[1] == "traffic":
         print(json.dumps(traffic(sys.argv[2], sys.argv[3], int(sys.argv[4]),
                                  sys.argv[5] if len(sys.argv) > 5 else None), indent=1))
