@@ -69,6 +69,8 @@ def trace(d):
             per[k].append(v)
         busy.append(sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in seg))
         wall.append(int(seg[-1]["End_Timestamp"]) - int(seg[0]["Start_Timestamp"]))
+    if not steps:   # a run without decode steps (prefill only): the kernel table alone
+        return "\n".join(out)
     out += ["", f"Decode steps analysed: {len(steps)}; kernels per step: {len(steps[-1]) if steps else 0}; "
             f"sum of kernel durations per step (median) {statistics.median(busy) / 1e3:.1f} us; "
             f"first start to last end {statistics.median(wall) / 1e3:.1f} us.", "",
