@@ -237,9 +237,10 @@ struct EmbedArgs {
 int embed_launch(const EmbedArgs &a, hipStream_t st);
 // out[t] (optional) = greedy argmax over amax[t][0..n_part); tok_out (optional)
 // receives the last row's id; hist/step (optional, T == 1 only) append it to a
-// device-side history and advance the step counter.
+// device-side history and advance the step counter; embed (optional, T == 1
+// only): the id's row of embed->w into embed->x (embed->tokens unused).
 int argmax_finalize_launch(const unsigned long long *amax, int n_part, int T, int32_t *out, int32_t *tok_out,
-                           int32_t *hist, int32_t *step, hipStream_t st);
+                           int32_t *hist, int32_t *step, hipStream_t st, const EmbedArgs *embed = nullptr);
 // Plain argmax of T rows of n floats (first maximum).
 int argmax_rows_launch(const float *x, int n, int T, int32_t *out, hipStream_t st);
 int norm_launch(int mode, const float *x, const float *w, int n, int rows, float eps, float *out, hipStream_t st);

@@ -21,25 +21,31 @@
 
 namespace xjk {
 
-__global__ __launch_bounds__(256) void embed_kernel(const EmbedArgs a) {
-    const int t = blockIdx.x;
-    const int32_t tok = a.tokens[t];
-    const int64_t K = a.w.k, nch = K / 32;
-    float *x = a.x + (int64_t)t * K;
-    const int64_t nblk = xjd::dev_nblk(a.w.type, a.w.n_rows, K);
+// Row tok of the embedding table into x by the 256 threads of a work-group.
+__device__ __forceinline__ void embed_row(const DevW &w, int32_t tok, float *x) {
+    const int64_t K = w.k, nch = K / 32;
+    const int64_t nblk = xjd::dev_nblk(w.type, w.n_rows, K);
     for (int64_t c = threadIdx.x; c < nch; c += 256) {
-        if (tok < 0 || tok >= a.w.n_rows) {
+        if (tok < 0 || tok >= w.n_rows) {
             for (int l = 0; l < 32; l++) x[c * 32 + l] = 0.f;
         } else {
-            xjd::dequant_chunk(a.w.p, a.w.type, K, nblk, tok, c, x + c * 32);
+            xjd::dequant_chunk(w.p, w.type, K, nblk, tok, c, x + c * 32);
         }
     }
 }
 
+__global__ __launch_bounds__(256) void embed_kernel(const EmbedArgs a) {
+    const int t = blockIdx.x;
+    embed_row(a.w, a.tokens[t], a.x + (int64_t)t * a.w.k);
+}
+
 // One work-group per token row t. out[t] = argmax; tok_out (optional) gets the
-// last row's id; hist/step (optional, T == 1) append it to the history.
+// last row's id; hist/step (optional, T == 1) append it to the history; e.x
+// (optional, T == 1): the id's embedding row into e.x, the next decode step's
+// input (so the step needs no embedding launch of its own).
 __global__ __launch_bounds__(256) void finalize_kernel(const unsigned long long *amax, int n_part, int T,
-                                                       int32_t *out, int32_t *tok_out, int32_t *hist, int32_t *step) {
+                                                       int32_t *out, int32_t *tok_out, int32_t *hist, int32_t *step,
+                                                       const EmbedArgs e) {
     const int t = blockIdx.x, tid = threadIdx.x;
     __shared__ unsigned long long red[256];
     unsigned long long m = 0ull;
@@ -56,8 +62,8 @@ __global__ __launch_bounds__(256) void finalize_kernel(const unsigned long long 
         if (tid < s && red[tid + s] > red[tid]) red[tid] = red[tid + s];
         __syncthreads();
     }
+    const int32_t id = (int32_t)xjd::argmax_key_index(red[0]);   // red[0] is final for every thread
     if (tid == 0) {
-        const int32_t id = (int32_t)xjd::argmax_key_index(red[0]);
         if (out) out[t] = id;
         if (tok_out && t == T - 1) *tok_out = id;
         if (hist && step) {
@@ -65,6 +71,7 @@ __global__ __launch_bounds__(256) void finalize_kernel(const unsigned long long 
             *step += 1;
         }
     }
+    if (e.x) embed_row(e.w, id, e.x);
 }
 
 __global__ __launch_bounds__(256) void argmax_rows_kernel(const float *x, int n, int32_t *out) {
@@ -106,9 +113,11 @@ int embed_launch(const EmbedArgs &a, hipStream_t st) {
 }
 
 int argmax_finalize_launch(const unsigned long long *amax, int n_part, int T, int32_t *out, int32_t *tok_out,
-                           int32_t *hist, int32_t *step, hipStream_t st) {
+                           int32_t *hist, int32_t *step, hipStream_t st, const EmbedArgs *embed) {
     if (hist && T != 1) return -1;
-    hipLaunchKernelGGL(finalize_kernel, dim3(T), dim3(256), 0, st, amax, n_part, T, out, tok_out, hist, step);
+    if (embed && (T != 1 || embed->w.k % 32 || !embed->x)) return -1;
+    const EmbedArgs e = embed ? *embed : EmbedArgs{};
+    hipLaunchKernelGGL(finalize_kernel, dim3(T), dim3(256), 0, st, amax, n_part, T, out, tok_out, hist, step, e);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -1171,13 +1171,22 @@ extern "C" int xjh_chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nl
 // One greedy decode step, entirely on the device: embedding of d_tok, every
 // stage (the last GEMV of each advances its n_past), the head, and the argmax
 // that writes d_tok and appends it to the history.
+// One decode step from the embedding already in c->x: the layers, the head,
+// and the argmax launch, which records the token and writes its embedding
+// into c->x for the next step (embed_first: the set-up's embedding of d_tok).
+static int embed_first(xjh_chain *c) {
+    EmbedArgs ea{c->d_tok, c->st[0]->tok_embd, c->x, 1};
+    return embed_launch(ea, c->stream);
+}
+
 static int enqueue_decode_step(xjh_chain *c) {
     HStage *head = c->st.back();
-    EmbedArgs ea{c->d_tok, c->st[0]->tok_embd, c->x, 1};
-    int rc = embed_launch(ea, c->stream);
+    int rc = 0;
     for (auto *S : c->st) rc = rc ? rc : enqueue_layers(S, c->x, 1, 0, true, c->stream);
     if (!rc) rc = enqueue_head(head, c->x, 1, head->logits, c->stream);
-    if (!rc) rc = argmax_finalize_launch(head->amax, head->head_nwg, 1, nullptr, c->d_tok, c->d_hist, c->d_step, c->stream);
+    const EmbedArgs next{nullptr, c->st[0]->tok_embd, c->x, 1};
+    if (!rc) rc = argmax_finalize_launch(head->amax, head->head_nwg, 1, nullptr, c->d_tok, c->d_hist, c->d_step,
+                                         c->stream, &next);
     return rc;
 }
 
@@ -1210,6 +1219,7 @@ static int decode_enqueue(xjh_chain *c, int tok, int n, bool direct, char *err, 
         snprintf(err, errlen, "decode setup failed"); return -1;
     }
     for (auto *S : c->st) if (set_npast(S, c->stream)) { snprintf(err, errlen, "decode setup failed"); return -1; }
+    if (embed_first(c)) { snprintf(err, errlen, "decode setup failed"); return -1; }
     if (chain_sync(c, err, errlen)) return -1;   // the pinned set-up words are reused below
     (void)hipEventRecord(c->ev0, c->stream);
     for (int i = 0; i < n; i++)
@@ -1316,6 +1326,7 @@ static int draft_run(xjh_chain *d, int t, int kk, int32_t *toks, char *err, size
         snprintf(err, errlen, "draft setup failed"); return -1;
     }
     for (auto *S : d->st) if (set_npast(S, d->stream)) { snprintf(err, errlen, "draft setup failed"); return -1; }
+    if (embed_first(d)) { snprintf(err, errlen, "draft setup failed"); return -1; }
     for (int j = 0; j < kk; j++) {
         if (direct ? enqueue_decode_step(d) != 0 : hipGraphLaunch(d->exec, d->stream) != hipSuccess) {
             snprintf(err, errlen, "draft step launch failed"); return -1;

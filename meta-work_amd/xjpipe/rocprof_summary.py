@@ -5,7 +5,7 @@
     python -m xjpipe.rocprof_summary passes <dir with *_kernel_trace.csv> <number of passes>
 
 trace    per-kernel statistics, and the decode step broken down by kernel
-         (steps delimited by the single-token embedding launch)
+         (steps delimited by the argmax launch that ends each of them)
 traffic  HBM bytes per single-token GEMV launch from FETCH_SIZE / WRITE_SIZE
          (KiB per dispatch), each scaled by the factor that makes the same
          counter read the known size of the calibration copy (the largest
@@ -22,6 +22,7 @@ import csv
 import glob
 import json
 import os
+import re
 import statistics
 import sys
 
@@ -53,10 +54,14 @@ def trace(d):
                    f"{float(r['TotalDurationNs']) / 1e6:.2f} | {float(r['Percentage']):.1f} |")
     rows = list(csv.DictReader(open(_one(d, "_kernel_trace.csv"))))
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
-    starts = [i for i, r in enumerate(rows) if r["Kernel_Name"].startswith("xjk::embed_kernel")
-              and int(r["Grid_Size_X"]) == 256]
-    steps = [rows[a:b] for a, b in zip(starts, starts[1:])
-             if any(r["Kernel_Name"].startswith("xjk::finalize") for r in rows[a:b])][2:]
+    # a decode step ends with its argmax launch (which also embeds the next
+    # token); steps are the spans between consecutive argmax launches that
+    # hold single-token GEMVs only
+    ends = [i for i, r in enumerate(rows) if r["Kernel_Name"].startswith("xjk::finalize")]
+    several = re.compile(r"xjk::(gemv_kernel|gemv_cu_kernel)<[2-9],|xjk::(gemm_mfma|dc_|conv_silu|prep_kernel)")
+    steps = [rows[a + 1:b + 1] for a, b in zip(ends, ends[1:])
+             if any(_gemv1(r["Kernel_Name"]) for r in rows[a + 1:b + 1])
+             and not any(several.match(_norm(r["Kernel_Name"])) for r in rows[a + 1:b + 1])][2:]
     per = collections.defaultdict(list)
     busy, wall = [], []
     for seg in steps:
