@@ -1,8 +1,9 @@
 """Batch-1 greedy decode throughput of the synthetic hybrid 4B-shape model on one MI355X.
 
 One step = one greedy decode token through all 32 layers and the LM head,
-entirely on the device (one HIP graph launch: embedding of the previous
-argmax, 24 DeltaNet + 8 gated-GQA layers, Q6_K LM head, argmax). The prompt
+entirely on the device (one HIP graph launch: 24 DeltaNet + 8 gated-GQA
+layers, Q6_K LM head, argmax, whose launch also writes the chosen token's
+embedding as the next step's input). The prompt
 (1024 uniform random ids) is prefilled first; W warm-up steps are not timed;
 exactly K steps are timed between device synchronisations.
 

@@ -5,8 +5,10 @@
 //                    never returns to the host between tokens.
 //   finalize_kernel  greedy argmax over the LM-head GEMV's per-work-group partial
 //                    keys: the first index of the maximum, the rule of
-//                    xj_spec.c:12-16; also records the token in the history and
-//                    advances the step counter (one work-group per token row).
+//                    xj_spec.c:12-16; also records the token in the history,
+//                    advances the step counter and (decode) writes the token's
+//                    embedding row, the next step's input (one work-group per
+//                    token row).
 //   argmax_rows      plain first-maximum argmax of T rows (test entry point).
 //   norm_kernel      RMSNorm / L2 rows (xj_cpu.c:56-61, :185-193); mode 2 is the
 //                    RMSNorm with the product order of xj_spec.c:19-25.
