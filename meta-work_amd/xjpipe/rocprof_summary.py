@@ -80,10 +80,12 @@ def trace(d):
             f"sum of kernel durations per step (median) {statistics.median(busy) / 1e3:.1f} us; "
             f"first start to last end {statistics.median(wall) / 1e3:.1f} us.", "",
             "| kernel (grid in work-groups) | launches/step | us/step | us/launch |", "|---|---:|---:|---:|"]
-    for k, v in sorted(per.items(), key=lambda kv: -statistics.median(x[0] for x in kv[1])):
-        t = statistics.median(x[0] for x in v) / 1e3
-        n = v[0][1]
-        out.append(f"| `{k}` | {n} | {t:.1f} | {t / n:.2f} |")
+    # means over the analysed steps (a decode call's set-up, e.g. its first
+    # embedding and copies, falls into one step of each call)
+    ns = len(steps)
+    for k, v in sorted(per.items(), key=lambda kv: -sum(x[0] for x in kv[1])):
+        t, n = sum(x[0] for x in v) / ns / 1e3, sum(x[1] for x in v) / ns
+        out.append(f"| `{k}` | {n:.2f} | {t:.1f} | {t / n:.2f} |")
     g1 = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for seg in steps for r in seg
           if _gemv1(r["Kernel_Name"])]
     if g1:
