@@ -772,21 +772,30 @@ __device__ __forceinline__ void epilogue(const GArgs &a, const GSeg &sg, int rg,
             for (int t = 0; t < T; t++) best[t] = xjd::argmax_key(acc[i][t], (uint32_t)r);
     }
     if (sg.amax) {  // uniform per work-group
-        // lanes 0..RPT-1 of each team hold one row's key each: reduce them first
+        // lanes 0..RPT-1 of each team hold one row's key each: reduce them
+        // first, then the teams of each wavefront (lane 0 of each team meets
+        // the same lane of the others), then the four wavefronts' maxima
 #pragma unroll
-        for (int t = 0; t < T; t++)
+        for (int t = 0; t < T; t++) {
 #pragma unroll
             for (int off = 1; off < RPT; off <<= 1) {
                 const unsigned long long q = __shfl_xor(best[t], off, 64);
                 best[t] = q > best[t] ? q : best[t];
             }
-        if (lane == 0)
 #pragma unroll
-            for (int t = 0; t < T; t++) amax_sh[team][t] = best[t];
+            for (int off = TS; off < 64; off <<= 1) {
+                const unsigned long long q = __shfl_xor(best[t], off, 64);
+                best[t] = q > best[t] ? q : best[t];
+            }
+        }
+        if ((tid & 63) == 0)
+#pragma unroll
+            for (int t = 0; t < T; t++) amax_sh[tid >> 6][t] = best[t];
         __syncthreads();
         if (tid < T) {
             unsigned long long m = 0ull;
-            for (int j = 0; j < NT; j++) m = amax_sh[j][tid] > m ? amax_sh[j][tid] : m;
+#pragma unroll
+            for (int j = 0; j < 4; j++) m = amax_sh[j][tid] > m ? amax_sh[j][tid] : m;
             sg.amax[(int64_t)tid * sg.nwg + (rg - sg.wg0)] = m;
         }
         __syncthreads();
