@@ -257,6 +257,13 @@ def gemv_leg(t, rows, k, copies, iters):
             "GBps": round(by / (ms * 1e-3) / 1e9, 1), "frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
 
 
+def gemv_legs():
+    """The LM-head shapes (Q4_K 151936x1024 of the 0.8B model, Q6_K 151936x2560 of the 4B model) and
+    config 1 (Q4_K 4096x1024), single token, cold weights."""
+    return [gemv_leg(xp.Q4_K, 151936, 1024, 8, 64), gemv_leg(xp.Q6_K, 151936, 2560, 3, 24),
+            gemv_leg(xp.Q4_K, 4096, 1024, 256, 512)]
+
+
 def gemv_tokens(t, rows, k, iters=200):
     """One weight shape at T = 1..5 activation rows (the speculative-verify widths), cold weights
     (rotating copies totalling more than 600 MB): us per launch (the per-op entry, activations built
@@ -428,6 +435,7 @@ def main():
     ap.add_argument("--delta-c3", action="store_true", help="only the chunked vs token-by-token DeltaNet prefill")
     ap.add_argument("--gemm-tokens", action="store_true", help="only the prefill-chunk GEMM vs GEMV-tile legs")
     ap.add_argument("--prefill-only", action="store_true", help="only the 4B 1024-token prefill, three times")
+    ap.add_argument("--gemv-legs", action="store_true", help="only the cold-cache single-token GEMV legs (LM heads)")
     ap.add_argument("--verify-only", nargs="?", const="1,2,3,4,5", default=None, metavar="WIDTHS",
                     help="only the 4B verification passes of the given widths (after a 0.2 s pause)")
     args = ap.parse_args()
@@ -459,6 +467,9 @@ def main():
         log(f"calibration: copied {n} bytes device-to-device")
         src.free()
         dst.free()
+    if args.gemv_legs:
+        print(json.dumps(gemv_legs()), flush=True)
+        return
     r = decode_run(xp.CONFIG_4B, "synth4b", 1024, args.steps, args.warmup, seed=20261107)
     tok_s = args.steps / r["wall"]
     ms_step = r["wall"] * 1e3 / args.steps
@@ -488,8 +499,7 @@ def main():
         extra["decode_0_8b"]["prefill_s"] = round(r8["prefill_s"], 4)
         r8["ch"].free()
         r8["st"].destroy()
-        extra["gemv_legs"] = [gemv_leg(xp.Q4_K, 151936, 1024, 8, 64), gemv_leg(xp.Q6_K, 151936, 2560, 3, 24),
-                              gemv_leg(xp.Q4_K, 4096, 1024, 256, 512)]
+        extra["gemv_legs"] = gemv_legs()
         # the mixed-quant batch (T = 1..5: Q6_K 3584x1024, Q8_0 1024x3584, Q4_K 151936x1024) and
         # the 4B shape's gate|up and down
         extra["gemv_tokens"] = [gemv_tokens(xp.Q6_K, 3584, 1024), gemv_tokens(xp.Q8_0, 1024, 3584),

@@ -444,9 +444,13 @@ __device__ __forceinline__ void rows_q4k(const uint8_t *__restrict__ W, int64_t 
             if (lane + m * TS < nu) q4k_unit<T>(r[m], p, g0 + 8 * DB * m, xl, ldsT, o, acc);
         }
     } else {
+        // the next unit of the row is requested during this one; after the
+        // row's last unit that is the same unit again (a cache hit, where the
+        // next row's bytes would come back from HBM long after that row's own
+        // reads)
         int g = g0;
         for (int u = lane; u < nu; u += TS) {
-            blk += DB * 144;
+            blk += u + TS < nu ? DB * 144 : 0;
             const RawU nxt = ld_q4k(blk, p);
             q4k_unit<T>(cur, p, g, xl, ldsT, o, acc);
             g += 8 * DB;
@@ -479,7 +483,8 @@ __device__ __forceinline__ void rows_q6k(const uint8_t *__restrict__ W, int64_t 
     } else {
         int gb = gb0;
         for (int u = lane; u < nu; u += TS) {
-            q.ql += DB * 128; q.qh += DB * 64; q.sc += DB * 16; q.dd += DB * 2;
+            const int st = u + TS < nu ? DB : 0;   // after the row's last unit: the same unit again
+            q.ql += st * 128; q.qh += st * 64; q.sc += st * 16; q.dd += st * 2;
             const RawU nxt = ld_q6k(q, 0);
             q6k_unit<T>(cur, hl, gb, xl, ldsT, o, acc);
             gb += 8 * DB;
@@ -501,8 +506,9 @@ __device__ __forceinline__ void rows2_q4k(const uint8_t *__restrict__ W, int64_t
     RawU c0 = w0, c1 = w1;
     int g = 8 * (lane >> 2) + 2 * p;
     for (int u = lane; u < nu; u += TS) {
-        b0 += DB * 144;
-        b1 += DB * 144;
+        const int st = u + TS < nu ? DB * 144 : 0;   // after the rows' last unit: the same unit again
+        b0 += st;
+        b1 += st;
         const RawU n0 = ld_q4k(b0, p), n1 = ld_q4k(b1, p);
         q4k_unit2<T>(c0, c1, p, g, xl, ldsT, o, acc0, acc1);
         g += 8 * DB;
@@ -525,8 +531,9 @@ __device__ __forceinline__ void rows2_q6k(const uint8_t *__restrict__ W, int64_t
     int gb = 8 * (lane >> 2) + 4 * h;
     RawU c0 = w0, c1 = w1;
     for (int u = lane; u < nu; u += TS) {
-        q0.ql += DB * 128; q0.qh += DB * 64; q0.sc += DB * 16; q0.dd += DB * 2;
-        q1.ql += DB * 128; q1.qh += DB * 64; q1.sc += DB * 16; q1.dd += DB * 2;
+        const int st = u + TS < nu ? DB : 0;   // after the rows' last unit: the same unit again
+        q0.ql += st * 128; q0.qh += st * 64; q0.sc += st * 16; q0.dd += st * 2;
+        q1.ql += st * 128; q1.qh += st * 64; q1.sc += st * 16; q1.dd += st * 2;
         const RawU n0 = ld_q6k(q0, 0), n1 = ld_q6k(q1, 0);
         q6k_unit2<T>(c0, c1, hl, gb, xl, ldsT, o, acc0, acc1);
         gb += 8 * DB;

@@ -3,6 +3,7 @@
     python -m xjpipe.rocprof_summary trace <dir with *_kernel_stats.csv and *_kernel_trace.csv>
     python -m xjpipe.rocprof_summary traffic <FETCH_SIZE dir> <WRITE_SIZE dir> <copy bytes> [out.json]
     python -m xjpipe.rocprof_summary passes <dir with *_kernel_trace.csv> <number of passes>
+    python -m xjpipe.rocprof_summary kernels <FETCH_SIZE dir> <WRITE_SIZE dir> <copy bytes>
 
 trace    per-kernel statistics, and the decode step broken down by kernel
          (steps delimited by the argmax launch that ends each of them)
@@ -11,6 +12,8 @@ traffic  HBM bytes per single-token GEMV launch from FETCH_SIZE / WRITE_SIZE
          counter read the known size of the calibration copy (the largest
          runtime copy-kernel dispatch of the run); the same per dispatch for
          the attention, DeltaNet and prefill kernels (KERNELS_OF_INTEREST)
+kernels  HBM bytes per dispatch of every kernel of the run (by template name),
+         calibrated as for traffic
 passes   the dispatches after the run's longest idle gap (a pause the
          program makes before its timed passes), per pass and kernel
 
@@ -136,6 +139,24 @@ def traffic(dfetch, dwrite, copy_bytes, out_json=None):
     return doc
 
 
+def kernels(dfetch, dwrite, copy_bytes):
+    per = collections.defaultdict(dict)
+    for name, d in (("FETCH_SIZE", dfetch), ("WRITE_SIZE", dwrite)):
+        vals = _counter(d, name)
+        factor = copy_bytes / (max(v for k, v in vals if k.startswith("__amd_rocclr_copyBuffer")) * 1024.0)
+        acc = collections.defaultdict(list)
+        for k, v in vals:
+            if not k.startswith("__amd_rocclr"):
+                acc[_short(k)].append(v * 1024.0 * factor)
+        for k, v in acc.items():
+            per[k]["dispatches"] = len(v)
+            per[k][name] = sum(v) / len(v)
+    out = ["| kernel | dispatches | FETCH MB / dispatch | WRITE MB / dispatch |", "|---|---:|---:|---:|"]
+    for k, v in sorted(per.items(), key=lambda kv: -kv[1].get("FETCH_SIZE", 0)):
+        out.append(f"| `{k}` | {v['dispatches']} | {v.get('FETCH_SIZE', 0) / 1e6:.2f} | {v.get('WRITE_SIZE', 0) / 1e6:.3f} |")
+    return "\n".join(out)
+
+
 def passes(d, n):
     ev = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"])
                 for r in csv.DictReader(open(_one(d, "_kernel_trace.csv"))))
@@ -157,6 +178,8 @@ def passes(d, n):
 if __name__ == "__main__":
     if len(sys.argv) >= 3 and sys.argv[1] == "trace":
         print(trace(sys.argv[2]))
+    elif len(sys.argv) >= 5 and sys.argv[1] == "kernels":
+        print(kernels(sys.argv[2], sys.argv[3], int(sys.argv[4])))
     elif len(sys.argv) >= 4 and sys.argv[1] == "passes":
         print(passes(sys.argv[2], int(sys.argv[3])))
     elif len(sys.argv) >= 5 and sys.argv[1] == "traffic":
