@@ -113,6 +113,7 @@ def test_gemv_secondary_types(t, rows, k, T):
     (xp.Q6_K, 3584, 1024, 5),                             # 14 rows per work-group, 64 lanes per row
     (xp.Q4_K, 7168, 1024, 5),                             # gate | up of the 0.8B shape: 32-lane teams
     (xp.Q6_K, 1024, 3584, 5),                             # down of the 0.8B shape: 16-lane teams
+    (xp.Q4_K, 3, 1024, 5), (xp.Q6_K, 5, 9216, 5),         # one row per work-group: a pair with one row
 ])
 def test_gemv_rows_do_not_depend_on_T(t, rows, k, tmax):
     """Row r of a T-token launch equals the single-token launch bit for bit
