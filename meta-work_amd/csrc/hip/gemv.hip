@@ -1441,18 +1441,31 @@ static int cu_teams(int rpw, int ts, bool h) {
     return h ? (rpw + tpw - 1) / tpw * tpw + rpw : rpw;
 }
 
+// Two rows per team (four or five tokens, teams of 16+ lanes); that kernel is
+// compiled for at most 512 threads per work-group.
+static bool cu_row_pairs(int T, int ts) { return T >= 4 && ts >= 16; }
+
+// Threads of a per-CU work-group of rpw rows at ts lanes per row: its teams,
+// raised for an input converted in the work-group and for the SwiGLU tail,
+// which emits token t from half-wavefront t.
+static int cu_block_threads(const GArgs &a, int rpw, int ts) {
+    const bool h = a.post.mode == POST_SWIGLU_H;
+    const int teams = h ? cu_teams(rpw, ts, true) : cu_row_pairs(a.T, ts) ? (rpw + 1) / 2 : rpw;
+    int threads = cu_threads(a, teams * ts);
+    if (a.post.mode == POST_SWIGLU && threads < (a.T * 32 + 63) / 64 * 64) threads = (a.T * 32 + 63) / 64 * 64;
+    return threads;
+}
+
 // Per-CU launch (gemv_cu_kernel) of a single-token GEMV under its plan
 // (cu_plan): lanes per row TS with at most 5 units per lane, rows per
 // work-group rpw with teams * TS <= 1024, every segment's work-groups counted
 // (POST_SWIGLU_H: shared by both segments), at most one per CU in total.
 template <int TS>
 static int launch_cu_ts(GArgs b, int rpw, int upl, bool q4, bool wf, hipStream_t st) {
-    // four or five tokens and teams of 16+ lanes: two rows per team
-    int wg = 0, teams = b.T >= 4 && TS >= 16 ? (rpw + 1) / 2 : rpw;
+    int wg = 0;
     if (b.post.mode == POST_SWIGLU_H) {   // gate and up rows of the same indices in each work-group
         wg = (b.seg[0].n_rows + rpw - 1) / rpw;
         for (int i = 0; i < 2; i++) b.seg[i].wg0 = 0, b.seg[i].nwg = wg;
-        teams = cu_teams(rpw, TS, true);
     } else {
         for (int i = 0; i < b.nseg; i++) {
             b.seg[i].wg0 = wg;
@@ -1461,9 +1474,8 @@ static int launch_cu_ts(GArgs b, int rpw, int upl, bool q4, bool wf, hipStream_t
         }
     }
     b.rpw = rpw;
-    int threads = cu_threads(b, teams * TS);
-    // the SwiGLU tail emits token t from half-wavefront t
-    if (b.post.mode == POST_SWIGLU && threads < (b.T * 32 + 63) / 64 * 64) threads = (b.T * 32 + 63) / 64 * 64;
+    const int threads = cu_block_threads(b, rpw, TS);
+    if (threads > (cu_row_pairs(b.T, TS) ? 512 : 1024)) return -1;
     size_t lds = cu_lds_bytes(b);
     // more than half of a CU's LDS keeps each work-group on a CU of its own
     if (b.pro != PRO_RMSU_X && g_lds_max > 80 * 1024 && lds < 80 * 1024 + 256) lds = 80 * 1024 + 256;
@@ -1554,6 +1566,9 @@ static bool cu_plan(const GArgs &a, CuPlan &p) {
     for (int ts = 64; ts >= 8; ts /= 2) {
         const int upl = (nu + ts - 1) / ts;
         if (upl > 5 || cu_teams(rpw, ts, H) * ts > 1024 || (a.post.mode == POST_SWIGLU && rpw > 226)) continue;
+        // the row-pair kernel's bound (an input built in the work-group can
+        // ask for K / 8 threads)
+        if (cu_block_threads(a, rpw, ts) > (cu_row_pairs(a.T, ts) ? 512 : 1024)) continue;
         p = CuPlan{rpw, ts, upl, q4, wf};
         return true;
     }
@@ -1578,10 +1593,29 @@ bool gemv_swiglu_h_ok(const GArgs &a) {
     return on && a.post.mode == POST_SWIGLU_H && cu_plan(a, p);
 }
 
+// Tokens [t0, t0 + n) of a launch: their activations, inputs, outputs and
+// argmax partials; the position increment stays with the last tokens.
+static GArgs token_range(const GArgs &a, int t0, int n) {
+    GArgs b = a;
+    b.T = n;
+    b.t0 = a.t0 + t0;
+    b.xq = a.xq + t0 * xq_off(a.K).stride;
+    if (a.x) b.x = a.x + (int64_t)t0 * a.xs;
+    if (a.x2) b.x2 = a.x2 + (int64_t)t0 * a.x2s;
+    if (a.post.mode != POST_NONE && a.post.xq) b.post.xq = a.post.xq + t0 * xq_off(a.seg[0].n_rows).stride;
+    for (int i = 0; i < a.nseg; i++) {
+        b.seg[i].y = a.seg[i].y + (int64_t)t0 * a.seg[i].ys;
+        if (a.seg[i].amax) b.seg[i].amax = a.seg[i].amax + (int64_t)t0 * a.seg[i].nwg;
+    }
+    if (t0 + n < a.T) b.inc_ptr = nullptr;
+    return b;
+}
+
 int gemv_launch(const GArgs &a, hipStream_t st) {
     if (a.T < 1 || a.T > kTileT || a.nseg < 1 || a.nseg > kMaxSeg || a.K < 32 || a.K % 32 || !a.xq) return -1;
-    // (the per-CU launch stages prepared tokens in fewer bytes)
-    if (gemv_lds_bytes(a) > (size_t)g_lds_max && cu_lds_bytes(a) > (size_t)g_lds_max) return -1;
+    // (the per-CU launch stages prepared tokens in fewer bytes; several
+    // tokens are split below when only that launch would fit them)
+    if (a.T == 1 && gemv_lds_bytes(a) > (size_t)g_lds_max && cu_lds_bytes(a) > (size_t)g_lds_max) return -1;
     int64_t total = 0;
     for (int i = 0; i < a.nseg; i++) total += a.seg[i].n_rows;
     const GemvPlan p = gemv_plan(a.K, total);
@@ -1615,22 +1649,8 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
         for (int i = 0; i < a.nseg; i++)
             secondary = secondary || a.seg[i].type == XJ_Q5_K || a.seg[i].type == XJ_F16 || a.seg[i].type == XJ_BF16;
         if (secondary) {   // one launch per token (multi-token kernels carry no Q5_K / F16 / BF16 rows)
-            const int64_t xs = xq_off(a.K).stride;
-            for (int t = 0; t < a.T; t++) {
-                GArgs b = a;
-                b.T = 1;
-                b.t0 = a.t0 + t;
-                b.xq = a.xq + t * xs;
-                if (a.x) b.x = a.x + (int64_t)t * a.xs;
-                if (a.x2) b.x2 = a.x2 + (int64_t)t * a.x2s;
-                if (a.post.mode != POST_NONE) b.post.xq = a.post.xq + t * xq_off(a.seg[0].n_rows).stride;
-                for (int i = 0; i < a.nseg; i++) {
-                    b.seg[i].y = a.seg[i].y + (int64_t)t * a.seg[i].ys;
-                    if (a.seg[i].amax) b.seg[i].amax = a.seg[i].amax + (int64_t)t * a.seg[i].nwg;
-                }
-                if (t + 1 < a.T) b.inc_ptr = nullptr;
-                if (gemv_launch(b, st)) return -1;
-            }
+            for (int t = 0; t < a.T; t++)
+                if (gemv_launch(token_range(a, t, 1), st)) return -1;
             return 0;
         }
     }
@@ -1638,7 +1658,15 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
         const int rc = gemv_launch_cu(a, st);
         if (rc <= 0) return rc;
     }
-    if (gemv_lds_bytes(a) > (size_t)g_lds_max) return -1;
+    if (gemv_lds_bytes(a) > (size_t)g_lds_max) {
+        // the looping kernel stages v_off bytes per token: as many tokens per
+        // launch as fit (a row's result does not depend on the split)
+        const int fit = a.T > 1 ? (int)((size_t)g_lds_max / xq_off(a.K).v_off) : 0;
+        if (fit < 1) return -1;
+        for (int t0 = 0; t0 < a.T; t0 += fit)
+            if (gemv_launch(token_range(a, t0, a.T - t0 < fit ? a.T - t0 : fit), st)) return -1;
+        return 0;
+    }
     const int n_rg = a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg;
     int grid = a.T == 1 ? (n_rg < g_grid_cap1 ? n_rg : g_grid_cap1) : (n_rg < g_grid_cap ? n_rg : g_grid_cap);
     // a single token with at most two units per lane: one row group per

@@ -89,6 +89,9 @@ struct HStage {
     int n_ck = 0;
     size_t conv_n = 0, ssm_n = 0;    // floats per layer
     size_t weight_bytes = 0;
+    // a reset whose clearing failed: the recurrent state is not known to be
+    // zero, so every forward and logits call reports this until a reset succeeds
+    std::string reset_err;
 };
 
 std::string g_name, g_note;
@@ -521,9 +524,17 @@ int set_npast(HStage *S, hipStream_t st) {
     return hipMemcpyAsync(S->npast, S->h_i, 4, hipMemcpyHostToDevice, st) == hipSuccess ? 0 : -1;
 }
 
+// the sticky error of a failed reset, if any
+int reset_check(HStage *S, char *err, size_t errlen) {
+    if (S->reset_err.empty()) return 0;
+    snprintf(err, errlen, "%s", S->reset_err.c_str());
+    return -1;
+}
+
 // forward-call bookkeeping shared by the vtable and the chain (xj_metal.m:426-431)
 int begin_forward(HStage *S, int T, int *keep_n, char *err, size_t errlen) {
     xj_stage *s = &S->s;
+    if (reset_check(S, err, errlen)) { s->keep = 0; return -1; }
     if (T <= 0 || T > s->max_batch) { snprintf(err, errlen, "%d tokens exceed max_batch %d", T, s->max_batch); s->keep = 0; return -1; }
     if (s->n_past + T > s->n_ctx) { snprintf(err, errlen, "context full (%d)", s->n_ctx); s->keep = 0; return -1; }
     if (s->keep && T > 1 && ensure_ck(S, T - 1, err, errlen)) { s->keep = 0; return -1; }
@@ -581,6 +592,7 @@ int hip_logits(xj_stage *s, const float *x, int T, float *logits, char *err, siz
     const int E = s->m->hp.n_embd;
     if (!s->has_head) { snprintf(err, errlen, "this stage has no output head"); return -1; }
     if (T < 1 || T > s->max_batch) { snprintf(err, errlen, "head called with %d tokens", T); return -1; }
+    if (reset_check(S, err, errlen)) return -1;
     memcpy(S->h_x, x, sizeof(float) * T * E);
     if (hipMemcpyAsync(S->x, S->h_x, sizeof(float) * T * E, hipMemcpyHostToDevice, S->st) != hipSuccess ||
         enqueue_head(S, S->x, T, S->logits, S->st)) {
@@ -625,14 +637,22 @@ int hip_rollback(xj_stage *s, int n_past, char *err, size_t errlen) {
     return 0;
 }
 
+// The vtable's reset returns nothing (xj_stage.h): a failure to clear the
+// state is kept and reported by every later forward / logits call until a
+// reset succeeds.
 void hip_reset(xj_stage *s) {
     HStage *S = H(s);
+    hipError_t e = hipSuccess;
     for (auto &L : S->L) {
         if (!L.rec) continue;
-        (void)hipMemsetAsync(L.conv, 0, S->conv_n * 4, S->st);
-        (void)hipMemsetAsync(L.ssm, 0, S->ssm_n * 4, S->st);
+        if (e == hipSuccess) e = hipMemsetAsync(L.conv, 0, S->conv_n * 4, S->st);
+        if (e == hipSuccess) e = hipMemsetAsync(L.ssm, 0, S->ssm_n * 4, S->st);
     }
-    (void)hipStreamSynchronize(S->st);
+    const hipError_t e2 = hipStreamSynchronize(S->st);
+    if (e == hipSuccess) e = e2;
+    if (e == hipSuccess) e = hipGetLastError();
+    if (e != hipSuccess) S->reset_err = std::string("stage reset failed, recurrent state not cleared: ") + hipGetErrorString(e);
+    else S->reset_err.clear();
     s->n_past = 0;
 }
 
@@ -1235,6 +1255,7 @@ extern "C" int xjh_chain_decode(xjh_chain *c, int n_steps, int32_t *out, char *e
     if (c->last_tok < 0) { snprintf(err, errlen, "decode needs a previous eval with logits"); return -1; }
     const xj_hparams &hp = c->st[0]->s.m->hp;
     if (is_end(hp, c->last_tok)) return 0;   // an end token is never fed (xj_spec.c:139)
+    for (auto *S : c->st) if (reset_check(S, err, errlen)) return -1;
     for (auto *S : c->st)
         if (S->s.n_past + n_steps > S->s.n_ctx) { snprintf(err, errlen, "context full (%d)", S->s.n_ctx); return -1; }
     // XJ_DECODE_GRAPH=0 enqueues the same kernels step by step instead of
@@ -1297,8 +1318,10 @@ extern "C" void xjh_chain_reset(xjh_chain *c) {
 
 // one greedy step of the draft fed with token t; returns its argmax
 static int draft_step(xjh_chain *d, int t, int *next, char *err, size_t errlen) {
-    for (auto *S : d->st)
+    for (auto *S : d->st) {
         if (S->s.n_past + 1 > S->s.n_ctx) { snprintf(err, errlen, "context full (%d)", S->s.n_ctx); return -1; }
+        if (reset_check(S, err, errlen)) return -1;
+    }
     const bool direct = env_int("XJ_DECODE_GRAPH", 1) == 0;
     if (!direct && !d->exec && build_decode_graph(d, err, errlen)) return -1;
     if (decode_enqueue(d, t, 1, direct, err, errlen) ||
@@ -1315,8 +1338,10 @@ static int draft_step(xjh_chain *d, int t, int *next, char *err, size_t errlen) 
 // snapshot copies between the replays on the chain's stream, one
 // synchronisation; toks receives the kk argmax tokens.
 static int draft_run(xjh_chain *d, int t, int kk, int32_t *toks, char *err, size_t errlen) {
-    for (auto *S : d->st)
+    for (auto *S : d->st) {
         if (S->s.n_past + kk > S->s.n_ctx) { snprintf(err, errlen, "context full (%d)", S->s.n_ctx); return -1; }
+        if (reset_check(S, err, errlen)) return -1;
+    }
     const bool direct = env_int("XJ_DECODE_GRAPH", 1) == 0;
     if (!direct && !d->exec && build_decode_graph(d, err, errlen)) return -1;
     d->h_buf[0] = 0;

@@ -50,6 +50,8 @@ def _weights(t, rows, k, seed):
     (xp.Q6_K, 517, 9216),
     (xp.Q4_K, 33, 256),
     (xp.F32, 300, 512),
+    (xp.Q8_0, 300, 9216),      # five tokens of K = 9216 need two launches of the looping kernel
+    (xp.F32, 130, 9216),
 ])
 @pytest.mark.parametrize("T", [1, 2, 3, 4, 5])
 def test_gemv_matches_oracle(t, rows, k, T):
@@ -109,7 +111,8 @@ def test_gemv_secondary_types(t, rows, k, T):
     (xp.Q4_K, 18432, 2560, 5),                            # gate | up of the 4B shape
     (xp.Q6_K, 18000, 2560, 5),                            # 8-lane teams of Q6_K rows
     (xp.Q4_K, 2560, 4096, 5),                             # ssm_out / wo
-    (xp.Q6_K, 2560, 9216, 4),                             # down (its tile: four tokens in LDS)
+    (xp.Q6_K, 2560, 9216, 5),                             # down (five tokens staged in one per-CU launch)
+    (xp.Q8_0, 2560, 9216, 5),                             # the looping kernel: five tokens as 4 + 1
     (xp.Q6_K, 3584, 1024, 5),                             # 14 rows per work-group, 64 lanes per row
     (xp.Q4_K, 7168, 1024, 5),                             # gate | up of the 0.8B shape: 32-lane teams
     (xp.Q6_K, 1024, 3584, 5),                             # down of the 0.8B shape: 16-lane teams
