@@ -21,6 +21,8 @@ Also reported, on the same run:
   gemv_*        stand-alone cold-cache GEMV legs (Q4_K / Q6_K LM-head shapes), and
                 at T = 1..5 activation rows the mixed-quant batch (Q6_K 3584x1024,
                 Q8_0 1024x3584, Q4_K 151936x1024) and the 4B gate|up and down shapes.
+  decode_sampled_4b  the same chain decoding with the app's sampler at temperature 0.7 (top-k 40,
+                top-p 0.95; the draw is the decode graph's last launch), 128 steps.
   decode_0_8b   the same measurement on the 0.8B-shape model.
   prefill_1024_two_stages  the 1024-token prefill with the 4B shape split 0-15 | 16-31, the two
                 stages' chunks pipelined on two streams.
@@ -69,10 +71,13 @@ def model_path(cfg, name):
     return xp.cached_model(cfg, name)
 
 
+SAMPLED_STEPS = 128
+
+
 def decode_run(cfg, name, n_prompt, steps, warmup, seed):
     m = xp.Model(model_path(cfg, name))
     hp = m.hp
-    n_ctx = n_prompt + warmup + steps + 8
+    n_ctx = n_prompt + warmup + steps + SAMPLED_STEPS + 8
     t = time.time()
     # prefill chunks of 64 tokens (the GEMM and chunked DeltaNet path); decode is one token
     st = xp.HipStage(m, 0, hp.n_layer, n_ctx, 64, True)
@@ -488,6 +493,16 @@ def main():
                 "bytes_per_launch": round(g_bytes / g_launch), "launches_per_step": g_launch,
                 "us_per_launch": round(g_ms * 1e3 / g_launch, 3), "gemv_share_of_step": round(g_ms / r["gpu_ms"], 3)}
     log(f"GEMV leg: {g_launch} launches/step, {g_bytes / 1e9:.3f} GB/step, {g_ms:.3f} ms -> {achieved:.0f} GB/s")
+    # the app's sampler on the same chain (temperature 0.7, the app's default): the decode graph's last
+    # launch draws the token instead of taking the argmax
+    r["ch"].set_sampler(0.7, np.random.default_rng(20261113).integers(0, 1 << 30, SAMPLED_STEPS).astype(np.uint32))
+    t0 = time.perf_counter()
+    st_toks = r["ch"].decode(SAMPLED_STEPS)
+    s_wall = time.perf_counter() - t0
+    sampled = {"temperature": 0.7, "steps": int(st_toks.size), "tok_s": round(st_toks.size / s_wall, 1),
+               "gpu_ms_per_step": round(r["ch"].last_decode_ms, 4),
+               "distinct_tokens": int(len(set(st_toks.tolist())))}
+    log(f"4B sampled decode: {sampled}")
     r["ch"].free()
     r["st"].destroy()
 
@@ -541,6 +556,7 @@ def main():
                    "global_batch": 1, "prompt": 1024, "parallelism": "single GPU"},
         "gpu_ms_per_step": round(r["gpu_ms"], 4),
         "prefill_1024_s": round(r["prefill_s"], 4),
+        "decode_sampled_4b": sampled,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

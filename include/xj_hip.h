@@ -159,19 +159,37 @@ void       xjh_chain_free(xjh_chain *c);
  * min(nlog, rows) rows of the final chunk are computed: copied to `logits`
  * [nlog][n_vocab] when it is not NULL, and their greedy argmax (first maximum)
  * written to `argmax`. keep != 0 turns this call into a verify (xj_net.c:668):
- * all n tokens in one chunk, recurrent checkpoints kept for rollback. */
+ * all n tokens in one chunk, recurrent checkpoints kept for rollback. The
+ * token the next decode step feeds is the last row's argmax or, with the
+ * sampler on (xjh_chain_set_sampler), its draw (one number consumed). */
 int  xjh_chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int keep,
                     float *logits, int32_t *argmax, char *err, size_t errlen);
-/* Up to n_steps greedy steps entirely on the device. The first input token is
- * the argmax left by the previous eval/decode; out[i] receives the token chosen
- * after step i (so out[0] is the argmax of the first step's logits). One step
- * is one HIP graph launch. Generation stops at the model's end token
+/* Up to n_steps steps entirely on the device. The first input token is the
+ * one left by the previous eval/decode; out[i] receives the token chosen after
+ * step i (so out[0] is the first step's argmax or, with the sampler on, its
+ * draw with the next number). One step is one HIP graph launch. Generation stops at the model's end token
  * (hp.eos / hp.eot, xj_spec.c:29,139): it is the last token written and it is
  * not fed, so the state is that of the tokens before it. Returns the number of
  * tokens written (0 when the previous token already was an end token), or -1. */
 int  xjh_chain_decode(xjh_chain *c, int n_steps, int32_t *out, char *err, size_t errlen);
-/* Greedy token that the next decode step would feed (the last argmax). */
+/* The token that the next decode step would feed (the last argmax or draw). */
 int  xjh_chain_last_token(xjh_chain *c);
+/* The app's sampler on the device-resident path: with temperature > 0 every
+ * token the chain produces - after xjh_chain_eval's last row, at each
+ * xjh_chain_decode step, and the target's tokens in both speculative drivers -
+ * is the draw of the app's top-k 40 / top-p 0.95 sampler from its logits row,
+ * with the next of the n numbers rand30[] (each < 2^30) standing in for its
+ * arc4random_uniform(1 << 30); numbers are consumed in order, one per token
+ * produced, and a call that would need more than are left fails.
+ * temperature <= 0 is greedy decoding (no number consumed, the app's rule).
+ * Drafts stay greedy, as the reference's MTP drafts are. A chain reset keeps
+ * the numbers and the count; this call restarts the count.
+ * Replaces: the app's sample_cb passed to xj_spec_next
+ * (src/xiaoju-pipe/ios/App/XJGlue.c:248-282, core/xj_spec.c:135,185). */
+int  xjh_chain_set_sampler(xjh_chain *c, float temperature, const uint32_t *rand30, int n,
+                           char *err, size_t errlen);
+/* Numbers consumed since the last xjh_chain_set_sampler. */
+int  xjh_chain_sampler_used(xjh_chain *c);
 int  xjh_chain_rollback(xjh_chain *c, int n_past, char *err, size_t errlen);
 void xjh_chain_reset(xjh_chain *c);
 int  xjh_chain_n_past(xjh_chain *c);
@@ -191,7 +209,10 @@ int  xjh_chain_time_gemv(xjh_chain *c, int iters, double *ms_per_step, double *b
  * the accept/rollback rule below is that function's). Each step feeds the
  * pending token t to the draft and lets it propose up to k tokens by greedy
  * T=1 steps, verifies [t, d1..dk] on the target in one batch, accepts the
- * longest prefix the target's argmax agrees with and rolls both models back.
+ * longest prefix the target's token agrees with (its argmax, or with the
+ * target's sampler on its draw, row i with the next number + i, so the output
+ * is that of plain sampled decoding with the same numbers) and rolls both
+ * models back.
  * oracle (optional, n_oracle ids) replaces the drafts, with every
  * (g*7+j) % oracle_miss == 0 draft made wrong, as xj_spec.c:173-177. */
 typedef struct {
@@ -208,7 +229,7 @@ int xjh_spec_generate(xjh_chain *target, xjh_chain *draft, int k, int n_gen,
                       int32_t *out, xjh_spec_stats *stats, char *err, size_t errlen);
 
 /* Speculative decoding with the model's own MTP stage as the drafter, the
- * reference's algorithm with greedy sampling (xj_spec.c:97-209: the MTP stage
+ * reference's algorithm (xj_spec.c:97-209, greedy or the chain's sampler: the MTP stage
  * takes every fed position with the token after it, drafts k <= 4 tokens, the
  * first from the pending positions and each further one from
  * [embedding(previous draft) | shared_head_norm(previous MTP output)]; the
@@ -218,7 +239,8 @@ int xjh_spec_generate(xjh_chain *target, xjh_chain *draft, int k, int n_gen,
  * as x * (sc * w) (the driver's defaults, XJ_MTP_MAIN_POST / XJ_MTP_CHAIN_POST
  * = 0 turn them off as in the reference).
  * Feeds the prompt itself (both models are reset first); out receives the
- * tokens of plain greedy decoding, end tokens handled as in xjh_spec_generate;
+ * tokens of plain greedy decoding (with the target's sampler on: of plain
+ * sampled decoding with the same numbers), end tokens handled as in xjh_spec_generate;
  * returns their count or -1. draft_log (optional) receives the first
  * draft_cap drafted tokens in order, before any oracle replacement. oracle /
  * oracle_miss as for xjh_spec_generate. mtp: xj_hip_stage_new(m, n_layer,

@@ -154,10 +154,14 @@ __device__ __forceinline__ float block_max(float v, float *red) {
 }
 
 // Greedy argmax key: larger key = larger value, ties -> lower index, NaN lowest.
+// Key of element idx for the first maximum of `if (x[i] > x[b]) b = i` from
+// b = 0 (xj_spec.c:12-16): the largest key wins, equal values (-0 == +0
+// included) give the lowest index, NaN never wins - except at index 0, which
+// no later value can replace.
 __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
-    uint32_t b = __float_as_uint(v);
+    const uint32_t b = v == 0.f ? 0u : __float_as_uint(v);
     uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    if (v != v) ord = 0;
+    if (v != v) ord = idx == 0 ? 0xFFFFFFFFu : 0u;
     return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
 }
 __device__ __forceinline__ uint32_t argmax_key_index(unsigned long long k) {

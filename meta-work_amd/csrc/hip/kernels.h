@@ -247,9 +247,23 @@ int norm_launch(int mode, const float *x, const float *w, int n, int rows, float
 // The same over rows r < rows of n elements at x + r * xs, into out + r * os.
 int norm_rows_launch(int mode, const float *x, int64_t xs, const float *w, int n, int rows, float eps, float *out,
                      int64_t os, hipStream_t st);
-// One token per row of lg [T][V]: top-k 40 / top-p 0.95 at temperature temp
-// with rnd[t] / 2^30 as the uniform number (temp <= 0: the first maximum).
-int sample_launch(const float *lg, int V, int T, float temp, const uint32_t *rnd, int32_t *out, hipStream_t st);
+// One token per row t of lg [T][V]: the app's top-k 40 / top-p 0.95 draw at
+// temperature temp (*temp_dev when given) with rnd[base + t] / 2^30 as the
+// uniform number, base = (*rbase if given) + (*step if given); temp <= 0: the
+// first maximum (no number read). out[t] (optional); tok_out (optional) gets
+// the last row's id; hist/step (optional, T == 1) append it to the history
+// and advance the step; embed.x (optional, T == 1): the id's embedding row.
+struct SampleArgs {
+    const float *lg;
+    int32_t V, T;
+    float temp;
+    const float *temp_dev;
+    const uint32_t *rnd;
+    const int32_t *rbase;
+    int32_t *out, *tok_out, *hist, *step;
+    EmbedArgs embed;
+};
+int sample_launch(const SampleArgs &a, hipStream_t st);
 // g = silu(g) * u over n floats.
 int swiglu_launch(float *g, const float *u, int64_t n, hipStream_t st);
 // NeoX RoPE in place of x[t * tok_stride + h * head_stride + i] for T tokens and

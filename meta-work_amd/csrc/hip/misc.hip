@@ -23,11 +23,11 @@
 
 namespace xjk {
 
-// Row tok of the embedding table into x by the 256 threads of a work-group.
-__device__ __forceinline__ void embed_row(const DevW &w, int32_t tok, float *x) {
+// Row tok of the embedding table into x by the first nthreads threads of a work-group.
+__device__ __forceinline__ void embed_row(const DevW &w, int32_t tok, float *x, int nthreads = 256) {
     const int64_t K = w.k, nch = K / 32;
     const int64_t nblk = xjd::dev_nblk(w.type, w.n_rows, K);
-    for (int64_t c = threadIdx.x; c < nch; c += 256) {
+    for (int64_t c = threadIdx.x; c < nch; c += nthreads) {
         if (tok < 0 || tok >= w.n_rows) {
             for (int l = 0; l < 32; l++) x[c * 32 + l] = 0.f;
         } else {
@@ -140,129 +140,361 @@ int swiglu_launch(float *g, const float *u, int64_t n, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// Row t of lg: radix-select the 40th largest value (ordered 32-bit keys, 8 bits
-// per pass, LDS histograms), take every value above it and the lowest indices
-// of those equal to it, then one thread sorts the 40 by value (equal values in
-// index order) - the app's result whenever the kept values are distinct (its
-// replace-the-minimum loop and exchange sort keep and order equal values by
-// slot, not index; a value tied at the 40th place is never drawn, the 0.95 cut
-// always ending before the last kept value) - forms
-// p_i = exp((v_i - v_0) / temp) in double, cuts where the running share first
-// reaches 0.95 and picks with r = rnd[t] / 2^30 times the kept mass.
+// ---------------------------------------------------------------- sampler --
+// The app's sampler (ios/App/XJGlue.c:251-282), one work-group of 1024
+// threads per row, the uniform number passed in. Its loop keeps 40 slots:
+// the first 40 values fill them, a later value v enters when v > val[mi] and
+// takes slot mi, mi being the first slot holding the minimum (a strict `<`
+// scan from slot 0); then an exchange sort orders the slots by value,
+// p_i = exp((v_i - v_0) / temp) in double, the kept prefix ends where the
+// running share first reaches 0.95, and r = rand30 / 2^30 times the kept mass
+// picks. The slots always hold the 40 largest values seen so far, so when the
+// kept values are distinct and no other element equals the smallest of them
+// (and no NaN occurs) the result is the 40 largest values in descending order
+// whatever the slot history: the fast path selects them (a histogram of the
+// top 11 key bits, the candidates at or above the 40th one's bin compacted in
+// LDS, a radix select of the rest of its key). Otherwise the slot history
+// decides the order of equal values and which of them are kept: one wavefront
+// replays the app's loop over the row in index order (tiles staged in LDS,
+// only values above the tile's starting minimum examined) and one thread runs
+// the exchange sort as written.
 constexpr int kTopK = 40;
+constexpr int kSmpThreads = 1024;
+constexpr int kSmpWaves = kSmpThreads / 64;
+constexpr int kSmpBins = 2048;   // key bits 31..21
+constexpr int kSmpCap = 4096;    // candidates held in LDS (fast path); tile of the replay
+static_assert(kSmpCap == 4 * kSmpThreads, "a replay tile is four elements per thread");
+
+// ordered key: larger value, larger key (NaN lowest)
 __device__ __forceinline__ uint32_t okey(float v) {
     const uint32_t b = __float_as_uint(v);
     return v != v ? 0u : (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-__global__ __launch_bounds__(256) void sample_kernel(const float *lg, int V, float temp, const uint32_t *rnd, int32_t *out) {
-    const int t = blockIdx.x, tid = threadIdx.x;
-    const float *x = lg + (int64_t)t * V;
-    __shared__ unsigned long long best_sh[4];
-    if (!(temp > 0.f)) {   // the greedy token: first maximum
-        unsigned long long b = 0ull;
-        for (int i = tid; i < V; i += 256) {
-            const unsigned long long k = xjd::argmax_key(x[i], (uint32_t)i);
-            b = k > b ? k : b;
-        }
-        for (int off = 32; off > 0; off >>= 1) {
-            const unsigned long long q = __shfl_xor(b, off, 64);
-            b = q > b ? q : b;
-        }
-        if ((tid & 63) == 0) best_sh[tid >> 6] = b;
-        __syncthreads();
-        if (tid == 0) {
-            unsigned long long m = best_sh[0];
-            for (int w = 1; w < 4; w++) m = best_sh[w] > m ? best_sh[w] : m;
-            out[t] = (int32_t)xjd::argmax_key_index(m);
-        }
-        return;
+struct SampleShared {
+    uint32_t hist[kSmpBins];
+    float cv[kSmpCap];
+    int32_t ci[kSmpCap];
+    unsigned long long gmask[kSmpCap / 64];
+    unsigned long long red[kSmpWaves];
+    uint32_t wsum[kSmpWaves];
+    float kv[kTopK];      // the kept values and indices, in the app's final order
+    int32_t kix[kTopK];
+    int n_kept, ncand, fast, bstar, above, tie;
+    uint32_t pre, rand30;
+    float thr;
+};
+
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long q = __shfl_xor(v, off, 64);
+        v = q > v ? q : v;
     }
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t pre_sh;
-    __shared__ int need_sh, ngt_sh;
-    __shared__ int cnt_eq[256];
-    __shared__ float cv[kTopK];
-    __shared__ int ci[kTopK];
-    const int K = V < kTopK ? V : kTopK;
-    uint32_t pre = 0, mask = 0;
-    int need = K;   // how many of the elements matching the prefix are still to be taken from the top
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        hist[tid] = 0;
-        __syncthreads();
-        for (int i = tid; i < V; i += 256) {
-            const uint32_t k = okey(x[i]);
-            if ((k & mask) == pre) atomicAdd(&hist[(k >> shift) & 255u], 1u);
-        }
-        __syncthreads();
-        if (tid == 0) {
-            int cum = 0, b = 255;
-            for (; b > 0; b--) {
-                if (cum + (int)hist[b] >= need) break;
-                cum += hist[b];
-            }
-            pre_sh = pre | ((uint32_t)b << shift);
-            need_sh = need - cum;
-        }
-        __syncthreads();
-        pre = pre_sh;
-        need = need_sh;
-        mask |= 0xFFu << shift;
-        __syncthreads();
+    return v;
+}
+__device__ __forceinline__ unsigned long long wave_min_u64(unsigned long long v) {
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long q = __shfl_xor(v, off, 64);
+        v = q < v ? q : v;
     }
-    // pre = the K-th largest key; take every key above it and the `need` lowest
-    // indices equal to it. Thread tid scans the contiguous chunk [i0, i1).
-    const int chunk = (V + 255) / 256, i0 = tid * chunk, i1 = i0 + chunk < V ? i0 + chunk : V;
-    int my_eq = 0;
-    for (int i = i0; i < i1; i++) my_eq += okey(x[i]) == pre;
-    cnt_eq[tid] = my_eq;
-    if (tid == 0) ngt_sh = 0;
-    __syncthreads();
-    int before = 0;
-    for (int j = 0; j < tid; j++) before += cnt_eq[j];
-    const int n_gt = K - need;
-    for (int i = i0; i < i1; i++) {
-        const uint32_t k = okey(x[i]);
-        if (k > pre) {
-            const int slot = atomicAdd(&ngt_sh, 1);
-            cv[slot] = x[i];
-            ci[slot] = i;
-        } else if (k == pre) {
-            if (before < need) {
-                cv[n_gt + before] = x[i];
-                ci[n_gt + before] = i;
-            }
-            before++;
-        }
+    return v;
+}
+// inclusive prefix sum over the lanes of a wavefront
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t v, int lane) {
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t q = __shfl_up(v, off, 64);
+        if (lane >= off) v += q;
     }
-    __syncthreads();
-    if (tid == 0) {
-        // descending by value, ties by index
-        for (int i = 1; i < K; i++) {
-            const float v = cv[i];
-            const int id = ci[i];
-            int j = i - 1;
-            while (j >= 0 && (cv[j] < v || (cv[j] == v && ci[j] > id))) { cv[j + 1] = cv[j]; ci[j + 1] = ci[j]; j--; }
-            cv[j + 1] = v;
-            ci[j + 1] = id;
-        }
-        double p[kTopK], sum = 0;
-        for (int i = 0; i < K; i++) { p[i] = exp((double)((cv[i] - cv[0]) / temp)); sum += p[i]; }
-        double acc = 0;
-        int cut = K;
-        for (int i = 0; i < K; i++) { acc += p[i] / sum; if (acc >= 0.95) { cut = i + 1; break; } }
-        double s2 = 0;
-        for (int i = 0; i < cut; i++) s2 += p[i];
-        double r = (double)rnd[t] / (double)(1u << 30) * s2;
-        int pick = ci[0];
-        for (int i = 0; i < cut; i++) { r -= p[i]; if (r <= 0) { pick = ci[i]; break; } }
-        out[t] = pick;
-    }
+    return v;
 }
 
-int sample_launch(const float *lg, int V, int T, float temp, const uint32_t *rnd, int32_t *out, hipStream_t st) {
-    if (V < 1 || T < 1) return -1;
-    hipLaunchKernelGGL(sample_kernel, dim3(T), dim3(256), 0, st, lg, V, temp, rnd, out);
+// The app's mi after a slot changed: the first slot holding the minimum by
+// `val[j] < val[mi]` from slot 0 - NaN slots are never below anything, and
+// nothing is below a NaN in slot 0 (mi stays 0); -0 and +0 are equal.
+// Lane j < k of wavefront 0 holds slot j's value sv.
+__device__ __forceinline__ int app_min_slot(float sv, int lane, int k, float sv0) {
+    const float c = sv == 0.f ? 0.f : sv;
+    const unsigned long long key =
+        lane < k && sv == sv ? ((unsigned long long)okey(c) << 32) | (unsigned long long)lane : ~0ull;
+    const unsigned long long m = wave_min_u64(key);
+    return sv0 != sv0 || m == ~0ull ? 0 : (int)(m & 0xFFFFFFFFull);
+}
+
+__device__ __forceinline__ double readlane_d(double v, int i) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)b, i), hi = __builtin_amdgcn_readlane((uint32_t)(b >> 32), i);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// The pick from the k kept slots in their final order (XJGlue.c:272-281, in
+// double, every sum in the app's order), by wavefront 0: lane i forms p_i and
+// p_i / sum, the running sums walk the lanes in order.
+__device__ int app_pick(const float *kv, const int32_t *kix, int k, float temp, uint32_t rand30, int lane) {
+    const float v0 = kv[0];
+    const double p = lane < k ? exp((double)((kv[lane] - v0) / temp)) : 0.0;
+    double sum = 0;
+    for (int i = 0; i < k; i++) sum += readlane_d(p, i);
+    const double q = p / sum;
+    double acc = 0;
+    int cut = k;
+    for (int i = 0; i < k; i++) {
+        acc += readlane_d(q, i);
+        if (acc >= 0.95) { cut = i + 1; break; }
+    }
+    double s2 = 0;
+    for (int i = 0; i < cut; i++) s2 += readlane_d(p, i);
+    double r = (double)rand30 / (double)(1u << 30) * s2;
+    for (int i = 0; i < cut; i++) {
+        r -= readlane_d(p, i);
+        if (r <= 0) return kix[i];
+    }
+    return kix[0];
+}
+
+// One row: the greedy token (temp <= 0) or the app's draw, returned to every
+// thread; rand30 matters on thread 0 only.
+__device__ int sample_row(const float *__restrict__ x, int V, float temp, uint32_t rand30, SampleShared &sh) {
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int K = kTopK;
+    const bool sampling = !(temp <= 0.f);
+    if (sampling)
+        for (int i = tid; i < kSmpBins; i += kSmpThreads) sh.hist[i] = 0;
+    if (tid == 0) { sh.ncand = 0; sh.n_kept = 0; sh.tie = 0; sh.fast = 0; sh.rand30 = rand30; }
+    __syncthreads();
+    // pass 1: the first maximum, NaN, the histogram of the top 11 key bits
+    unsigned long long best = 0ull;
+    int nan = 0;
+    for (int i0 = tid; i0 < V; i0 += 4 * kSmpThreads) {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = i0 + j * kSmpThreads < V ? x[i0 + j * kSmpThreads] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = i0 + j * kSmpThreads;
+            if (i < V) {
+                const unsigned long long kk = xjd::argmax_key(v[j], (uint32_t)i);
+                best = kk > best ? kk : best;
+                if (v[j] != v[j]) nan = 1;
+                else if (sampling) atomicAdd(&sh.hist[okey(v[j]) >> 21], 1u);
+            }
+        }
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) sh.red[wid] = best;
+    nan = __syncthreads_or(nan);
+    if (!sampling) {
+        unsigned long long m = sh.red[0];
+        for (int w = 1; w < kSmpWaves; w++) m = sh.red[w] > m ? sh.red[w] : m;
+        return (int)xjd::argmax_key_index(m);
+    }
+    // the bin of the 40th largest key: thread t holds bins 2047-2t and 2046-2t
+    {
+        const uint32_t h0 = sh.hist[kSmpBins - 1 - 2 * tid], h1 = sh.hist[kSmpBins - 2 - 2 * tid];
+        const uint32_t incl = wave_incl_sum(h0 + h1, lane);
+        if (lane == 63) sh.wsum[wid] = incl;
+        __syncthreads();
+        uint32_t before = 0;
+        for (int w = 0; w < wid; w++) before += sh.wsum[w];
+        const uint32_t hi = before + incl, lo = hi - h0 - h1;   // elements in the bins above this thread's / through them
+        if (!nan && V >= K && lo < (uint32_t)K && hi >= (uint32_t)K) {
+            const bool first = lo + h0 >= (uint32_t)K;
+            sh.bstar = kSmpBins - 1 - 2 * tid - (first ? 0 : 1);
+            sh.above = first ? (int)lo : (int)(lo + h0);
+            sh.fast = (first ? lo + h0 : hi) <= (uint32_t)kSmpCap;
+        }
+    }
+    __syncthreads();
+    bool kept = false;   // the fast path settled the kept values and their order
+    if (sh.fast) {
+        // pass 2: every element in bin bstar or above, compacted (any order)
+        const uint32_t bstar = (uint32_t)sh.bstar;
+        for (int i0 = tid; i0 < V; i0 += 4 * kSmpThreads) {
+            float v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = i0 + j * kSmpThreads < V ? x[i0 + j * kSmpThreads] : 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const bool c = i0 + j * kSmpThreads < V && (okey(v[j]) >> 21) >= bstar;
+                const unsigned long long m = __ballot(c);
+                if (!m) continue;
+                int base = 0;
+                if (lane == 0) base = atomicAdd(&sh.ncand, __popcll(m));
+                base = __shfl(base, 0, 64);
+                if (c) {
+                    const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
+                    sh.cv[pos] = v[j];
+                    sh.ci[pos] = i0 + j * kSmpThreads;
+                }
+            }
+        }
+        __syncthreads();
+        // the rest of the 40th key: three 7-bit radix passes over the candidates
+        // of bin bstar; eq = how many carry exactly that key
+        const int C = sh.ncand;
+        uint32_t pre = bstar << 21, mask = 0xFFE00000u;
+        int need = K - sh.above, eq = 0;
+        for (int shift = 14; shift >= 0; shift -= 7) {
+            if (tid < 128) sh.hist[tid] = 0;
+            __syncthreads();
+            for (int j = tid; j < C; j += kSmpThreads) {
+                const uint32_t kk = okey(sh.cv[j]);
+                if ((kk & mask) == pre) atomicAdd(&sh.hist[(kk >> shift) & 127u], 1u);
+            }
+            __syncthreads();
+            if (wid == 0) {   // bins 127-2l and 126-2l on lane l, counted from the top
+                const uint32_t h0 = sh.hist[127 - 2 * lane], h1 = sh.hist[126 - 2 * lane];
+                const uint32_t hi = wave_incl_sum(h0 + h1, lane), lo = hi - h0 - h1;
+                if (lo < (uint32_t)need && hi >= (uint32_t)need) {
+                    const bool first = lo + h0 >= (uint32_t)need;
+                    sh.pre = pre | ((127u - 2 * lane - (first ? 0 : 1)) << shift);
+                    sh.above = need - (int)(first ? lo : lo + h0);   // still needed from that bin
+                    sh.bstar = (int)(first ? h0 : h1);               // elements in that bin
+                }
+            }
+            __syncthreads();
+            pre = sh.pre;
+            need = sh.above;
+            eq = sh.bstar;
+            mask |= 127u << shift;
+            __syncthreads();
+        }
+        // pre = the 40th largest key; a tie there, or a zero (whose sign the key
+        // tells apart and the app's comparisons do not), needs the replay
+        const float v40 = __uint_as_float((pre & 0x80000000u) ? (pre & 0x7FFFFFFFu) : ~pre);
+        if (eq == need && v40 != 0.f) {
+            for (int j = tid; j < C; j += kSmpThreads)
+                if (okey(sh.cv[j]) >= pre) {
+                    const int pos = atomicAdd(&sh.n_kept, 1);
+                    if (pos < K) { sh.kv[pos] = sh.cv[j]; sh.kix[pos] = sh.ci[j]; }
+                }
+            __syncthreads();
+            if (wid == 0) {
+                // the 40 in descending order (bitonic over the wavefront); equal
+                // neighbours are a tie among the kept values
+                const bool in = lane < K && lane < sh.n_kept;
+                unsigned long long key = in ? ((unsigned long long)okey(sh.kv[lane]) << 32) | (uint32_t)sh.kix[lane] : 0ull;
+                for (int kk = 2; kk <= 64; kk <<= 1)
+                    for (int j = kk >> 1; j > 0; j >>= 1) {
+                        const unsigned long long q = __shfl_xor(key, j, 64);
+                        const bool desc = (lane & kk) == 0, low = (lane & j) == 0;
+                        key = (low == desc) ? (q > key ? q : key) : (q < key ? q : key);
+                    }
+                const uint32_t ok = (uint32_t)(key >> 32);
+                const float v = __uint_as_float((ok & 0x80000000u) ? (ok & 0x7FFFFFFFu) : ~ok);
+                const float prev = __shfl_up(v, 1, 64);
+                if (__ballot(lane > 0 && lane < K && v == prev)) {
+                    if (lane == 0) sh.tie = 1;
+                } else if (lane < K) {
+                    sh.kv[lane] = v;
+                    sh.kix[lane] = (int32_t)(key & 0xFFFFFFFFull);
+                }
+            }
+            __syncthreads();
+            kept = sh.n_kept == K && !sh.tie;
+        }
+    }
+    int k = K;
+    if (!kept) {
+        // the app's loop replayed in index order by wavefront 0 (lane j < kf
+        // holds slot j), the row staged in LDS a tile at a time
+        const int kf = V < K ? V : K;
+        k = kf;
+        float sv = 0.f, thr = 0.f;
+        int si = 0, mi = 0;
+        if (wid == 0) {
+            if (lane < kf) { sv = x[lane]; si = lane; }
+            const float sv0 = __shfl(sv, 0, 64);
+            mi = app_min_slot(sv, lane, kf, sv0);
+            thr = __shfl(sv, mi, 64);
+            if (lane == 0) sh.thr = thr;
+        }
+        __syncthreads();
+        // once slot 0 holds NaN nothing can enter (v > NaN is false)
+        const bool stop = sh.thr != sh.thr;
+        for (int t0 = kf; t0 < V && !stop; t0 += kSmpCap) {
+            const int n = V - t0 < kSmpCap ? V - t0 : kSmpCap;
+            const float thr0 = sh.thr;   // the minimum at the tile's start bounds every entry below
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int e = r * kSmpThreads + tid;
+                const float v = e < n ? x[t0 + e] : __builtin_nanf("");
+                sh.cv[e] = v;
+                const unsigned long long m = __ballot(v > thr0);
+                if (lane == 0) sh.gmask[r * kSmpWaves + wid] = m;
+            }
+            __syncthreads();
+            if (wid == 0) {
+                for (int g = 0; g * 64 < n; g++) {
+                    if (!sh.gmask[g]) continue;
+                    const float v = sh.cv[g * 64 + lane];
+                    unsigned long long m = __ballot(v > thr);
+                    while (m) {
+                        const int l = __ffsll((long long)m) - 1;
+                        const float nv = __shfl(v, l, 64);
+                        if (lane == mi) { sv = nv; si = t0 + g * 64 + l; }
+                        const float sv0 = __shfl(sv, 0, 64);
+                        mi = app_min_slot(sv, lane, kf, sv0);
+                        thr = __shfl(sv, mi, 64);
+                        m = l == 63 ? 0ull : __ballot(v > thr) & (~0ull << (l + 1));
+                    }
+                }
+                if (lane == 0) sh.thr = thr;
+            }
+            __syncthreads();
+        }
+        if (wid == 0 && lane < kf) { sh.kv[lane] = sv; sh.kix[lane] = si; }
+        __syncthreads();
+        if (tid == 0) {   // the exchange sort as written (XJGlue.c:271)
+            float v[kTopK];
+            int32_t id[kTopK];
+#pragma unroll
+            for (int i = 0; i < kTopK; i++) { v[i] = i < kf ? sh.kv[i] : 0.f; id[i] = i < kf ? sh.kix[i] : 0; }
+#pragma unroll
+            for (int i = 0; i < kTopK; i++)
+#pragma unroll
+                for (int j = i + 1; j < kTopK; j++)
+                    if (j < kf && v[j] > v[i]) {
+                        const float tv = v[i]; v[i] = v[j]; v[j] = tv;
+                        const int32_t ti = id[i]; id[i] = id[j]; id[j] = ti;
+                    }
+#pragma unroll
+            for (int i = 0; i < kTopK; i++)
+                if (i < kf) { sh.kv[i] = v[i]; sh.kix[i] = id[i]; }
+        }
+        __syncthreads();
+    }
+    if (wid == 0) {
+        const int pick = app_pick(sh.kv, sh.kix, k, temp, sh.rand30, lane);
+        if (lane == 0) sh.ncand = pick;
+    }
+    __syncthreads();
+    return sh.ncand;
+}
+
+__global__ __launch_bounds__(kSmpThreads) void sample_kernel(const SampleArgs a) {
+    __shared__ SampleShared sh;
+    const int t = blockIdx.x;
+    const float temp = a.temp_dev ? *a.temp_dev : a.temp;
+    uint32_t r30 = 0;
+    if (threadIdx.x == 0 && !(temp <= 0.f)) r30 = a.rnd[(a.rbase ? *a.rbase : 0) + (a.step ? *a.step : 0) + t];
+    const int id = sample_row(a.lg + (int64_t)t * a.V, a.V, temp, r30, sh);
+    if (threadIdx.x == 0) {
+        if (a.out) a.out[t] = id;
+        if (a.tok_out && t == a.T - 1) *a.tok_out = id;
+        if (a.hist && a.step) {
+            a.hist[*a.step] = id;
+            *a.step += 1;
+        }
+    }
+    if (a.embed.x) embed_row(a.embed.w, id, a.embed.x, kSmpThreads);
+}
+
+int sample_launch(const SampleArgs &a, hipStream_t st) {
+    if (a.V < 1 || a.T < 1) return -1;
+    if ((a.hist || a.embed.x) && a.T != 1) return -1;
+    if (a.embed.x && a.embed.w.k % 32) return -1;
+    if (a.hist && !a.step) return -1;
+    hipLaunchKernelGGL(sample_kernel, dim3(a.T), dim3(kSmpThreads), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

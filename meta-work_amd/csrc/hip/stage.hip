@@ -1015,6 +1015,15 @@ struct xjh_chain {
     int32_t *d_prompt = nullptr;
     int prompt_cap = 0;
     std::vector<hipEvent_t> ev_done, ev_taken;
+    // the app's sampler (xjh_chain_set_sampler): temperature, the uniform
+    // numbers on the device, how many are drawn; the sampled decode graph
+    float temp = 0.f;
+    uint32_t *d_rnd = nullptr;
+    int n_rnd = 0, rnd_cap = 0, used = 0;
+    float *d_temp = nullptr;
+    int32_t *d_rbase = nullptr, *d_pick = nullptr;
+    hipGraphExec_t exec_s = nullptr;
+    hipGraph_t graph_s = nullptr;
 };
 
 extern "C" void xjh_chain_free(xjh_chain *c) {
@@ -1022,13 +1031,17 @@ extern "C" void xjh_chain_free(xjh_chain *c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     if (c->exec) (void)hipGraphExecDestroy(c->exec);
     if (c->graph) (void)hipGraphDestroy(c->graph);
+    if (c->exec_s) (void)hipGraphExecDestroy(c->exec_s);
+    if (c->graph_s) (void)hipGraphDestroy(c->graph_s);
+    if (c->d_rnd) (void)hipFree(c->d_rnd);
+    if (c->d_temp) (void)hipFree(c->d_temp);
     for (auto *S : c->st) if (S->st) (void)hipStreamSynchronize(S->st);
     if (c->ev0) (void)hipEventDestroy(c->ev0);
     if (c->ev1) (void)hipEventDestroy(c->ev1);
     for (hipEvent_t e : c->ev_done) if (e) (void)hipEventDestroy(e);
     for (hipEvent_t e : c->ev_taken) if (e) (void)hipEventDestroy(e);
     if (c->d_prompt) (void)hipFree(c->d_prompt);
-    for (int32_t *p : {c->d_tokens, c->d_argmax, c->d_tok, c->d_hist, c->d_step}) if (p) (void)hipFree(p);
+    for (int32_t *p : {c->d_tokens, c->d_argmax, c->d_tok, c->d_hist, c->d_step, c->d_rbase, c->d_pick}) if (p) (void)hipFree(p);
     if (c->h_buf) (void)hipHostFree(c->h_buf);
     delete c;
 }
@@ -1057,7 +1070,9 @@ extern "C" xjh_chain *xjh_chain_new(xj_stage **stages, int n, char *err, size_t 
     c->hist_cap = 1 << 16;
     if (hipMalloc(&c->d_tokens, 4 * c->mb) != hipSuccess || hipMalloc(&c->d_argmax, 4 * c->mb) != hipSuccess ||
         hipMalloc(&c->d_tok, 4) != hipSuccess || hipMalloc(&c->d_hist, 4 * c->hist_cap) != hipSuccess ||
-        hipMalloc(&c->d_step, 4) != hipSuccess || hipHostMalloc((void **)&c->h_buf, 4 * (c->mb + 16), hipHostMallocDefault) != hipSuccess ||
+        hipMalloc(&c->d_step, 4) != hipSuccess || hipMalloc(&c->d_rbase, 4) != hipSuccess ||
+        hipMalloc(&c->d_pick, 4 * c->mb) != hipSuccess || hipMalloc(&c->d_temp, 4) != hipSuccess ||
+        hipHostMalloc((void **)&c->h_buf, 4 * (c->mb + 16), hipHostMallocDefault) != hipSuccess ||
         hipEventCreate(&c->ev0) != hipSuccess || hipEventCreate(&c->ev1) != hipSuccess) {
         snprintf(err, errlen, "chain allocation failed");
         xjh_chain_free(c);
@@ -1091,8 +1106,8 @@ static int chain_sync(xjh_chain *c, char *err, size_t errlen) {
 // stage's n_past advances on the device at the end of each chunk, so no host
 // round trip separates the chunks; XJ_CHAIN_OVERLAP=0 runs all stages on one
 // stream.
-extern "C" int xjh_chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int keep, float *logits,
-                              int32_t *argmax, char *err, size_t errlen) {
+static int chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int keep, float *logits, int32_t *argmax,
+                      char *err, size_t errlen) {
     const int B = c->mb, E = c->st[0]->s.m->hp.n_embd, ns = (int)c->st.size();
     if (n <= 0) { snprintf(err, errlen, "no tokens"); return -1; }
     if (keep && n > B) { snprintf(err, errlen, "verify batch %d exceeds max_batch %d", n, B); return -1; }
@@ -1188,6 +1203,79 @@ extern "C" int xjh_chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nl
     return 0;
 }
 
+static bool sampling(const xjh_chain *c) { return !(c->temp <= 0.f); }
+
+// The sampler's tokens after rows [row0, row0 + n) of the head's last logits,
+// row row0 + i drawn with number used + i (the caller counts what it
+// consumes); the argmax of those rows when the sampler is off.
+static int chain_draw(xjh_chain *c, int row0, int n, int32_t *out, char *err, size_t errlen) {
+    HStage *head = c->st.back();
+    if (n < 1 || n > c->mb) { snprintf(err, errlen, "draw of %d rows", n); return -1; }
+    if (sampling(c) && c->used + n > c->n_rnd) {
+        snprintf(err, errlen, "sampler: %d random numbers left, %d needed", c->n_rnd - c->used, n); return -1;
+    }
+    SampleArgs sa{};
+    sa.lg = head->logits + (int64_t)row0 * head->output.n_rows;
+    sa.V = (int32_t)head->output.n_rows;
+    sa.T = n;
+    sa.temp = c->temp;
+    sa.rnd = c->d_rnd ? c->d_rnd + c->used : nullptr;
+    sa.out = c->d_pick;
+    if (sample_launch(sa, c->stream) ||
+        hipMemcpyAsync(c->h_buf, c->d_pick, 4 * (size_t)n, hipMemcpyDeviceToHost, c->stream) != hipSuccess) {
+        snprintf(err, errlen, "sample launch failed"); return -1;
+    }
+    if (chain_sync(c, err, errlen)) return -1;
+    memcpy(out, c->h_buf, 4 * (size_t)n);
+    return 0;
+}
+
+// The public eval: with the sampler on, the token after the last row is drawn
+// (one number) and becomes the token the next step feeds.
+extern "C" int xjh_chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int keep, float *logits,
+                              int32_t *argmax, char *err, size_t errlen) {
+    const bool draw = nlog > 0 && sampling(c);
+    if (draw && c->used + 1 > c->n_rnd) { snprintf(err, errlen, "sampler: no random numbers left"); return -1; }
+    if (chain_eval(c, tokens, n, nlog, keep, logits, argmax, err, errlen)) return -1;
+    if (draw) {
+        const int T = keep ? n : n - (n - 1) / c->mb * c->mb;   // rows of the last chunk
+        const int nl = nlog < T ? nlog : T;
+        int32_t t;
+        if (chain_draw(c, nl - 1, 1, &t, err, errlen)) return -1;
+        c->last_tok = t;
+        c->used += 1;
+    }
+    return 0;
+}
+
+extern "C" int xjh_chain_set_sampler(xjh_chain *c, float temperature, const uint32_t *rand30, int n, char *err,
+                                     size_t errlen) {
+    if (n < 0 || (n > 0 && !rand30)) { snprintf(err, errlen, "sampler: bad random numbers"); return -1; }
+    for (int i = 0; i < n; i++)
+        if (rand30[i] >= (1u << 30)) { snprintf(err, errlen, "sampler: number %d (%u) not below 2^30", i, rand30[i]); return -1; }
+    if (n > c->rnd_cap) {   // the sampled graph holds the array's address: rebuilt on its next use
+        if (c->exec_s) (void)hipGraphExecDestroy(c->exec_s);
+        if (c->graph_s) (void)hipGraphDestroy(c->graph_s);
+        c->exec_s = nullptr;
+        c->graph_s = nullptr;
+        if (c->d_rnd) (void)hipFree(c->d_rnd);
+        c->d_rnd = nullptr;
+        c->rnd_cap = 0;
+        if (hipMalloc(&c->d_rnd, 4 * (size_t)n) != hipSuccess) { snprintf(err, errlen, "sampler: hipMalloc failed"); return -1; }
+        c->rnd_cap = n;
+    }
+    if ((n > 0 && hipMemcpy(c->d_rnd, rand30, 4 * (size_t)n, hipMemcpyHostToDevice) != hipSuccess) ||
+        hipMemcpy(c->d_temp, &temperature, 4, hipMemcpyHostToDevice) != hipSuccess) {
+        snprintf(err, errlen, "sampler: upload failed"); return -1;
+    }
+    c->temp = temperature;
+    c->n_rnd = n;
+    c->used = 0;
+    return 0;
+}
+
+extern "C" int xjh_chain_sampler_used(xjh_chain *c) { return c->used; }
+
 // One greedy decode step, entirely on the device: embedding of d_tok, every
 // stage (the last GEMV of each advances its n_past), the head, and the argmax
 // that writes d_tok and appends it to the history.
@@ -1199,29 +1287,45 @@ static int embed_first(xjh_chain *c) {
     return embed_launch(ea, c->stream);
 }
 
-static int enqueue_decode_step(xjh_chain *c) {
+// sampled: the app's draw (temperature and numbers read from the device,
+// number d_rbase + step) in place of the argmax launch.
+static int enqueue_decode_step(xjh_chain *c, bool sampled) {
     HStage *head = c->st.back();
     int rc = 0;
     for (auto *S : c->st) rc = rc ? rc : enqueue_layers(S, c->x, 1, 0, true, c->stream);
     if (!rc) rc = enqueue_head(head, c->x, 1, head->logits, c->stream);
     const EmbedArgs next{nullptr, c->st[0]->tok_embd, c->x, 1};
-    if (!rc) rc = argmax_finalize_launch(head->amax, head->head_nwg, 1, nullptr, c->d_tok, c->d_hist, c->d_step,
-                                         c->stream, &next);
-    return rc;
+    if (rc) return rc;
+    if (!sampled)
+        return argmax_finalize_launch(head->amax, head->head_nwg, 1, nullptr, c->d_tok, c->d_hist, c->d_step, c->stream,
+                                      &next);
+    SampleArgs sa{};
+    sa.lg = head->logits;
+    sa.V = (int32_t)head->output.n_rows;
+    sa.T = 1;
+    sa.temp_dev = c->d_temp;
+    sa.rnd = c->d_rnd;
+    sa.rbase = c->d_rbase;
+    sa.tok_out = c->d_tok;
+    sa.hist = c->d_hist;
+    sa.step = c->d_step;
+    sa.embed = next;
+    return sample_launch(sa, c->stream);
 }
 
-static int build_decode_graph(xjh_chain *c, char *err, size_t errlen) {
+static int build_decode_graph(xjh_chain *c, bool sampled, char *err, size_t errlen) {
     if (hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
         snprintf(err, errlen, "graph capture failed to start"); return -1;
     }
-    const int rc = enqueue_decode_step(c);
+    const int rc = enqueue_decode_step(c, sampled);
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(c->stream, &g);
     if (rc || e != hipSuccess) { snprintf(err, errlen, "graph capture failed"); if (g) (void)hipGraphDestroy(g); return -1; }
-    if (hipGraphInstantiate(&c->exec, g, nullptr, nullptr, 0) != hipSuccess) {
-        snprintf(err, errlen, "graph instantiation failed"); (void)hipGraphDestroy(g); return -1;
+    hipGraphExec_t &ex = sampled ? c->exec_s : c->exec;
+    if (hipGraphInstantiate(&ex, g, nullptr, nullptr, 0) != hipSuccess) {
+        snprintf(err, errlen, "graph instantiation failed"); (void)hipGraphDestroy(g); ex = nullptr; return -1;
     }
-    c->graph = g;
+    (sampled ? c->graph_s : c->graph) = g;
     return 0;
 }
 
@@ -1231,11 +1335,13 @@ static bool has_end(const xj_hparams &hp) { return hp.eos != UINT32_MAX || hp.eo
 
 // n replays of the decode step from token `tok` at the stages' current n_past
 // (enqueued, not synchronised); the tokens land in d_hist[0, n).
-static int decode_enqueue(xjh_chain *c, int tok, int n, bool direct, char *err, size_t errlen) {
+static int decode_enqueue(xjh_chain *c, int tok, int n, bool direct, bool sampled, char *err, size_t errlen) {
     c->h_buf[0] = 0;
     c->h_buf[1] = tok;
+    c->h_buf[3] = c->used;   // sampled: step i draws number used + i
     if (hipMemcpyAsync(c->d_step, &c->h_buf[0], 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
-        hipMemcpyAsync(c->d_tok, &c->h_buf[1], 4, hipMemcpyHostToDevice, c->stream) != hipSuccess) {
+        hipMemcpyAsync(c->d_tok, &c->h_buf[1], 4, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+        (sampled && hipMemcpyAsync(c->d_rbase, &c->h_buf[3], 4, hipMemcpyHostToDevice, c->stream) != hipSuccess)) {
         snprintf(err, errlen, "decode setup failed"); return -1;
     }
     for (auto *S : c->st) if (set_npast(S, c->stream)) { snprintf(err, errlen, "decode setup failed"); return -1; }
@@ -1243,7 +1349,8 @@ static int decode_enqueue(xjh_chain *c, int tok, int n, bool direct, char *err, 
     if (chain_sync(c, err, errlen)) return -1;   // the pinned set-up words are reused below
     (void)hipEventRecord(c->ev0, c->stream);
     for (int i = 0; i < n; i++)
-        if (direct ? enqueue_decode_step(c) != 0 : hipGraphLaunch(c->exec, c->stream) != hipSuccess) {
+        if (direct ? enqueue_decode_step(c, sampled) != 0
+                   : hipGraphLaunch(sampled ? c->exec_s : c->exec, c->stream) != hipSuccess) {
             snprintf(err, errlen, "decode step launch failed"); return -1;
         }
     (void)hipEventRecord(c->ev1, c->stream);
@@ -1258,10 +1365,15 @@ extern "C" int xjh_chain_decode(xjh_chain *c, int n_steps, int32_t *out, char *e
     for (auto *S : c->st) if (reset_check(S, err, errlen)) return -1;
     for (auto *S : c->st)
         if (S->s.n_past + n_steps > S->s.n_ctx) { snprintf(err, errlen, "context full (%d)", S->s.n_ctx); return -1; }
+    // with the sampler on, step i draws number used + i
+    const bool smp = sampling(c);
+    if (smp && c->used + n_steps > c->n_rnd) {
+        snprintf(err, errlen, "sampler: %d random numbers left, %d steps asked", c->n_rnd - c->used, n_steps); return -1;
+    }
     // XJ_DECODE_GRAPH=0 enqueues the same kernels step by step instead of
     // replaying the captured graph (for tracing tools that do not follow graphs)
     const bool direct = env_int("XJ_DECODE_GRAPH", 1) == 0;
-    if (!direct && !c->exec && build_decode_graph(c, err, errlen)) return -1;
+    if (!direct && !(smp ? c->exec_s : c->exec) && build_decode_graph(c, smp, err, errlen)) return -1;
     // With end tokens the steps run in windows, the recurrent state saved at
     // the start of each: when step j of a window yields an end token, the
     // window is replayed from the saved state for j + 1 steps only, so the
@@ -1278,7 +1390,7 @@ extern "C" int xjh_chain_decode(xjh_chain *c, int n_steps, int32_t *out, char *e
                 if (snapshot_enqueue(S, kDecodeSlot, c->stream, err, errlen)) return -1;
             }
         const int tok0 = c->last_tok;
-        if (decode_enqueue(c, tok0, n, direct, err, errlen) || chain_sync(c, err, errlen)) return -1;
+        if (decode_enqueue(c, tok0, n, direct, smp, err, errlen) || chain_sync(c, err, errlen)) return -1;
         float ms = 0;
         (void)hipEventElapsedTime(&ms, c->ev0, c->ev1);
         total_ms += ms;
@@ -1290,9 +1402,10 @@ extern "C" int xjh_chain_decode(xjh_chain *c, int n_steps, int32_t *out, char *e
         if (ran < n) {
             for (size_t i = 0; i < c->st.size(); i++)
                 if (restore_enqueue(c->st[i], kDecodeSlot, past0[i], c->stream, err, errlen)) return -1;
-            if (decode_enqueue(c, tok0, ran, direct, err, errlen) || chain_sync(c, err, errlen)) return -1;
+            if (decode_enqueue(c, tok0, ran, direct, smp, err, errlen) || chain_sync(c, err, errlen)) return -1;
         }
         for (auto *S : c->st) S->s.n_past += ran;
+        if (smp) c->used += ran;
         c->last_tok = out[done + ran - 1];
         done += ran;
         if (ran < n) break;
@@ -1323,8 +1436,8 @@ static int draft_step(xjh_chain *d, int t, int *next, char *err, size_t errlen) 
         if (reset_check(S, err, errlen)) return -1;
     }
     const bool direct = env_int("XJ_DECODE_GRAPH", 1) == 0;
-    if (!direct && !d->exec && build_decode_graph(d, err, errlen)) return -1;
-    if (decode_enqueue(d, t, 1, direct, err, errlen) ||
+    if (!direct && !d->exec && build_decode_graph(d, false, err, errlen)) return -1;
+    if (decode_enqueue(d, t, 1, direct, false, err, errlen) ||
         hipMemcpyAsync(&d->h_buf[2], d->d_hist, 4, hipMemcpyDeviceToHost, d->stream) != hipSuccess ||
         chain_sync(d, err, errlen))
         return -1;
@@ -1343,7 +1456,7 @@ static int draft_run(xjh_chain *d, int t, int kk, int32_t *toks, char *err, size
         if (reset_check(S, err, errlen)) return -1;
     }
     const bool direct = env_int("XJ_DECODE_GRAPH", 1) == 0;
-    if (!direct && !d->exec && build_decode_graph(d, err, errlen)) return -1;
+    if (!direct && !d->exec && build_decode_graph(d, false, err, errlen)) return -1;
     d->h_buf[0] = 0;
     d->h_buf[1] = t;
     if (hipMemcpyAsync(d->d_step, &d->h_buf[0], 4, hipMemcpyHostToDevice, d->stream) != hipSuccess ||
@@ -1353,7 +1466,7 @@ static int draft_run(xjh_chain *d, int t, int kk, int32_t *toks, char *err, size
     for (auto *S : d->st) if (set_npast(S, d->stream)) { snprintf(err, errlen, "draft setup failed"); return -1; }
     if (embed_first(d)) { snprintf(err, errlen, "draft setup failed"); return -1; }
     for (int j = 0; j < kk; j++) {
-        if (direct ? enqueue_decode_step(d) != 0 : hipGraphLaunch(d->exec, d->stream) != hipSuccess) {
+        if (direct ? enqueue_decode_step(d, false) != 0 : hipGraphLaunch(d->exec, d->stream) != hipSuccess) {
             snprintf(err, errlen, "draft step launch failed"); return -1;
         }
         for (auto *S : d->st)
@@ -1386,18 +1499,20 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
     int produced = 0;
     long n_gen_tok = 0;
     int pending = tgt->last_tok;
+    const bool smp = sampling(tgt);
     while (produced < n_gen) {
         if (is_end(hp, pending)) { out[produced++] = pending; break; }   // returned, never fed (xj_spec.c:139)
         const int P = tgt->st[0]->s.n_past;
         int kk = k;
         if (kk > n_gen - produced - 1) kk = n_gen - produced - 1;
         for (auto *S : tgt->st) if (kk > S->s.n_ctx - P - 1) kk = S->s.n_ctx - P - 1;
-        if (kk <= 0) {   // no room to speculate: plain step on both models
+        if (smp && kk > tgt->n_rnd - tgt->used - 1) kk = tgt->n_rnd - tgt->used - 1;   // numbers for kk + 1 draws
+        if (kk <= 0) {   // no room to speculate: plain step on both models (the target's token drawn)
             out[produced++] = pending;
             int32_t nt, dn;
             if (xjh_chain_eval(tgt, &pending, 1, 1, 0, nullptr, &nt, err, errlen) ||
                 xjh_chain_eval(dft, &pending, 1, 1, 0, nullptr, &dn, err, errlen)) return -1;
-            pending = nt;
+            pending = tgt->last_tok;
             n_gen_tok++;
             continue;
         }
@@ -1412,9 +1527,12 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
             if (gi < n_oracle) toks[j] = oracle[gi];
             if (oracle_miss && (gi * 7 + j) % oracle_miss == 0) toks[j] = (toks[j] + 1) % V;
         }
-        // 2) verify [t, d1..dk] on the target in one batch with checkpoints
+        // 2) verify [t, d1..dk] on the target in one batch with checkpoints;
+        //    the target's token after each row: its argmax, or with the
+        //    sampler on its draw (row i with number used + i, xj_spec.c:185)
         int32_t am[5];
-        if (xjh_chain_eval(tgt, toks, kk + 1, kk + 1, 1, nullptr, am, err, errlen)) return -1;
+        if (chain_eval(tgt, toks, kk + 1, kk + 1, 1, nullptr, am, err, errlen) ||
+            (smp && chain_draw(tgt, 0, kk + 1, am, err, errlen))) return -1;
         // 3) accept the longest agreeing prefix (xj_spec.c:184-191); an accepted
         //    end token is returned but neither it nor what follows is fed (:193-194)
         int a = 0;
@@ -1422,6 +1540,7 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
         int fed = a + 1, n_out = a + 1;
         for (int i = 1; i <= a; i++)
             if (is_end(hp, toks[i])) { fed = i; n_out = i + 1; break; }
+        if (smp) tgt->used += n_out > fed ? fed : a + 1;   // one number per token produced
         for (int i = 0; i < n_out && produced < n_gen; i++) out[produced++] = toks[i];
         n_gen_tok += fed;
         st.n_steps++; st.n_drafted += kk; st.n_accepted += fed - 1 < a ? fed - 1 : a;
@@ -1586,13 +1705,14 @@ extern "C" int xjh_spec_generate_mtp(xjh_chain *tgt, xj_stage *mtp, int k, const
             push_hidden(R, T, err, errlen))
             return done(-1);
         for (int j = 0; j < T; j++) R.pt.push_back(i + j + 1 < n_prompt ? prompt[i + j + 1] : -1);
-        if (i + T == n_prompt) t = am;
+        if (i + T == n_prompt) t = tgt->last_tok;   // the argmax, or the sampler's draw
     }
     const double t_start = now_ms();
     if ((int)R.pt.size() > 1 && mtp_flush(R, (int)R.pt.size() - 1, false, nullptr, err, errlen)) return done(-1);
     int produced = 0;
+    const bool smp = sampling(tgt);
     while (produced < n_gen) {
-        out[produced++] = t;   // t: the greedy token after everything fed so far (xj_spec.c:135-140)
+        out[produced++] = t;   // t: the token after everything fed so far (xj_spec.c:135-140)
         if (produced == n_gen || is_end(hp, t)) break;   // an end token is returned, never fed
         const int P = tgt->st[0]->s.n_past;
         R.pt.back() = t;
@@ -1601,11 +1721,12 @@ extern "C" int xjh_spec_generate_mtp(xjh_chain *tgt, xj_stage *mtp, int k, const
         for (auto *S : tgt->st) if (kk > S->s.n_ctx - P - 1) kk = S->s.n_ctx - P - 1;
         const int mroom = R.S->s.n_ctx - R.S->s.n_past - (int)R.pt.size() - 1;
         if (kk > mroom) kk = mroom;
+        if (smp && kk > tgt->n_rnd - tgt->used - 1) kk = tgt->n_rnd - tgt->used - 1;   // numbers for kk + 1 draws
         if (kk <= 0) {   // no room to speculate: feed t alone (xj_spec.c:145-152)
             int32_t am = -1;
             if (xjh_chain_eval(tgt, &t, 1, 1, 0, nullptr, &am, err, errlen) || push_hidden(R, 1, err, errlen)) return done(-1);
             R.pt.push_back(-1);
-            t = am;
+            t = tgt->last_tok;
             continue;
         }
         // 1) the MTP stage drafts kk tokens (xj_spec.c:154-171): the pending
@@ -1637,13 +1758,17 @@ extern "C" int xjh_spec_generate_mtp(xjh_chain *tgt, xj_stage *mtp, int k, const
         // 2) verify [t, d1..dk] in one batch with checkpoints; 3) accept the
         //    agreeing prefix; an accepted end token is returned, and neither it
         //    nor what follows is fed (xj_spec.c:179-201)
+        //    (the target's token after each row: its argmax, or the sampler's
+        //    draw, row i with number used + i, xj_spec.c:185)
         int32_t am[5];
-        if (xjh_chain_eval(tgt, toks, kk + 1, kk + 1, 1, nullptr, am, err, errlen)) return done(-1);
+        if (chain_eval(tgt, toks, kk + 1, kk + 1, 1, nullptr, am, err, errlen) ||
+            (smp && chain_draw(tgt, 0, kk + 1, am, err, errlen))) return done(-1);
         int a = 0;
         while (a < kk && am[a] == toks[a + 1]) { st.acc_at[a]++; a++; }
         int fed = a + 1, n_out = a + 1;
         for (int i = 1; i <= a; i++)
             if (is_end(hp, toks[i])) { fed = i; n_out = i + 1; break; }
+        if (smp) tgt->used += n_out > fed ? fed : a + 1;   // one number per token produced
         for (int i = 1; i < n_out && produced < n_gen; i++) out[produced++] = toks[i];
         st.n_steps++; st.n_drafted += kk; st.n_accepted += fed - 1 < a ? fed - 1 : a;
         // 4) the fed positions become pending for the MTP stage (xj_spec.c:204-207)
@@ -2053,13 +2178,17 @@ extern "C" int xjh_sample(const float *logits, int n, int T, float temperature, 
                           char *err, size_t errlen) {
     if (!ops_stream()) return -1;
     if (n < 1 || T < 1) { snprintf(err, errlen, "sample: bad shape (n=%d, T=%d)", n, T); return -1; }
-    for (int t = 0; t < T; t++)
+    const bool draw = !(temperature <= 0.f);   // the app's test: temperature <= 0 is greedy, no number drawn
+    if (draw && !rand30) { snprintf(err, errlen, "sample: no random numbers"); return -1; }
+    for (int t = 0; draw && t < T; t++)
         if (rand30[t] >= (1u << 30)) { snprintf(err, errlen, "sample: random number %u not below 2^30", rand30[t]); return -1; }
     uint32_t *d = nullptr;
     if (hipMalloc(&d, 8 * (size_t)T) != hipSuccess) { snprintf(err, errlen, "hipMalloc failed"); return -1; }
     int32_t *o = (int32_t *)(d + T);
-    int rc = hipMemcpy(d, rand30, 4 * (size_t)T, hipMemcpyHostToDevice) == hipSuccess ? 0 : -1;
-    if (!rc && sample_launch(logits, n, T, temperature, d, o, g_stream)) rc = -1;
+    int rc = !draw || hipMemcpy(d, rand30, 4 * (size_t)T, hipMemcpyHostToDevice) == hipSuccess ? 0 : -1;
+    SampleArgs sa{};
+    sa.lg = logits; sa.V = n; sa.T = T; sa.temp = temperature; sa.rnd = d; sa.out = o;
+    if (!rc && sample_launch(sa, g_stream)) rc = -1;
     if (!rc) rc = ops_done(err, errlen);
     else snprintf(err, errlen, "sample launch failed");
     if (!rc && hipMemcpy(out_host, o, 4 * (size_t)T, hipMemcpyDeviceToHost) != hipSuccess) rc = -1;

@@ -148,6 +148,8 @@ def lib():
     _sig(L, "xjh_chain_eval", I, P, P, I, I, I, P, P, CP, S)
     _sig(L, "xjh_chain_decode", I, P, I, P, CP, S)
     _sig(L, "xjh_chain_last_token", I, P)
+    _sig(L, "xjh_chain_set_sampler", I, P, F, P, I, CP, S)
+    _sig(L, "xjh_chain_sampler_used", I, P)
     _sig(L, "xjh_chain_rollback", I, P, I, CP, S)
     _sig(L, "xjh_chain_reset", None, P)
     _sig(L, "xjh_chain_n_past", I, P)
@@ -399,8 +401,21 @@ class Chain:
         _check(rc, err, "chain eval")
         return (am[:nl], lg[:nl]) if want_logits else am[:nl]
 
+    def set_sampler(self, temperature, rand30=()):
+        """The app's sampler for every token this chain produces (temperature <= 0: greedy),
+        drawing rand30[i] / 2^30 in order, one number per token."""
+        r = np.ascontiguousarray(rand30, np.uint32).reshape(-1)
+        err = _err()
+        _check(lib().xjh_chain_set_sampler(self.ptr, float(temperature), _ptr(r) if r.size else None, r.size, err,
+                                           ERR), err, "set sampler")
+
+    @property
+    def sampler_used(self):
+        return lib().xjh_chain_sampler_used(self.ptr)
+
     def decode(self, n):
-        """Up to n greedy tokens; fewer when an end token came (it is the last one returned)."""
+        """Up to n tokens (greedy, or drawn by the sampler); fewer when an end token came
+        (it is the last one returned)."""
         out = np.empty(max(n, 1), np.int32)
         err = _err()
         rc = lib().xjh_chain_decode(self.ptr, n, _ptr(out), err, ERR)

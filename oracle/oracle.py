@@ -58,6 +58,7 @@ def olib():
         _sig(L, "xjo_delta_recurrent", None, I, I, I, P, P, P, P, P, F, P, P)
         _sig(L, "xjo_conv_silu", None, I, I, P, P, P)
         _sig(L, "xjo_sample", I, P, I, F, U32)
+        _sig(L, "xjo_sampler_cb", I, P, P, I)
         _sig(L, "xjo_utf8_emit", I, P, P, I, P)
         _sig(L, "xjo_swiglu", None, S, P, P)
         _sig(L, "xjo_delta_step", None, I, I, I, F, F, P, P, P, P, P, P, P, P, P, P)
@@ -100,16 +101,25 @@ def rlib(native=False):
         _sig(L, "ref_abi_offsets", I, C.POINTER(C.c_long), I)
         _sig(L, "ref_spec_run", I, PM, PS, PS, PS, I, P, I, I, P, I, I, P, C.POINTER(C.c_long), P, I,
              C.POINTER(C.c_int), CP, S)
+        _sig(L, "ref_spec_run_s", I, PM, PS, PS, PS, I, P, I, I, P, I, I, P, P, P, C.POINTER(C.c_long), P, I,
+             C.POINTER(C.c_int), CP, S)
         _r[key] = L
     return _r[key]
 
 
-def ref_spec_run(model_ptr, a, b, mtp, k, prompt, n_gen, oracle=None, oracle_miss=0, drafts=False):
-    """The reference's own pipeline + speculative driver (greedy) over the given
-    stage pointers (any backend behind the xj_stage vtable; b and mtp may be None).
+class XjoSampler(C.Structure):
+    _fields_ = [("temp", C.c_float), ("rand30", C.c_void_p), ("n", C.c_int), ("used", C.c_int)]
+
+
+def ref_spec_run(model_ptr, a, b, mtp, k, prompt, n_gen, oracle=None, oracle_miss=0, drafts=False, sampler=None):
+    """The reference's own pipeline + speculative driver over the given stage
+    pointers (any backend behind the xj_stage vtable; b and mtp may be None),
+    greedy, or with sampler = (temperature, rand30 numbers) the app's sampler
+    (the oracle's restatement, xjo_sampler_cb) drawing one number per call.
     Stops after an end token, as xjpipe-host does (the token is kept).
     Returns (tokens, (verify steps, drafted, accepted)) and, with drafts, the
-    MTP stage's proposals in order as a third item."""
+    MTP stage's proposals in order as a third item; with a sampler, the count
+    of numbers drawn as the last item."""
     PS = C.POINTER(xp.XjStage)
     p = np.ascontiguousarray(prompt, np.int32)
     o = np.ascontiguousarray(oracle, np.int32) if oracle is not None else None
@@ -119,14 +129,25 @@ def ref_spec_run(model_ptr, a, b, mtp, k, prompt, n_gen, oracle=None, oracle_mis
     log = np.full(cap, -1, np.int32)
     nd = C.c_int(0)
     err = C.create_string_buffer(ERR)
-    rc = rlib().ref_spec_run(C.cast(model_ptr, C.POINTER(xp.XjModel)), C.cast(a, PS), C.cast(b, PS) if b else None,
-                             C.cast(mtp, PS) if mtp else None, k, _ptr(p), len(p), n_gen,
-                             _ptr(o) if o is not None else None, len(o) if o is not None else 0, oracle_miss,
-                             _ptr(out), st, _ptr(log), cap, C.byref(nd), err, ERR)
+    if sampler is None:
+        rc = rlib().ref_spec_run(C.cast(model_ptr, C.POINTER(xp.XjModel)), C.cast(a, PS), C.cast(b, PS) if b else None,
+                                 C.cast(mtp, PS) if mtp else None, k, _ptr(p), len(p), n_gen,
+                                 _ptr(o) if o is not None else None, len(o) if o is not None else 0, oracle_miss,
+                                 _ptr(out), st, _ptr(log), cap, C.byref(nd), err, ERR)
+    else:
+        r = np.ascontiguousarray(sampler[1], np.uint32)
+        ctx = XjoSampler(float(sampler[0]), _ptr(r), len(r), 0)
+        cb = C.cast(olib().xjo_sampler_cb, C.c_void_p)
+        rc = rlib().ref_spec_run_s(C.cast(model_ptr, C.POINTER(xp.XjModel)), C.cast(a, PS),
+                                   C.cast(b, PS) if b else None, C.cast(mtp, PS) if mtp else None, k, _ptr(p), len(p),
+                                   n_gen, _ptr(o) if o is not None else None, len(o) if o is not None else 0,
+                                   oracle_miss, cb, C.byref(ctx), _ptr(out), st, _ptr(log), cap, C.byref(nd), err, ERR)
     if rc < 0:
         raise RuntimeError(err.value.decode())
     res = (out[:rc], (st[0], st[1], st[2]))
-    return res + (log[:nd.value],) if drafts else res
+    if drafts:
+        res = res + (log[:nd.value],)
+    return res + (ctx.used,) if sampler is not None else res
 
 
 # ---------------------------------------------------------------- oracle --

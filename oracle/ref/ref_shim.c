@@ -142,9 +142,24 @@ static int is_end_tok(const xj_model *m, int32_t t) { return (uint32_t)t == m->h
  * (tools/xjpipe-host.c:129-136; the end token is kept here); returns their
  * count. stats = {verify steps, drafted, accepted}; drafts (optional) gets the
  * MTP stage's proposals in order. */
+int ref_spec_run_s(const xj_model *m, xj_stage *a, xj_stage *b, xj_stage *mtp, int k, const int32_t *prompt,
+                   int n_prompt, int n_gen, const int32_t *oracle, int n_oracle, int oracle_miss, xj_sample_fn sample,
+                   void *sctx, int32_t *out, long *stats, int32_t *drafts, int draft_cap, int *n_drafts, char *err,
+                   size_t errlen);
+
 int ref_spec_run(const xj_model *m, xj_stage *a, xj_stage *b, xj_stage *mtp, int k, const int32_t *prompt, int n_prompt,
                  int n_gen, const int32_t *oracle, int n_oracle, int oracle_miss, int32_t *out, long *stats,
                  int32_t *drafts, int draft_cap, int *n_drafts, char *err, size_t errlen) {
+    return ref_spec_run_s(m, a, b, mtp, k, prompt, n_prompt, n_gen, oracle, n_oracle, oracle_miss, greedy_pick, NULL,
+                          out, stats, drafts, draft_cap, n_drafts, err, errlen);
+}
+
+/* The same with the caller's sampler in place of the greedy pick (the app
+ * passes its sample_cb here, ios/App/XJGlue.c:333). */
+int ref_spec_run_s(const xj_model *m, xj_stage *a, xj_stage *b, xj_stage *mtp, int k, const int32_t *prompt,
+                   int n_prompt, int n_gen, const int32_t *oracle, int n_oracle, int oracle_miss, xj_sample_fn sample,
+                   void *sctx, int32_t *out, long *stats, int32_t *drafts, int draft_cap, int *n_drafts, char *err,
+                   size_t errlen) {
     xj_pipeline p;
     xj_spec sp;
     rec_stage rec;
@@ -161,7 +176,7 @@ int ref_spec_run(const xj_model *m, xj_stage *a, xj_stage *b, xj_stage *mtp, int
     int produced = 0, ended = 0;
     while (!rc && produced < n_gen && !ended) {
         int32_t o[XJ_SPEC_MAXK + 1];
-        const int n = xj_spec_next(&sp, greedy_pick, NULL, o, n_gen - produced, err, errlen);
+        const int n = xj_spec_next(&sp, sample, sctx, o, n_gen - produced, err, errlen);
         if (n < 1) { rc = -1; break; }
         for (int i = 0; i < n && produced < n_gen && !ended; i++) {
             out[produced++] = o[i];

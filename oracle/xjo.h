@@ -58,6 +58,14 @@ int xjo_argmax(const float *x, int n);
 /* The app's top-k 40 / top-p 0.95 sampler (ios/App/XJGlue.c:251-282), the
  * uniform number rand30 / 2^30 passed in. */
 int xjo_sample(const float *lg, int n, float temp, uint32_t rand30);
+/* The app's sample_cb over a stream of numbers (rand30[used++] per draw at
+ * temp > 0), for the reference's own driver (xj_sample_fn). */
+typedef struct {
+    float temp;
+    const uint32_t *rand30;
+    int n, used;
+} xjo_sampler;
+int xjo_sampler_cb(void *ctx, const float *lg, int n);
 /* The app's UTF-8 piece streaming (ios/App/XJGlue.c:285-305): piece (its first
  * 256 bytes) after the held-back bytes; the bytes up to an incomplete trailing
  * character go to *out (returned count), that character is held back. */

@@ -64,6 +64,19 @@ int xjo_sample(const float *lg, int n, float temp, uint32_t rand30) {
     return idx[0];
 }
 
+/* The app's sample_cb (ios/App/XJGlue.c:248) over a given stream of numbers:
+ * each call with temp > 0 takes the next one (arc4random_uniform's place);
+ * temp <= 0 takes none. Past the end of the stream the draw uses 0. */
+int xjo_sampler_cb(void *ctx, const float *lg, int n) {
+    xjo_sampler *s = (xjo_sampler *)ctx;
+    uint32_t r = 0;
+    if (s->temp > 0) {
+        if (s->used < s->n) r = s->rand30[s->used];
+        s->used++;
+    }
+    return xjo_sample(lg, n, s->temp, r);
+}
+
 /* The app's emit (ios/App/XJGlue.c:285-305): the held-back bytes, then at most
  * 256 bytes of the piece; from the end, skip up to 4 bytes of continuation
  * (10xxxxxx) to the last lead byte, whose sequence length (4 from 0xF0, 3 from

@@ -170,14 +170,21 @@ def test_norm(mode):
 
 
 def test_argmax_first_maximum():
-    x = xp.fill_normal(4 * 151936, 8, 1.0).reshape(4, 151936)
+    """`if (x[i] > x[b]) b = i` from b = 0: ties and -0 == +0 keep the lowest
+    index, NaN never wins - except at index 0, where nothing compares above it."""
+    x = xp.fill_normal(7 * 151936, 8, 1.0).reshape(7, 151936)
     x[1, 1000] = x[1, 50000] = x[1, 150000] = 99.0     # ties: lowest index wins
     x[2, :] = -3.0                                     # all equal -> index 0
     x[3, 151935] = 1e30
+    x[4, 0] = np.nan                                   # NaN first: 0
+    x[5, 77] = np.nan                                  # NaN elsewhere: ignored
+    x[5, 78] = 50.0
+    x[6, :] = -1.0
+    x[6, 5], x[6, 7] = -0.0, 0.0                       # -0 first, +0 is not above it
     got = xp.argmax(x)
     want = [orc.olib().xjo_argmax(row.ctypes.data_as(orc.C.c_void_p), row.size) for row in x]
     assert got.tolist() == want
-    assert got.tolist()[1:] == [1000, 0, 151935]
+    assert got.tolist()[1:] == [1000, 0, 151935, 0, 78, 5]
 
 
 def _delta_inputs(T, H, S, seed):

@@ -15,7 +15,7 @@ import pytest
 
 import oracle as orc
 import xjpipe as xp
-from helpers import np_sample
+from helpers import draw_from_order, slot_history_cases
 from conftest import rel_l2
 from test_oracle import attn_inputs
 
@@ -181,22 +181,64 @@ def test_delta_step_forms_agree_bit_for_bit(monkeypatch):
 
 
 @pytest.mark.parametrize("V", [40, 1000, 151936])
-def test_sample_equal_values_by_index(V):
-    """Logits with many exact ties (multiples of 1/4, so the kept set holds
-    equal values and values equal to the 40th straddle the cut): the device
-    sampler follows its stated rule, equal values in index order (np_sample),
-    row by row. The app's exchange sort orders equal kept values differently
-    (test_oracle.py::test_sampler_equal_values_keep_the_apps_order)."""
+def test_sample_equal_values_match_the_app(V):
+    """Logits with many exact ties (multiples of 1/4: equal values inside the
+    kept set and values equal to the 40th straddling its edge), so the app's
+    slot history and exchange sort decide the order: the device's draw equals
+    the oracle's restatement of the app row by row."""
     rng = np.random.default_rng(V + 11)
     T = 12
     lg = (np.round(rng.standard_normal((T, V)) * 8) / 4).astype(np.float32)
     r30 = rng.integers(0, 1 << 30, T).astype(np.uint32)
     for temp in (0.0, 0.3, 1.0, 10.0):
         got = xp.sample(lg, temp, r30)
-        want = [np_sample(lg[t], temp, int(r30[t])) for t in range(T)]
+        want = [orc.sample(lg[t], temp, int(r30[t])) for t in range(T)]
         assert got.tolist() == want, temp
     lg = np.array([[3.0, 3.0, 5.0]], np.float32)
-    assert xp.sample(lg, 10.0, np.array([1 << 29], np.uint32)).tolist() == [0]
+    assert xp.sample(lg, 10.0, np.array([1 << 29], np.uint32)).tolist() == [1]
+
+
+def test_sample_slot_history_cases():
+    """The hand-worked slot orders (all values equal, replacements of the first
+    minimum, interleaved values, the exchange sort's swaps, -0 == +0): the
+    device draws what a draw from that order gives, for draws landing on every
+    kept position."""
+    for lg, order in slot_history_cases():
+        vals = lg[order]
+        r = np.array([0, 1, (1 << 30) - 1] + [int(x * (1 << 30)) for x in np.linspace(0.01, 0.99, 37)], np.uint32)
+        for temp in (1e4, 3.0):
+            got = xp.sample(np.tile(lg, (len(r), 1)), temp, r)
+            want = [draw_from_order(vals, order, temp, int(x)) for x in r]
+            assert got.tolist() == want, (lg[:6], temp)
+
+
+@pytest.mark.parametrize("V", [3, 39, 40, 41, 5000, 151936])
+def test_sample_edge_rows_match_the_app(V):
+    """Rows that leave the fast path: NaN at index 0 and elsewhere, signed
+    zeros at the 40th place, one repeated value, a rising row (every element
+    enters), a falling row, large equal runs at the top; plus a row of
+    distinct values. Device draws equal the oracle's for every row, greedy
+    included (first maximum; NaN at index 0 wins as in `x[i] > x[b]`)."""
+    rng = np.random.default_rng(V)
+    rows = []
+    base = rng.standard_normal(V).astype(np.float32)
+    rows.append(base.copy())
+    r = base.copy(); r[0] = np.nan; rows.append(r)
+    r = base.copy(); r[V // 2] = np.nan; rows.append(r)
+    r = np.where(rng.random(V) < 0.5, np.float32(-0.0), np.float32(0.0)).astype(np.float32)
+    r[: min(V, 30)] = np.abs(rng.standard_normal(min(V, 30))).astype(np.float32) + 1
+    rows.append(r)
+    rows.append(np.full(V, 0.25, np.float32))
+    rows.append(np.linspace(-3, 3, V).astype(np.float32))
+    rows.append(np.linspace(3, -3, V).astype(np.float32))
+    r = (np.round(rng.standard_normal(V)) / 2).astype(np.float32); r[rng.integers(0, V, 50)] = 4.0; rows.append(r)
+    lg = np.stack(rows)
+    T = lg.shape[0]
+    for temp in (0.0, 0.7, 2.0):
+        r30 = rng.integers(0, 1 << 30, T).astype(np.uint32)
+        got = xp.sample(lg, temp, r30)
+        want = [orc.sample(lg[t], temp, int(r30[t])) for t in range(T)]
+        assert got.tolist() == want, temp
 
 
 @pytest.mark.parametrize("V", [25, 1000, 151936])

@@ -23,7 +23,7 @@ import pytest
 import oracle as orc
 import xjpipe as xp
 from conftest import GOLDEN, rel_l2
-from helpers import np_sample, random_blocks
+from helpers import draw_from_order, np_sample, random_blocks, slot_history_cases
 
 needs_ref = pytest.mark.skipif(not orc.ref_available(), reason="reference build (oracle/_ref) not present")
 
@@ -630,11 +630,9 @@ def test_sampler_matches_definition(n):
 def test_sampler_equal_values_keep_the_apps_order():
     """Equal values inside the kept set: the app's exchange sort (ios/App/XJGlue.c:270)
     is not stable, so for logits [3, 3, 5] it ranks index 1 before index 0, and a
-    draw landing on the second kept value returns 1. The device sampler ranks
-    equal values by index (np_sample's rule) and returns 0 there; this test pins
-    the oracle to the app's order, test_gpu_ops.py pins the device to its rule.
-    (A value tied at the 40th place is never drawn: the last kept value holds at
-    most 1/40 of the kept mass, and the 0.95 cut always ends before it.)"""
+    draw landing on the second kept value returns 1, where ranking equal values
+    by index (np_sample's rule) returns 0. The device follows the app
+    (test_gpu_ops.py)."""
     lg = np.array([3.0, 3.0, 5.0], np.float32)
     r30 = 1 << 29                       # r = 0.5 of the mass: past p_0 = 1, within p_1
     assert orc.sample(lg, 10.0, r30) == 1
@@ -642,3 +640,61 @@ def test_sampler_equal_values_keep_the_apps_order():
     # without equal values the two orders agree
     lg = np.array([3.0, 3.5, 5.0], np.float32)
     assert orc.sample(lg, 10.0, r30) == np_sample(lg, 10.0, r30) == 1
+
+
+def test_sampler_slot_history_closed_forms():
+    """The oracle's draws equal draws from the hand-derived slot orders, for
+    draws landing on every kept position, at two temperatures."""
+    for lg, order in slot_history_cases():
+        vals = lg[order]
+        for temp in (1e4, 3.0):
+            for r30 in [0, 1, (1 << 30) - 1] + [int(x * (1 << 30)) for x in np.linspace(0.01, 0.99, 37)]:
+                assert orc.sample(lg, temp, r30) == draw_from_order(vals, order, temp, r30), (lg[:6], temp, r30)
+
+
+def test_sampler_nan_cases():
+    """NaN never compares true: with NaN at index 0 the greedy pick is 0 and no
+    later value enters slot 0's minimum, p_0 is NaN and the draw falls through
+    to the first kept index (0); a NaN elsewhere keeps its slot and makes the
+    mass NaN, so the draw returns the first kept index after the sort."""
+    lg = np.full(41, 1.0, np.float32)
+    lg[0] = np.nan
+    lg[40] = 2.0
+    for temp, r30 in ((0.0, 0), (0.7, 0), (0.7, 123456), (5.0, (1 << 30) - 1)):
+        assert orc.sample(lg, temp, r30) == 0
+    lg = np.full(41, 1.0, np.float32)
+    lg[1] = np.nan
+    lg[40] = 2.0                                  # 40 takes slot 0 (the first non-NaN minimum), sorts first
+    for r30 in (0, 1 << 29, (1 << 30) - 1):
+        assert orc.sample(lg, 0.7, r30) == 40
+    assert orc.sample(lg, 0.0, 0) == 40
+
+
+def test_sampler_callback_draws_one_number_per_token(tiny_path):
+    """The reference's own driver (xj_spec_next over oracle stages, k = 0) with
+    the app's sample_cb over a stream of numbers: token g is the draw from the
+    logits after the prompt and tokens < g, with number g."""
+    m = xp.Model(tiny_path)
+    L, V = m.hp.n_layer, m.hp.n_vocab
+    rng = np.random.default_rng(404)
+    prompt = rng.integers(0, V, 9).astype(np.int32)
+    r30 = rng.integers(0, 1 << 30, 24).astype(np.uint32)
+    a = orc.CpuStage(m.ptr, 0, L, 128, 8, True, kv_f16=True)
+    out, _, used = orc.ref_spec_run(m.ptr, a.ptr, None, None, 0, prompt, 24, sampler=(0.7, r30))
+    a.destroy()
+    assert used == 24
+    s = orc.CpuStage(m.ptr, 0, L, 128, 8, True, kv_f16=True)
+    x = np.stack([orc.embed(m.ptr, int(t)) for t in prompt])
+    x = np.concatenate([s.forward(x[:8].copy()), s.forward(x[8:].copy())])   # the driver's chunks of max_batch
+    toks = []
+    for g in range(24):
+        t = orc.sample(s.logits(x[-1:])[0], 0.7, int(r30[g]))
+        toks.append(t)
+        x = s.forward(orc.embed(m.ptr, t)[None].copy())
+    s.destroy()
+    assert out.tolist() == toks
+    # greedy draws no number
+    a = orc.CpuStage(m.ptr, 0, L, 128, 8, True, kv_f16=True)
+    _, _, used = orc.ref_spec_run(m.ptr, a.ptr, None, None, 0, prompt, 8, sampler=(0.0, r30))
+    a.destroy()
+    assert used == 0
