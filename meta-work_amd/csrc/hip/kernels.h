@@ -250,12 +250,16 @@ int norm_rows_launch(int mode, const float *x, int64_t xs, const float *w, int n
 // One token per row t of lg [T][V]: the app's top-k 40 / top-p 0.95 draw at
 // temperature temp (*temp_dev when given) with rnd[base + t] / 2^30 as the
 // uniform number, base = (*rbase if given) + (*step if given); temp <= 0: the
-// first maximum (no number read). out[t] (optional); tok_out (optional) gets
-// the last row's id; hist/step (optional, T == 1) append it to the history
-// and advance the step; embed.x (optional, T == 1): the id's embedding row.
+// first maximum (no number read). part [T][n_part]: the largest argmax key of
+// each part_rows elements of the row (the LM head's argmax partials, or
+// sample_part_launch's). out[t] (optional); tok_out (optional) gets the last
+// row's id; hist/step (optional, T == 1) append it to the history and advance
+// the step; embed.x (optional, T == 1): the id's embedding row.
 struct SampleArgs {
     const float *lg;
     int32_t V, T;
+    const unsigned long long *part;
+    int32_t n_part, part_rows;
     float temp;
     const float *temp_dev;
     const uint32_t *rnd;
@@ -264,6 +268,10 @@ struct SampleArgs {
     EmbedArgs embed;
 };
 int sample_launch(const SampleArgs &a, hipStream_t st);
+// Partials for sample_launch when no LM head made them: sample_part_rows(V)
+// elements each, ceil(V / rows) per row, into part [T][n].
+int sample_part_rows(int V);
+int sample_part_launch(const float *lg, int V, int T, unsigned long long *part, hipStream_t st);
 // g = silu(g) * u over n floats.
 int swiglu_launch(float *g, const float *u, int64_t n, hipStream_t st);
 // NeoX RoPE in place of x[t * tok_stride + h * head_stride + i] for T tokens and

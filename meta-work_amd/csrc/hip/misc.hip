@@ -148,39 +148,46 @@ int swiglu_launch(float *g, const float *u, int64_t n, hipStream_t st) {
 // scan from slot 0); then an exchange sort orders the slots by value,
 // p_i = exp((v_i - v_0) / temp) in double, the kept prefix ends where the
 // running share first reaches 0.95, and r = rand30 / 2^30 times the kept mass
-// picks. The slots always hold the 40 largest values seen so far, so when the
-// kept values are distinct and no other element equals the smallest of them
-// (and no NaN occurs) the result is the 40 largest values in descending order
-// whatever the slot history: the fast path selects them (a histogram of the
-// top 11 key bits, the candidates at or above the 40th one's bin compacted in
-// LDS, a radix select of the rest of its key). Otherwise the slot history
-// decides the order of equal values and which of them are kept: one wavefront
-// replays the app's loop over the row in index order (tiles staged in LDS,
-// only values above the tile's starting minimum examined) and one thread runs
-// the exchange sort as written.
+// picks. The slots always hold the 40 largest values seen so far (a NaN
+// never enters), so when the first 40 values hold no NaN, the kept values are
+// distinct and no other element equals the smallest of them, the result is
+// the 40 largest in descending order whatever the slot history. The fast path
+// finds them from the row's partial maxima (the LM head's argmax partials, or
+// a partials launch): the 40th largest partial maximum T bounds the 40th
+// value from below, so only partials whose maximum reaches T are read; their
+// elements at or above T are compacted in LDS and radix-selected. Otherwise
+// the slot history decides the order of equal values and which of them are
+// kept: one wavefront replays the app's loop over the row in index order
+// (tiles staged in LDS, only values above the tile's starting minimum
+// examined) and one thread runs the exchange sort as written.
 constexpr int kTopK = 40;
 constexpr int kSmpThreads = 1024;
 constexpr int kSmpWaves = kSmpThreads / 64;
-constexpr int kSmpBins = 2048;   // key bits 31..21
-constexpr int kSmpCap = 4096;    // candidates held in LDS (fast path); tile of the replay
+constexpr int kSmpCap = 4096;      // candidates held in LDS (fast path); tile of the replay
+constexpr int kSmpScan = 16384;    // elements of the partials read by the fast path, at most
+constexpr int kSmpParts = 1024;    // partials read by the fast path, at most
+constexpr int kSmpPartLds = 6144;  // partial maxima staged in LDS (more: read from memory)
 static_assert(kSmpCap == 4 * kSmpThreads, "a replay tile is four elements per thread");
 
-// ordered key: larger value, larger key (NaN lowest)
+// ordered key: larger value, larger key (NaN lowest; -0 below +0)
 __device__ __forceinline__ uint32_t okey(float v) {
     const uint32_t b = __float_as_uint(v);
     return v != v ? 0u : (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
+// the value part of an argmax key (zeros of either sign alike)
+__device__ __forceinline__ uint32_t ordc(float v) { return (uint32_t)(xjd::argmax_key(v, 1u) >> 32); }
 
 struct SampleShared {
-    uint32_t hist[kSmpBins];
+    uint32_t hist[256];
+    uint32_t pord[kSmpPartLds];   // value parts of the partial maxima
     float cv[kSmpCap];
     int32_t ci[kSmpCap];
+    int32_t plist[kSmpParts];
     unsigned long long gmask[kSmpCap / 64];
     unsigned long long red[kSmpWaves];
-    uint32_t wsum[kSmpWaves];
     float kv[kTopK];      // the kept values and indices, in the app's final order
     int32_t kix[kTopK];
-    int n_kept, ncand, fast, bstar, above, tie;
+    int n_kept, ncand, npart, tie, need, cnt;
     uint32_t pre, rand30;
     float thr;
 };
@@ -206,6 +213,50 @@ __device__ __forceinline__ uint32_t wave_incl_sum(uint32_t v, int lane) {
         if (lane >= off) v += q;
     }
     return v;
+}
+
+// The k-th largest (1 <= k <= n) of the n keys get(i), by 8-bit radix
+// passes with LDS histograms; *gt = how many keys are larger, *eq = how many
+// equal it. With fewer than four passes the result is that key with its
+// remaining low bits cleared (a lower bound; gt and eq then count prefixes).
+// Every thread of the work-group calls it.
+template <class Get>
+__device__ uint32_t block_kth_largest(Get get, int n, int k, SampleShared &sh, int *gt, int *eq, int passes = 4) {
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    uint32_t pre = 0, mask = 0;
+    int need = k, cnt = n;
+    for (int shift = 24; shift >= 32 - 8 * passes; shift -= 8) {
+        if (tid < 256) sh.hist[tid] = 0;
+        __syncthreads();
+        for (int i = tid; i < n; i += kSmpThreads) {
+            const uint32_t v = get(i);
+            if ((v & mask) == pre) atomicAdd(&sh.hist[(v >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (wid == 0) {   // lane l holds bins 255-4l .. 252-4l, counted from the top
+            uint32_t h[4], tot = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) { h[j] = sh.hist[255 - 4 * lane - j]; tot += h[j]; }
+            const uint32_t hi = wave_incl_sum(tot, lane), lo = hi - tot;
+            if (lo < (uint32_t)need && hi >= (uint32_t)need) {
+                uint32_t c = lo;
+                int j = 0;
+                while (c + h[j] < (uint32_t)need) c += h[j++];
+                sh.pre = pre | ((uint32_t)(255 - 4 * lane - j) << shift);
+                sh.need = need - (int)c;   // still to take from that bin
+                sh.cnt = (int)h[j];        // keys in that bin
+            }
+        }
+        __syncthreads();
+        pre = sh.pre;
+        need = sh.need;
+        cnt = sh.cnt;
+        mask |= 255u << shift;
+        __syncthreads();
+    }
+    *gt = k - need;
+    *eq = cnt;
+    return pre;
 }
 
 // The app's mi after a slot changed: the first slot holding the minimum by
@@ -252,145 +303,117 @@ __device__ int app_pick(const float *kv, const int32_t *kix, int k, float temp, 
 }
 
 // One row: the greedy token (temp <= 0) or the app's draw, returned to every
-// thread; rand30 matters on thread 0 only.
-__device__ int sample_row(const float *__restrict__ x, int V, float temp, uint32_t rand30, SampleShared &sh) {
+// thread; rand30 matters on thread 0 only. part[p] (n_part of them) is the
+// largest argmax key of elements [p * part_rows, (p + 1) * part_rows).
+__device__ int sample_row(const float *__restrict__ x, int V, float temp, uint32_t rand30,
+                          const unsigned long long *__restrict__ part, int n_part, int part_rows, SampleShared &sh) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int K = kTopK;
     const bool sampling = !(temp <= 0.f);
-    if (sampling)
-        for (int i = tid; i < kSmpBins; i += kSmpThreads) sh.hist[i] = 0;
-    if (tid == 0) { sh.ncand = 0; sh.n_kept = 0; sh.tie = 0; sh.fast = 0; sh.rand30 = rand30; }
-    __syncthreads();
-    // pass 1: the first maximum, NaN, the histogram of the top 11 key bits
+    if (tid == 0) { sh.ncand = 0; sh.n_kept = 0; sh.tie = 0; sh.npart = 0; sh.rand30 = rand30; }
+    // the first maximum: the largest partial key; the fill's values checked
+    // for NaN and the partials' value parts staged in LDS on the way
+    const bool lds_part = n_part <= kSmpPartLds;
+    int bad = V < K || n_part < K;
+    float f = 0.f;
+    if (sampling && !bad && tid < K) f = x[tid];
     unsigned long long best = 0ull;
-    int nan = 0;
-    for (int i0 = tid; i0 < V; i0 += 4 * kSmpThreads) {
-        float v[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) v[j] = i0 + j * kSmpThreads < V ? x[i0 + j * kSmpThreads] : 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int i = i0 + j * kSmpThreads;
-            if (i < V) {
-                const unsigned long long kk = xjd::argmax_key(v[j], (uint32_t)i);
-                best = kk > best ? kk : best;
-                if (v[j] != v[j]) nan = 1;
-                else if (sampling) atomicAdd(&sh.hist[okey(v[j]) >> 21], 1u);
-            }
-        }
+    for (int p = tid; p < n_part; p += kSmpThreads) {
+        const unsigned long long q = part[p];
+        best = q > best ? q : best;
+        if (lds_part) sh.pord[p] = (uint32_t)(q >> 32);
     }
     best = wave_max_u64(best);
     if (lane == 0) sh.red[wid] = best;
-    nan = __syncthreads_or(nan);
+    bad = bad || f != f;
+    bad = __syncthreads_or(bad);
     if (!sampling) {
         unsigned long long m = sh.red[0];
         for (int w = 1; w < kSmpWaves; w++) m = sh.red[w] > m ? sh.red[w] : m;
         return (int)xjd::argmax_key_index(m);
     }
-    // the bin of the 40th largest key: thread t holds bins 2047-2t and 2046-2t
-    {
-        const uint32_t h0 = sh.hist[kSmpBins - 1 - 2 * tid], h1 = sh.hist[kSmpBins - 2 - 2 * tid];
-        const uint32_t incl = wave_incl_sum(h0 + h1, lane);
-        if (lane == 63) sh.wsum[wid] = incl;
-        __syncthreads();
-        uint32_t before = 0;
-        for (int w = 0; w < wid; w++) before += sh.wsum[w];
-        const uint32_t hi = before + incl, lo = hi - h0 - h1;   // elements in the bins above this thread's / through them
-        if (!nan && V >= K && lo < (uint32_t)K && hi >= (uint32_t)K) {
-            const bool first = lo + h0 >= (uint32_t)K;
-            sh.bstar = kSmpBins - 1 - 2 * tid - (first ? 0 : 1);
-            sh.above = first ? (int)lo : (int)(lo + h0);
-            sh.fast = (first ? lo + h0 : hi) <= (uint32_t)kSmpCap;
-        }
-    }
-    __syncthreads();
+    // the fast path needs 40 values without NaN in the fill and 40 partials
     bool kept = false;   // the fast path settled the kept values and their order
-    if (sh.fast) {
-        // pass 2: every element in bin bstar or above, compacted (any order)
-        const uint32_t bstar = (uint32_t)sh.bstar;
-        for (int i0 = tid; i0 < V; i0 += 4 * kSmpThreads) {
-            float v[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = i0 + j * kSmpThreads < V ? x[i0 + j * kSmpThreads] : 0.f;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const bool c = i0 + j * kSmpThreads < V && (okey(v[j]) >> 21) >= bstar;
+    if (!bad) {
+        // T: the 40th largest partial maximum, its low 16 bits cleared (a lower
+        // bound of the 40th value); the partials reaching it, listed
+        int gt, eq;
+        auto pv = [&](int i) { return lds_part ? sh.pord[i] : (uint32_t)(part[i] >> 32); };
+        const uint32_t T = block_kth_largest(pv, n_part, K, sh, &gt, &eq, 2);
+        for (int p0 = 0; p0 < n_part; p0 += kSmpThreads) {
+            const int p = p0 + tid;
+            const bool c = p < n_part && pv(p) >= T;
+            const unsigned long long m = __ballot(c);
+            if (!m) continue;
+            int base = 0;
+            if (lane == 0) base = atomicAdd(&sh.npart, __popcll(m));
+            base = __shfl(base, 0, 64);
+            const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
+            if (c && pos < kSmpParts) sh.plist[pos] = p;
+        }
+        __syncthreads();
+        const int np = sh.npart;
+        if (T > 0u && np <= kSmpParts && (int64_t)np * part_rows <= kSmpScan) {   // (T = 0: NaN partials)
+            // their elements at or above T, compacted (any order)
+            const int ne = np * part_rows;
+            for (int e0 = 0; e0 < ne; e0 += kSmpThreads) {
+                const int e = e0 + tid;
+                int i = V;
+                float v = 0.f;
+                if (e < ne) {
+                    i = sh.plist[e / part_rows] * part_rows + e % part_rows;
+                    if (i < V) v = x[i];
+                }
+                const bool c = i < V && v == v && ordc(v) >= T;
                 const unsigned long long m = __ballot(c);
                 if (!m) continue;
                 int base = 0;
                 if (lane == 0) base = atomicAdd(&sh.ncand, __popcll(m));
                 base = __shfl(base, 0, 64);
-                if (c) {
-                    const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
-                    sh.cv[pos] = v[j];
-                    sh.ci[pos] = i0 + j * kSmpThreads;
-                }
-            }
-        }
-        __syncthreads();
-        // the rest of the 40th key: three 7-bit radix passes over the candidates
-        // of bin bstar; eq = how many carry exactly that key
-        const int C = sh.ncand;
-        uint32_t pre = bstar << 21, mask = 0xFFE00000u;
-        int need = K - sh.above, eq = 0;
-        for (int shift = 14; shift >= 0; shift -= 7) {
-            if (tid < 128) sh.hist[tid] = 0;
-            __syncthreads();
-            for (int j = tid; j < C; j += kSmpThreads) {
-                const uint32_t kk = okey(sh.cv[j]);
-                if ((kk & mask) == pre) atomicAdd(&sh.hist[(kk >> shift) & 127u], 1u);
+                const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
+                if (c && pos < kSmpCap) { sh.cv[pos] = v; sh.ci[pos] = i; }
             }
             __syncthreads();
-            if (wid == 0) {   // bins 127-2l and 126-2l on lane l, counted from the top
-                const uint32_t h0 = sh.hist[127 - 2 * lane], h1 = sh.hist[126 - 2 * lane];
-                const uint32_t hi = wave_incl_sum(h0 + h1, lane), lo = hi - h0 - h1;
-                if (lo < (uint32_t)need && hi >= (uint32_t)need) {
-                    const bool first = lo + h0 >= (uint32_t)need;
-                    sh.pre = pre | ((127u - 2 * lane - (first ? 0 : 1)) << shift);
-                    sh.above = need - (int)(first ? lo : lo + h0);   // still needed from that bin
-                    sh.bstar = (int)(first ? h0 : h1);               // elements in that bin
-                }
-            }
-            __syncthreads();
-            pre = sh.pre;
-            need = sh.above;
-            eq = sh.bstar;
-            mask |= 127u << shift;
-            __syncthreads();
-        }
-        // pre = the 40th largest key; a tie there, or a zero (whose sign the key
-        // tells apart and the app's comparisons do not), needs the replay
-        const float v40 = __uint_as_float((pre & 0x80000000u) ? (pre & 0x7FFFFFFFu) : ~pre);
-        if (eq == need && v40 != 0.f) {
-            for (int j = tid; j < C; j += kSmpThreads)
-                if (okey(sh.cv[j]) >= pre) {
-                    const int pos = atomicAdd(&sh.n_kept, 1);
-                    if (pos < K) { sh.kv[pos] = sh.cv[j]; sh.kix[pos] = sh.ci[j]; }
-                }
-            __syncthreads();
-            if (wid == 0) {
-                // the 40 in descending order (bitonic over the wavefront); equal
-                // neighbours are a tie among the kept values
-                const bool in = lane < K && lane < sh.n_kept;
-                unsigned long long key = in ? ((unsigned long long)okey(sh.kv[lane]) << 32) | (uint32_t)sh.kix[lane] : 0ull;
-                for (int kk = 2; kk <= 64; kk <<= 1)
-                    for (int j = kk >> 1; j > 0; j >>= 1) {
-                        const unsigned long long q = __shfl_xor(key, j, 64);
-                        const bool desc = (lane & kk) == 0, low = (lane & j) == 0;
-                        key = (low == desc) ? (q > key ? q : key) : (q < key ? q : key);
+            const int C = sh.ncand;
+            if (C <= kSmpCap && C >= K) {
+                // the 40th largest key among them; a tie there, or a zero (whose
+                // sign the key tells apart and the app's comparisons do not),
+                // needs the replay
+                const uint32_t pre = block_kth_largest([&](int i) { return okey(sh.cv[i]); }, C, K, sh, &gt, &eq);
+                const float v40 = __uint_as_float((pre & 0x80000000u) ? (pre & 0x7FFFFFFFu) : ~pre);
+                if (eq == K - gt && v40 != 0.f) {
+                    for (int j = tid; j < C; j += kSmpThreads)
+                        if (okey(sh.cv[j]) >= pre) {
+                            const int pos = atomicAdd(&sh.n_kept, 1);
+                            if (pos < K) { sh.kv[pos] = sh.cv[j]; sh.kix[pos] = sh.ci[j]; }
+                        }
+                    __syncthreads();
+                    if (wid == 0) {
+                        // the 40 in descending order (bitonic over the wavefront);
+                        // equal neighbours are a tie among the kept values
+                        const bool in = lane < K && lane < sh.n_kept;
+                        unsigned long long key =
+                            in ? ((unsigned long long)okey(sh.kv[lane]) << 32) | (uint32_t)sh.kix[lane] : 0ull;
+                        for (int kk = 2; kk <= 64; kk <<= 1)
+                            for (int j = kk >> 1; j > 0; j >>= 1) {
+                                const unsigned long long q = __shfl_xor(key, j, 64);
+                                const bool desc = (lane & kk) == 0, low = (lane & j) == 0;
+                                key = (low == desc) ? (q > key ? q : key) : (q < key ? q : key);
+                            }
+                        const uint32_t ok = (uint32_t)(key >> 32);
+                        const float v = __uint_as_float((ok & 0x80000000u) ? (ok & 0x7FFFFFFFu) : ~ok);
+                        const float prev = __shfl_up(v, 1, 64);
+                        if (__ballot(lane > 0 && lane < K && v == prev)) {
+                            if (lane == 0) sh.tie = 1;
+                        } else if (lane < K) {
+                            sh.kv[lane] = v;
+                            sh.kix[lane] = (int32_t)(key & 0xFFFFFFFFull);
+                        }
                     }
-                const uint32_t ok = (uint32_t)(key >> 32);
-                const float v = __uint_as_float((ok & 0x80000000u) ? (ok & 0x7FFFFFFFu) : ~ok);
-                const float prev = __shfl_up(v, 1, 64);
-                if (__ballot(lane > 0 && lane < K && v == prev)) {
-                    if (lane == 0) sh.tie = 1;
-                } else if (lane < K) {
-                    sh.kv[lane] = v;
-                    sh.kix[lane] = (int32_t)(key & 0xFFFFFFFFull);
+                    __syncthreads();
+                    kept = sh.n_kept == K && !sh.tie;
                 }
             }
-            __syncthreads();
-            kept = sh.n_kept == K && !sh.tie;
         }
     }
     int k = K;
@@ -471,13 +494,33 @@ __device__ int sample_row(const float *__restrict__ x, int V, float temp, uint32
     return sh.ncand;
 }
 
+// Partial maxima for the sampler: part[t][p] = the largest argmax key of row
+// t's elements [p * part_rows, (p + 1) * part_rows), one wavefront per partial.
+__global__ __launch_bounds__(256) void sample_part_kernel(const float *lg, int V, int part_rows, int n_part,
+                                                          unsigned long long *part) {
+    const int t = blockIdx.y, p = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (p >= n_part) return;
+    const float *x = lg + (int64_t)t * V;
+    unsigned long long m = 0ull;
+    for (int j = lane; j < part_rows; j += 64) {
+        const int i = p * part_rows + j;
+        if (i < V) {
+            const unsigned long long k = xjd::argmax_key(x[i], (uint32_t)i);
+            m = k > m ? k : m;
+        }
+    }
+    m = wave_max_u64(m);
+    if (lane == 0) part[(int64_t)t * n_part + p] = m;
+}
+
 __global__ __launch_bounds__(kSmpThreads) void sample_kernel(const SampleArgs a) {
     __shared__ SampleShared sh;
     const int t = blockIdx.x;
     const float temp = a.temp_dev ? *a.temp_dev : a.temp;
     uint32_t r30 = 0;
     if (threadIdx.x == 0 && !(temp <= 0.f)) r30 = a.rnd[(a.rbase ? *a.rbase : 0) + (a.step ? *a.step : 0) + t];
-    const int id = sample_row(a.lg + (int64_t)t * a.V, a.V, temp, r30, sh);
+    const int id = sample_row(a.lg + (int64_t)t * a.V, a.V, temp, r30, a.part + (int64_t)t * a.n_part, a.n_part,
+                              a.part_rows, sh);
     if (threadIdx.x == 0) {
         if (a.out) a.out[t] = id;
         if (a.tok_out && t == a.T - 1) *a.tok_out = id;
@@ -489,8 +532,21 @@ __global__ __launch_bounds__(kSmpThreads) void sample_kernel(const SampleArgs a)
     if (a.embed.x) embed_row(a.embed.w, id, a.embed.x, kSmpThreads);
 }
 
+int sample_part_rows(int V) {
+    const int r = V / 64;
+    return r < 1 ? 1 : r > 256 ? 256 : r;
+}
+
+int sample_part_launch(const float *lg, int V, int T, unsigned long long *part, hipStream_t st) {
+    if (V < 1 || T < 1) return -1;
+    const int rows = sample_part_rows(V), n = (V + rows - 1) / rows;
+    hipLaunchKernelGGL(sample_part_kernel, dim3((n + 3) / 4, T), dim3(256), 0, st, lg, V, rows, n, part);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 int sample_launch(const SampleArgs &a, hipStream_t st) {
-    if (a.V < 1 || a.T < 1) return -1;
+    if (a.V < 1 || a.T < 1 || !a.part || a.n_part < 1 || a.part_rows < 1) return -1;
+    if ((int64_t)a.n_part * a.part_rows < a.V) return -1;
     if ((a.hist || a.embed.x) && a.T != 1) return -1;
     if (a.embed.x && a.embed.w.k % 32) return -1;
     if (a.hist && !a.step) return -1;

@@ -69,7 +69,7 @@ struct HStage {
           *alpha = nullptr, *o = nullptr, *g = nullptr, *u = nullptr, *qr = nullptr, *scores = nullptr,
           *logits = nullptr;
     unsigned long long *amax = nullptr;
-    int head_nwg = 0;
+    int head_nwg = 0, head_rows = 0;   // argmax partials per logits row, rows per partial
     int32_t *npast = nullptr;
     // prepared GEMV activations, max_batch tokens each: inputs of K = n_embd
     // (attention/DeltaNet in-projections, gate|up, head), d_inner (ssm_out),
@@ -888,6 +888,7 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
         S->logits = dalloc<float>(S, mb * (size_t)S->output.n_rows, err, errlen);
         const int rows = gemv_plan((int)S->output.k, S->output.n_rows).rows_per_group;
         S->head_nwg = (int)((S->output.n_rows + rows - 1) / rows);
+        S->head_rows = rows;
         S->amax = dalloc<unsigned long long>(S, mb * (size_t)S->head_nwg, err, errlen);
         if (!S->logits || !S->amax) return fail();
     }
@@ -1221,6 +1222,9 @@ static int chain_draw(xjh_chain *c, int row0, int n, int32_t *out, char *err, si
     sa.temp = c->temp;
     sa.rnd = c->d_rnd ? c->d_rnd + c->used : nullptr;
     sa.out = c->d_pick;
+    sa.part = head->amax + (int64_t)row0 * head->head_nwg;
+    sa.n_part = head->head_nwg;
+    sa.part_rows = head->head_rows;
     if (sample_launch(sa, c->stream) ||
         hipMemcpyAsync(c->h_buf, c->d_pick, 4 * (size_t)n, hipMemcpyDeviceToHost, c->stream) != hipSuccess) {
         snprintf(err, errlen, "sample launch failed"); return -1;
@@ -1303,6 +1307,9 @@ static int enqueue_decode_step(xjh_chain *c, bool sampled) {
     sa.lg = head->logits;
     sa.V = (int32_t)head->output.n_rows;
     sa.T = 1;
+    sa.part = head->amax;
+    sa.n_part = head->head_nwg;
+    sa.part_rows = head->head_rows;
     sa.temp_dev = c->d_temp;
     sa.rnd = c->d_rnd;
     sa.rbase = c->d_rbase;
@@ -2182,13 +2189,16 @@ extern "C" int xjh_sample(const float *logits, int n, int T, float temperature, 
     if (draw && !rand30) { snprintf(err, errlen, "sample: no random numbers"); return -1; }
     for (int t = 0; draw && t < T; t++)
         if (rand30[t] >= (1u << 30)) { snprintf(err, errlen, "sample: random number %u not below 2^30", rand30[t]); return -1; }
+    const int prow = sample_part_rows(n), np = (n + prow - 1) / prow;
     uint32_t *d = nullptr;
-    if (hipMalloc(&d, 8 * (size_t)T) != hipSuccess) { snprintf(err, errlen, "hipMalloc failed"); return -1; }
+    if (hipMalloc(&d, 8 * (size_t)T + 8 * (size_t)T * np) != hipSuccess) { snprintf(err, errlen, "hipMalloc failed"); return -1; }
     int32_t *o = (int32_t *)(d + T);
+    unsigned long long *part = (unsigned long long *)(d + 2 * T);
     int rc = !draw || hipMemcpy(d, rand30, 4 * (size_t)T, hipMemcpyHostToDevice) == hipSuccess ? 0 : -1;
     SampleArgs sa{};
     sa.lg = logits; sa.V = n; sa.T = T; sa.temp = temperature; sa.rnd = d; sa.out = o;
-    if (!rc && sample_launch(sa, g_stream)) rc = -1;
+    sa.part = part; sa.n_part = np; sa.part_rows = prow;
+    if (!rc && (sample_part_launch(logits, n, T, part, g_stream) || sample_launch(sa, g_stream))) rc = -1;
     if (!rc) rc = ops_done(err, errlen);
     else snprintf(err, errlen, "sample launch failed");
     if (!rc && hipMemcpy(out_host, o, 4 * (size_t)T, hipMemcpyDeviceToHost) != hipSuccess) rc = -1;
