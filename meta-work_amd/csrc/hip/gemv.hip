@@ -148,6 +148,13 @@ struct RawU {
     uint32_t f;
 };
 
+// One Q4_K sub-block term S ds - SX dm: SX dm rounded, then one fused
+// multiply-add (the rounding the compiler gives the plain expression), written
+// out so that every kernel forming it rounds alike.
+__device__ __forceinline__ float q4k_part(int S, float ds, float SX, float dm) {
+    return __builtin_fmaf((float)S, ds, -(SX * dm));
+}
+
 // Q4_K unit = scale pair p of a block: elements 64p..64p+63, i.e. sub-blocks
 // 2p (low nibbles of qs[32p..32p+31]) and 2p+1 (high nibbles), whose
 // activations are x-groups g0 and g0+1. Scale/min decoding as
@@ -183,7 +190,7 @@ __device__ __forceinline__ void q4k_unit(const RawU &w, int p, int g0, const uin
             const int2 sxp = ((const int2 *)(xt + o.sx_off))[g];
             const float SX = (float)(sxp.x + sxp.y);
             const int S = qdot<8>(nib, pa, pb, pc);
-            const float part = (float)S * ds[s] - SX * dm[s];
+            const float part = q4k_part(S, ds[s], SX, dm[s]);
             acc[t] = fmaf(part, f, acc[t]);
         }
     }
@@ -267,8 +274,8 @@ __device__ __forceinline__ void q4k_unit2(const RawU &w0, const RawU &w1, int p,
             const int2 sxp = ((const int2 *)(xt + o.sx_off))[g];
             const float SX = (float)(sxp.x + sxp.y);
             const int S0 = qdot<8>(n0, pa, pb, pc), S1 = qdot<8>(n1, pa, pb, pc);
-            const float part0 = (float)S0 * ds[0][s] - SX * dm[0][s];
-            const float part1 = (float)S1 * ds[1][s] - SX * dm[1][s];
+            const float part0 = q4k_part(S0, ds[0][s], SX, dm[0][s]);
+            const float part1 = q4k_part(S1, ds[1][s], SX, dm[1][s]);
             acc0[t] = fmaf(part0, f, acc0[t]);
             acc1[t] = fmaf(part1, f, acc1[t]);
         }
