@@ -263,10 +263,10 @@ def gemv_leg(t, rows, k, copies, iters):
 
 
 def gemv_legs():
-    """The LM-head shapes (Q4_K 151936x1024 of the 0.8B model, Q6_K 151936x2560 of the 4B model) and
-    config 1 (Q4_K 4096x1024), single token, cold weights."""
-    return [gemv_leg(xp.Q4_K, 151936, 1024, 8, 64), gemv_leg(xp.Q6_K, 151936, 2560, 3, 24),
-            gemv_leg(xp.Q4_K, 4096, 1024, 256, 512)]
+    """The LM-head shapes (151936x1024 of the 0.8B model, as Q4_K and as the synthetic model's Q6_K;
+    Q6_K 151936x2560 of the 4B model) and config 1 (Q4_K 4096x1024), single token, cold weights."""
+    return [gemv_leg(xp.Q4_K, 151936, 1024, 8, 64), gemv_leg(xp.Q6_K, 151936, 1024, 6, 48),
+            gemv_leg(xp.Q6_K, 151936, 2560, 3, 24), gemv_leg(xp.Q4_K, 4096, 1024, 256, 512)]
 
 
 def gemv_tokens(t, rows, k, iters=200):

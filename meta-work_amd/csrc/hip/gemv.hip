@@ -1075,14 +1075,20 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
     // the lane's first units of row group rg, loaded before the work that
     // precedes their use (units past the row read the tensor's padding)
     constexpr int NW = Win<MU, Q4>::N;
-    RawU win[NW];
-    auto first_units = [&](int rg) {
+    // LW: single-token Q4_K / Q6_K rows of at most two units per lane in a
+    // looping launch: the next row group's whole window is requested before
+    // this group's dot products, so the work-group's stream never waits on
+    // its own epilogue
+    constexpr bool LW = T == 1 && MU > 0 && MU <= 2;
+    RawU win[NW], wnx[LW ? NW : 1];
+    auto units_into = [&](int rg, RawU (&dst)[NW]) {
         const GSeg &sg = a.seg[seg_of(a, rg)];
         const int64_t rb = row_of(sg, rg) * blocks_per_row(sg.type);
         const int u0 = lane < nu ? lane : nu - 1;
 #pragma unroll
-        for (int m = 0; m < NW; m++) win[m] = load_unit<Q4>(sg.type, sg.w, sg.nblk, rb, u0 + m * TS);
+        for (int m = 0; m < NW; m++) dst[m] = load_unit<Q4>(sg.type, sg.w, sg.nblk, rb, u0 + m * TS);
     };
+    auto first_units = [&](int rg) { units_into(rg, win); };
     int rg = blockIdx.x;
     uint8_t *lds = (uint8_t *)lds_v;
     if (pro_inwg(a.pro) && T > 1) {
@@ -1122,6 +1128,10 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         float acc[1][T];
 #pragma unroll
         for (int t = 0; t < T; t++) acc[0][t] = 0.f;
+        const int rn = rg + gridDim.x;
+        if constexpr (LW) {
+            if (rn < n_rg) units_into(rn, wnx);
+        }
         if (Q4 || sg.type == XJ_Q4_K) {
             rows_q4k<T, TS, MU, Win<MU, Q4>::PD>(sg.w, rb, nu, lane, win, xl, o.v_off, o, acc[0]);
         } else if constexpr (Q4) {
@@ -1137,6 +1147,11 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
                 if constexpr (T == 1) rows_h16<T, TS, 1>(sg.w, rr, K, lane, sg.type == XJ_BF16, a.xq, o, acc);
             } else rows_f32<T, TS, 1>(sg.w, rr, K, lane, a.xq, o, acc);
         }
+        // MU == 0: the next row group's first units are requested before this
+        // group's epilogue (its barriers), not after it
+        if constexpr (MU == 0) {
+            if (rn < n_rg) first_units(rn);
+        }
 #pragma unroll
         for (int t = 0; t < T; t++) {
             acc[0][t] = team_sum<TS>(acc[0][t]);
@@ -1144,11 +1159,14 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         }
         epilogue<T, TS, 1>(a, sg, rg, team, lane, tid, acc, amax_sh, ein);
         if (a.post.mode == POST_SWIGLU) tail_swiglu<T, NT>(a, rg, &flag_sh);
-        rg += gridDim.x;
-        // MU > 0: one row group per work-group (the launch covers them all), so
-        // no window is carried around a loop edge
-        if (MU > 0 || rg >= n_rg) break;
-        first_units(rg);
+        rg = rn;
+        // MU > 0 (but LW): one row group per work-group (the launch covers
+        // them all), so no window is carried around a loop edge
+        if ((MU > 0 && !LW) || rg >= n_rg) break;
+        if constexpr (LW) {
+#pragma unroll
+            for (int m = 0; m < NW; m++) win[m] = wnx[m];
+        }
     }
     if (a.inc_ptr && blockIdx.x == 0 && tid == 0) *a.inc_ptr += a.inc_by;
 }
@@ -1383,9 +1401,23 @@ static hipError_t launch_v(const GArgs &a, int grid, hipStream_t st) {
     return hipGetLastError();
 }
 
+// Single-token Q4_K / Q6_K rows of at most two units per lane loop over row
+// groups with the next group's window in flight (XJ_GEMV_LW=0: one row group
+// per work-group, as many work-groups as row groups)
+static bool loop_window() {
+    static const bool on = env_or("XJ_GEMV_LW", 1) != 0;
+    return on;
+}
+
 static bool all_q4k(const GArgs &a) {
     for (int i = 0; i < a.nseg; i++)
         if (a.seg[i].type != XJ_Q4_K) return false;
+    return true;
+}
+
+static bool all_k(const GArgs &a) {   // Q4_K and Q6_K rows only
+    for (int i = 0; i < a.nseg; i++)
+        if (a.seg[i].type != XJ_Q4_K && a.seg[i].type != XJ_Q6_K) return false;
     return true;
 }
 
@@ -1395,7 +1427,13 @@ static hipError_t launch_ts(const GArgs &a, int grid, hipStream_t st) {
     const int n_rg = a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg;
     switch (a.T) {
     case 1:
-        if (grid < n_rg) return launch_v<1, TS, 0>(a, grid, st);   // work-groups loop over row groups
+        if (grid < n_rg) {   // work-groups loop over row groups
+            if (upl <= 2 && loop_window() && all_k(a)) {
+                if (all_q4k(a)) return upl == 1 ? launch_v<1, TS, 1, true>(a, grid, st) : launch_v<1, TS, 2, true>(a, grid, st);
+                return upl == 1 ? launch_v<1, TS, 1>(a, grid, st) : launch_v<1, TS, 2>(a, grid, st);
+            }
+            return launch_v<1, TS, 0>(a, grid, st);
+        }
         if (all_q4k(a) && upl <= 5) switch (upl) {
             case 1: return launch_v<1, TS, 1, true>(a, grid, st);
             case 2: return launch_v<1, TS, 2, true>(a, grid, st);
@@ -1676,11 +1714,15 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
     }
     const int n_rg = a.seg[a.nseg - 1].wg0 + a.seg[a.nseg - 1].nwg;
     int grid = a.T == 1 ? (n_rg < g_grid_cap1 ? n_rg : g_grid_cap1) : (n_rg < g_grid_cap ? n_rg : g_grid_cap);
-    // a single token with at most two units per lane: one row group per
-    // work-group, whose whole window is requested at once, streams faster than
-    // work-groups that loop with one unit in flight (151936 x 1024 Q4_K:
-    // 30.4 -> 22.1 us with its prep launch)
-    if (a.T == 1 && !g_grid_forced && (a.K / 64 + p.lanes - 1) / p.lanes <= 2 && n_rg <= 64 * g_cus) grid = n_rg;
+    // a single token with at most two units per lane: Q4_K / Q6_K rows loop
+    // with the next row group's whole window in flight (151936 x 1024 Q4_K
+    // 23.6 -> 21.4 us, Q6_K 67.8 -> 55.2 us against one row group per
+    // work-group); other rows take one row group per work-group, whose whole
+    // window is requested at once, which streams faster than work-groups that
+    // loop with one unit in flight (Q4_K: 30.4 -> 22.1 us)
+    if (a.T == 1 && !g_grid_forced && (a.K / 64 + p.lanes - 1) / p.lanes <= 2 && n_rg <= 64 * g_cus &&
+        !(all_k(a) && loop_window()))
+        grid = n_rg;
     hipError_t e;
     switch (p.lanes) {
     case 8: e = launch_ts<8>(a, grid, st); break;

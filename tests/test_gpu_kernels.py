@@ -141,16 +141,18 @@ def test_gemv_residual_add():
     assert np.array_equal(got, want.astype(np.float32))
 
 
-def test_gemv_lm_head_shape():
-    """Q4_K 151936 x 1024 (the LM-head shape of the mixed batch) at every
+@pytest.mark.parametrize("t", [xp.Q4_K, xp.Q6_K])
+def test_gemv_lm_head_shape(t):
+    """151936 x 1024 (the 0.8B model's LM-head shape; a single token loops
+    over row groups with the next group's units in flight) at every
     speculative-verify width T = 1..5."""
     rows, k = 151936, 1024
-    blob = _weights(xp.Q4_K, rows, k, 31)
-    w = xp.DevWeight(xp.Q4_K, blob, rows, k)
+    blob = _weights(t, rows, k, 31)
+    w = xp.DevWeight(t, blob, rows, k)
     for T in (1, 2, 3, 4, 5):
         xs = xp.fill_normal(T * k, 40 + T, 1.0).reshape(T, k)
         got = xp.gemv(w, xs)
-        want = orc.matmul(xp.Q4_K, blob, k, rows, xs)
+        want = orc.matmul(t, blob, k, rows, xs)
         assert rel_l2(got, want) < 1e-3
         assert np.array_equal(np.argmax(got, 1), np.argmax(want, 1))
 
