@@ -122,27 +122,44 @@ __global__ __launch_bounds__(256) void attn_part_kernel(const AttnArgs a) {
     const int nsub = a.H / (a.Hkv * G), gk = g / nsub;
     const int team = tid >> 4, l16 = tid & 15;
     const int nk = a.Hkv * D;
-    const int pos = *a.npast + t, j0 = sp * kSplitP;
+    // the kernel arguments read together (each read would otherwise be
+    // waited for in turn)
+    asm volatile("" ::"s"(a.npast), "s"(a.kc), "s"(a.vc), "s"(a.qg), "s"(a.kn), "s"(a.vn), "s"(a.qnorm_w),
+                 "s"(a.knorm_w), "s"(a.rope), "s"(a.n_rot), "s"(a.qr), "s"(a.scores), "s"(a.n_split));
+    // F: the token's raw queries, key, value and norm weights do not depend
+    // on the position: they are requested with it and waited for together
+    // (lanes past D keep zeros)
+    float v[G + 1], vv = 0.f;
+    float2 csv = {0.f, 0.f};
+    float qnw = 0.f, knw = 0.f;
+    const int npast = *a.npast;
+    if constexpr (F) {
+        const bool in = tid < D;
+        const int dc = in ? tid : D - 1;
+        const float q_w = a.qnorm_w[dc], k_w = a.knorm_w[dc], kx = a.kn[gk * D + dc], vx = a.vn[gk * D + dc];
+        qnw = in ? q_w : 0.f;
+        knw = in ? k_w : 0.f;
+#pragma unroll
+        for (int i = 0; i < G; i++) {
+            const float qx = a.qg[(int64_t)(g * G + i) * 2 * D + dc];
+            v[i] = in ? qx : 0.f;
+            asm volatile("" ::"v"(v[i]));
+        }
+        v[G] = in ? kx : 0.f;
+        vv = in ? vx : 0.f;
+        asm volatile("" ::"v"(v[G]), "v"(vv), "v"(qnw), "v"(knw), "v"(npast));
+    }
+    const int pos = npast + t, j0 = sp * kSplitP;
     if (j0 > pos) return;                       // uniform per work-group
     const int n = (j0 + kSplitP - 1 < pos ? j0 + kSplitP - 1 : pos) - j0 + 1;
     __shared__ float e[G][kSplitP];
     __shared__ float ml[G][2];
     __shared__ float po[PG][HC][D];
-    // F: the token's raw queries (and in the split holding pos its key and
-    // value), requested ahead of the cache so that their use waits for them only
     const bool last = F && pos - j0 < kSplitP;   // this split holds pos (uniform)
-    float v[G + 1], vv = 0.f;
-    float2 csv = {0.f, 0.f};
-    float qnw = 0.f, knw = 0.f;
-    if constexpr (F) {
-        const bool in = tid < D;
-        qnw = in ? a.qnorm_w[tid] : 0.f;
-        knw = in && last ? a.knorm_w[tid] : 0.f;
-#pragma unroll
-        for (int i = 0; i < G; i++) v[i] = in ? a.qg[(int64_t)(g * G + i) * 2 * D + tid] : 0.f;
-        v[G] = in && last ? a.kn[gk * D + tid] : 0.f;
-        vv = in && last ? a.vn[gk * D + tid] : 0.f;
-        if (tid < a.n_rot / 2) csv = a.rope[(int64_t)pos * (a.n_rot / 2) + tid];   // n_rot <= D <= 256
+    if constexpr (F) {   // n_rot <= D <= 256; a clamped read, so the cache reads below need not wait for it
+        const int half = a.n_rot / 2, rc = tid < half ? tid : half - 1;
+        const float2 cv = a.rope[(int64_t)pos * half + rc];
+        csv = tid < half ? cv : float2{0.f, 0.f};
     }
     // every key and value of the split, clamped to valid positions
     u32x4 kw[NPT][(DL + 7) / 8];
@@ -326,14 +343,27 @@ __global__ __launch_bounds__(256) void attn_part_kernel(const AttnArgs a) {
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-    const int pos = *a.npast + t, ns = pos / kSplitP + 1;
+    asm volatile("" ::"s"(a.npast), "s"(a.scores), "s"(a.qg), "s"(a.qg_s), "s"(a.out), "s"(a.xq), "s"(a.n_split), "s"(a.H));
     const float *part = a.scores + ((int64_t)t * a.H + h) * a.n_split * (D + 2);
+    // the first 64 splits' partials are requested before the position is
+    // known (addresses clamped to the buffer; entries past the position are
+    // never used, whatever they hold)
+    const int d = tid;   // D <= 256
+    const bool in = d < D;
+    const int dc = in ? d : D - 1;
+    const int sl = tid < a.n_split ? tid : a.n_split - 1;
+    const float ms_l = part[(int64_t)sl * (D + 2)], ls_l = part[(int64_t)sl * (D + 2) + 1];
+    float pv[64];
+#pragma unroll
+    for (int s = 0; s < 64; s++) pv[s] = part[(int64_t)(s < a.n_split ? s : a.n_split - 1) * (D + 2) + 2 + dc];
+    const float gx = a.qg[(int64_t)t * a.qg_s + (int64_t)h * 2 * D + D + dc];   // the output gate
+    const int pos = *a.npast + t, ns = pos / kSplitP + 1;
     __shared__ float w[64];
     __shared__ float inv_l;
     if (tid < 64) {
         // split s < 64 on lane s; the weights and the total are formed in a fixed order
-        const float ms = tid < ns ? part[(int64_t)tid * (D + 2)] : -INFINITY;
-        const float ls = tid < ns ? part[(int64_t)tid * (D + 2) + 1] : 0.f;
+        const float ms = tid < ns ? ms_l : -INFINITY;
+        const float ls = tid < ns ? ls_l : 0.f;
         float M = ms;
         for (int s = tid + 64; s < ns; s += 64) M = fmaxf(M, part[(int64_t)s * (D + 2)]);
         for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
@@ -344,22 +374,14 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
         for (int s = 64; s < ns; s++) L = fmaf(expf(part[(int64_t)s * (D + 2)] - M), part[(int64_t)s * (D + 2) + 1], L);
         if (tid == 0) inv_l = 1.0f / L;
     }
-    const float *qr = a.qg + (int64_t)t * a.qg_s + (int64_t)h * 2 * D;
-    const int d = tid;   // D <= 256
-    const bool in = d < D;
     float r = 0.f;
     if (ns <= 64) {
-        // every split's value of dim d requested before the weights are known
-        // (clamped addresses, so the loads need no branch), summed in order
-        const int dc = in ? d : D - 1;
-        float pv[64];
-#pragma unroll
-        for (int s = 0; s < 64; s++) pv[s] = part[(int64_t)(s < ns ? s : ns - 1) * (D + 2) + 2 + dc];
+        // every split's value of dim d (requested above), summed in order
         __syncthreads();
         float o = 0.f;
 #pragma unroll
         for (int s = 0; s < 64; s++) if (s < ns) o = fmaf(w[s], pv[s], o);
-        r = o * inv_l * (in ? xjd::sigm(qr[D + dc]) : 0.f);
+        r = o * inv_l * (in ? xjd::sigm(gx) : 0.f);
     } else {
         __syncthreads();
         if (in) {
@@ -367,7 +389,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
             float o = 0.f, M2 = -INFINITY;
             for (int s = 0; s < ns; s++) M2 = fmaxf(M2, part[(int64_t)s * (D + 2)]);
             for (int s = 0; s < ns; s++) o = fmaf(expf(part[(int64_t)s * (D + 2)] - M2), part[(int64_t)s * (D + 2) + 2 + d], o);
-            r = o * inv_l * xjd::sigm(qr[D + d]);
+            r = o * inv_l * xjd::sigm(gx);
         }
     }
     if (in) a.out[(int64_t)t * a.H * D + (int64_t)h * D + d] = r;

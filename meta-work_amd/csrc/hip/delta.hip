@@ -147,6 +147,12 @@ __global__ __launch_bounds__(512) void delta_part_kernel(const DeltaArgs a) {
     constexpr int IPL = S / 16, RW = 32;
     const int hv = blockIdx.x, p = blockIdx.y, tid = threadIdx.x, team = tid >> 4, l16 = tid & 15, i0 = l16 * IPL;
     const int hk = hv % a.Hk, j = p * RW + team;
+    // the kernel arguments of the token loop read together, with the state
+    // (each read would otherwise be waited for in turn before the inputs are
+    // requested)
+    asm volatile("" ::"s"(a.qkv), "s"(a.qkv_s), "s"(a.k_off), "s"(a.v_off), "s"(a.beta), "s"(a.beta_s), "s"(a.alpha),
+                 "s"(a.alpha_s), "s"(a.out), "s"(a.out_s), "s"(a.T), "s"(a.xq), "s"(a.z), "s"(a.z_s), "s"(a.norm_w),
+                 "s"(a.keep_n), "s"(a.dt), "s"(a.A));
     __shared__ float qs[S], ks[S], os[RW];
     __shared__ double red[16];
     float m[IPL];

@@ -677,9 +677,13 @@ __device__ __forceinline__ float team_sum(float v) {
     return v;
 }
 
+// Segment of row group rg: every segment's first work-group is read at once
+// (a loop over the segments would wait for each read in turn); the ranges
+// ascend, so the count of later segments starting at or before rg is its index.
 __device__ __forceinline__ int seg_of(const GArgs &a, int rg) {
     int si = 0;
-    while (si + 1 < a.nseg && rg >= a.seg[si + 1].wg0) si++;
+#pragma unroll
+    for (int i = 1; i < kMaxSeg; i++) si += i < a.nseg && rg >= a.seg[i].wg0 ? 1 : 0;
     return si;
 }
 
@@ -837,10 +841,12 @@ __device__ __forceinline__ void tail_swiglu(const GArgs &a, int rg, int *flag_sh
 // (global_load_lds_dwordx4: lane l of a wavefront writes LDS base + 16 * l).
 // Issued before the weight window, the copies hold no registers, and waiting
 // for them (vmcnt drains in issue order) does not wait for the weights.
-// Completion: the caller's wait for vmcnt and barrier.
-__device__ __forceinline__ void dma_lds(const uint8_t *src, uint8_t *lds, int n16) {
+// Completion: the caller's wait for vmcnt and barrier. nthr = the
+// work-group's threads, read once by the kernel (each read of blockDim.x is
+// a scalar load that would wait before every copy loop).
+__device__ __forceinline__ void dma_lds(const uint8_t *src, uint8_t *lds, int n16, int nthr) {
     const int w = threadIdx.x >> 6;
-    for (int j0 = 0; j0 < n16; j0 += blockDim.x) {
+    for (int j0 = 0; j0 < n16; j0 += nthr) {
         const int i = j0 + threadIdx.x;
         if (i < n16)
             __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1))) *)(src + 16 * (int64_t)i),
@@ -869,9 +875,9 @@ __device__ __forceinline__ void barrier_lds() {
 
 // The T tokens' prepared activations, [0, v_off) of each, into LDS.
 template <int T>
-__device__ __forceinline__ void dma_xq(const GArgs &a, const XqOff &o, uint8_t *lds) {
+__device__ __forceinline__ void dma_xq(const GArgs &a, const XqOff &o, uint8_t *lds, int nthr) {
 #pragma unroll
-    for (int t = 0; t < T; t++) dma_lds(a.xq + (int64_t)t * o.stride, lds + t * o.v_off, o.v_off >> 4);
+    for (int t = 0; t < T; t++) dma_lds(a.xq + (int64_t)t * o.stride, lds + t * o.v_off, o.v_off >> 4, nthr);
 }
 
 // PRO_RMSU_X / PRO_X: eight consecutive inputs k..k+7 of one token (u = x * w,
@@ -962,22 +968,22 @@ __device__ __forceinline__ bool pro_inwg(int pro) { return pro == PRO_RMSU_X || 
 // xl + T * v_off + T * 4K), then converted into token t's activations
 // (PRO_X: u = x * 1, exact).
 template <int T>
-__device__ __forceinline__ void rmsx1_issue(const GArgs &a, const XqOff &o, uint8_t *xl) {
+__device__ __forceinline__ void rmsx1_issue(const GArgs &a, const XqOff &o, uint8_t *xl, int nthr) {
     uint8_t *base = xl + T * o.v_off;
 #pragma unroll
-    for (int t = 0; t < T; t++) dma_lds((const uint8_t *)(a.x + (int64_t)t * a.xs), base + t * 4 * a.K, a.K >> 2);
-    if (a.pro == PRO_RMSU_X) dma_lds((const uint8_t *)a.pro_w, base + T * 4 * a.K, a.K >> 2);
+    for (int t = 0; t < T; t++) dma_lds((const uint8_t *)(a.x + (int64_t)t * a.xs), base + t * 4 * a.K, a.K >> 2, nthr);
+    if (a.pro == PRO_RMSU_X) dma_lds((const uint8_t *)a.pro_w, base + T * 4 * a.K, a.K >> 2, nthr);
 }
 
 template <int T>
-__device__ __forceinline__ void rmsx1_finish(const GArgs &a, const XqOff &o, uint8_t *xl) {
+__device__ __forceinline__ void rmsx1_finish(const GArgs &a, const XqOff &o, uint8_t *xl, int nthr) {
     const uint8_t *base = xl + T * o.v_off;
     const f32x4 *ws = (const f32x4 *)(base + T * 4 * a.K);
     const int n8 = a.K >> 3;
 #pragma unroll
     for (int t = 0; t < T; t++) {
         const f32x4 *xs = (const f32x4 *)(base + t * 4 * a.K);
-        for (int i0 = 0; i0 < n8; i0 += blockDim.x) {
+        for (int i0 = 0; i0 < n8; i0 += nthr) {
             const int i = i0 + threadIdx.x, ic = i < n8 ? i : n8 - 1;
             const f32x4 x[2] = {xs[2 * ic], xs[2 * ic + 1]};
             if (a.pro == PRO_X) {
@@ -1023,10 +1029,10 @@ __device__ __forceinline__ void rmsx_stage(const GArgs &a, const XqOff &o, uint8
 // scale 1/sqrt(sum of its groups' ss / group + eps), folded into the f of
 // each of its groups (each thread sums the head's doubles in the same order).
 // Completion: the caller's barrier.
-__device__ __forceinline__ void head_scale(const GArgs &a, const XqOff &o, uint8_t *xl, int t) {
+__device__ __forceinline__ void head_scale(const GArgs &a, const XqOff &o, uint8_t *xl, int t, int nthr) {
     uint8_t *x = xl + t * o.v_off;
     const int gph = a.group >> 5;
-    for (int g = threadIdx.x; g < o.G; g += blockDim.x) {
+    for (int g = threadIdx.x; g < o.G; g += nthr) {
         const double *ss = (const double *)(x + o.ss_off) + g / gph * gph;
         double s = 0;
         for (int i = 0; i < gph; i++) s += ss[i];
@@ -1098,20 +1104,20 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
     } else {
         // LDS copies first, then the window's loads: waiting for vmcnt <=
         // their number completes the copies only
-        if (pro_inwg(a.pro)) rmsx1_issue<1>(a, o, lds);
-        else dma_xq<T>(a, o, lds);
+        if (pro_inwg(a.pro)) rmsx1_issue<1>(a, o, lds, 256);
+        else dma_xq<T>(a, o, lds, 256);
         barrier_raw();   // the group's copies are queued ahead of its weight requests
         first_units(rg);
         __builtin_amdgcn_sched_barrier(0);
         wait_vm<Win<MU, Q4>::LOADS>();
         barrier_raw();
         if (pro_inwg(a.pro)) {
-            rmsx1_finish<1>(a, o, lds);
+            rmsx1_finish<1>(a, o, lds, 256);
             barrier_lds();
         }
         if (a.pro == PRO_HEADRMS) {
 #pragma unroll
-            for (int t = 0; t < T; t++) head_scale(a, o, lds, t);
+            for (int t = 0; t < T; t++) head_scale(a, o, lds, t, 256);
             barrier_lds();
         }
     }
@@ -1163,9 +1169,9 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         // MU > 0 (but LW): one row group per work-group (the launch covers
         // them all), so no window is carried around a loop edge
         if ((MU > 0 && !LW) || rg >= n_rg) break;
-        if constexpr (LW) {
-#pragma unroll
-            for (int m = 0; m < NW; m++) win[m] = wnx[m];
+        if constexpr (LW) {   // NW is 1 or 2 here
+            win[0] = wnx[0];
+            if constexpr (NW > 1) win[NW - 1] = wnx[NW - 1];
         }
     }
     if (a.inc_ptr && blockIdx.x == 0 && tid == 0) *a.inc_ptr += a.inc_by;
@@ -1264,6 +1270,16 @@ __global__ __launch_bounds__(T >= 4 && TS >= 16 ? 512 : 1024, 1) void gemv_cu_ke
     XqOff o = xq_off(K);
     if (a.pro == PRO_NONE) o.v_off = o.ss_off;
     const int tid = threadIdx.x, team = tid / TS, lane = tid % TS;
+    const int nthr = blockDim.x;   // read once (a scalar load)
+    // the activation copies go first (they need no segment field), with the
+    // kernel arguments they read loaded together rather than each waited for
+    // in turn
+    asm volatile("" ::"s"(a.x), "s"(a.pro_w), "s"(a.xq), "s"(a.xs), "s"(nthr), "s"(a.post.mode), "s"(a.rpw), "s"(a.nseg),
+                 "s"(a.seg[1].wg0), "s"(a.seg[2].wg0), "s"(a.seg[3].wg0));
+    uint8_t *lds = (uint8_t *)lds_v;
+    const bool inwg = pro_inwg(a.pro);
+    if (inwg) rmsx1_issue<T>(a, o, lds, nthr);
+    else dma_xq<T>(a, o, lds, nthr);
     const int rg = blockIdx.x;
     const bool H = a.post.mode == POST_SWIGLU_H;
     constexpr int TPW = 64 / TS;   // teams per wavefront
@@ -1271,6 +1287,7 @@ __global__ __launch_bounds__(T >= 4 && TS >= 16 ? 512 : 1024, 1) void gemv_cu_ke
     // uniform over the wavefront (ho is a multiple of TPW)
     const int si = H ? __builtin_amdgcn_readfirstlane((int)(team >= ho)) : seg_of(a, rg);
     const GSeg &sg = a.seg[si];
+    asm volatile("" ::"s"(sg.w), "s"(sg.n_rows), "s"(sg.wg0), "s"(sg.nblk), "s"(sg.type));   // read together
     const int tr = H && si ? team - ho : team;
     bool mine[R];
     int64_t row[R], rb[R];
@@ -1281,10 +1298,6 @@ __global__ __launch_bounds__(T >= 4 && TS >= 16 ? 512 : 1024, 1) void gemv_cu_ke
         row[i] = mine[i] ? r0 : (int64_t)sg.n_rows - 1;
         rb[i] = row[i] * (K / 256);
     }
-    uint8_t *lds = (uint8_t *)lds_v;
-    const bool inwg = pro_inwg(a.pro);
-    if (inwg) rmsx1_issue<T>(a, o, lds);
-    else dma_xq<T>(a, o, lds);
     if (!WF) wait_vm<0>();   // the activations complete before any weight request
     barrier_raw();
     RawU win[R][NW];
@@ -1299,12 +1312,12 @@ __global__ __launch_bounds__(T >= 4 && TS >= 16 ? 512 : 1024, 1) void gemv_cu_ke
         barrier_raw();
     }
     if (inwg) {
-        rmsx1_finish<T>(a, o, lds);
+        rmsx1_finish<T>(a, o, lds, nthr);
         barrier_lds();
     }
     if (a.pro == PRO_HEADRMS) {   // prepared: the copies completed before the weight requests
 #pragma unroll
-        for (int t = 0; t < T; t++) head_scale(a, o, lds, t);
+        for (int t = 0; t < T; t++) head_scale(a, o, lds, t, nthr);
         barrier_lds();
     }
     float sc[T];
