@@ -677,10 +677,16 @@ __device__ __forceinline__ float team_sum(float v) {
     return v;
 }
 
-// Segment of row group rg: every segment's first work-group is read at once
-// (a loop over the segments would wait for each read in turn); the ranges
-// ascend, so the count of later segments starting at or before rg is its index.
+// Segment of row group rg (the looping kernels: one segment costs one read).
 __device__ __forceinline__ int seg_of(const GArgs &a, int rg) {
+    int si = 0;
+    while (si + 1 < a.nseg && rg >= a.seg[si + 1].wg0) si++;
+    return si;
+}
+// The same with every segment's first work-group read at once (a loop over
+// the segments waits for each read in turn); the ranges ascend, so the count
+// of later segments starting at or before rg is its index.
+__device__ __forceinline__ int seg_of_flat(const GArgs &a, int rg) {
     int si = 0;
 #pragma unroll
     for (int i = 1; i < kMaxSeg; i++) si += i < a.nseg && rg >= a.seg[i].wg0 ? 1 : 0;
@@ -1057,11 +1063,13 @@ __device__ __forceinline__ float rmsu_scale(const GArgs &a, const XqOff &o, cons
 // launches with one work-group per row group, kept to three work-groups per
 // CU so that up to 3 x CUs of them run in one wave): every lane owns at most
 // MU units of its row, and the work-group issues the weight window of its row
-// group while the T tokens' activations are copied into LDS. MU == 0: the
-// same for the first unit, then a loop over row groups with stride gridDim.x
-// that prefetches each next group's first unit after the previous group's
-// epilogue.
-template <int T, int TS, int MU, bool Q4>
+// group while the T tokens' activations are copied into LDS (single-token
+// rows of at most two units per lane also loop, below). MU == 0: the same
+// for the first unit, then a loop over row groups with stride gridDim.x
+// that requests each next group's first unit before the current group's
+// epilogue. Q4: Q4_K rows only; K6: Q4_K and Q6_K rows only (fewer
+// registers than the kernel for every type).
+template <int T, int TS, int MU, bool Q4, bool K6 = false>
 __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a) {
     extern __shared__ u32x4 lds_v[];
     constexpr int NT = 256 / TS;
@@ -1085,8 +1093,8 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
     // looping launch: the next row group's whole window is requested before
     // this group's dot products, so the work-group's stream never waits on
     // its own epilogue
-    constexpr bool LW = T == 1 && MU > 0 && MU <= 2;
-    RawU win[NW], wnx[LW ? NW : 1];
+    constexpr bool LW = T == 1 && MU > 0 && MU <= 2 && (Q4 || K6);
+    RawU win[NW], wnx[NW];
     auto units_into = [&](int rg, RawU (&dst)[NW]) {
         const GSeg &sg = a.seg[seg_of(a, rg)];
         const int64_t rb = row_of(sg, rg) * blocks_per_row(sg.type);
@@ -1141,9 +1149,9 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         if (Q4 || sg.type == XJ_Q4_K) {
             rows_q4k<T, TS, MU, Win<MU, Q4>::PD>(sg.w, rb, nu, lane, win, xl, o.v_off, o, acc[0]);
         } else if constexpr (Q4) {
-        } else if (sg.type == XJ_Q6_K) {
+        } else if (K6 || sg.type == XJ_Q6_K) {
             rows_q6k<T, TS, MU, Win<MU, false>::PD>(sg.w, sg.nblk, rb, nu, lane, win, xl, o.v_off, o, acc[0]);
-        } else {
+        } else if constexpr (!K6) {
             const int64_t rr[1] = {row}, rbb[1] = {rb};
             if (sg.type == XJ_Q8_0) rows_q80<T, TS, 1>(sg.w, sg.nblk, rbb, K / 32, lane, xl, o.v_off, o, acc);
             // the types no configuration uses come one token per launch (their
@@ -1169,9 +1177,8 @@ __global__ __launch_bounds__(256, T == 1 ? 3 : 1) void gemv_kernel(const GArgs a
         // MU > 0 (but LW): one row group per work-group (the launch covers
         // them all), so no window is carried around a loop edge
         if ((MU > 0 && !LW) || rg >= n_rg) break;
-        if constexpr (LW) {   // NW is 1 or 2 here
-            win[0] = wnx[0];
-            if constexpr (NW > 1) win[NW - 1] = wnx[NW - 1];
+        if constexpr (LW) {
+            for (int m = 0; m < NW; m++) win[m] = wnx[m];
         }
     }
     if (a.inc_ptr && blockIdx.x == 0 && tid == 0) *a.inc_ptr += a.inc_by;
@@ -1285,9 +1292,11 @@ __global__ __launch_bounds__(T >= 4 && TS >= 16 ? 512 : 1024, 1) void gemv_cu_ke
     constexpr int TPW = 64 / TS;   // teams per wavefront
     const int ho = (a.rpw + TPW - 1) / TPW * TPW;
     // uniform over the wavefront (ho is a multiple of TPW)
-    const int si = H ? __builtin_amdgcn_readfirstlane((int)(team >= ho)) : seg_of(a, rg);
-    const GSeg &sg = a.seg[si];
-    asm volatile("" ::"s"(sg.w), "s"(sg.n_rows), "s"(sg.wg0), "s"(sg.nblk), "s"(sg.type));   // read together
+    const int si = H ? __builtin_amdgcn_readfirstlane((int)(team >= ho)) : seg_of_flat(a, rg);
+    // one token: the segment copied by value (its fields read together, never
+    // reloaded; several tokens keep the reference, which spills less)
+    const GSeg sg_v = a.seg[si];
+    const GSeg &sg = T == 1 ? sg_v : a.seg[si];
     const int tr = H && si ? team - ho : team;
     bool mine[R];
     int64_t row[R], rb[R];
@@ -1408,9 +1417,9 @@ static size_t gemv_lds_bytes(const GArgs &a) {
     return a.pro == PRO_RMSU_X ? b + 8 * (size_t)a.K : a.pro == PRO_X ? b + 4 * (size_t)a.K : b;
 }
 
-template <int T, int TS, int MU = 0, bool Q4 = false>
+template <int T, int TS, int MU = 0, bool Q4 = false, bool K6 = false>
 static hipError_t launch_v(const GArgs &a, int grid, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_kernel<T, TS, MU, Q4>), dim3(grid), dim3(256), gemv_lds_bytes(a), st, a);
+    hipLaunchKernelGGL((gemv_kernel<T, TS, MU, Q4, K6>), dim3(grid), dim3(256), gemv_lds_bytes(a), st, a);
     return hipGetLastError();
 }
 
@@ -1443,7 +1452,7 @@ static hipError_t launch_ts(const GArgs &a, int grid, hipStream_t st) {
         if (grid < n_rg) {   // work-groups loop over row groups
             if (upl <= 2 && loop_window() && all_k(a)) {
                 if (all_q4k(a)) return upl == 1 ? launch_v<1, TS, 1, true>(a, grid, st) : launch_v<1, TS, 2, true>(a, grid, st);
-                return upl == 1 ? launch_v<1, TS, 1>(a, grid, st) : launch_v<1, TS, 2>(a, grid, st);
+                return upl == 1 ? launch_v<1, TS, 1, false, true>(a, grid, st) : launch_v<1, TS, 2, false, true>(a, grid, st);
             }
             return launch_v<1, TS, 0>(a, grid, st);
         }
@@ -1753,8 +1762,8 @@ static void raise_ts(int bytes) {
                        (const void *)gemv_kernel<1, TS, 4, false>,
                        (const void *)gemv_kernel<1, TS, 1, true>, (const void *)gemv_kernel<1, TS, 2, true>,
                        (const void *)gemv_kernel<1, TS, 3, true>, (const void *)gemv_kernel<1, TS, 4, true>,
-                       (const void *)gemv_kernel<1, TS, 5, true>,
-                       (const void *)gemv_kernel<2, TS, 0, false>, (const void *)gemv_kernel<3, TS, 0, false>,
+                       (const void *)gemv_kernel<1, TS, 5, true>, (const void *)gemv_kernel<1, TS, 1, false, true>,
+                       (const void *)gemv_kernel<1, TS, 2, false, true>, (const void *)gemv_kernel<2, TS, 0, false>, (const void *)gemv_kernel<3, TS, 0, false>,
                        (const void *)gemv_kernel<4, TS, 0, false>, (const void *)gemv_kernel<5, TS, 0, false>,
                        (const void *)gemv_kernel<6, TS, 0, false>, (const void *)gemv_kernel<7, TS, 0, false>,
                        (const void *)gemv_kernel<8, TS, 0, false>};
