@@ -437,6 +437,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the 0.8B run and the GEMV legs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB")
+    ap.add_argument("--greedy-only", action="store_true",
+                    help="no sampled-decode leg (the counter runs: rocprofv3 --pmc has crashed in its own code on it)")
     ap.add_argument("--delta-c3", action="store_true", help="only the chunked vs token-by-token DeltaNet prefill")
     ap.add_argument("--gemm-tokens", action="store_true", help="only the prefill-chunk GEMM vs GEMV-tile legs")
     ap.add_argument("--prefill-only", action="store_true", help="only the 4B 1024-token prefill, three times")
@@ -495,14 +497,16 @@ def main():
     log(f"GEMV leg: {g_launch} launches/step, {g_bytes / 1e9:.3f} GB/step, {g_ms:.3f} ms -> {achieved:.0f} GB/s")
     # the app's sampler on the same chain (temperature 0.7, the app's default): the decode graph's last
     # launch draws the token instead of taking the argmax
-    r["ch"].set_sampler(0.7, np.random.default_rng(20261113).integers(0, 1 << 30, SAMPLED_STEPS).astype(np.uint32))
-    t0 = time.perf_counter()
-    st_toks = r["ch"].decode(SAMPLED_STEPS)
-    s_wall = time.perf_counter() - t0
-    sampled = {"temperature": 0.7, "steps": int(st_toks.size), "tok_s": round(st_toks.size / s_wall, 1),
-               "gpu_ms_per_step": round(r["ch"].last_decode_ms, 4),
-               "distinct_tokens": int(len(set(st_toks.tolist())))}
-    log(f"4B sampled decode: {sampled}")
+    sampled = None
+    if not args.greedy_only:
+        r["ch"].set_sampler(0.7, np.random.default_rng(20261113).integers(0, 1 << 30, SAMPLED_STEPS).astype(np.uint32))
+        t0 = time.perf_counter()
+        st_toks = r["ch"].decode(SAMPLED_STEPS)
+        s_wall = time.perf_counter() - t0
+        sampled = {"temperature": 0.7, "steps": int(st_toks.size), "tok_s": round(st_toks.size / s_wall, 1),
+                   "gpu_ms_per_step": round(r["ch"].last_decode_ms, 4),
+                   "distinct_tokens": int(len(set(st_toks.tolist())))}
+        log(f"4B sampled decode: {sampled}")
     r["ch"].free()
     r["st"].destroy()
 

@@ -228,6 +228,18 @@ int delta_chunked_launch(int H, int S, int T, int chunk, const float *q, const f
                          float *state, float *out, float *work, hipStream_t st);
 size_t delta_chunked_work_bytes(int H, int S, int T, int chunk);
 
+// Several device-to-device copies of float arrays in one launch (the
+// recurrent states of every DeltaNet layer of a stage: snapshots, restores,
+// rollbacks to a checkpoint). Entries past kCopyMax take further launches.
+constexpr int kCopyMax = 48;
+struct CopyList {
+    const float *src[kCopyMax];
+    float *dst[kCopyMax];
+    int64_t n[kCopyMax];   // floats
+    int32_t cnt;
+};
+int copy_list_launch(const CopyList &c, hipStream_t st);
+
 // Embedding rows for T tokens: x[t] = dequant(tok_embd row tokens[t]).
 struct EmbedArgs {
     const int32_t *tokens;

@@ -128,6 +128,40 @@ int argmax_rows_launch(const float *x, int n, int T, int32_t *out, hipStream_t s
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// Entry blockIdx.y of the list, 16 bytes per thread and step where both ends
+// are 16-byte aligned and the count a multiple of 4 (the states), else 4.
+__global__ __launch_bounds__(256) void copy_list_kernel(const CopyList c) {
+    const int e = blockIdx.y;
+    if (e >= c.cnt) return;
+    const float *s = c.src[e];
+    float *d = c.dst[e];
+    const int64_t n = c.n[e], stride = (int64_t)gridDim.x * 256;
+    const int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (!(((uintptr_t)s | (uintptr_t)d) & 15) && !(n & 3)) {
+        const float4 *s4 = (const float4 *)s;
+        float4 *d4 = (float4 *)d;
+        for (int64_t i = i0; i < n / 4; i += stride) d4[i] = s4[i];
+    } else {
+        for (int64_t i = i0; i < n; i += stride) d[i] = s[i];
+    }
+}
+
+int copy_list_launch(const CopyList &c, hipStream_t st) {
+    if (c.cnt < 0 || c.cnt > kCopyMax) return -1;
+    if (c.cnt == 0) return 0;
+    int64_t most = 0;
+    for (int i = 0; i < c.cnt; i++) {
+        if (c.n[i] < 0 || (c.n[i] && (!c.src[i] || !c.dst[i]))) return -1;
+        most = c.n[i] > most ? c.n[i] : most;
+    }
+    if (!most) return 0;
+    // up to 64 work-groups per entry, each copying 4 KB per step
+    const int64_t want = (most / 4 + 255) / 256;
+    const unsigned gx = (unsigned)(want < 1 ? 1 : want > 64 ? 64 : want);
+    hipLaunchKernelGGL(copy_list_kernel, dim3(gx, c.cnt), dim3(256), 0, st, c);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 __global__ __launch_bounds__(256) void swiglu_kernel(float *g, const float *u, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i < n) g[i] = xjd::silu(g[i]) * u[i];

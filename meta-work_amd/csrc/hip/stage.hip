@@ -608,6 +608,27 @@ int hip_logits(xj_stage *s, const float *x, int T, float *logits, char *err, siz
     return 0;
 }
 
+// The conv and recurrent states of every DeltaNet layer copied in one launch
+// (per-layer copies cost a launch each): pick(L, conv_src, conv_dst,
+// ssm_src, ssm_dst) names each layer's ends.
+template <class F>
+static int states_copy(HStage *S, hipStream_t st, F pick) {
+    CopyList c{};
+    for (auto &L : S->L) {
+        if (!L.rec) continue;
+        const float *cs = nullptr, *ss = nullptr;
+        float *cd = nullptr, *sd = nullptr;
+        pick(L, cs, cd, ss, sd);
+        if (c.cnt + 2 > kCopyMax) {
+            if (copy_list_launch(c, st)) return -1;
+            c.cnt = 0;
+        }
+        c.src[c.cnt] = cs; c.dst[c.cnt] = cd; c.n[c.cnt++] = (int64_t)S->conv_n;
+        c.src[c.cnt] = ss; c.dst[c.cnt] = sd; c.n[c.cnt++] = (int64_t)S->ssm_n;
+    }
+    return copy_list_launch(c, st);
+}
+
 int hip_rollback(xj_stage *s, int n_past, char *err, size_t errlen) {
     HStage *S = H(s);
     if (n_past == s->n_past) { s->ck_T = 0; return 0; }
@@ -623,13 +644,12 @@ int hip_rollback(xj_stage *s, int n_past, char *err, size_t errlen) {
         snprintf(err, errlen, "cannot roll back to %d (checkpoints %d+%d, now %d)", n_past, s->ck_start, s->ck_T, s->n_past);
         return -1;
     }
-    for (auto &L : S->L) {
-        if (!L.rec) continue;
-        if (hipMemcpyAsync(L.conv, L.ck_conv + j * S->conv_n, S->conv_n * 4, hipMemcpyDeviceToDevice, S->st) != hipSuccess ||
-            hipMemcpyAsync(L.ssm, L.ck_ssm + j * S->ssm_n, S->ssm_n * 4, hipMemcpyDeviceToDevice, S->st) != hipSuccess) {
-            snprintf(err, errlen, "checkpoint copy failed");
-            return -1;
-        }
+    if (states_copy(S, S->st, [&](HLayer &L, const float *&cs, float *&cd, const float *&ss, float *&sd) {
+            cs = L.ck_conv + j * S->conv_n; cd = L.conv;
+            ss = L.ck_ssm + j * S->ssm_n; sd = L.ssm;
+        })) {
+        snprintf(err, errlen, "checkpoint copy failed");
+        return -1;
     }
     if (sync_check(S, err, errlen)) return -1;
     s->n_past = n_past;
@@ -923,18 +943,18 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
 static int snapshot_enqueue(HStage *S, int slot, hipStream_t st, char *err, size_t errlen) {
     if (slot < 0 || slot >= kSnapSlots) { snprintf(err, errlen, "snapshot slot %d out of range", slot); return -1; }
     for (auto &L : S->L) {
-        if (!L.rec) continue;
-        if (!L.snap_conv[slot]) {
-            if (hipMalloc(&L.snap_conv[slot], S->conv_n * 4) != hipSuccess || hipMalloc(&L.snap_ssm[slot], S->ssm_n * 4) != hipSuccess) {
-                snprintf(err, errlen, "out of HBM for snapshots");
-                return -1;
-            }
-        }
-        if (hipMemcpyAsync(L.snap_conv[slot], L.conv, S->conv_n * 4, hipMemcpyDeviceToDevice, st) != hipSuccess ||
-            hipMemcpyAsync(L.snap_ssm[slot], L.ssm, S->ssm_n * 4, hipMemcpyDeviceToDevice, st) != hipSuccess) {
-            snprintf(err, errlen, "snapshot copy failed");
+        if (!L.rec || L.snap_conv[slot]) continue;
+        if (hipMalloc(&L.snap_conv[slot], S->conv_n * 4) != hipSuccess || hipMalloc(&L.snap_ssm[slot], S->ssm_n * 4) != hipSuccess) {
+            snprintf(err, errlen, "out of HBM for snapshots");
             return -1;
         }
+    }
+    if (states_copy(S, st, [&](HLayer &L, const float *&cs, float *&cd, const float *&ss, float *&sd) {
+            cs = L.conv; cd = L.snap_conv[slot];
+            ss = L.ssm; sd = L.snap_ssm[slot];
+        })) {
+        snprintf(err, errlen, "snapshot copy failed");
+        return -1;
     }
     return 0;
 }
@@ -964,14 +984,14 @@ extern "C" int xj_hip_stage_fill_kv(xj_stage *s, int pos0, uint16_t bits, char *
 static int restore_enqueue(HStage *S, int slot, int n_past, hipStream_t st, char *err, size_t errlen) {
     xj_stage *s = &S->s;
     if (n_past < 0 || n_past > s->n_ctx) { snprintf(err, errlen, "bad n_past %d", n_past); return -1; }
-    for (auto &L : S->L) {
-        if (!L.rec) continue;
-        if (!L.snap_conv[slot]) { snprintf(err, errlen, "snapshot slot %d is empty", slot); return -1; }
-        if (hipMemcpyAsync(L.conv, L.snap_conv[slot], S->conv_n * 4, hipMemcpyDeviceToDevice, st) != hipSuccess ||
-            hipMemcpyAsync(L.ssm, L.snap_ssm[slot], S->ssm_n * 4, hipMemcpyDeviceToDevice, st) != hipSuccess) {
-            snprintf(err, errlen, "restore copy failed");
-            return -1;
-        }
+    for (auto &L : S->L)
+        if (L.rec && !L.snap_conv[slot]) { snprintf(err, errlen, "snapshot slot %d is empty", slot); return -1; }
+    if (states_copy(S, st, [&](HLayer &L, const float *&cs, float *&cd, const float *&ss, float *&sd) {
+            cs = L.snap_conv[slot]; cd = L.conv;
+            ss = L.snap_ssm[slot]; sd = L.ssm;
+        })) {
+        snprintf(err, errlen, "restore copy failed");
+        return -1;
     }
     s->n_past = n_past;
     s->ck_T = 0;
@@ -981,18 +1001,7 @@ static int restore_enqueue(HStage *S, int slot, int n_past, hipStream_t st, char
 extern "C" int xj_hip_stage_restore(xj_stage *s, int slot, int n_past, char *err, size_t errlen) {
     HStage *S = H(s);
     if (slot < 0 || slot >= kDecodeSlot) { snprintf(err, errlen, "snapshot slot %d out of range", slot); return -1; }
-    if (n_past < 0 || n_past > s->n_ctx) { snprintf(err, errlen, "bad n_past %d", n_past); return -1; }
-    for (auto &L : S->L) {
-        if (!L.rec) continue;
-        if (!L.snap_conv[slot]) { snprintf(err, errlen, "snapshot slot %d is empty", slot); return -1; }
-        if (hipMemcpyAsync(L.conv, L.snap_conv[slot], S->conv_n * 4, hipMemcpyDeviceToDevice, S->st) != hipSuccess ||
-            hipMemcpyAsync(L.ssm, L.snap_ssm[slot], S->ssm_n * 4, hipMemcpyDeviceToDevice, S->st) != hipSuccess) {
-            snprintf(err, errlen, "restore copy failed");
-            return -1;
-        }
-    }
-    s->n_past = n_past;
-    s->ck_T = 0;
+    if (restore_enqueue(S, slot, n_past, S->st, err, errlen)) return -1;
     return sync_check(S, err, errlen);
 }
 
@@ -1454,12 +1463,37 @@ static int draft_step(xjh_chain *d, int t, int *next, char *err, size_t errlen) 
 }
 
 // kk greedy steps of the draft fed with token t, the state after step j in
-// snapshot slot j: one set-up, the decode graph replayed kk times with the
+// snapshot slot j (j < kk - 1; the last state is the draft's own): one set-up, the decode graph replayed kk times with the
 // snapshot copies between the replays on the chain's stream, one
-// synchronisation; toks receives the kk argmax tokens.
-static int draft_run(xjh_chain *d, int t, int kk, int32_t *toks, char *err, size_t errlen) {
+// synchronisation; toks receives the kk argmax tokens. catch_tok >= 0: a
+// token the draft has not been fed yet, before t (the last draft of a fully
+// accepted round): it and t go in as one two-token pass, whose rows are
+// those of two steps bit for bit, instead of a step of their own.
+static int draft_run(xjh_chain *d, int catch_tok, int t, int kk, int32_t *toks, char *err, size_t errlen) {
+    if (catch_tok >= 0 && d->mb < 2) {
+        int nx;
+        if (draft_step(d, catch_tok, &nx, err, errlen)) return -1;
+        catch_tok = -1;
+    }
+    int done = 0;
+    if (catch_tok >= 0) {
+        const int32_t in2[2] = {catch_tok, t};
+        int32_t am = -1;
+        if (chain_eval(d, in2, 2, 1, 0, nullptr, &am, err, errlen)) return -1;
+        if (kk > 1)
+            for (auto *S : d->st)
+                if (snapshot_enqueue(S, 0, d->stream, err, errlen)) return -1;
+        toks[0] = am;
+        t = am;
+        done = 1;
+        if (kk == 1) {
+            d->last_tok = am;
+            return chain_sync(d, err, errlen);
+        }
+    }
+    const int n = kk - done;
     for (auto *S : d->st) {
-        if (S->s.n_past + kk > S->s.n_ctx) { snprintf(err, errlen, "context full (%d)", S->s.n_ctx); return -1; }
+        if (S->s.n_past + n > S->s.n_ctx) { snprintf(err, errlen, "context full (%d)", S->s.n_ctx); return -1; }
         if (reset_check(S, err, errlen)) return -1;
     }
     const bool direct = env_int("XJ_DECODE_GRAPH", 1) == 0;
@@ -1472,19 +1506,20 @@ static int draft_run(xjh_chain *d, int t, int kk, int32_t *toks, char *err, size
     }
     for (auto *S : d->st) if (set_npast(S, d->stream)) { snprintf(err, errlen, "draft setup failed"); return -1; }
     if (embed_first(d)) { snprintf(err, errlen, "draft setup failed"); return -1; }
-    for (int j = 0; j < kk; j++) {
+    for (int j = 0; j < n; j++) {
         if (direct ? enqueue_decode_step(d, false) != 0 : hipGraphLaunch(d->exec, d->stream) != hipSuccess) {
             snprintf(err, errlen, "draft step launch failed"); return -1;
         }
-        for (auto *S : d->st)
-            if (snapshot_enqueue(S, j, d->stream, err, errlen)) return -1;
+        if (done + j < kk - 1)   // the state after the last step stays in place
+            for (auto *S : d->st)
+                if (snapshot_enqueue(S, done + j, d->stream, err, errlen)) return -1;
     }
-    if (hipMemcpyAsync(&d->h_buf[2], d->d_hist, 4 * kk, hipMemcpyDeviceToHost, d->stream) != hipSuccess) {
+    if (hipMemcpyAsync(&d->h_buf[2], d->d_hist, 4 * n, hipMemcpyDeviceToHost, d->stream) != hipSuccess) {
         snprintf(err, errlen, "draft history copy failed"); return -1;
     }
     if (chain_sync(d, err, errlen)) return -1;
-    for (int j = 0; j < kk; j++) toks[j] = d->h_buf[2 + j];
-    for (auto *S : d->st) S->s.n_past += kk;
+    for (int j = 0; j < n; j++) toks[done + j] = d->h_buf[2 + j];
+    for (auto *S : d->st) S->s.n_past += n;
     d->last_tok = toks[kk - 1];
     return 0;
 }
@@ -1507,6 +1542,7 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
     long n_gen_tok = 0;
     int pending = tgt->last_tok;
     const bool smp = sampling(tgt);
+    int catch_tok = -1;   // the last draft of a fully accepted round, not fed to the draft yet
     while (produced < n_gen) {
         if (is_end(hp, pending)) { out[produced++] = pending; break; }   // returned, never fed (xj_spec.c:139)
         const int P = tgt->st[0]->s.n_past;
@@ -1517,6 +1553,8 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
         if (kk <= 0) {   // no room to speculate: plain step on both models (the target's token drawn)
             out[produced++] = pending;
             int32_t nt, dn;
+            if (catch_tok >= 0 && xjh_chain_eval(dft, &catch_tok, 1, 1, 0, nullptr, &dn, err, errlen)) return -1;
+            catch_tok = -1;
             if (xjh_chain_eval(tgt, &pending, 1, 1, 0, nullptr, &nt, err, errlen) ||
                 xjh_chain_eval(dft, &pending, 1, 1, 0, nullptr, &dn, err, errlen)) return -1;
             pending = tgt->last_tok;
@@ -1527,7 +1565,8 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
         const double t0 = now_ms();
         int32_t toks[5];
         toks[0] = pending;
-        if (draft_run(dft, pending, kk, toks + 1, err, errlen)) return -1;
+        if (draft_run(dft, catch_tok, pending, kk, toks + 1, err, errlen)) return -1;
+        catch_tok = -1;
         st.t_draft_ms += now_ms() - t0;
         for (int j = 1; j <= kk && oracle; j++) {
             const long gi = n_gen_tok + j;   // index of the generated token this draft stands for
@@ -1554,16 +1593,21 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
         if (fed < kk + 1 && xjh_chain_rollback(tgt, P + fed, err, errlen)) return -1;
         // 4) bring the draft to the same prefix [.., t, d1..d(fed-1)]: slot j holds
         //    its state after feeding toks[0..j]
-        if (fed < kk + 1) {
+        if (fed < kk) {
             for (auto *S : dft->st)
                 if (xj_hip_stage_restore(&S->s, fed - 1, P + fed, err, errlen)) return -1;
+        } else if (fed == kk) {
+            // the draft already holds the state after toks[0..kk-1] at n_past P + kk
         } else {
-            int nx;
-            if (draft_step(dft, toks[kk], &nx, err, errlen)) return -1;
+            catch_tok = toks[kk];   // fed with the next round's first token
         }
         if (n_out > fed) { pending = toks[fed]; break; }   // stopped at an accepted end token
         pending = am[a];
         tgt->last_tok = pending;
+    }
+    if (catch_tok >= 0) {   // the draft ends fed with the target's prefix, as each round leaves it
+        int nx;
+        if (draft_step(dft, catch_tok, &nx, err, errlen)) return -1;
     }
     (void)hipEventRecord(tgt->ev1, tgt->stream);
     st.t_total_ms = now_ms() - t_start;
