@@ -181,7 +181,7 @@ struct AttnArgs {
     uint8_t *xq;                         // optional: prepared activations of out (no prologue)
 };
 int attn_launch(const AttnArgs &a, hipStream_t st);
-int attn_splits(int n_ctx);             // 32-position splits covering n_ctx
+int attn_splits(int n_ctx);             // 64-position splits covering n_ctx
 
 struct DeltaArgs {
     const float *qkv; int32_t qkv_s;    // conv+SiLU outputs [T][conv_dim]

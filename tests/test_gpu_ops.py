@@ -93,7 +93,8 @@ ATTN_CASES = [
     # T, H, Hkv, D, n_rot, n_past, n_ctx
     (1, 16, 4, 256, 64, 0, 64),        # first token
     (1, 16, 4, 256, 64, 777, 1024),    # fused single-token path
-    (1, 8, 2, 256, 64, 2500, 4096),    # 79 splits (> 64) in the combine
+    (1, 8, 2, 256, 64, 2500, 4096),    # 40 splits of 64 positions
+    (1, 8, 2, 128, 64, 4200, 4608),    # 66 splits (> 64) in the combine
     (4, 16, 4, 256, 64, 2600, 4096),   # kv_store + split path
     (3, 8, 2, 128, 128, 31, 128),      # the batch crosses a split boundary
     (5, 8, 8, 64, 32, 60, 96),         # G = 1
