@@ -106,6 +106,10 @@ __global__ __launch_bounds__(256) void prep_kernel(const GArgs a) {
         const double ss = xjd::group_ss(xr);
         if (in && (k & 31) == 0) ((double *)(dst + o.ss_off))[k >> 5] = ss;
     }
+    if (a.hq) {   // K % 256 == 0: every thread holds an element
+        __shared__ float hred[4];
+        xjd::emit_hq(v, tid, a.hq + (int64_t)t * hq_stride(K) + (int64_t)blockIdx.x * kHqBlk, hred);
+    }
 }
 
 // -------------------------------------------------------- unit kernels --
@@ -1405,6 +1409,7 @@ int prep_launch(const GArgs &a, hipStream_t st) {
     if (a.T < 1 || a.K < 32 || a.K % 32 || !a.xq) return -1;
     if (a.pro == PRO_GATED_RMS && (a.group < 1 || a.K % a.group)) return -1;
     if ((a.pro == PRO_RMSU || a.pro == PRO_GATED_RMS) && !a.pro_w) return -1;
+    if (a.hq && a.K % 256) return -1;
     hipLaunchKernelGGL(prep_kernel, dim3((a.K + 255) / 256, a.T), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -93,6 +93,7 @@ struct GArgs {
     int32_t rpw;                   // rows per work-group (set by the launcher for per-CU launches)
     int32_t nseg;
     GSeg seg[kMaxSeg];
+    uint8_t *hq;                   // prep launch, K % 256 == 0: also the GEMM's activations [T][hq_stride(K)]
 };
 
 // Launch plan of one GEMV over `rows` output rows of inner size K: a team of
@@ -103,7 +104,8 @@ struct GemvPlan {
 };
 GemvPlan gemv_plan(int K, int64_t rows);
 
-// prep kernel: xq for the T tokens of a tile (grid ceil(K/256) x T)
+// prep kernel: xq for the T tokens of a tile (grid ceil(K/256) x T), and hq
+// when a.hq is set
 int prep_launch(const GArgs &a, hipStream_t st);
 // One GEMV launch (T <= kTileT) over all segments, reading a.xq. Segment i
 // covers row groups [wg0, wg0+nwg) with nwg = ceil(n_rows / rows_per_group)
@@ -118,7 +120,7 @@ size_t gemv_xq_bytes(int K);                    // xq bytes for the largest tile
 
 // Multi-token GEMM on the matrix cores (gemm.hip): for each segment i,
 // y_i[t][r] (+)= (W_i[r] . v[t]) (* tsc[t]) for T in 1..gemm_max_tokens()
-// tokens of prepared activations (xq, stride xs per token); every segment of
+// tokens of the prep launch's hq records (stride hs per token); every segment of
 // one launch has the same type (Q4_K or Q6_K) and inner size K. One
 // persistent work-group per CU takes an equal, contiguous share of the
 // (row group of 128 rows, 256-element block) units of all segments; a row
@@ -132,7 +134,7 @@ struct GemmSeg {
 };
 struct GemmArgs {
     uint32_t type; int32_t K, T;
-    const uint8_t *xq; int64_t xs;
+    const uint8_t *hq; int64_t hs;      // the T tokens' hq records (xq.h), token stride hs
     int32_t nseg;
     GemmSeg seg[kGemmMaxSeg];
     // optional: y[t][r] = (sum) * tsc[t] before the add (an RMSNorm input's
@@ -153,6 +155,9 @@ int gemm_counters(int64_t rows);
 // stride xs): tsc[t] = 1 / sqrt(sum of the groups' ss / K + eps), the
 // GEMV's rmsu_scale.
 int rms_scale_launch(const uint8_t *xq, int64_t xs, int K, int T, float eps, float *tsc, hipStream_t st);
+// hq records (token stride hq_stride(K)) of T tokens of prepared activations
+// (xq, token stride xq_off(K).stride) from their v values.
+int hq_from_v_launch(const uint8_t *xq, int K, int T, uint8_t *hq, hipStream_t st);
 // *p += by on the device, in stream order (one thread).
 int inc_launch(int32_t *p, int32_t by, hipStream_t st);
 int gemm_max_tokens();

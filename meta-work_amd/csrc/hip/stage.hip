@@ -80,6 +80,7 @@ struct HStage {
     // prefill on the matrix cores: per-token RMSNorm scales, the GEMM's K-split
     // partials and the chunked delta rule's work area
     float *tsc = nullptr, *gpart = nullptr, *dwork = nullptr;
+    uint8_t *hq = nullptr;     // the GEMM's activations, max_batch tokens of the largest input
     int64_t gpart_floats = 0;
     int32_t *gcnt = nullptr;   // the GEMM's arrival counters (zero between launches)
     int32_t n_gcnt = 0;
@@ -184,8 +185,9 @@ struct Gemv {
     Profile *prof = nullptr;
     bool prepared = false;
     explicit Gemv(uint8_t *xq, Profile *p = nullptr) : prof(p) { a.xq = xq; }
-    Gemv(uint8_t *xq, Profile *p, float *tsc_, float *part_, int64_t part_floats_, int32_t *cnt_, int32_t n_cnt_)
-        : prof(p), tsc(tsc_), part(part_), part_floats(part_floats_), cnt(cnt_), n_cnt(n_cnt_) {
+    Gemv(uint8_t *xq, Profile *p, float *tsc_, float *part_, int64_t part_floats_, int32_t *cnt_, int32_t n_cnt_,
+         uint8_t *hq_)
+        : prof(p), tsc(tsc_), part(part_), part_floats(part_floats_), cnt(cnt_), n_cnt(n_cnt_), hq(hq_) {
         a.xq = xq;
     }
     Gemv &seg(const DevW &w, float *y, int ys, int epi) {
@@ -235,6 +237,12 @@ struct Gemv {
     int64_t part_floats = 0;
     int32_t *cnt = nullptr;
     int32_t n_cnt = 0;
+    // the GEMM's activations (hq records, xq.h): built by the prep launch; for
+    // a prepared input, already built by the previous GEMM's SwiGLU prep
+    // (hq_ready) or else from the prepared values
+    uint8_t *hq = nullptr;
+    bool hq_ready = false;
+    bool hq_out = false;   // set by a GEMM run whose SwiGLU prep built the next input's hq
     // Chunks of at least kGemmMinT tokens take the matrix-core GEMM
     // (gemm.hip): the prep launch builds the T tokens' activations once, the
     // RMSNorm scale is applied per token after the dot products (as the GEMV
@@ -244,7 +252,7 @@ struct Gemv {
     static constexpr int kGemmMinT = 16;
     bool gemm_ok(int T) const {
         static const bool on = env_int("XJ_PREFILL_GEMM", 1) != 0;
-        if (!on || T < kGemmMinT || prof || !tsc || !part || !cnt || !a.xq) return false;
+        if (!on || T < kGemmMinT || prof || !tsc || !part || !cnt || !a.xq || !hq) return false;
         if (a.pro != PRO_NONE && a.pro != PRO_RMSU && a.pro != PRO_SWIGLU && a.pro != PRO_GATED_RMS) return false;
         if (a.post.mode != POST_NONE && a.post.mode != POST_SWIGLU) return false;
         if (a.K % 256) return false;
@@ -253,11 +261,14 @@ struct Gemv {
         return any;
     }
     int run_gemm(int T, hipStream_t st) {
-        const int64_t xs = xq_off(a.K).stride;
+        const int64_t xs = xq_off(a.K).stride, hs = hq_stride(a.K);
         if (!prepared) {   // the T tokens' activations, once
             GArgs b = a;
             b.T = T;
+            b.hq = hq;
             if (prep_launch(b, st)) return -1;
+        } else if (!hq_ready && hq_from_v_launch(a.xq, a.K, T, hq, st)) {
+            return -1;
         }
         const bool rms = a.pro == PRO_RMSU;
         if (rms && rms_scale_launch(a.xq, xs, a.K, T, a.eps, tsc, st)) return -1;
@@ -265,7 +276,7 @@ struct Gemv {
         // the segments of each type in one launch, sharing the activations
         for (uint32_t ty : {(uint32_t)XJ_Q4_K, (uint32_t)XJ_Q6_K}) {
             GemmArgs g{};
-            g.type = ty; g.K = a.K; g.xs = xs; g.part = part; g.cnt = cnt;
+            g.type = ty; g.K = a.K; g.hs = hs; g.part = part; g.cnt = cnt;
             for (int i = 0; i < a.nseg; i++) {
                 const GSeg &s = a.seg[i];
                 if (s.type != ty) continue;
@@ -275,7 +286,7 @@ struct Gemv {
             for (int t0 = 0; t0 < T; t0 += mt) {
                 GemmArgs b = g;
                 b.T = T - t0 < mt ? T - t0 : mt;
-                b.xq = a.xq + t0 * xs;
+                b.hq = hq + t0 * hs;
                 for (int i = 0; i < b.nseg; i++) b.seg[i].y = g.seg[i].y + (int64_t)t0 * g.seg[i].ys;
                 b.tsc = rms ? tsc + t0 : nullptr;
                 if (gemm_launch(b, part_floats, n_cnt, st)) return -1;
@@ -313,7 +324,9 @@ struct Gemv {
             GArgs b{};
             b.x = a.seg[0].y; b.xs = a.seg[0].ys; b.x2 = a.seg[1].y; b.x2s = a.seg[1].ys;
             b.pro = PRO_SWIGLU; b.K = a.seg[0].n_rows; b.T = T; b.xq = a.post.xq;
+            if (b.K % 256 == 0) b.hq = hq;   // the down projection's GEMM input as well
             if (prep_launch(b, st)) return -1;
+            hq_out = b.hq != nullptr;
         }
         if (a.inc_ptr && inc_launch(a.inc_ptr, a.inc_by, st)) return -1;
         return 0;
@@ -374,7 +387,7 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
     HLayer &L = S->L[il - S->s.l0];
     const int E = hp.n_embd, FF = hp.n_ff;
     // every GEMV of the layer with the stage's prefill buffers
-    auto gemv = [&](uint8_t *xq) { return Gemv(xq, pf, S->tsc, S->gpart, S->gpart_floats, S->gcnt, S->n_gcnt); };
+    auto gemv = [&](uint8_t *xq) { return Gemv(xq, pf, S->tsc, S->gpart, S->gpart_floats, S->gcnt, S->n_gcnt, S->hq); };
     auto rms_in = [&](Gemv &g, const float *w) {
         g.a.x = x; g.a.xs = E; g.a.pro = PRO_RMSU; g.a.pro_w = w; g.a.eps = hp.eps;
     };
@@ -474,6 +487,7 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
         dn.a.x = S->g; dn.a.xs = FF; dn.a.pro = PRO_X;
     } else {
         dn.prepared = true;
+        dn.hq_ready = f.hq_out;
     }
     dn.a.inc_ptr = inc; dn.a.inc_by = T;
     dn.seg(L.ffn_down, x, E, EPI_ADD);
@@ -735,7 +749,7 @@ extern "C" uint64_t xj_hip_stage_state_bytes(const xj_model *m, int l0, int l1, 
     // prefill on the matrix cores: RMSNorm scales, K-split partials and counters, chunked-rule work
     const int64_t grows = 2 * (int64_t)scratch_floats(hp) + 2 * (int64_t)hp.h_v;
     b += 4ull * max_batch + 4ull * gemm_part_floats(grows, max_batch < gemm_max_tokens() ? max_batch : gemm_max_tokens()) +
-         4ull * gemm_counters(grows);
+         4ull * gemm_counters(grows) + (uint64_t)max_batch * hq_stride((int)scratch_floats(hp));
     bool rec = false;
     for (int il = l0; il < l1 && il < (int)hp.n_layer; il++) rec = rec || m->layers[il].recurrent;
     if (rec) b += delta_chunked_work_bytes(hp.h_v, hp.s_k, max_batch, 64);
@@ -876,7 +890,8 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
     S->gpart = dalloc<float>(S, (size_t)S->gpart_floats, err, errlen);
     S->n_gcnt = gemm_counters(grows);
     S->gcnt = dalloc<int32_t>(S, (size_t)S->n_gcnt, err, errlen);
-    if (!S->tsc || !S->gpart || !S->gcnt) return fail();
+    S->hq = dalloc<uint8_t>(S, mb * (size_t)hq_stride((int)sf), err, errlen);
+    if (!S->tsc || !S->gpart || !S->gcnt || !S->hq) return fail();
     XJ_CHECK(hipMemset(S->gcnt, 0, (size_t)S->n_gcnt * 4), err, errlen, fail());
     {
         bool rec = false;
@@ -2020,17 +2035,24 @@ extern "C" int xjh_gemv_noalloc(uint32_t type, const void *dw, int64_t n_rows, i
 // Prepared activations of T tokens (prep launch) and the matrix-core GEMM.
 static int gemm_enqueue(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T, float *y, int add,
                         hipStream_t st) {
-    static uint8_t *xq = nullptr;   // grown on demand; the per-op entries are synchronous on one stream
+    static uint8_t *xq = nullptr, *hq = nullptr;   // grown on demand; the per-op entries are synchronous on one stream
     static float *part = nullptr;
     static int32_t *cnt = nullptr;
-    static size_t xq_cap = 0, part_cap = 0, cnt_cap = 0;
-    const int64_t xs = xq_off((int)k).stride;
-    const size_t need = (size_t)T * xs, pneed = (size_t)gemm_part_floats(n_rows, T), cneed = (size_t)gemm_counters(n_rows);
+    static size_t xq_cap = 0, hq_cap = 0, part_cap = 0, cnt_cap = 0;
+    const int64_t xs = xq_off((int)k).stride, hs = hq_stride((int)k);
+    const size_t need = (size_t)T * xs, hneed = (size_t)T * hs, pneed = (size_t)gemm_part_floats(n_rows, T),
+                 cneed = (size_t)gemm_counters(n_rows);
     if (need > xq_cap) {
         if (xq) (void)hipFree(xq);
         xq = nullptr, xq_cap = 0;
         if (hipMalloc(&xq, need) != hipSuccess) return -1;
         xq_cap = need;
+    }
+    if (hneed > hq_cap) {
+        if (hq) (void)hipFree(hq);
+        hq = nullptr, hq_cap = 0;
+        if (hipMalloc(&hq, hneed) != hipSuccess) return -1;
+        hq_cap = hneed;
     }
     if (pneed > part_cap) {
         if (part) (void)hipFree(part);
@@ -2045,10 +2067,10 @@ static int gemm_enqueue(uint32_t type, const void *dw, int64_t n_rows, int64_t k
         cnt_cap = cneed;
     }
     GArgs p{};
-    p.x = x; p.xs = (int32_t)k; p.pro = PRO_NONE; p.xq = xq; p.K = (int32_t)k; p.T = T;
+    p.x = x; p.xs = (int32_t)k; p.pro = PRO_NONE; p.xq = xq; p.K = (int32_t)k; p.T = T; p.hq = hq;
     if (prep_launch(p, st)) return -1;
     GemmArgs g{};
-    g.type = type; g.K = (int32_t)k; g.T = T; g.xq = xq; g.xs = xs; g.part = part; g.cnt = cnt;
+    g.type = type; g.K = (int32_t)k; g.T = T; g.hq = hq; g.hs = hs; g.part = part; g.cnt = cnt;
     g.nseg = 1;
     g.seg[0] = GemmSeg{(const uint8_t *)dw, (int32_t)n_rows, y, (int32_t)n_rows, add};
     return gemm_launch(g, (int64_t)part_cap, (int)cnt_cap, st);

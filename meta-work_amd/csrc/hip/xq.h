@@ -38,6 +38,19 @@ __host__ __device__ inline XqOff xq_off(int K) {
     return o;
 }
 
+// The matrix-core GEMM's activations ("hq"), built by the same prep launches
+// for chunks of tokens. Per token, for each 256-element block b of the K
+// inputs, a record of kHqBlk bytes:
+//   hi [256] f16, lo [256] f16   v * 2^-e = hi + lo, each rounded to nearest:
+//                                e is the block's exponent, max|v| < 2^(e+14),
+//                                so hi + lo carries about 22 bits of v
+//   sx [8] float                 sum of (hi + lo) * 2^e over each 32-element group
+//   e  int32, then 12 bytes of padding
+// The record is 67 chunks of 16 bytes (an odd count, so the GEMM's LDS reads
+// of 16 tokens fall on distinct banks); tokens are hq_stride(K) bytes apart.
+constexpr int kHqBlk = 1072;
+__host__ __device__ inline int64_t hq_stride(int K) { return ((int64_t)(K / 256) * kHqBlk + 255) & ~(int64_t)255; }
+
 }  // namespace xjk
 
 #ifdef __HIPCC__
@@ -85,6 +98,29 @@ __device__ __forceinline__ void emit_xq(float v, int k, bool in, uint8_t *dst, c
     if (l == 0) ((float *)(dst + o.f_off))[g] = ldexpf(1.0f, E - 20);
     if ((k & 15) == 0) ((int *)(dst + o.sx_off))[k >> 4] = sx;
     if (with_v) ((float *)(dst + o.v_off))[k] = v;
+}
+
+// Writes element tid (value v) of one token's block record rec (kHqBlk bytes,
+// layout above). Called by all 256 threads of a work-group, tid = threadIdx.x,
+// with the block's 256 elements; red4 is 4 floats of LDS. Contains a barrier.
+__device__ __forceinline__ void emit_hq(float v, int tid, uint8_t *rec, float *red4) {
+    float m = wave_max(fabsf(v));
+    if ((tid & 63) == 0) red4[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3]));
+    int E = 0;
+    (void)frexpf(m, &E);   // m < 2^E
+    if (E < -100) E = -100;
+    const int e = E - 14;
+    const float s = ldexpf(v, -e);
+    const _Float16 hi = (_Float16)s;
+    const _Float16 lo = (_Float16)(s - (float)hi);   // s - hi is exact in fp32
+    ((_Float16 *)rec)[tid] = hi;
+    ((_Float16 *)(rec + 512))[tid] = lo;
+    float r = (float)hi + (float)lo;
+    for (int off = 1; off < 32; off <<= 1) r += __shfl_xor(r, off, 64);
+    if ((tid & 31) == 0) ((float *)(rec + 1024))[tid >> 5] = ldexpf(r, e);
+    if (tid < 4) ((int *)(rec + 1056))[tid] = tid ? 0 : e;
 }
 
 // Sum of x^2 (double) over the 32 lanes of a half-wavefront, in a fixed

@@ -1,7 +1,9 @@
 """The matrix-core GEMM for prefill chunks (xjh_gemm) against the oracle's
 matmul (src/xiaoju-pipe/core/xj_cpu.c:36-54), a float64 product of the same
-dequantized weights, and the dot-product GEMV (xjh_gemv), whose integer
-sub-block sums it shares."""
+dequantized weights, and the dot-product GEMV (xjh_gemv). The GEMM's
+products are exact (f16 halves of the activations times small-integer
+weights) and only its fp32 accumulation rounds: ~1e-7 of the float64
+product; the GEMV's 21-bit activations put it ~1e-6 away."""
 import numpy as np
 import pytest
 
@@ -34,11 +36,12 @@ def test_gemm_matches_oracle_and_gemv(t, rows, k, T):
     assert rel_l2(got, want) < 1e-3
     wd = orc.dequant_rows(t, blob, rows, k).astype(np.float64)
     ref64 = xs.astype(np.float64) @ wd.T
-    assert rel_l2(got, ref64) < 1e-5
-    # same integer sums as the GEMV: only the fp32 order of the sub-block terms differs
+    assert rel_l2(got, ref64) < 1e-6
+    # the GEMV on the same inputs: both within ~1e-6 of the float64 product
     gv = np.concatenate([xp.gemv(w, xs[i:i + 5]) for i in range(0, T, 5)])
-    assert rel_l2(got, gv) < 1e-6
-    assert np.max(np.abs(got - gv)) <= 1e-5 * np.max(np.abs(gv))
+    assert rel_l2(gv, ref64) < 3e-6
+    assert rel_l2(got, gv) < 3e-6
+    assert np.max(np.abs(got - gv)) <= 5e-6 * np.max(np.abs(gv))
 
 
 @pytest.mark.parametrize("t", [xp.Q4_K, xp.Q6_K])
@@ -53,7 +56,7 @@ def test_gemm_random_blocks_and_residual_add(t):
     finite = np.isfinite(wd).all(axis=1)
     ref64 = xs.astype(np.float64) @ np.where(np.isfinite(wd), wd, 0).T
     got = xp.gemm(w, xs)
-    assert rel_l2(got[:, finite], ref64[:, finite]) < 1e-5
+    assert rel_l2(got[:, finite], ref64[:, finite]) < 1e-6
     base = xp.fill_normal(T * rows, 9, 1.0).reshape(T, rows)
     got2 = xp.gemm(w, xs, add_to=base)
     assert np.array_equal(got2[:, finite], (base + got)[:, finite])
