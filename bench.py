@@ -550,9 +550,10 @@ def main():
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32",
-        "dtype_note": ("fp32 arithmetic; the GEMV/GEMM inputs enter as 21-bit fixed point per 32-element group "
+        "dtype_note": ("fp32 arithmetic; the GEMV inputs enter as 21-bit fixed point per 32-element group "
                        "(three int8 digit planes, exact int32 sub-block sums, <= 2^-21 of the group maximum per "
-                       "element), KV cache fp16"),
+                       "element); the prefill GEMM's as two f16 planes per 256-element block (exact f16 products "
+                       "with integer-valued weights, fp32 accumulation); KV cache fp16"),
         "data": "synthetic (random-init weights, uniform random prompt ids)",
         "config": {"workload": "greedy decode, synthetic hybrid 4B shape: hidden 2560, 32 layers (24 Gated-DeltaNet "
                                "32x128 + 8 gated GQA 16q/4kv d256), FFN 9216, vocab 151936, Q4_K_M-style "
