@@ -292,9 +292,11 @@ int xjh_gemv(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const flo
 int xjh_gemv_noalloc(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T,
                      float *y, int add, char *err, size_t errlen);
 /* The same product for a prefill chunk on the matrix cores: Q4_K or Q6_K
- * rows, k % 256 == 0, T in 1..64. Integer sub-block sums are those of
- * xjh_gemv (v_mfma_i32_16x16x32_i8 in place of dot4), so the two agree to
- * fp32 rounding. Counterpart of the Metal batched kernel mvb
+ * rows, k % 256 == 0, T in 1..64. The activations enter as two f16 planes per
+ * 256-element block (v * 2^-e = hi + lo) and the weights as integers exact in
+ * f16, so every product is exact and only the fp32 accumulation rounds
+ * (~1e-7 of the float64 product; xjh_gemv, with 21-bit activations, agrees
+ * to ~1e-6). Counterpart of the Metal batched kernel mvb
  * (src/xiaoju-pipe/metal/xj_kernels.metal:84-388) for long batches. */
 int xjh_gemm(uint32_t type, const void *dw, int64_t n_rows, int64_t k, const float *x, int T,
              float *y, int add, char *err, size_t errlen);
