@@ -494,10 +494,16 @@ int enqueue_layer(HStage *S, int il, float *x, int T, int keep_n, int32_t *inc, 
     return dn.run(T, st);
 }
 
-int enqueue_layers(HStage *S, float *x, int T, int keep_n, bool inc, hipStream_t st, Profile *pf = nullptr) {
-    for (int il = S->s.l0; il < S->s.l1; il++)
-        if (enqueue_layer(S, il, x, T, keep_n, inc && il + 1 == S->s.l1 ? S->npast : nullptr, st, pf)) return -1;
+// Layers [lo, hi) of the stage; inc: the stage's position counter advances
+// by T after the last of them.
+int enqueue_layer_range(HStage *S, int lo, int hi, float *x, int T, int keep_n, bool inc, hipStream_t st,
+                        Profile *pf = nullptr) {
+    for (int il = lo; il < hi; il++)
+        if (enqueue_layer(S, il, x, T, keep_n, inc && il + 1 == hi ? S->npast : nullptr, st, pf)) return -1;
     return 0;
+}
+int enqueue_layers(HStage *S, float *x, int T, int keep_n, bool inc, hipStream_t st, Profile *pf = nullptr) {
+    return enqueue_layer_range(S, S->s.l0, S->s.l1, x, T, keep_n, inc, st, pf);
 }
 
 // logits[t] = output . rmsnorm(x[t]) * output_norm; greedy partial keys into S->amax
@@ -690,6 +696,109 @@ void hip_reset(xj_stage *s) {
     s->n_past = 0;
 }
 
+static size_t scratch_floats(const xj_hparams &hp) {
+    size_t n = (size_t)hp.n_ff;
+    const size_t qkv = 2 * (size_t)hp.n_head * hp.head_dim + 2 * (size_t)hp.n_head_kv * hp.head_dim;
+    if (qkv > n) n = qkv;
+    if ((size_t)hp.conv_dim > n) n = hp.conv_dim;
+    if ((size_t)hp.n_embd * 2 > n) n = 2 * (size_t)hp.n_embd;
+    return n;
+}
+
+// The scratch of a stage's forward passes (max_batch tokens): hidden rows,
+// projections, attention partials, prepared activations, the prefill
+// GEMM's buffers and the chunked rule's work area, and its position counter.
+static bool alloc_scratch(HStage *S, char *err, size_t errlen) {
+    const xj_hparams &hp = S->s.m->hp;
+    const size_t mb = S->s.max_batch, E = hp.n_embd;
+    const int n_ctx = S->s.n_ctx;
+    const size_t sf = scratch_floats(hp);
+    S->x = dalloc<float>(S, mb * E, err, errlen);
+    S->qkv = dalloc<float>(S, mb * sf, err, errlen);
+    S->kb = dalloc<float>(S, mb * sf, err, errlen);
+    S->vb = dalloc<float>(S, mb * sf, err, errlen);
+    S->z = dalloc<float>(S, mb * sf, err, errlen);
+    S->beta = dalloc<float>(S, mb * (hp.h_v + 1), err, errlen);
+    S->alpha = dalloc<float>(S, mb * (hp.h_v + 1), err, errlen);
+    S->o = dalloc<float>(S, mb * sf, err, errlen);
+    S->g = dalloc<float>(S, mb * sf, err, errlen);
+    S->u = dalloc<float>(S, mb * sf, err, errlen);
+    S->qr = dalloc<float>(S, mb * hp.n_head * (size_t)hp.head_dim, err, errlen);
+    S->scores = dalloc<float>(S, mb * hp.n_head * (size_t)attn_splits(n_ctx) * (hp.head_dim + 2), err, errlen);
+    S->npast = dalloc<int32_t>(S, 1, err, errlen);
+    // prefill on the matrix cores (chunks of at least 16 tokens)
+    S->tsc = dalloc<float>(S, mb, err, errlen);
+    // every GEMM launch covers at most 2 sf + 2 h_v rows (gate|up, the DeltaNet in-projection)
+    const int64_t grows = 2 * (int64_t)sf + 2 * (int64_t)hp.h_v;
+    S->gpart_floats = gemm_part_floats(grows, (int)(mb < gemm_max_tokens() ? mb : gemm_max_tokens()));
+    S->gpart = dalloc<float>(S, (size_t)S->gpart_floats, err, errlen);
+    S->n_gcnt = gemm_counters(grows);
+    S->gcnt = dalloc<int32_t>(S, (size_t)S->n_gcnt, err, errlen);
+    S->hq = dalloc<uint8_t>(S, mb * (size_t)hq_stride((int)sf), err, errlen);
+    if (!S->tsc || !S->gpart || !S->gcnt || !S->hq) return false;
+    XJ_CHECK(hipMemset(S->gcnt, 0, (size_t)S->n_gcnt * 4), err, errlen, false);
+    {
+        bool rec = false;
+        for (int il = S->s.l0; il < S->s.l1 && il < hp.n_layer; il++) rec = rec || S->s.m->layers[il].recurrent;
+        const size_t wb = rec ? delta_chunked_work_bytes(hp.h_v, hp.s_k, (int)mb, 64) : 0;
+        if (wb) {
+            S->dwork = (float *)dalloc<uint8_t>(S, wb, err, errlen);
+            if (!S->dwork) return false;
+        }
+    }
+    {
+        auto xqb = [&](int K) { return K >= 32 ? mb * (size_t)xq_off(K).stride : 256; };
+        S->xq_e = dalloc<uint8_t>(S, xqb(hp.n_embd), err, errlen);
+        S->xq_di = dalloc<uint8_t>(S, xqb(hp.d_inner), err, errlen);
+        S->xq_att = dalloc<uint8_t>(S, xqb(hp.n_head * hp.head_dim), err, errlen);
+        S->xq_ff = dalloc<uint8_t>(S, xqb(hp.n_ff), err, errlen);
+        const size_t nc = (size_t)(hp.n_ff / 32) + 1;
+        int32_t *cnt = dalloc<int32_t>(S, nc, err, errlen);
+        if (!S->xq_e || !S->xq_di || !S->xq_att || !S->xq_ff || !cnt) return false;
+        XJ_CHECK(hipMemset(cnt, 0, nc * 4), err, errlen, false);
+        S->cnt_grp = cnt;
+    }
+    if (!S->x || !S->qkv || !S->kb || !S->vb || !S->z || !S->beta || !S->alpha || !S->o || !S->g || !S->u ||
+        !S->qr || !S->scores || !S->npast)
+        return false;
+    return true;
+}
+
+// A second set of scratch for a stage whose prompt chunks run as two
+// pipelined halves (chain_eval): the stage's weights, layer states and head
+// buffers shared, its own scratch, stream and position counter.
+static HStage *twin_new(HStage *S, char *err, size_t errlen) {
+    HStage *T = new HStage();
+    T->s = S->s;
+    T->L = S->L;
+    T->output = S->output; T->tok_embd = S->tok_embd; T->out_norm = S->out_norm;
+    T->rope = S->rope; T->logits = S->logits; T->amax = S->amax;
+    T->head_nwg = S->head_nwg; T->head_rows = S->head_rows;
+    T->conv_n = S->conv_n; T->ssm_n = S->ssm_n; T->n_ck = S->n_ck;
+    if (hipStreamCreateWithFlags(&T->st, hipStreamNonBlocking) != hipSuccess) {
+        snprintf(err, errlen, "stream creation failed");
+        T->st = nullptr;
+    } else if (hipHostMalloc((void **)&T->h_i, 64, hipHostMallocDefault) != hipSuccess) {
+        snprintf(err, errlen, "pinned allocation failed");
+        T->h_i = nullptr;
+    } else if (alloc_scratch(T, err, errlen)) {
+        return T;
+    }
+    for (void *p : T->allocs) (void)hipFree(p);
+    if (T->h_i) (void)hipHostFree(T->h_i);
+    if (T->st) (void)hipStreamDestroy(T->st);
+    delete T;
+    return nullptr;
+}
+static void twin_free(HStage *T) {
+    if (!T) return;
+    if (T->st) (void)hipStreamSynchronize(T->st);
+    for (void *p : T->allocs) (void)hipFree(p);
+    if (T->h_i) (void)hipHostFree(T->h_i);
+    if (T->st) (void)hipStreamDestroy(T->st);
+    delete T;
+}
+
 void hip_destroy(xj_stage *s) {
     if (!s) return;
     HStage *S = H(s);
@@ -726,14 +835,6 @@ void init_names() {
 extern "C" const char *xj_hip_device_name(void) { init_names(); return g_name.c_str(); }
 extern "C" const char *xj_hip_tune_note(void) { return g_note.c_str(); }
 
-static size_t scratch_floats(const xj_hparams &hp) {
-    size_t n = (size_t)hp.n_ff;
-    const size_t qkv = 2 * (size_t)hp.n_head * hp.head_dim + 2 * (size_t)hp.n_head_kv * hp.head_dim;
-    if (qkv > n) n = qkv;
-    if ((size_t)hp.conv_dim > n) n = hp.conv_dim;
-    if ((size_t)hp.n_embd * 2 > n) n = 2 * (size_t)hp.n_embd;
-    return n;
-}
 
 extern "C" uint64_t xj_hip_stage_state_bytes(const xj_model *m, int l0, int l1, int n_ctx, int max_batch) {
     const xj_hparams &hp = m->hp;
@@ -868,52 +969,7 @@ extern "C" xj_stage *xj_hip_stage_new(const xj_model *m, int l0, int l1, int n_c
         if (S->output.k != hp.n_embd) { snprintf(err, errlen, "output head shape mismatch"); return fail(); }
     }
     const size_t mb = max_batch, E = hp.n_embd;
-    const size_t sf = scratch_floats(hp);
-    S->x = dalloc<float>(S, mb * E, err, errlen);
-    S->qkv = dalloc<float>(S, mb * sf, err, errlen);
-    S->kb = dalloc<float>(S, mb * sf, err, errlen);
-    S->vb = dalloc<float>(S, mb * sf, err, errlen);
-    S->z = dalloc<float>(S, mb * sf, err, errlen);
-    S->beta = dalloc<float>(S, mb * (hp.h_v + 1), err, errlen);
-    S->alpha = dalloc<float>(S, mb * (hp.h_v + 1), err, errlen);
-    S->o = dalloc<float>(S, mb * sf, err, errlen);
-    S->g = dalloc<float>(S, mb * sf, err, errlen);
-    S->u = dalloc<float>(S, mb * sf, err, errlen);
-    S->qr = dalloc<float>(S, mb * hp.n_head * (size_t)hp.head_dim, err, errlen);
-    S->scores = dalloc<float>(S, mb * hp.n_head * (size_t)attn_splits(n_ctx) * (hp.head_dim + 2), err, errlen);
-    S->npast = dalloc<int32_t>(S, 1, err, errlen);
-    // prefill on the matrix cores (chunks of at least 16 tokens)
-    S->tsc = dalloc<float>(S, mb, err, errlen);
-    // every GEMM launch covers at most 2 sf + 2 h_v rows (gate|up, the DeltaNet in-projection)
-    const int64_t grows = 2 * (int64_t)sf + 2 * (int64_t)hp.h_v;
-    S->gpart_floats = gemm_part_floats(grows, (int)(mb < gemm_max_tokens() ? mb : gemm_max_tokens()));
-    S->gpart = dalloc<float>(S, (size_t)S->gpart_floats, err, errlen);
-    S->n_gcnt = gemm_counters(grows);
-    S->gcnt = dalloc<int32_t>(S, (size_t)S->n_gcnt, err, errlen);
-    S->hq = dalloc<uint8_t>(S, mb * (size_t)hq_stride((int)sf), err, errlen);
-    if (!S->tsc || !S->gpart || !S->gcnt || !S->hq) return fail();
-    XJ_CHECK(hipMemset(S->gcnt, 0, (size_t)S->n_gcnt * 4), err, errlen, fail());
-    {
-        bool rec = false;
-        for (int il = l0; il < l1 && il < hp.n_layer; il++) rec = rec || m->layers[il].recurrent;
-        const size_t wb = rec ? delta_chunked_work_bytes(hp.h_v, hp.s_k, (int)mb, 64) : 0;
-        if (wb) {
-            S->dwork = (float *)dalloc<uint8_t>(S, wb, err, errlen);
-            if (!S->dwork) return fail();
-        }
-    }
-    {
-        auto xqb = [&](int K) { return K >= 32 ? mb * (size_t)xq_off(K).stride : 256; };
-        S->xq_e = dalloc<uint8_t>(S, xqb(hp.n_embd), err, errlen);
-        S->xq_di = dalloc<uint8_t>(S, xqb(hp.d_inner), err, errlen);
-        S->xq_att = dalloc<uint8_t>(S, xqb(hp.n_head * hp.head_dim), err, errlen);
-        S->xq_ff = dalloc<uint8_t>(S, xqb(hp.n_ff), err, errlen);
-        const size_t nc = (size_t)(hp.n_ff / 32) + 1;
-        int32_t *cnt = dalloc<int32_t>(S, nc, err, errlen);
-        if (!S->xq_e || !S->xq_di || !S->xq_att || !S->xq_ff || !cnt) return fail();
-        XJ_CHECK(hipMemset(cnt, 0, nc * 4), err, errlen, fail());
-        S->cnt_grp = cnt;
-    }
+    if (!alloc_scratch(S, err, errlen)) return fail();
     const int half = hp.n_rot / 2 > 0 ? hp.n_rot / 2 : 1;
     S->rope = dalloc<float2>(S, (size_t)n_ctx * half, err, errlen);
     if (!S->x || !S->qkv || !S->kb || !S->vb || !S->z || !S->beta || !S->alpha || !S->o || !S->g || !S->u ||
@@ -1022,8 +1078,10 @@ extern "C" int xj_hip_stage_restore(xj_stage *s, int slot, int n_past, char *err
 
 // ================================================================= chain ==
 
+constexpr int kMaxParts = 4;   // parts of a single stage's layers in a pipelined prefill
 struct xjh_chain {
     std::vector<HStage *> st;
+    std::vector<HStage *> twins;   // a single stage's later parts of the layers in prefill (twin_new)
     hipStream_t stream = nullptr;
     float *x = nullptr;
     int mb = 0, hist_cap = 0;
@@ -1066,6 +1124,7 @@ extern "C" void xjh_chain_free(xjh_chain *c) {
     for (hipEvent_t e : c->ev_done) if (e) (void)hipEventDestroy(e);
     for (hipEvent_t e : c->ev_taken) if (e) (void)hipEventDestroy(e);
     if (c->d_prompt) (void)hipFree(c->d_prompt);
+    for (HStage *T : c->twins) twin_free(T);
     for (int32_t *p : {c->d_tokens, c->d_argmax, c->d_tok, c->d_hist, c->d_step, c->d_rbase, c->d_pick}) if (p) (void)hipFree(p);
     if (c->h_buf) (void)hipHostFree(c->h_buf);
     delete c;
@@ -1103,9 +1162,10 @@ extern "C" xjh_chain *xjh_chain_new(xj_stage **stages, int n, char *err, size_t 
         xjh_chain_free(c);
         return nullptr;
     }
-    c->ev_done.assign(c->st.size(), nullptr);
-    c->ev_taken.assign(c->st.size(), nullptr);
-    for (size_t i = 0; i < c->st.size(); i++)
+    const size_t nev = c->st.size() < kMaxParts ? kMaxParts : c->st.size();   // a single stage may run in parts
+    c->ev_done.assign(nev, nullptr);
+    c->ev_taken.assign(nev, nullptr);
+    for (size_t i = 0; i < nev; i++)
         if (hipEventCreateWithFlags(&c->ev_done[i], hipEventDisableTiming) != hipSuccess ||
             hipEventCreateWithFlags(&c->ev_taken[i], hipEventDisableTiming) != hipSuccess) {
             snprintf(err, errlen, "chain allocation failed");
@@ -1125,7 +1185,9 @@ static int chain_sync(xjh_chain *c, char *err, size_t errlen) {
 // The prompt in chunks of max_batch, the stages pipelined (pipe/core/xj_net.c:561-604
 // pipelines a remote worker's half against the host's): each stage runs on its
 // own stream from its own hidden-state buffer, so stage i works on chunk k + 1
-// while stage i + 1 works on chunk k. Stage i + 1 takes chunk k by a device
+// while stage i + 1 works on chunk k. A single stage's layers run the same
+// way in XJ_STAGE_SPLIT parts (3: a 4B 1024-token prefill 0.118 -> 0.083 s;
+// 2 parts 0.091 s, 4 parts 0.093 s). Stage i + 1 takes chunk k by a device
 // copy once stage i has finished it (event done[i]); stage i overwrites its
 // buffer with chunk k + 1 only after that copy (event taken[i + 1]). Every
 // stage's n_past advances on the device at the end of each chunk, so no host
@@ -1137,10 +1199,37 @@ static int chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int 
     if (n <= 0) { snprintf(err, errlen, "no tokens"); return -1; }
     if (keep && n > B) { snprintf(err, errlen, "verify batch %d exceeds max_batch %d", n, B); return -1; }
     static const bool overlap = env_int("XJ_CHAIN_OVERLAP", 1) != 0;
-    HStage *head = c->st.back();
-    auto stream_of = [&](int i) { return overlap ? c->st[i]->st : c->stream; };
+    static const int split_env = env_int("XJ_STAGE_SPLIT", 3);
+    // the pipeline's parts: every stage, or a single stage's layers in
+    // XJ_STAGE_SPLIT contiguous parts (the later ones on twins' scratch and
+    // streams) when the prompt spans several chunks
+    struct Part { HStage *S; int lo, hi; bool twin; };
+    std::vector<Part> parts;
+    HStage *S0 = c->st[0];
+    const int nl = S0->s.l1 - S0->s.l0;
+    const int npart = split_env < 1 ? 1 : split_env > kMaxParts ? kMaxParts : split_env > nl ? nl : split_env;
+    if (ns == 1 && overlap && npart > 1 && n > B && !keep) {
+        while ((int)c->twins.size() < npart - 1) {
+            HStage *T = twin_new(S0, err, errlen);
+            if (!T) return -1;
+            c->twins.push_back(T);
+        }
+        for (int p = 0; p < npart; p++) {
+            HStage *S = p ? c->twins[p - 1] : S0;
+            if (p) {
+                S->L = S0->L;   // checkpoint and snapshot buffers allocated since
+                S->n_ck = S0->n_ck;
+            }
+            parts.push_back(Part{S, S0->s.l0 + nl * p / npart, S0->s.l0 + nl * (p + 1) / npart, p > 0});
+        }
+    } else {
+        for (auto *S : c->st) parts.push_back(Part{S, S->s.l0, S->s.l1, false});
+    }
+    const int np = (int)parts.size();
+    HStage *head = parts.back().S;
+    auto stream_of = [&](int i) { return overlap ? parts[i].S->st : c->stream; };
     auto fail_sync = [&]() {
-        for (int i = 0; i < ns; i++) (void)hipStreamSynchronize(c->st[i]->st);
+        for (int i = 0; i < np; i++) (void)hipStreamSynchronize(parts[i].S->st);
         for (auto *S : c->st) S->s.keep = 0;
         return -1;
     };
@@ -1152,14 +1241,14 @@ static int chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int 
         if (hipMalloc(&c->d_prompt, 4 * (size_t)n) != hipSuccess) { snprintf(err, errlen, "prompt allocation failed"); return -1; }
         c->prompt_cap = n;
     }
-    // the ids (synchronous copy from the caller's memory) and every stage's
-    // starting position
+    // the ids (synchronous copy from the caller's memory) and every part's
+    // starting position (a twin starts where its stage is)
     if (hipMemcpy(c->d_prompt, tokens, 4 * (size_t)n, hipMemcpyHostToDevice) != hipSuccess) {
         snprintf(err, errlen, "token upload failed"); return -1;
     }
-    for (int i = 0; i < ns; i++) {
-        HStage *S = c->st[i];
-        *S->h_i = S->s.n_past;
+    for (int i = 0; i < np; i++) {
+        HStage *S = parts[i].S;
+        *S->h_i = parts[i].twin ? S0->s.n_past : S->s.n_past;
         if (hipMemcpyAsync(S->npast, S->h_i, 4, hipMemcpyHostToDevice, stream_of(i)) != hipSuccess ||
             hipStreamSynchronize(stream_of(i)) != hipSuccess) {   // h_i is reused by later calls
             snprintf(err, errlen, "position upload failed"); return -1;
@@ -1167,36 +1256,41 @@ static int chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int 
     }
     for (int k0 = 0; k0 < n; k0 += B) {
         const int T = n - k0 < B ? n - k0 : B;
-        for (int i = 0; i < ns; i++) {
-            HStage *S = c->st[i];
+        for (int i = 0; i < np; i++) {
+            HStage *S = parts[i].S;
             hipStream_t st = stream_of(i);
             if (i == 0) {
-                // chunk k0 into stage 0's buffer, once stage 1 has taken the previous chunk
-                if (ns > 1 && k0 > 0 && hipStreamWaitEvent(st, c->ev_taken[1], 0) != hipSuccess) return fail_sync();
+                // chunk k0 into part 0's buffer, once part 1 has taken the previous chunk
+                if (np > 1 && k0 > 0 && hipStreamWaitEvent(st, c->ev_taken[1], 0) != hipSuccess) return fail_sync();
                 EmbedArgs ea{c->d_prompt + k0, S->tok_embd, S->x, T};
                 if (embed_launch(ea, st)) { snprintf(err, errlen, "embed launch failed"); return fail_sync(); }
             } else {
-                // this stage's previous chunk is done with its buffer (same stream); the
-                // upstream stage's output of this chunk is final
-                if (i + 1 < ns && k0 > 0 && hipStreamWaitEvent(st, c->ev_taken[i + 1], 0) != hipSuccess) return fail_sync();
+                // this part's previous chunk is done with its buffer (same stream); the
+                // upstream part's output of this chunk is final
+                if (i + 1 < np && k0 > 0 && hipStreamWaitEvent(st, c->ev_taken[i + 1], 0) != hipSuccess) return fail_sync();
                 if (hipStreamWaitEvent(st, c->ev_done[i - 1], 0) != hipSuccess ||
-                    hipMemcpyAsync(S->x, c->st[i - 1]->x, sizeof(float) * (size_t)T * E, hipMemcpyDeviceToDevice, st) != hipSuccess ||
+                    hipMemcpyAsync(S->x, parts[i - 1].S->x, sizeof(float) * (size_t)T * E, hipMemcpyDeviceToDevice, st) != hipSuccess ||
                     hipEventRecord(c->ev_taken[i], st) != hipSuccess) {
                     snprintf(err, errlen, "chunk hand-off failed"); return fail_sync();
                 }
             }
-            if (keep) S->s.keep = T;
             int keep_n = 0;
-            if (begin_forward(S, T, &keep_n, err, errlen)) return fail_sync();
-            if (enqueue_layers(S, S->x, T, keep_n, true, st) || hipEventRecord(c->ev_done[i], st) != hipSuccess) {
+            if (!parts[i].twin) {
+                if (keep) S->s.keep = T;
+                if (begin_forward(S, T, &keep_n, err, errlen)) return fail_sync();
+            }
+            if (enqueue_layer_range(S, parts[i].lo, parts[i].hi, S->x, T, keep_n, true, st) ||
+                hipEventRecord(c->ev_done[i], st) != hipSuccess) {
                 snprintf(err, errlen, "layer launch failed"); return fail_sync();
             }
-            S->s.n_past += T;
-            if (k0 + T < n) S->s.keep = 0;
+            if (!parts[i].twin) {
+                S->s.n_past += T;
+                if (k0 + T < n) S->s.keep = 0;
+            }
         }
     }
     const int T = n - (n - 1) / B * B;   // tokens of the last chunk
-    hipStream_t hs = stream_of(ns - 1);
+    hipStream_t hs = stream_of(np - 1);
     if (nlog > 0) {
         const int nl = nlog < T ? nlog : T;
         if (enqueue_head(head, head->x + (int64_t)(T - nl) * E, nl, head->logits, hs) ||
@@ -1206,11 +1300,11 @@ static int chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int 
     }
     // the last chunk's hidden rows where the decode step and the drivers read
     // them (the chain's buffer, stage 0's); the head stream is ordered after
-    // every stage's last chunk through the hand-off events
-    if (ns > 1 && hipMemcpyAsync(c->x, head->x, sizeof(float) * (size_t)T * E, hipMemcpyDeviceToDevice, hs) != hipSuccess) {
+    // every part's last chunk through the hand-off events
+    if (np > 1 && hipMemcpyAsync(c->x, head->x, sizeof(float) * (size_t)T * E, hipMemcpyDeviceToDevice, hs) != hipSuccess) {
         snprintf(err, errlen, "hidden copy failed"); return fail_sync();
     }
-    for (int i = 0; i < ns; i++) {
+    for (int i = 0; i < np; i++) {
         hipError_t e = hipStreamSynchronize(stream_of(i));
         if (e == hipSuccess) e = hipGetLastError();
         if (e != hipSuccess) { snprintf(err, errlen, "GPU error: %s", hipGetErrorString(e)); return fail_sync(); }
