@@ -68,7 +68,9 @@ const char *xj_hip_device_name(void);
 const char *xj_hip_tune_note(void);
 
 /* Bytes of HBM a stage holds besides the repacked weights
- * (counterpart of xj_stage_state_bytes, xj_stage.h:57). */
+ * (counterpart of xj_stage_state_bytes, xj_stage.h:57). A single-stage
+ * chain (xjh_chain_new) that prefills a prompt of several chunks adds up to
+ * XJ_STAGE_SPLIT - 1 further sets of the stage's scratch on first use. */
 uint64_t    xj_hip_stage_state_bytes(const xj_model *m, int l0, int l1, int n_ctx, int max_batch);
 
 /* Copy the whole recurrent state (conv + DeltaNet state of every layer) of a
