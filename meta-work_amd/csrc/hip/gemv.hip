@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const GArgs a) {
         if (in) v = x[k];
     }
     uint8_t *dst = a.xq + (int64_t)t * o.stride;
-    xjd::emit_xq(v, k, in, dst, o);
+    if (!a.hq_only) xjd::emit_xq(v, k, in, dst, o);
     if (a.pro == PRO_RMSU) {
         const double ss = xjd::group_ss(xr);
         if (in && (k & 31) == 0) ((double *)(dst + o.ss_off))[k >> 5] = ss;
@@ -1410,6 +1410,7 @@ int prep_launch(const GArgs &a, hipStream_t st) {
     if (a.pro == PRO_GATED_RMS && (a.group < 1 || a.K % a.group)) return -1;
     if ((a.pro == PRO_RMSU || a.pro == PRO_GATED_RMS) && !a.pro_w) return -1;
     if (a.hq && a.K % 256) return -1;
+    if (a.hq_only && !a.hq) return -1;
     hipLaunchKernelGGL(prep_kernel, dim3((a.K + 255) / 256, a.T), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -94,6 +94,7 @@ struct GArgs {
     int32_t nseg;
     GSeg seg[kMaxSeg];
     uint8_t *hq;                   // prep launch, K % 256 == 0: also the GEMM's activations [T][hq_stride(K)]
+    int32_t hq_only;               // ... and of xq only the groups' sums of x^2 (PRO_RMSU)
 };
 
 // Launch plan of one GEMV over `rows` output rows of inner size K: a team of

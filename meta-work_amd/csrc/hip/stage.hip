@@ -262,10 +262,13 @@ struct Gemv {
     }
     int run_gemm(int T, hipStream_t st) {
         const int64_t xs = xq_off(a.K).stride, hs = hq_stride(a.K);
-        if (!prepared) {   // the T tokens' activations, once
+        if (!prepared) {   // the T tokens' activations, once (no digits when no segment takes the GEMV)
             GArgs b = a;
             b.T = T;
             b.hq = hq;
+            b.hq_only = 1;
+            for (int i = 0; i < a.nseg; i++)
+                if (a.seg[i].type != XJ_Q4_K && a.seg[i].type != XJ_Q6_K) b.hq_only = 0;
             if (prep_launch(b, st)) return -1;
         } else if (!hq_ready && hq_from_v_launch(a.xq, a.K, T, hq, st)) {
             return -1;
