@@ -214,13 +214,20 @@ int  xjh_chain_time_gemv(xjh_chain *c, int iters, double *ms_per_step, double *b
  * longest prefix the target's token agrees with (its argmax, or with the
  * target's sampler on its draw, row i with the next number + i, so the output
  * is that of plain sampled decoding with the same numbers) and rolls both
- * models back.
+ * models back. Greedy with k = 4, after rounds whose drafts were all
+ * accepted, the draft makes the next round's drafts while the target
+ * verifies (from the round's last draft: one step for the target's next
+ * token, then k); they are used when the target accepts every draft and its
+ * next token is the guessed one, so the tokens are those of the sequential
+ * rounds (XJ_SPEC_PIPE=0: always sequential).
  * oracle (optional, n_oracle ids) replaces the drafts, with every
- * (g*7+j) % oracle_miss == 0 draft made wrong, as xj_spec.c:173-177. */
+ * (g*7+j) % oracle_miss == 0 draft made wrong, as xj_spec.c:173-177; the
+ * guess of the target's next token is then the oracle's. */
 typedef struct {
     long n_steps, n_drafted, n_accepted;
     long acc_at[4];
     double t_total_ms, t_draft_ms;
+    long n_overlap, n_overlap_held;   /* rounds drafted ahead during a verification; of them used */
 } xjh_spec_stats;
 /* Returns the number of tokens written to out (at most n_gen): generation
  * stops after an end token (hp.eos / hp.eot), which is written but not fed,

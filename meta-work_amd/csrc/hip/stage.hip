@@ -1196,9 +1196,13 @@ static int chain_sync(xjh_chain *c, char *err, size_t errlen) {
 // stage's n_past advances on the device at the end of each chunk, so no host
 // round trip separates the chunks; XJ_CHAIN_OVERLAP=0 runs all stages on one
 // stream.
+static int chain_finish(xjh_chain *c, int nl, int32_t *argmax, char *err, size_t errlen);
+// wait = false: returns once everything is enqueued (nlog > 0, no logits);
+// chain_finish collects the argmax of the nlog rows.
 static int chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int keep, float *logits, int32_t *argmax,
-                      char *err, size_t errlen) {
+                      char *err, size_t errlen, bool wait = true) {
     const int B = c->mb, E = c->st[0]->s.m->hp.n_embd, ns = (int)c->st.size();
+    if (!wait && (nlog < 1 || logits || n > B)) { snprintf(err, errlen, "asynchronous eval of one chunk with argmax only"); return -1; }
     if (n <= 0) { snprintf(err, errlen, "no tokens"); return -1; }
     if (keep && n > B) { snprintf(err, errlen, "verify batch %d exceeds max_batch %d", n, B); return -1; }
     static const bool overlap = env_int("XJ_CHAIN_OVERLAP", 1) != 0;
@@ -1307,6 +1311,13 @@ static int chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int 
     if (np > 1 && hipMemcpyAsync(c->x, head->x, sizeof(float) * (size_t)T * E, hipMemcpyDeviceToDevice, hs) != hipSuccess) {
         snprintf(err, errlen, "hidden copy failed"); return fail_sync();
     }
+    if (!wait) {   // a single part: the head stream is the chain's
+        const int nl = nlog < T ? nlog : T;
+        if (hipMemcpyAsync(c->h_buf, c->d_argmax, 4 * nl, hipMemcpyDeviceToHost, hs) != hipSuccess) {
+            snprintf(err, errlen, "argmax copy failed"); return fail_sync();
+        }
+        return 0;
+    }
     for (int i = 0; i < np; i++) {
         hipError_t e = hipStreamSynchronize(stream_of(i));
         if (e == hipSuccess) e = hipGetLastError();
@@ -1322,6 +1333,26 @@ static int chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int 
         c->last_tok = c->h_buf[nl - 1];
     }
     for (auto *S : c->st) S->s.keep = 0;
+    return 0;
+}
+
+// The end of an asynchronous chain_eval of a single chunk: every stage's
+// stream synchronised, the argmax of its nl rows.
+static int chain_finish(xjh_chain *c, int nl, int32_t *argmax, char *err, size_t errlen) {
+    int rc = 0;
+    for (auto *S : c->st) {
+        hipError_t e = hipStreamSynchronize(S->st);
+        if (e == hipSuccess) e = hipGetLastError();
+        if (e != hipSuccess && !rc) { snprintf(err, errlen, "GPU error: %s", hipGetErrorString(e)); rc = -1; }
+    }
+    if (c->stream) {
+        hipError_t e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess && !rc) { snprintf(err, errlen, "GPU error: %s", hipGetErrorString(e)); rc = -1; }
+    }
+    for (auto *S : c->st) S->s.keep = 0;
+    if (rc) return rc;
+    memcpy(argmax, c->h_buf, 4 * (size_t)nl);
+    c->last_tok = c->h_buf[nl - 1];
     return 0;
 }
 
@@ -1574,36 +1605,11 @@ static int draft_step(xjh_chain *d, int t, int *next, char *err, size_t errlen) 
     return 0;
 }
 
-// kk greedy steps of the draft fed with token t, the state after step j in
-// snapshot slot j (j < kk - 1; the last state is the draft's own): one set-up, the decode graph replayed kk times with the
-// snapshot copies between the replays on the chain's stream, one
-// synchronisation; toks receives the kk argmax tokens. catch_tok >= 0: a
-// token the draft has not been fed yet, before t (the last draft of a fully
-// accepted round): it and t go in as one two-token pass, whose rows are
-// those of two steps bit for bit, instead of a step of their own.
-static int draft_run(xjh_chain *d, int catch_tok, int t, int kk, int32_t *toks, char *err, size_t errlen) {
-    if (catch_tok >= 0 && d->mb < 2) {
-        int nx;
-        if (draft_step(d, catch_tok, &nx, err, errlen)) return -1;
-        catch_tok = -1;
-    }
-    int done = 0;
-    if (catch_tok >= 0) {
-        const int32_t in2[2] = {catch_tok, t};
-        int32_t am = -1;
-        if (chain_eval(d, in2, 2, 1, 0, nullptr, &am, err, errlen)) return -1;
-        if (kk > 1)
-            for (auto *S : d->st)
-                if (snapshot_enqueue(S, 0, d->stream, err, errlen)) return -1;
-        toks[0] = am;
-        t = am;
-        done = 1;
-        if (kk == 1) {
-            d->last_tok = am;
-            return chain_sync(d, err, errlen);
-        }
-    }
-    const int n = kk - done;
+// n greedy steps of the draft fed with token t, enqueued on its stream: one
+// set-up, the decode graph replayed n times, after step j the recurrent state
+// copied into snapshot slot slots[j] (< 0: none), the n argmax tokens copied
+// to the host buffer; draft_collect waits for them.
+static int draft_enqueue(xjh_chain *d, int t, int n, const int *slots, char *err, size_t errlen) {
     for (auto *S : d->st) {
         if (S->s.n_past + n > S->s.n_ctx) { snprintf(err, errlen, "context full (%d)", S->s.n_ctx); return -1; }
         if (reset_check(S, err, errlen)) return -1;
@@ -1622,18 +1628,56 @@ static int draft_run(xjh_chain *d, int catch_tok, int t, int kk, int32_t *toks, 
         if (direct ? enqueue_decode_step(d, false) != 0 : hipGraphLaunch(d->exec, d->stream) != hipSuccess) {
             snprintf(err, errlen, "draft step launch failed"); return -1;
         }
-        if (done + j < kk - 1)   // the state after the last step stays in place
+        if (slots[j] >= 0)
             for (auto *S : d->st)
-                if (snapshot_enqueue(S, done + j, d->stream, err, errlen)) return -1;
+                if (snapshot_enqueue(S, slots[j], d->stream, err, errlen)) return -1;
     }
     if (hipMemcpyAsync(&d->h_buf[2], d->d_hist, 4 * n, hipMemcpyDeviceToHost, d->stream) != hipSuccess) {
         snprintf(err, errlen, "draft history copy failed"); return -1;
     }
-    if (chain_sync(d, err, errlen)) return -1;
-    for (int j = 0; j < n; j++) toks[done + j] = d->h_buf[2 + j];
-    for (auto *S : d->st) S->s.n_past += n;
-    d->last_tok = toks[kk - 1];
     return 0;
+}
+static int draft_collect(xjh_chain *d, int n, int32_t *toks, char *err, size_t errlen) {
+    if (chain_sync(d, err, errlen)) return -1;
+    for (int j = 0; j < n; j++) toks[j] = d->h_buf[2 + j];
+    for (auto *S : d->st) S->s.n_past += n;
+    d->last_tok = toks[n - 1];
+    return 0;
+}
+
+// kk greedy steps of the draft fed with token t, the state after step j in
+// snapshot slot base + j (j < kk - 1; the last state is the draft's own), one
+// synchronisation; toks receives the kk argmax tokens. catch_tok >= 0: a
+// token the draft has not been fed yet, before t (the last draft of a fully
+// accepted round): it and t go in as one two-token pass, whose rows are
+// those of two steps bit for bit, instead of a step of their own.
+static int draft_run(xjh_chain *d, int catch_tok, int t, int kk, int32_t *toks, int base, char *err, size_t errlen) {
+    if (catch_tok >= 0 && d->mb < 2) {
+        int nx;
+        if (draft_step(d, catch_tok, &nx, err, errlen)) return -1;
+        catch_tok = -1;
+    }
+    int done = 0;
+    if (catch_tok >= 0) {
+        const int32_t in2[2] = {catch_tok, t};
+        int32_t am = -1;
+        if (chain_eval(d, in2, 2, 1, 0, nullptr, &am, err, errlen)) return -1;
+        if (kk > 1)
+            for (auto *S : d->st)
+                if (snapshot_enqueue(S, base, d->stream, err, errlen)) return -1;
+        toks[0] = am;
+        t = am;
+        done = 1;
+        if (kk == 1) {
+            d->last_tok = am;
+            return chain_sync(d, err, errlen);
+        }
+    }
+    const int n = kk - done;
+    int slots[8];
+    for (int j = 0; j < n; j++) slots[j] = done + j < kk - 1 ? base + done + j : -1;   // the last state stays in place
+    if (draft_enqueue(d, t, n, slots, err, errlen)) return -1;
+    return draft_collect(d, n, toks + done, err, errlen);
 }
 
 extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_gen, const int32_t *oracle, int n_oracle,
@@ -1654,7 +1698,33 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
     long n_gen_tok = 0;
     int pending = tgt->last_tok;
     const bool smp = sampling(tgt);
+    // Greedy rounds overlap after `need` rounds in a row whose drafts were all
+    // accepted (2, doubled after each overlap that failed, back to 2 after one
+    // that held): while
+    // the target verifies round r, the draft goes on from round r's last
+    // draft, one step for the target's next token and k for round r + 1
+    // (XJ_SPEC_PIPE=0: never; the two models' launches share the CUs, so the
+    // ahead steps slow a verification whose drafts then fail). When the target accepts
+    // every draft and its next token is the draft's, round r + 1's drafts are
+    // those and its verification starts at once; otherwise the draft returns
+    // to a snapshot, as after a sequential round. Snapshot slots come in two
+    // banks of four: slot base + j holds the state after the round's token j
+    // (j = 3: taken before the draft runs ahead), and slot 3 of the other
+    // bank the state after the round's last draft.
+    static const bool pipe_env = env_int("XJ_SPEC_PIPE", 1) != 0;
+    const bool pipe = pipe_env && !smp && k == 4;
+    int base = 0;
     int catch_tok = -1;   // the last draft of a fully accepted round, not fed to the draft yet
+    bool have_next = false;
+    int full = 0, need = 2;   // rounds in a row whose drafts were all accepted
+    int32_t next_toks[5];
+    auto oracle_fill = [&](int32_t *toks, int kk) {   // oracle drafts stand in for the draft's
+        for (int j = 1; j <= kk && oracle; j++) {
+            const long gi = n_gen_tok + j;   // index of the generated token this draft stands for
+            if (gi < n_oracle) toks[j] = oracle[gi];
+            if (oracle_miss && (gi * 7 + j) % oracle_miss == 0) toks[j] = (toks[j] + 1) % V;
+        }
+    };
     while (produced < n_gen) {
         if (is_end(hp, pending)) { out[produced++] = pending; break; }   // returned, never fed (xj_spec.c:139)
         const int P = tgt->st[0]->s.n_past;
@@ -1662,6 +1732,9 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
         if (kk > n_gen - produced - 1) kk = n_gen - produced - 1;
         for (auto *S : tgt->st) if (kk > S->s.n_ctx - P - 1) kk = S->s.n_ctx - P - 1;
         if (smp && kk > tgt->n_rnd - tgt->used - 1) kk = tgt->n_rnd - tgt->used - 1;   // numbers for kk + 1 draws
+        if (have_next && kk != k) {   // cannot happen: the ahead drafts were only made with room for a full round
+            snprintf(err, errlen, "speculation pipeline out of step"); return -1;
+        }
         if (kk <= 0) {   // no room to speculate: plain step on both models (the target's token drawn)
             out[produced++] = pending;
             int32_t nt, dn;
@@ -1674,40 +1747,83 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
             continue;
         }
         // 1) draft proposes kk tokens by greedy T=1 steps, snapshot after each
+        //    (or they were made while the previous round was verified)
         const double t0 = now_ms();
         int32_t toks[5];
         toks[0] = pending;
-        if (draft_run(dft, catch_tok, pending, kk, toks + 1, err, errlen)) return -1;
-        catch_tok = -1;
-        st.t_draft_ms += now_ms() - t0;
-        for (int j = 1; j <= kk && oracle; j++) {
-            const long gi = n_gen_tok + j;   // index of the generated token this draft stands for
-            if (gi < n_oracle) toks[j] = oracle[gi];
-            if (oracle_miss && (gi * 7 + j) % oracle_miss == 0) toks[j] = (toks[j] + 1) % V;
+        if (have_next) {
+            for (int j = 1; j <= kk; j++) toks[j] = next_toks[j];
+            have_next = false;
+        } else {
+            if (draft_run(dft, catch_tok, pending, kk, toks + 1, base, err, errlen)) return -1;
+            catch_tok = -1;
         }
+        st.t_draft_ms += now_ms() - t0;
+        oracle_fill(toks, kk);
         // 2) verify [t, d1..dk] on the target in one batch with checkpoints;
         //    the target's token after each row: its argmax, or with the
         //    sampler on its draw (row i with number used + i, xj_spec.c:185)
         int32_t am[5];
-        if (chain_eval(tgt, toks, kk + 1, kk + 1, 1, nullptr, am, err, errlen) ||
-            (smp && chain_draw(tgt, 0, kk + 1, am, err, errlen))) return -1;
+        const int nb = base ^ 4;   // the other bank
+        const long rest = (long)n_gen - produced - (kk + 1);
+        bool ahead = pipe && full >= need && kk == k && rest - 1 >= k;
+        for (auto *S : tgt->st) ahead = ahead && S->s.n_ctx - (P + kk + 1) - 1 >= k;
+        for (auto *S : dft->st) ahead = ahead && S->s.n_past + 1 + k <= S->s.n_ctx;
+        int32_t at[5];
+        if (ahead) {
+            if (chain_eval(tgt, toks, kk + 1, kk + 1, 1, nullptr, nullptr, err, errlen, false)) return -1;
+            // the draft's state after toks[0..kk-1], then the draft fed round
+            // r's last draft and its own tokens: the target's next token, then
+            // round r + 1's drafts
+            for (auto *S : dft->st)
+                if (snapshot_enqueue(S, base + kk - 1, dft->stream, err, errlen)) return -1;
+            const int slots[5] = {nb + 3, nb, nb + 1, nb + 2, -1};
+            if (draft_enqueue(dft, toks[kk], k + 1, slots, err, errlen) ||
+                chain_finish(tgt, kk + 1, am, err, errlen) || draft_collect(dft, k + 1, at, err, errlen))
+                return -1;
+        } else if (chain_eval(tgt, toks, kk + 1, kk + 1, 1, nullptr, am, err, errlen) ||
+                   (smp && chain_draw(tgt, 0, kk + 1, am, err, errlen))) {
+            return -1;
+        }
         // 3) accept the longest agreeing prefix (xj_spec.c:184-191); an accepted
         //    end token is returned but neither it nor what follows is fed (:193-194)
         int a = 0;
         while (a < kk && am[a] == toks[a + 1]) { st.acc_at[a]++; a++; }
+        full = a == kk ? full + 1 : 0;
         int fed = a + 1, n_out = a + 1;
         for (int i = 1; i <= a; i++)
             if (is_end(hp, toks[i])) { fed = i; n_out = i + 1; break; }
         if (smp) tgt->used += n_out > fed ? fed : a + 1;   // one number per token produced
         for (int i = 0; i < n_out && produced < n_gen; i++) out[produced++] = toks[i];
+        const long gi_next = n_gen_tok + kk + 1;   // index of the target's token after a full round
         n_gen_tok += fed;
         st.n_steps++; st.n_drafted += kk; st.n_accepted += fed - 1 < a ? fed - 1 : a;
         if (fed < kk + 1 && xjh_chain_rollback(tgt, P + fed, err, errlen)) return -1;
-        // 4) bring the draft to the same prefix [.., t, d1..d(fed-1)]: slot j holds
-        //    its state after feeding toks[0..j]
-        if (fed < kk) {
+        // 4) bring the draft to the same prefix [.., t, d1..d(fed-1)]: slot base + j
+        //    holds its state after feeding toks[0..j]
+        if (ahead) {
+            // the guess of the target's next token (with oracle drafts the
+            // oracle's, as the draft's own stand in for nothing)
+            const int32_t guess = oracle && gi_next < n_oracle ? oracle[gi_next] : at[0];
+            need = fed == kk + 1 && am[kk] == guess ? 2 : (need < 64 ? 2 * need : need);
+            st.n_overlap++;
+            if (fed == kk + 1 && n_out == fed && am[kk] == guess) {
+                for (int j = 1; j <= k; j++) next_toks[j] = at[j];
+                have_next = true;
+                base = nb;
+                st.n_overlap_held++;
+            } else if (fed == kk + 1) {
+                // every draft accepted, the next token not the guess: the draft
+                // back to its state after round r's last draft
+                for (auto *S : dft->st)
+                    if (xj_hip_stage_restore(&S->s, nb + 3, P + kk + 1, err, errlen)) return -1;
+            } else {
+                for (auto *S : dft->st)
+                    if (xj_hip_stage_restore(&S->s, base + fed - 1, P + fed, err, errlen)) return -1;
+            }
+        } else if (fed < kk) {
             for (auto *S : dft->st)
-                if (xj_hip_stage_restore(&S->s, fed - 1, P + fed, err, errlen)) return -1;
+                if (xj_hip_stage_restore(&S->s, base + fed - 1, P + fed, err, errlen)) return -1;
         } else if (fed == kk) {
             // the draft already holds the state after toks[0..kk-1] at n_past P + kk
         } else {
@@ -1716,6 +1832,11 @@ extern "C" int xjh_spec_generate(xjh_chain *tgt, xjh_chain *dft, int k, int n_ge
         if (n_out > fed) { pending = toks[fed]; break; }   // stopped at an accepted end token
         pending = am[a];
         tgt->last_tok = pending;
+    }
+    if (have_next) {   // the draft ran ahead of the last round: back to the target's prefix
+        const int P = tgt->st[0]->s.n_past;
+        for (auto *S : dft->st)
+            if (xj_hip_stage_restore(&S->s, base + 3, P, err, errlen)) return -1;
     }
     if (catch_tok >= 0) {   // the draft ends fed with the target's prefix, as each round leaves it
         int nx;

@@ -82,7 +82,8 @@ XjStage._fields_ = [("m", C.POINTER(XjModel)), ("l0", C.c_int), ("l1", C.c_int),
 
 class XjhSpecStats(C.Structure):
     _fields_ = [("n_steps", C.c_long), ("n_drafted", C.c_long), ("n_accepted", C.c_long), ("acc_at", C.c_long * 4),
-                ("t_total_ms", C.c_double), ("t_draft_ms", C.c_double)]
+                ("t_total_ms", C.c_double), ("t_draft_ms", C.c_double), ("n_overlap", C.c_long),
+                ("n_overlap_held", C.c_long)]
 
 
 class XjsConfig(C.Structure):

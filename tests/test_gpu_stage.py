@@ -251,8 +251,13 @@ def test_verify_pass_logits_equal_single_steps(tiny):
     g2.destroy()
 
 
-@pytest.mark.parametrize("mode", ["draft", "oracle_all", "oracle_miss"])
+@pytest.mark.parametrize("mode", ["draft", "oracle_all", "oracle_miss", "oracle_guess_miss"])
 def test_spec_decode_equals_greedy(tiny, tiny_draft_path, mode):
+    """Speculative generation equals plain greedy decoding. oracle_guess_miss:
+    oracle drafts with wrong tokens at positions 15 and 31, where fully
+    accepted rounds that overlap the next round's drafting with their
+    verification guess the target's next token (the guess fails, the draft
+    returns to its state after the round's last draft)."""
     m, L = tiny, tiny.hp.n_layer
     dm = xp.Model(tiny_draft_path)
     prompt = prompt_ids(m, 13, 9)
@@ -267,12 +272,19 @@ def test_spec_decode_equals_greedy(tiny, tiny_draft_path, mode):
     tc, dc = xp.Chain([t]), xp.Chain([d])
     tc.eval(prompt)
     dc.eval(prompt)
-    oracle = None if mode == "draft" else plain
+    oracle = None if mode == "draft" else plain.copy()
+    if mode == "oracle_guess_miss":
+        V = int(m.hp.n_vocab)
+        for gi in (15, 31):
+            oracle[gi] = (oracle[gi] + 1) % V
     miss = 3 if mode == "oracle_miss" else 0
     out, st = xp.spec_generate(tc, dc, 4, n_gen, oracle=oracle, oracle_miss=miss)
     assert out.tolist() == plain.tolist()
     if mode == "oracle_all":
         assert st.n_accepted == st.n_drafted
+        assert st.n_overlap_held == st.n_overlap > 0
+    if mode == "oracle_guess_miss":
+        assert 0 < st.n_overlap_held < st.n_overlap
     for o in (tc, dc):
         o.free()
     t.destroy()
