@@ -84,13 +84,15 @@ def decode_run(cfg, name, n_prompt, steps, warmup, seed):
     log(f"{name}: uploaded in {time.time() - t:.1f} s ({xp.tune_note()})")
     ch = xp.Chain([st])
     prompt = np.random.default_rng(seed).integers(0, hp.n_vocab, n_prompt).astype(np.int32)
-    ch.eval(prompt[:64])                 # warm-up of the prefill path, then a fresh stage state
+    # warm-up of the prefill path over two chunks (so the pipelined parts' scratch
+    # is allocated and their kernels loaded), then a fresh stage state
+    ch.eval(prompt[:128])
     ch.reset()
     t = time.perf_counter()
     first = ch.eval(prompt)
     prefill_s = time.perf_counter() - t
     log(f"{name}: prefill {n_prompt} tokens in {prefill_s:.3f} s, first token {int(first[0])}")
-    assert n_prompt >= 64
+    assert n_prompt >= 128
     if warmup:
         ch.decode(warmup)
     t0 = time.perf_counter()
