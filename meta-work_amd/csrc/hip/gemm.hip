@@ -292,17 +292,20 @@ __device__ __forceinline__ void end_blk(const WReg<Q6, RT> &r, const Q4Scales (&
 // Work-group holding unit u: the w whose range [w P / G, (w + 1) P / G) holds u.
 __device__ __forceinline__ int wg_of(int u, int P, int G) { return ((u + 1) * G - 1) / P; }
 
+// The units of one weight type: work-group wb + w of this type's G takes its
+// equal contiguous share of the type's P units, which start at unit ub (and
+// at row group ub / nb) of the launch.
 template <bool Q6, int NTG>
-__global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(const GemmArgs a) {
+__device__ __forceinline__ void gemm_units(const GemmArgs &a, uint8_t *lds, int *last_sh_p, int wb, int w, int G,
+                                           int P, int ub) {
     // NTG 16-token column groups: above two, a wavefront takes two row tiles x
     // two token tiles (four row pairs x two token halves), else one row tile x
     // all of them
     constexpr int RT = NTG > 2 ? 2 : 1, TT = NTG > 2 ? 2 : NTG;
-    extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ int last_sh;
+    int &last_sh = *last_sh_p;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, kq = lane >> 4;
-    const int nb = a.nb, G = a.G, w = blockIdx.x, P = (int)a.P;
-    const int u0 = w * P / G, u1 = (w + 1) * P / G;
+    const int nb = a.nb;
+    const int u0 = ub + w * P / G, u1 = ub + (w + 1) * P / G;
     uint8_t *const buf0 = lds, *const buf1 = lds + a.T * kHqBlk;
     const int wrow = RT == 2 ? 32 * (wv >> 1) : 16 * wv;   // this wavefront's first row in the row group
     const int tile0 = RT == 2 ? TT * (wv & 1) : 0;          // ... and first token tile
@@ -367,7 +370,7 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(const GemmArgs a) {
         }
         if (u + 1 == u1 || blk == nb - 1) {   // the last of this row group's blocks here (uniform)
             const int first = g * nb;
-            const int wf = wg_of(first, P, G), wl = wg_of(first + nb - 1, P, G);
+            const int wf = wb + wg_of(first - ub, P, G), wl = wb + wg_of(first + nb - 1 - ub, P, G);
             const int r0 = (g - a.rg0[s]) * kRG;
             if (wf == wl) {
                 // lane holds rows rb + 16 rt + 4 kq + i of token 16 (tile0 + tt) + li
@@ -389,7 +392,7 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(const GemmArgs a) {
             } else {
                 // this work-group's partial sum of the row group, [t][row - r0]
                 // (rows past N too: in bounds of the slot, never read)
-                float *slot = a.part + (int64_t)(w + g) * a.T * kRG;
+                float *slot = a.part + (int64_t)(wb + w + g) * a.T * kRG;
 #pragma unroll
                 for (int rt = 0; rt < RT; rt++)
 #pragma unroll
@@ -457,6 +460,26 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(const GemmArgs a) {
     }
 }
 
+template <bool Q6, int NTG>
+__global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(const GemmArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ int last_sh;
+    gemm_units<Q6, NTG>(a, lds, &last_sh, 0, blockIdx.x, a.G, (int)a.P, 0);
+}
+
+// Q4_K segments then Q6_K segments sharing the activations in one launch:
+// work-groups [0, G4) take the Q4_K units [0, P4), the others the Q6_K units
+// (each type's work-groups its own instruction sequence, so a row's sums are
+// formed as in a single-type launch over the same work-group shares).
+template <int NTG>
+__global__ __launch_bounds__(kThreads) void gemm_mfma_mixed_kernel(const GemmArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ int last_sh;
+    const int w = blockIdx.x;
+    if (w < a.G4) gemm_units<false, NTG>(a, lds, &last_sh, 0, w, a.G4, (int)a.P4, 0);
+    else gemm_units<true, NTG>(a, lds, &last_sh, a.G4, w - a.G4, a.G - a.G4, (int)(a.P - a.P4), (int)a.P4);
+}
+
 // The hq records of T tokens from the v values of prepared activations (xq,
 // token stride xs): for inputs whose producer wrote only xq.
 __global__ __launch_bounds__(256) void hq_from_v_kernel(const uint8_t *xq, int64_t xs, int K, uint8_t *hq) {
@@ -488,6 +511,14 @@ void launch_g(const GemmArgs &a, size_t lds, hipStream_t st) {
     (void)raised;
     hipLaunchKernelGGL((gemm_mfma_kernel<Q6, NTG>), dim3(a.G), dim3(kThreads), lds, st, a);
 }
+template <int NTG>
+void launch_m(const GemmArgs &a, size_t lds, hipStream_t st) {
+    static const bool raised =
+        hipFuncSetAttribute((const void *)gemm_mfma_mixed_kernel<NTG>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            2 * kGemmMaxT * kHqBlk) == hipSuccess;
+    (void)raised;
+    hipLaunchKernelGGL((gemm_mfma_mixed_kernel<NTG>), dim3(a.G), dim3(kThreads), lds, st, a);
+}
 
 int cu_count() {
     static int n = 0;
@@ -514,7 +545,7 @@ int gemm_counters(int64_t rows) { return (int)(rows / kRG) + kGemmMaxSeg; }
 int gemm_launch(const GemmArgs &in, int64_t part_floats, int n_cnt, hipStream_t st) {
     GemmArgs a = in;
     if ((a.type != XJ_Q4_K && a.type != XJ_Q6_K) || a.K < 256 || a.K % 256 || a.T < 1 || a.T > kGemmMaxT ||
-        a.nseg < 1 || a.nseg > kGemmMaxSeg)
+        a.nseg < 1 || a.nseg > kGemmMaxSeg || a.n6 < 0 || a.n6 >= a.nseg || (a.n6 && a.type != XJ_Q4_K))
         return -1;
     if (!a.hq || !a.part || !a.cnt || (a.hs & 255) || ((uintptr_t)a.hq & 255) || a.hs < hq_stride(a.K)) return -1;
     a.rg0[0] = 0;
@@ -529,13 +560,36 @@ int gemm_launch(const GemmArgs &in, int64_t part_floats, int n_cnt, hipStream_t 
     a.G = (int)(a.P < cu_count() ? a.P : cu_count());
     if (a.P >= (1 << 23)) return -1;   // unit indices times G stay in 32 bits
     if (a.rg0[a.nseg] > n_cnt || (int64_t)(a.G + a.rg0[a.nseg]) * a.T * kRG > part_floats) return -1;
+    // mixed: the work-groups shared out in proportion to the two types' units
+    // (each type at least one, at most its unit count)
+    a.P4 = (int64_t)a.rg0[a.nseg - a.n6] * a.nb;
+    a.G4 = a.G;
+    if (a.n6) {
+        const int64_t P6 = a.P - a.P4;
+        if (a.G < 2) a.G = 2;
+        int64_t g4 = (a.G * a.P4 + a.P / 2) / a.P;
+        g4 = g4 < 1 ? 1 : g4 > a.G - 1 ? a.G - 1 : g4;
+        if (g4 > a.P4) g4 = a.P4;
+        if (a.G - g4 > P6) g4 = a.G - P6;
+        a.G4 = (int)g4;
+    }
     const size_t lds = 2 * (size_t)a.T * kHqBlk;
     const bool q6 = a.type == XJ_Q6_K;
-    switch ((a.T + 15) / 16) {
-    case 1: q6 ? launch_g<true, 1>(a, lds, st) : launch_g<false, 1>(a, lds, st); break;
-    case 2: q6 ? launch_g<true, 2>(a, lds, st) : launch_g<false, 2>(a, lds, st); break;
-    case 3: q6 ? launch_g<true, 3>(a, lds, st) : launch_g<false, 3>(a, lds, st); break;
-    default: q6 ? launch_g<true, 4>(a, lds, st) : launch_g<false, 4>(a, lds, st); break;
+    const int ntg = (a.T + 15) / 16;
+    if (a.n6) {
+        switch (ntg) {
+        case 1: launch_m<1>(a, lds, st); break;
+        case 2: launch_m<2>(a, lds, st); break;
+        case 3: launch_m<3>(a, lds, st); break;
+        default: launch_m<4>(a, lds, st); break;
+        }
+    } else {
+        switch (ntg) {
+        case 1: q6 ? launch_g<true, 1>(a, lds, st) : launch_g<false, 1>(a, lds, st); break;
+        case 2: q6 ? launch_g<true, 2>(a, lds, st) : launch_g<false, 2>(a, lds, st); break;
+        case 3: q6 ? launch_g<true, 3>(a, lds, st) : launch_g<false, 3>(a, lds, st); break;
+        default: q6 ? launch_g<true, 4>(a, lds, st) : launch_g<false, 4>(a, lds, st); break;
+        }
     }
     if (hipGetLastError() != hipSuccess) return -1;
     if (a.inc_ptr) {

@@ -1751,6 +1751,11 @@ int gemv_launch(const GArgs &a, hipStream_t st) {
     if (a.T == 1 && !g_grid_forced && (a.K / 64 + p.lanes - 1) / p.lanes <= 2 && n_rg <= 64 * g_cus &&
         !(all_k(a) && loop_window()))
         grid = n_rg;
+    // Q4_K-only rows looping with their window in flight: four work-groups
+    // per CU (151936 x 1024: 21.1 / 19.7 / 22.0 us at 3 / 4 / 5 per CU; the
+    // Q6_K rows of that shape 30.4 / 33.9 us at 3 / 4)
+    if (a.T == 1 && !g_grid_forced && (a.K / 64 + p.lanes - 1) / p.lanes <= 2 && all_q4k(a) && loop_window())
+        grid = n_rg < 4 * g_cus ? n_rg : 4 * g_cus;
     hipError_t e;
     switch (p.lanes) {
     case 8: e = launch_ts<8>(a, grid, st); break;

@@ -144,10 +144,14 @@ struct GemmArgs {
     float *part;     // partial sums: gemm_part_floats(rows, T) floats
     int32_t *cnt;    // arrival counters: gemm_counters(rows) ints, zero before the first launch
     int32_t *inc_ptr; int32_t inc_by;   // optional: *inc_ptr += inc_by once
+    // n6 > 0: the last n6 segments hold Q6_K rows, the others Q4_K rows (type
+    // = XJ_Q4_K); one launch, each type on its own share of the work-groups
+    int32_t n6;
     // set by gemm_launch
     int32_t rg0[kGemmMaxSeg + 1];       // first row group of each segment (prefix)
     int32_t nb, G;                      // blocks per row, work-groups
     int64_t P;                          // units
+    int32_t G4; int64_t P4;             // the Q4_K work-groups and units of a mixed launch
 };
 // Capacities for a launch over `rows` rows in all (at most kGemmMaxSeg) segments.
 int64_t gemm_part_floats(int64_t rows, int T);

@@ -276,16 +276,12 @@ struct Gemv {
         const bool rms = a.pro == PRO_RMSU;
         if (rms && rms_scale_launch(a.xq, xs, a.K, T, a.eps, tsc, st)) return -1;
         const int mt = gemm_max_tokens(), tile = gemv_max_tile(a.K);
-        // the segments of each type in one launch, sharing the activations
-        for (uint32_t ty : {(uint32_t)XJ_Q4_K, (uint32_t)XJ_Q6_K}) {
-            GemmArgs g{};
-            g.type = ty; g.K = a.K; g.hs = hs; g.part = part; g.cnt = cnt;
-            for (int i = 0; i < a.nseg; i++) {
-                const GSeg &s = a.seg[i];
-                if (s.type != ty) continue;
-                g.seg[g.nseg++] = GemmSeg{s.w, s.n_rows, s.y, s.ys, s.epi == EPI_ADD};
-            }
-            if (!g.nseg) continue;
+        // the Q4_K and Q6_K segments in one launch sharing the activations,
+        // each type on its own share of the work-groups (an attention
+        // layer's q|k and v: 20 us less per chunk than a launch of its own
+        // for v); XJ_GEMM_MIXED=0: one launch per type
+        static const bool mixed_on = env_int("XJ_GEMM_MIXED", 1) != 0;
+        auto launch_tokens = [&](const GemmArgs &g) {
             for (int t0 = 0; t0 < T; t0 += mt) {
                 GemmArgs b = g;
                 b.T = T - t0 < mt ? T - t0 : mt;
@@ -294,6 +290,26 @@ struct Gemv {
                 b.tsc = rms ? tsc + t0 : nullptr;
                 if (gemm_launch(b, part_floats, n_cnt, st)) return -1;
             }
+            return 0;
+        };
+        GemmArgs gk[2]{};
+        for (int k = 0; k < 2; k++) {
+            const uint32_t ty = k ? XJ_Q6_K : XJ_Q4_K;
+            GemmArgs &g = gk[k];
+            g.type = ty; g.K = a.K; g.hs = hs; g.part = part; g.cnt = cnt;
+            for (int i = 0; i < a.nseg; i++) {
+                const GSeg &s = a.seg[i];
+                if (s.type == ty) g.seg[g.nseg++] = GemmSeg{s.w, s.n_rows, s.y, s.ys, s.epi == EPI_ADD};
+            }
+        }
+        if (mixed_on && gk[0].nseg && gk[1].nseg) {
+            GemmArgs g = gk[0];
+            for (int i = 0; i < gk[1].nseg; i++) g.seg[g.nseg++] = gk[1].seg[i];
+            g.n6 = gk[1].nseg;
+            if (launch_tokens(g)) return -1;
+        } else {
+            for (int k = 0; k < 2; k++)
+                if (gk[k].nseg && launch_tokens(gk[k])) return -1;
         }
         for (int i = 0; i < a.nseg; i++) {
             const GSeg &s = a.seg[i];
