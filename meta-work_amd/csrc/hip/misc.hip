@@ -45,26 +45,33 @@ __global__ __launch_bounds__(256) void embed_kernel(const EmbedArgs a) {
 // last row's id; hist/step (optional, T == 1) append it to the history; e.x
 // (optional, T == 1): the id's embedding row into e.x, the next decode step's
 // input (so the step needs no embedding launch of its own).
-__global__ __launch_bounds__(256) void finalize_kernel(const unsigned long long *amax, int n_part, int T,
-                                                       int32_t *out, int32_t *tok_out, int32_t *hist, int32_t *step,
-                                                       const EmbedArgs e) {
+constexpr int kFinThreads = 1024;
+__global__ __launch_bounds__(kFinThreads) void finalize_kernel(const unsigned long long *amax, int n_part, int T,
+                                                               int32_t *out, int32_t *tok_out, int32_t *hist,
+                                                               int32_t *step, const EmbedArgs e) {
     const int t = blockIdx.x, tid = threadIdx.x;
-    __shared__ unsigned long long red[256];
+    __shared__ unsigned long long red[kFinThreads / 64];
     unsigned long long m = 0ull;
-    for (int i0 = tid; i0 < n_part; i0 += 256 * 8) {   // eight loads in flight per thread
+    // eight loads in flight per thread: the 4B head's 4748 partials in one round
+    for (int i0 = tid; i0 < n_part; i0 += kFinThreads * 8) {
         unsigned long long k[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) k[j] = i0 + 256 * j < n_part ? amax[(int64_t)t * n_part + i0 + 256 * j] : 0ull;
+        for (int j = 0; j < 8; j++)
+            k[j] = i0 + kFinThreads * j < n_part ? amax[(int64_t)t * n_part + i0 + kFinThreads * j] : 0ull;
 #pragma unroll
         for (int j = 0; j < 8; j++) m = k[j] > m ? k[j] : m;
     }
-    red[tid] = m;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (tid < s && red[tid + s] > red[tid]) red[tid] = red[tid + s];
-        __syncthreads();
+    // the keys are distinct (each holds its index), so any order of maxima gives the same key
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long q = __shfl_xor(m, off, 64);
+        m = q > m ? q : m;
     }
-    const int32_t id = (int32_t)xjd::argmax_key_index(red[0]);   // red[0] is final for every thread
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = 0ull;
+#pragma unroll
+    for (int w = 0; w < kFinThreads / 64; w++) m = red[w] > m ? red[w] : m;
+    const int32_t id = (int32_t)xjd::argmax_key_index(m);
     if (tid == 0) {
         if (out) out[t] = id;
         if (tok_out && t == T - 1) *tok_out = id;
@@ -73,7 +80,7 @@ __global__ __launch_bounds__(256) void finalize_kernel(const unsigned long long 
             *step += 1;
         }
     }
-    if (e.x) embed_row(e.w, id, e.x);
+    if (e.x) embed_row(e.w, id, e.x, kFinThreads);
 }
 
 __global__ __launch_bounds__(256) void argmax_rows_kernel(const float *x, int n, int32_t *out) {
@@ -119,7 +126,7 @@ int argmax_finalize_launch(const unsigned long long *amax, int n_part, int T, in
     if (hist && T != 1) return -1;
     if (embed && (T != 1 || embed->w.k % 32 || !embed->x)) return -1;
     const EmbedArgs e = embed ? *embed : EmbedArgs{};
-    hipLaunchKernelGGL(finalize_kernel, dim3(T), dim3(256), 0, st, amax, n_part, T, out, tok_out, hist, step, e);
+    hipLaunchKernelGGL(finalize_kernel, dim3(T), dim3(kFinThreads), 0, st, amax, n_part, T, out, tok_out, hist, step, e);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
