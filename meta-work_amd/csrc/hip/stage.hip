@@ -1128,6 +1128,24 @@ struct xjh_chain {
     hipGraph_t graph_s = nullptr;
 };
 
+// Parts of a single stage's layers in a prompt of several chunks
+// (XJ_STAGE_SPLIT, with chunks overlapped on the parts' streams), else 1.
+static int stage_parts(const xjh_chain *c) {
+    static const bool overlap = env_int("XJ_CHAIN_OVERLAP", 1) != 0;
+    static const int split_env = env_int("XJ_STAGE_SPLIT", 3);
+    if (c->st.size() != 1 || !overlap) return 1;
+    const int nl = c->st[0]->s.l1 - c->st[0]->s.l0;
+    return split_env < 1 ? 1 : split_env > kMaxParts ? kMaxParts : split_env > nl ? nl : split_env;
+}
+// the later parts' scratch sets (twin_new), created once
+static int chain_twins(xjh_chain *c, int npart, char *err, size_t errlen) {
+    while ((int)c->twins.size() < npart - 1) {
+        HStage *T = twin_new(c->st[0], err, errlen);
+        if (!T) return -1;
+        c->twins.push_back(T);
+    }
+    return 0;
+}
 extern "C" void xjh_chain_free(xjh_chain *c) {
     if (!c) return;
     if (c->stream) (void)hipStreamSynchronize(c->stream);
@@ -1191,6 +1209,13 @@ extern "C" xjh_chain *xjh_chain_new(xj_stage **stages, int n, char *err, size_t 
             xjh_chain_free(c);
             return nullptr;
         }
+    // a stage whose chunks take the prefill GEMM gets its parts' scratch now,
+    // so that its first long prompt does not pay for the allocations
+    // (a 4B 1024-token prefill: 0.083 s on the first call, 0.073 s after)
+    if (c->mb >= Gemv::kGemmMinT && stage_parts(c) > 1 && chain_twins(c, stage_parts(c), err, errlen)) {
+        xjh_chain_free(c);
+        return nullptr;
+    }
     return c;
 }
 
@@ -1222,7 +1247,6 @@ static int chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int 
     if (n <= 0) { snprintf(err, errlen, "no tokens"); return -1; }
     if (keep && n > B) { snprintf(err, errlen, "verify batch %d exceeds max_batch %d", n, B); return -1; }
     static const bool overlap = env_int("XJ_CHAIN_OVERLAP", 1) != 0;
-    static const int split_env = env_int("XJ_STAGE_SPLIT", 3);
     // the pipeline's parts: every stage, or a single stage's layers in
     // XJ_STAGE_SPLIT contiguous parts (the later ones on twins' scratch and
     // streams) when the prompt spans several chunks
@@ -1230,13 +1254,9 @@ static int chain_eval(xjh_chain *c, const int32_t *tokens, int n, int nlog, int 
     std::vector<Part> parts;
     HStage *S0 = c->st[0];
     const int nl = S0->s.l1 - S0->s.l0;
-    const int npart = split_env < 1 ? 1 : split_env > kMaxParts ? kMaxParts : split_env > nl ? nl : split_env;
-    if (ns == 1 && overlap && npart > 1 && n > B && !keep) {
-        while ((int)c->twins.size() < npart - 1) {
-            HStage *T = twin_new(S0, err, errlen);
-            if (!T) return -1;
-            c->twins.push_back(T);
-        }
+    const int npart = stage_parts(c);
+    if (npart > 1 && n > B && !keep) {
+        if (chain_twins(c, npart, err, errlen)) return -1;
         for (int p = 0; p < npart; p++) {
             HStage *S = p ? c->twins[p - 1] : S0;
             if (p) {
