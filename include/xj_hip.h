@@ -69,8 +69,9 @@ const char *xj_hip_tune_note(void);
 
 /* Bytes of HBM a stage holds besides the repacked weights
  * (counterpart of xj_stage_state_bytes, xj_stage.h:57). A single-stage
- * chain (xjh_chain_new) that prefills a prompt of several chunks adds up to
- * XJ_STAGE_SPLIT - 1 further sets of the stage's scratch on first use. */
+ * chain (xjh_chain_new) adds up to XJ_STAGE_SPLIT - 1 further sets of the
+ * stage's scratch for prompts of several chunks: when it is built if
+ * max_batch >= 16, else on the first such prompt. */
 uint64_t    xj_hip_stage_state_bytes(const xj_model *m, int l0, int l1, int n_ctx, int max_batch);
 
 /* Copy the whole recurrent state (conv + DeltaNet state of every layer) of a
