@@ -25,6 +25,8 @@ def _weights(t, rows, k, seed):
     (xp.Q4_K, 1000, 2560),     # rows not a multiple of 16 or 64
     (xp.Q6_K, 517, 9216),      # few rows: K split over work-groups, reduce launch
     (xp.Q4_K, 33, 256),        # one block per row
+    (xp.Q4_K, 2560, 4096),     # 320 units: 160 work-groups of two (ssm_out / wo)
+    (xp.Q6_K, 1024, 9216),     # 288 units: 144 work-groups of two, a row group over 18
 ])
 @pytest.mark.parametrize("T", [1, 16, 17, 40, 64])
 def test_gemm_matches_oracle_and_gemv(t, rows, k, T):
