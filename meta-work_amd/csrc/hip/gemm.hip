@@ -39,6 +39,7 @@
 #include "xj_hip.h"
 #include "xq.h"
 
+#include <algorithm>
 #include <cstdint>
 
 namespace xjk {
@@ -566,20 +567,26 @@ int gemm_launch(const GemmArgs &in, int64_t part_floats, int n_cnt, hipStream_t 
         a.G = (int)((a.P + per - 1) / per);
     }
     if (a.P >= (1 << 23)) return -1;   // unit indices times G stay in 32 bits
-    if (a.rg0[a.nseg] > n_cnt || (int64_t)(a.G + a.rg0[a.nseg]) * a.T * kRG > part_floats) return -1;
-    // mixed: the work-groups shared out in proportion to the two types' units
-    // (each type at least one, at most its unit count)
+    // mixed: the CUs shared out so that the longer of the two types' shares
+    // is shortest, a Q6_K unit counted as 3/2 of a Q4_K unit (its three
+    // products per group against two), then each type on the fewest
+    // work-groups that keep its share
     a.P4 = (int64_t)a.rg0[a.nseg - a.n6] * a.nb;
     a.G4 = a.G;
     if (a.n6) {
-        const int64_t P6 = a.P - a.P4;
-        if (a.G < 2) a.G = 2;
-        int64_t g4 = (a.G * a.P4 + a.P / 2) / a.P;
-        g4 = g4 < 1 ? 1 : g4 > a.G - 1 ? a.G - 1 : g4;
-        if (g4 > a.P4) g4 = a.P4;
-        if (a.G - g4 > P6) g4 = a.G - P6;
-        a.G4 = (int)g4;
+        const int64_t P6 = a.P - a.P4, ncu = cu_count();
+        int64_t best = -1, b4 = 1, b6 = 1;
+        for (int64_t g6 = 1; g6 < ncu && g6 <= P6; g6++) {
+            const int64_t g4 = ncu - g6 < a.P4 ? ncu - g6 : a.P4;
+            if (g4 < 1) break;
+            const int64_t c = std::max(2 * ((a.P4 + g4 - 1) / g4), 3 * ((P6 + g6 - 1) / g6));
+            if (best < 0 || c < best) best = c, b4 = g4, b6 = g6;
+        }
+        const int64_t s4 = (a.P4 + b4 - 1) / b4, s6 = (P6 + b6 - 1) / b6;
+        a.G4 = (int)((a.P4 + s4 - 1) / s4);
+        a.G = a.G4 + (int)((P6 + s6 - 1) / s6);
     }
+    if (a.rg0[a.nseg] > n_cnt || (int64_t)(a.G + a.rg0[a.nseg]) * a.T * kRG > part_floats) return -1;
     const size_t lds = 2 * (size_t)a.T * kHqBlk;
     const bool q6 = a.type == XJ_Q6_K;
     const int ntg = (a.T + 15) / 16;
